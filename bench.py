@@ -1,0 +1,259 @@
+"""Benchmark of the MI355X multi-LoRA linear (forward + backward).
+
+One step = forward + backward of the six LoRA linears of one Wan-1.3B DiT
+block (q, k, v, o: 1536->1536; ffn.0: 1536->8960; ffn.2: 8960->1536) over
+65520 tokens = two roles (generator, fake critic) of 32760 tokens, each with
+its own rank-64 adapter on the shared frozen bf16 base,
+through the drop-in autograd op with inputs resident in HBM.
+
+Prints one JSON line: metric/value (TFLOP/s of the whole step), the roofline
+of the dominant kernel measured with HIP events, the LoRA kernels' HBM GB/s,
+and a CPU baseline (the reference per-adapter path in fp32 torch on host
+cores, timed on a bounded sample of the same workload).
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--config wan13b]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+HBM_PEAK_GBS = 8000.0          # MI355X HBM3E
+MFMA_BF16_PEAK_TFLOPS = 2500.0  # dense bf16
+
+
+def parse():
+    p = argparse.ArgumentParser()
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=10)
+    p.add_argument("--warmup", type=int, default=3)
+    p.add_argument("--config", default="wan13b")
+    p.add_argument("--kernel-reps", type=int, default=10)
+    p.add_argument("--cpu-seconds", type=float, default=12.0, help="bounded CPU-baseline sample budget")
+    p.add_argument("--no-cpu-baseline", action="store_true")
+    return p.parse_args()
+
+
+def main():
+    args = parse()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(json.dumps({"error": "this build measures one GPU only: the multi-LoRA linear is benchmarked "
+                                   "at N=1 (multi-GPU sharding is a design note, not a launched path); "
+                                   f"--gpus {args.gpus} / WORLD_SIZE {world} is not supported"}), flush=True)
+        sys.exit(2)
+
+    import torch
+    import __graft_entry__
+    pkg = __graft_entry__.load_package()
+    pkg.load_library()
+    from dmd_system_amd import kernels, workloads
+
+    if not torch.cuda.is_available():
+        raise RuntimeError("bench.py needs a ROCm GPU")
+    dev = torch.device("cuda:0")
+    props = torch.cuda.get_device_properties(dev)
+    cfg = workloads.CONFIGS[args.config]
+    routing = cfg.routing
+    scales = [cfg.scale] * len(cfg.ranks)
+
+    # ---------------- inputs (resident in HBM)
+    lins = []
+    for i, (name, K, N) in enumerate(cfg.linears()):
+        x, w, b, As, Bs, dy = workloads.make_linear(cfg, K, N, dev, seed=cfg.seed * 100 + i)
+        x.requires_grad_(True)
+        for t in As + Bs:
+            t.requires_grad_(True)
+        lins.append(dict(name=name, K=K, N=N, x=x, w=w, b=b, As=As, Bs=Bs, dy=dy))
+    torch.cuda.synchronize()
+
+    def step():
+        for L in lins:
+            for t in [L["x"], *L["As"], *L["Bs"]]:
+                t.grad = None
+            y = pkg.multi_lora_linear(L["x"], L["w"], L["b"], L["As"], L["Bs"], scales, routing)
+            y.backward(L["dy"])
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    ev0.record()
+    for _ in range(args.steps):
+        step()
+    ev1.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    gpu_ms = ev0.elapsed_time(ev1)
+    ms_per_step = max(gpu_ms, wall * 1e3) / args.steps
+    flops_step = sum(cfg.flops_fwd_bwd(L["K"], L["N"]) for L in lins)
+    tflops = flops_step / (ms_per_step * 1e-3) / 1e12
+    print(f"# step {ms_per_step:.3f} ms, {tflops:.1f} TFLOP/s", file=sys.stderr, flush=True)
+
+    # ---------------- per-kernel timing with HIP events on the launch stream
+    reps = args.kernel_reps
+    stream = torch.cuda.current_stream(dev)
+
+    def timed(fn):
+        fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(reps):
+            fn()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / reps * 1e-3  # seconds per launch
+
+    from dmd_system_amd.function import _as_operand
+    seg = list(zip(cfg.seg_lengths, cfg.seg_adapters))
+    R = kernels.padded_rank(cfg.ranks)
+    fam = {k: {"time": 0.0, "flops": 0, "bytes": 0, "launches": 0}
+           for k in ("gemm_fwd", "gemm_dx", "shrink_x", "shrink_dy", "seg_outer_dB", "seg_outer_dA")}
+    with torch.no_grad():
+        for L in lins:
+            M, K, N = cfg.tokens, L["K"], L["N"]
+            A_ops = [_as_operand(a) for a in L["As"]]
+            B_ops = [_as_operand(v) for v in L["Bs"]]
+            x, dy = L["x"].detach(), L["dy"]
+            h_rows, h_cols = kernels.shrink(x, A_ops, 0, scales, routing, True, R)
+            g_rows, g_cols = kernels.shrink(dy, B_ops, 1, scales, routing, True, R)
+            lora_mr = sum(m * cfg.ranks[a] for m, a in seg if a >= 0)
+            r_sum = sum(cfg.ranks)
+            runs = {
+                "gemm_fwd": (lambda: kernels.gemm_fwd(x, L["w"], L["b"], h_rows, B_ops, routing),
+                             2 * M * K * N + 2 * lora_mr * N, 0),
+                "gemm_dx": (lambda: kernels.gemm_dx(dy, L["w"], g_rows, A_ops, routing),
+                            2 * M * K * N + 2 * lora_mr * K, 0),
+                "shrink_x": (lambda: kernels.shrink(x, A_ops, 0, scales, routing, True, R),
+                             2 * lora_mr * K, M * K * 2 + r_sum * K * 2 + lora_mr * (2 + 4)),
+                "shrink_dy": (lambda: kernels.shrink(dy, B_ops, 1, scales, routing, True, R),
+                              2 * lora_mr * N, M * N * 2 + r_sum * N * 2 + lora_mr * (2 + 4)),
+                "seg_outer_dB": (lambda: kernels.seg_outer(dy, h_cols, cfg.ranks, routing, 0,
+                                                           [torch.bfloat16] * len(cfg.ranks)),
+                                 2 * lora_mr * N, M * N * 2 + lora_mr * 4 + r_sum * N * 2),
+                "seg_outer_dA": (lambda: kernels.seg_outer(x, g_cols, cfg.ranks, routing, 1,
+                                                           [torch.bfloat16] * len(cfg.ranks)),
+                                 2 * lora_mr * K, M * K * 2 + lora_mr * 4 + r_sum * K * 2),
+            }
+            for k, (fn, fl, by) in runs.items():
+                t = timed(fn)
+                fam[k]["time"] += t
+                fam[k]["flops"] += fl
+                fam[k]["bytes"] += by
+                fam[k]["launches"] += 1
+            del h_rows, h_cols, g_rows, g_cols
+    kern = {}
+    for k, v in fam.items():
+        avg = v["time"] / v["launches"]
+        kern[k] = {"avg_us": round(avg * 1e6, 2), "launches_per_step": v["launches"],
+                   "tflops": round(v["flops"] / v["time"] / 1e12, 1),
+                   "gbs": round(v["bytes"] / v["time"] / 1e9, 1) if v["bytes"] else None}
+    gem = fam["gemm_fwd"]
+    gem_ach = gem["flops"] / gem["time"] / 1e12
+    roofline = {"kernel": "gemm_kernel NT (base GEMM + fused LoRA expand), avg over the 6 block linears",
+                "bound": "mfma", "achieved": round(gem_ach, 1), "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                "frac": round(gem_ach / MFMA_BF16_PEAK_TFLOPS, 4), "traffic": None,
+                "avg_launch_us": round(gem["time"] / gem["launches"] * 1e6, 2),
+                "flops_per_launch": gem["flops"] // gem["launches"]}
+    lora = {}
+    for k in ("shrink_x", "shrink_dy", "seg_outer_dB", "seg_outer_dA"):
+        v = fam[k]
+        gbs = v["bytes"] / v["time"] / 1e9
+        lora[k] = {"achieved_gbs": round(gbs, 1), "frac_hbm": round(gbs / HBM_PEAK_GBS, 4),
+                   "avg_us": kern[k]["avg_us"]}
+
+    # ---------------- vendor GEMM reference (context only): torch bf16 matmul, same shapes
+    vendor = {}
+    with torch.no_grad():
+        for L in lins[3:6]:
+            x = L["x"].detach()
+            t = timed(lambda: torch.matmul(x, L["w"].T))
+            vendor[f"{L['name']} {L['K']}->{L['N']}"] = round(2 * cfg.tokens * L["K"] * L["N"] / t / 1e12, 1)
+
+    # ---------------- CPU baseline: reference per-adapter path, fp32 torch, bounded sample
+    cpu = None
+    if not args.no_cpu_baseline:
+        cpu = cpu_baseline(cfg, args.cpu_seconds)
+
+    out = {
+        "metric": "multi-LoRA linear fwd+bwd TFLOP/s at Wan-1.3B shape",
+        "value": round(tflops, 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1) activations, N(0,1/in) frozen base, Kaiming-uniform A, N(0,0.02) B)",
+        "config": {"workload": f"{cfg.name}: fwd+bwd of the 6 DiT block linears "
+                               f"(q,k,v,o {cfg.hidden}->{cfg.hidden}; ffn {cfg.hidden}->{cfg.ffn}->{cfg.hidden}), "
+                               f"{cfg.tokens} tokens in segments {list(cfg.seg_lengths)}, ranks {list(cfg.ranks)}, "
+                               f"scale {cfg.scale}, bias on",
+                   "tokens": cfg.tokens, "flops_per_step": flops_step, "pct_mfma_peak": round(
+                       tflops / MFMA_BF16_PEAK_TFLOPS * 100, 2)},
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+        "lora_hbm": lora,
+        "kernels": kern,
+        "vendor_gemm_tflops": vendor,
+        "device": {"name": props.name, "cus": props.multi_processor_count,
+                   "gcn_arch": getattr(props, "gcnArchName", "")},
+    }
+    print(json.dumps(out), flush=True)
+
+
+def cpu_baseline(cfg, budget_s: float):
+    """Reference per-adapter path (training/low_rank.py:26-28 per segment + autograd) in fp32 on host cores."""
+    import torch
+    from oracle import torch_reference as TR
+    from dmd_system_amd import workloads
+
+    rows_per_seg = 1024
+    sample = workloads.LoraConfig(
+        name="cpu-sample", tokens=rows_per_seg * len(cfg.seg_lengths), hidden=cfg.hidden, ffn=cfg.ffn,
+        ranks=cfg.ranks, seg_lengths=(rows_per_seg,) * len(cfg.seg_lengths), seg_adapters=cfg.seg_adapters,
+        scale=cfg.scale, seed=cfg.seed)
+    cpu = torch.device("cpu")
+    lin = []
+    for i, (name, K, N) in enumerate(sample.linears()):
+        x, w, b, As, Bs, dy = workloads.make_linear(sample, K, N, cpu, seed=7 + i, dtype=torch.float32)
+        lin.append((K, N, x, w, b, As, Bs, dy))
+    off = sample.routing.seg_offsets
+    ids = sample.routing.adapter_ids
+    scales = [cfg.scale] * len(cfg.ranks)
+
+    def one_block():
+        for K, N, x, w, b, As, Bs, dy in lin:
+            TR.per_adapter_step(x, w, b, As, Bs, scales, off, ids, dy)
+
+    one_block()  # warmup
+    t0 = time.perf_counter()
+    reps = 0
+    while True:
+        one_block()
+        reps += 1
+        el = time.perf_counter() - t0
+        if el >= budget_s or reps >= 50:
+            break
+    flops = sum(sample.flops_fwd_bwd(K, N) for _, K, N in sample.linears())
+    return {"value": round(flops * reps / el / 1e12, 4), "unit": "TFLOP/s", "cores": torch.get_num_threads(),
+            "kind": "port",
+            "sample": f"{reps} x fwd+bwd of the 6 block linears at {sample.tokens} tokens "
+                      f"({rows_per_seg} per segment), fp32 torch per-adapter path, {el:.1f} s; "
+                      f"host os.cpu_count()={os.cpu_count()}"}
+
+
+if __name__ == "__main__":
+    main()

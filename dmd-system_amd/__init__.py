@@ -1,0 +1,27 @@
+"""MI355X-native batched multi-LoRA linear (gfx950 HIP kernels behind a C ABI).
+
+Public API:
+    SegmentRouting, BASE_ONLY            row-segment -> adapter routing
+    MultiLoRAFunction, multi_lora_linear autograd op
+    TrainableLowRankLinear, trainable_scope, MultiLoRALinear   drop-in modules
+    kernels                              torch front end of each C-ABI entry point
+    load_library()                       load libmlora.so (raises if missing)
+
+The directory name is not a Python identifier; importers load it as
+``dmd_system_amd`` by path (see ``load_package`` in the repository's
+``__graft_entry__.py``).
+"""
+from . import _lib, kernels
+from .function import MultiLoRAFunction, multi_lora_linear
+from .low_rank import MultiLoRALinear, TrainableLowRankLinear, trainable_scope
+from .routing import BASE_ONLY, SegmentRouting
+
+
+def load_library():
+    return _lib.load()
+
+
+__all__ = [
+    "BASE_ONLY", "SegmentRouting", "MultiLoRAFunction", "multi_lora_linear", "MultiLoRALinear",
+    "TrainableLowRankLinear", "trainable_scope", "kernels", "load_library",
+]

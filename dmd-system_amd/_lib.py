@@ -1,0 +1,94 @@
+"""ctypes binding of the C ABI in ``include/mlora.h`` (``libmlora.so``).
+
+The library is built in-tree by ``build.py``. Loading it never falls back to
+anything else: a missing or stale library is an error for every caller.
+"""
+from __future__ import annotations
+
+import ctypes
+from pathlib import Path
+
+LIB_PATH = Path(__file__).resolve().parent / "libmlora.so"
+
+ABI_VERSION = 1
+MAX_SEGMENTS = 128
+MAX_ADAPTERS = 32
+MAX_RANK = 256
+
+F32, BF16, FP8_E4M3 = 0, 1, 2
+
+OK = 0
+ERR_INVALID, ERR_UNSUPPORTED, ERR_WORKSPACE, ERR_LAUNCH, ERR_LIMIT = -1, -2, -3, -4, -5
+
+# Every entry point declared in include/mlora.h with its ctypes signature.
+_vp, _i64, _i32, _int = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int32, ctypes.c_int
+_pvp = ctypes.POINTER(ctypes.c_void_p)
+_pi32 = ctypes.POINTER(ctypes.c_int32)
+_pi64 = ctypes.POINTER(ctypes.c_int64)
+_pf32 = ctypes.POINTER(ctypes.c_float)
+
+SIGNATURES = {
+    "mlora_abi_version": (_int, []),
+    "mlora_status_string": (ctypes.c_char_p, [_int]),
+    "mlora_shrink": (_int, [_vp, _i64, _i64, _i64, _pvp, _int, _pi32, _pf32, _i32,
+                            _pi64, _pi32, _i32, _vp, _i64, _vp, _i64, _vp]),
+    "mlora_gemm_fwd": (_int, [_vp, _i64, _i64, _i64, _vp, _i64, _i64, _vp, _int, _vp, _i64,
+                              _pvp, _pi32, _i32, _pi64, _pi32, _i32, _vp, _i64, _int, _vp]),
+    "mlora_gemm_dx": (_int, [_vp, _i64, _i64, _i64, _vp, _i64, _i64, _vp, _i64,
+                             _pvp, _pi32, _i32, _pi64, _pi32, _i32, _vp, _i64, _vp]),
+    "mlora_seg_outer": (_int, [_vp, _i64, _i64, _i64, _vp, _i64, _pvp, _int, _int, _pi32, _i32,
+                               _pi64, _pi32, _i32, _vp, _i64, _vp]),
+    "mlora_seg_outer_workspace_bytes": (_i64, [_i64, _i64, _pi32, _i32, _pi64, _pi32, _i32]),
+}
+
+_LIB = None
+
+
+class MloraError(RuntimeError):
+    """A C-ABI call returned a negative status."""
+
+    def __init__(self, name: str, status: int, message: str):
+        super().__init__(f"{name} failed with status {status}: {message}")
+        self.status = status
+
+
+def load():
+    """Load ``libmlora.so`` once and bind every declared symbol."""
+    global _LIB
+    if _LIB is not None:
+        return _LIB
+    if not LIB_PATH.exists():
+        raise RuntimeError(f"{LIB_PATH} is missing: build it with `python dmd-system_amd/build.py` "
+                           "(or __graft_entry__.build()) before using the HIP path")
+    lib = ctypes.CDLL(str(LIB_PATH))
+    for name, (res, args) in SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    version = lib.mlora_abi_version()
+    if version != ABI_VERSION:
+        raise RuntimeError(f"libmlora ABI version {version} != expected {ABI_VERSION}; rebuild the library")
+    _LIB = lib
+    return lib
+
+
+def check(name: str, status: int) -> None:
+    if status != OK:
+        msg = load().mlora_status_string(status).decode()
+        raise MloraError(name, status, msg)
+
+
+def ptr_array(values) -> ctypes.Array:
+    return (ctypes.c_void_p * max(1, len(values)))(*[v or None for v in values])
+
+
+def i32_array(values) -> ctypes.Array:
+    return (ctypes.c_int32 * max(1, len(values)))(*values)
+
+
+def i64_array(values) -> ctypes.Array:
+    return (ctypes.c_int64 * max(1, len(values)))(*values)
+
+
+def f32_array(values) -> ctypes.Array:
+    return (ctypes.c_float * max(1, len(values)))(*values)

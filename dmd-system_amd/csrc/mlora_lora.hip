@@ -1,0 +1,528 @@
+// Segment-gathered LoRA kernels (HBM-bound): shrink and the adapter-gradient
+// reductions.
+//
+// shrink     h[m, j]   = s_a · Σ_k P[m,k]·Op_a(j,k)           (X·Aᵀ forward, s·dY·B backward)
+// seg_outer  D_a[c, j] = Σ_{m ∈ rows of a} P[m,c]·Qt[j,m]      (dB_a = s·dYᵀ·h, dA_a = gᵀ·X)
+//
+// Both stream the big operand P (X or dY) exactly once at full width and keep
+// the adapter operands, which are small, in LDS or L2. Work is organised per
+// segment, so a workgroup never mixes adapters. Reference semantics:
+// training/low_rank.py:26-28 and its autograd backward.
+#include "mlora_common.h"
+#include "mlora_host.h"
+
+namespace mlora {
+
+// ============================================================== shrink
+//
+// Workgroup: 4 waves x WT row-tiles of 32 rows of one segment, all r <= 32*RT
+// columns of its adapter. P fragments go straight from HBM to registers
+// (each lane streams 64 contiguous bytes of one row per 64-wide k-chunk; the
+// k order inside a chunk is permuted identically for both operands). The
+// adapter operand chunk [32*RT x 64] is shared through double-buffered LDS.
+// v_mfma_f32_32x32x16_bf16: rows <- P (m), columns <- Op (j), so each lane
+// holds 4 consecutive m of one j: the transposed fp32 copy is written as
+// 4 consecutive floats.
+
+struct ShrinkArgs {
+  const uint16_t *P;
+  uint16_t *Hr;  // bf16 [M, ldh]
+  float *Hc;     // fp32 [ldh, ldhc] or null
+  int64_t ldp, ldh, ldhc;
+  int32_t M, K;
+  int32_t op_layout;  // 0: [r, K]; 1: [K, r]
+  int32_t tile_rows;
+  int32_t tile_start[kMaxSeg + 1];
+  AdapterTable op;
+  SegTable seg;
+};
+
+template <int WT, int RT, int OPL>
+__global__ __launch_bounds__(256) void shrink_kernel(const ShrinkArgs args) {
+  constexpr int BMS = 4 * WT * 32;
+  constexpr int OPROWS = 32 * RT;
+  __shared__ uint4 lds[2 * OPROWS * 8];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+
+  // workgroup -> (segment, tile)
+  const int bid = blockIdx.x;
+  int s = 0;
+  while (s + 1 < args.seg.n && args.tile_start[s + 1] <= bid) ++s;
+  const int a = args.seg.aid[s];
+  const int r = args.op.rank[a];
+  const float scale = args.op.scale[a];
+  const uint16_t *op = args.op.ptr[a];
+  const int m0 = args.seg.off[s] + (bid - args.tile_start[s]) * BMS;
+  const int mend = args.seg.off[s + 1];
+  const int K = args.K;
+  const int nk = (K + 63) / 64;
+
+  // ---- operand loaders
+  const uint4 zero = make_uint4(0, 0, 0, 0);
+  constexpr int OP_CH = (OPROWS * 8 + 255) / 256;  // layout 0: chunks per thread
+  uint4 opr[OPL == 0 ? OP_CH : 8];
+  auto load_op = [&](int kc) {
+    const int k0 = kc * 64;
+    if constexpr (OPL == 0) {
+#pragma unroll
+      for (int i = 0; i < OP_CH; ++i) {
+        const int q = tid + i * 256;
+        const int j = q >> 3, c = q & 7;
+        const int kk = k0 + 8 * c;
+        opr[i] = (q < OPROWS * 8 && j < r && kk < K) ? *reinterpret_cast<const uint4 *>(op + (int64_t)j * K + kk) : zero;
+      }
+    } else {
+      // [K, r]: thread b < 8*(OPROWS/8) loads an 8x8 block (8 k rows x 8 j)
+      const int b = tid;
+      const int kb = b / (OPROWS / 8), jb = b % (OPROWS / 8);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int kk = k0 + 8 * kb + e;
+        opr[e] = (b < OPROWS && 8 * jb < r && kk < K) ? *reinterpret_cast<const uint4 *>(op + (int64_t)kk * r + 8 * jb)
+                                                        : zero;
+      }
+    }
+  };
+  auto store_op = [&](uint4 *dst) {
+    if constexpr (OPL == 0) {
+#pragma unroll
+      for (int i = 0; i < OP_CH; ++i) {
+        const int q = tid + i * 256;
+        if (q < OPROWS * 8) dst[lds_chunk_offset(q >> 3, q & 7)] = opr[i];
+      }
+    } else {
+      const int b = tid;
+      if (b < OPROWS) {
+        const int kb = b / (OPROWS / 8), jb = b % (OPROWS / 8);
+        uint4 tr[8];
+        transpose8x8_b16(opr, tr);
+#pragma unroll
+        for (int t = 0; t < 8; ++t) dst[lds_chunk_offset(8 * jb + t, kb)] = tr[t];
+      }
+    }
+  };
+  uint4 pc[WT][4], pn[WT][4];
+  auto load_p = [&](uint4 (&dst)[WT][4], int kc) {
+#pragma unroll
+    for (int i = 0; i < WT; ++i) {
+      const int row = m0 + 32 * (wave * WT + i) + (lane & 31);
+      const bool ok = row < mend;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int kk = kc * 64 + 32 * (lane >> 5) + 8 * q;
+        dst[i][q] = (ok && kk < K) ? *reinterpret_cast<const uint4 *>(args.P + (int64_t)row * args.ldp + kk) : zero;
+      }
+    }
+  };
+
+  f32x16 acc[WT][RT];
+#pragma unroll
+  for (int i = 0; i < WT; ++i)
+#pragma unroll
+    for (int j = 0; j < RT; ++j)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
+
+  load_op(0);
+  load_p(pc, 0);
+  store_op(lds);
+  __syncthreads();
+  for (int kc = 0; kc < nk; ++kc) {
+    const bool more = kc + 1 < nk;
+    if (more) {
+      load_op(kc + 1);
+      load_p(pn, kc + 1);
+    }
+    const uint4 *cur = lds + (kc & 1) * OPROWS * 8;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int c = 4 * (lane >> 5) + q;
+      bf16x8 of[RT];
+#pragma unroll
+      for (int j = 0; j < RT; ++j) of[j] = as_bf16x8(cur[lds_chunk_offset(32 * j + (lane & 31), c)]);
+#pragma unroll
+      for (int i = 0; i < WT; ++i)
+#pragma unroll
+        for (int j = 0; j < RT; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(pc[i][q]), of[j], acc[i][j], 0, 0, 0);
+    }
+    if (more) store_op(lds + ((kc + 1) & 1) * OPROWS * 8);
+    __syncthreads();
+    if (more) {
+#pragma unroll
+      for (int i = 0; i < WT; ++i)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) pc[i][q] = pn[i][q];
+    }
+  }
+
+  // ---- epilogue: scale, bf16 row-major copy and fp32 transposed copy
+#pragma unroll
+  for (int i = 0; i < WT; ++i) {
+#pragma unroll
+    for (int j = 0; j < RT; ++j) {
+      const int col = 32 * j + (lane & 31);
+      if (col >= r) continue;
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int row = m0 + 32 * (wave * WT + i) + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
+        if (row >= mend) continue;
+        const float h = acc[i][j][v] * scale;
+        args.Hr[(int64_t)row * args.ldh + col] = f32_to_bf16_rne(h);
+        if (args.Hc) args.Hc[(int64_t)col * args.ldhc + row] = h;
+      }
+    }
+  }
+}
+
+template <int WT, int RT>
+static void launch_shrink_rt(const ShrinkArgs &a, int nblocks, hipStream_t stream) {
+  if (a.op_layout == 0)
+    hipLaunchKernelGGL((shrink_kernel<WT, RT, 0>), dim3(nblocks), dim3(256), 0, stream, a);
+  else
+    hipLaunchKernelGGL((shrink_kernel<WT, RT, 1>), dim3(nblocks), dim3(256), 0, stream, a);
+}
+
+// ============================================================== seg_outer
+//
+// Work item = (row chunk of one segment, 64-wide j block, 128-wide c block).
+// The 4 waves of a workgroup take interleaved 32-row steps of the chunk and
+// are summed through LDS at the end (fixed order), so each item leaves one
+// fp32 partial [128 c x 64 j]. A second kernel adds an adapter's partials in
+// chunk order.
+// Per 32-row step a lane loads an 8x8 block of P (8 rows x 8 columns),
+// transposes it in registers into 8 MFMA A-fragments (one per column), and
+// loads 8 consecutive m of Qt per j, split into bf16 hi + lo parts.
+// v_mfma_f32_16x16x32_bf16: rows <- c (stride 8: c = c0 + 8*i + t for
+// fragment t), columns <- j, contraction <- m.
+
+constexpr int OUT_C = 128;  // c per workgroup
+constexpr int OUT_J = 64;   // j per workgroup
+
+struct OuterArgs {
+  const uint16_t *P;
+  const float *Qt;
+  float *ws;
+  int64_t ldp, ldq;
+  int32_t M, C;
+  int32_t chunk_rows;
+  int32_t cblocks, jblocks;  // jblocks = ceil(max rank / 64)
+  int32_t rpad;              // 64 * jblocks: partial row length
+  int32_t chunk_start[kMaxSeg + 1];
+  int32_t rank[kMaxAdapters];
+  SegTable seg;
+};
+
+__global__ __launch_bounds__(256) void seg_outer_kernel(const OuterArgs args) {
+  __shared__ f32x4 red[3][32][64];  // waves 1..3: 32 f32x4 accumulators x 64 lanes
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int item = blockIdx.x;
+  const int cb = item % args.cblocks;
+  const int jb = (item / args.cblocks) % args.jblocks;
+  const int chunk = item / (args.cblocks * args.jblocks);
+  int s = 0;
+  while (s + 1 < args.seg.n && args.chunk_start[s + 1] <= chunk) ++s;
+  const int a = args.seg.aid[s];
+  const int r = args.rank[a];
+  const int j0 = jb * OUT_J;
+  if (j0 >= r) return;  // whole workgroup exits together
+  const int row0 = args.seg.off[s] + (chunk - args.chunk_start[s]) * args.chunk_rows;
+  const int rend = min(row0 + args.chunk_rows, args.seg.off[s + 1]);
+  const int c0 = cb * OUT_C;
+  const int li = lane & 15, lq = lane >> 4;
+  const int ccol = c0 + 8 * li;  // this lane's 8 columns
+  const bool col_ok = ccol < args.C;
+  const uint4 zero = make_uint4(0, 0, 0, 0);
+
+  f32x4 acc[8][4];
+#pragma unroll
+  for (int t = 0; t < 8; ++t)
+#pragma unroll
+    for (int q = 0; q < 4; ++q) acc[t][q] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  for (int m0 = row0 + 32 * wave; m0 < rend; m0 += 128) {
+    uint4 blk[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int m = m0 + 8 * lq + e;
+      blk[e] = (col_ok && m < rend) ? *reinterpret_cast<const uint4 *>(args.P + (int64_t)m * args.ldp + ccol) : zero;
+    }
+    uint4 qhi[4], qlo[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int j = j0 + 16 * q + li;
+      float v[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int m = m0 + 8 * lq + e;
+        v[e] = (j < r && m < rend) ? args.Qt[(int64_t)j * args.ldq + m] : 0.f;
+      }
+      split_hi_lo(v, qhi[q], qlo[q]);
+    }
+    uint4 frag[8];
+    transpose8x8_b16(blk, frag);
+#pragma unroll
+    for (int t = 0; t < 8; ++t)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        acc[t][q] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(frag[t]), as_bf16x8(qhi[q]), acc[t][q], 0, 0, 0);
+        acc[t][q] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(frag[t]), as_bf16x8(qlo[q]), acc[t][q], 0, 0, 0);
+      }
+  }
+
+  // fixed-order cross-wave sum: wave0 + wave1 + wave2 + wave3
+  if (wave > 0) {
+#pragma unroll
+    for (int t = 0; t < 8; ++t)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) red[wave - 1][t * 4 + q][lane] = acc[t][q];
+  }
+  __syncthreads();
+  if (wave != 0) return;
+#pragma unroll
+  for (int w = 0; w < 3; ++w)
+#pragma unroll
+    for (int t = 0; t < 8; ++t)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) acc[t][q] += red[w][t * 4 + q][lane];
+
+  // partial layout: ws[chunk][c][rpad]; lane holds c = c0 + 8*(4*lq + v) + t, j = j0 + 16*q + li
+  float *dst = args.ws + (int64_t)chunk * args.C * args.rpad;
+#pragma unroll
+  for (int t = 0; t < 8; ++t)
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const int c = c0 + 8 * (4 * lq + v) + t;
+      if (c >= args.C) continue;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int j = j0 + 16 * q + li;
+        if (j < r) dst[(int64_t)c * args.rpad + j] = acc[t][q][v];
+      }
+    }
+}
+
+struct ReduceArgs {
+  const float *ws;
+  int64_t C;
+  int32_t rpad;
+  int32_t out_layout, out_dtype;
+  int32_t n_adapters;
+  int32_t chunk_start[kMaxSeg + 1];
+  int32_t rank[kMaxAdapters];
+  void *out[kMaxAdapters];
+  SegTable seg;
+};
+
+// One thread per (adapter, c, j): partials summed in chunk order.
+__global__ __launch_bounds__(256) void seg_outer_reduce_kernel(const ReduceArgs args) {
+  const int a = blockIdx.y;
+  const int r = args.rank[a];
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (r == 0 || args.out[a] == nullptr || idx >= args.C * r) return;
+  const int64_t c = idx / r;
+  const int j = (int)(idx % r);
+  float sum = 0.f;
+  for (int s = 0; s < args.seg.n; ++s) {
+    if (args.seg.aid[s] != a) continue;
+    for (int ch = args.chunk_start[s]; ch < args.chunk_start[s + 1]; ++ch)
+      sum += args.ws[((int64_t)ch * args.C + c) * args.rpad + j];
+  }
+  const int64_t o = args.out_layout == 0 ? c * r + j : (int64_t)j * args.C + c;
+  if (args.out_dtype == MLORA_F32)
+    static_cast<float *>(args.out[a])[o] = sum;
+  else
+    static_cast<uint16_t *>(args.out[a])[o] = f32_to_bf16_rne(sum);
+}
+
+// Chunking shared by the entry point and the workspace query.
+struct OuterPlan {
+  int32_t chunk_rows = 0, cblocks = 0, jblocks = 0, rpad = 0, n_chunks = 0;
+  int32_t chunk_start[kMaxSeg + 1];
+};
+
+static void plan_outer(OuterPlan &pl, const SegTable &st, const int32_t *rank, int64_t C) {
+  int rmax = 0;
+  int64_t rows = 0;
+  for (int s = 0; s < st.n; ++s) {
+    const int a = st.aid[s];
+    const int len = st.off[s + 1] - st.off[s];
+    if (a >= 0 && rank[a] > 0 && len > 0) {
+      rows += len;
+      rmax = rank[a] > rmax ? rank[a] : rmax;
+    }
+  }
+  pl.cblocks = (int32_t)((C + OUT_C - 1) / OUT_C);
+  pl.jblocks = (rmax + OUT_J - 1) / OUT_J;
+  pl.rpad = pl.jblocks * OUT_J;
+  // aim at ~512 work items (2 per CU) with chunks of at least 512 rows
+  const int64_t target_items = 512;
+  int64_t cr = rows * pl.cblocks * (pl.jblocks > 0 ? pl.jblocks : 1) / target_items;
+  cr = cr < 512 ? 512 : cr;
+  cr = (cr + 127) / 128 * 128;
+  pl.chunk_rows = (int32_t)(cr > INT32_MAX / 2 ? INT32_MAX / 2 : cr);
+  int32_t n = 0;
+  for (int s = 0; s < st.n; ++s) {
+    pl.chunk_start[s] = n;
+    const int a = st.aid[s];
+    const int len = st.off[s + 1] - st.off[s];
+    if (a >= 0 && rank[a] > 0 && len > 0) n += (len + pl.chunk_rows - 1) / pl.chunk_rows;
+  }
+  pl.chunk_start[st.n] = n;
+  pl.n_chunks = n;
+}
+
+}  // namespace mlora
+
+using namespace mlora;
+
+extern "C" int mlora_shrink(const void *p, int64_t ldp, int64_t M, int64_t K, const void *const *op_ptrs, int op_layout,
+                            const int32_t *ranks, const float *scales, int32_t n_adapters, const int64_t *seg_offsets,
+                            const int32_t *adapter_ids, int32_t n_segments, void *h_rows, int64_t ldh, void *h_cols,
+                            int64_t ldhc, void *stream) {
+  ShrinkArgs a{};
+  int st = build_segtable(a.seg, M, seg_offsets, adapter_ids, n_segments, n_adapters);
+  if (st) return st;
+  if ((st = build_adapters(a.op, a.seg, op_ptrs, ranks, scales, n_adapters))) return st;
+  if (op_layout != 0 && op_layout != 1) return MLORA_ERR_INVALID;
+  if (K < 0 || K > INT32_MAX - 1024) return MLORA_ERR_INVALID;
+  const int rmax = max_used_rank(a.seg, a.op);
+  if (rmax == 0 || M == 0) return MLORA_OK;
+  if ((st = check_bf16_matrix(p, ldp, M, K))) return st;
+  if ((st = check_bf16_matrix(h_rows, ldh, M, rmax))) return st;
+  if (h_cols != nullptr) {
+    if (ldhc < M) return MLORA_ERR_INVALID;
+    if (ldh < rmax) return MLORA_ERR_INVALID;
+  }
+  a.P = static_cast<const uint16_t *>(p);
+  a.Hr = static_cast<uint16_t *>(h_rows);
+  a.Hc = static_cast<float *>(h_cols);
+  a.ldp = ldp;
+  a.ldh = ldh;
+  a.ldhc = ldhc;
+  a.M = (int32_t)M;
+  a.K = (int32_t)K;
+  a.op_layout = op_layout;
+  constexpr int WT = 1;
+  a.tile_rows = 4 * WT * 32;
+  int64_t n = 0;
+  for (int s = 0; s < a.seg.n; ++s) {
+    a.tile_start[s] = (int32_t)n;
+    const int ad = a.seg.aid[s];
+    const int len = a.seg.off[s + 1] - a.seg.off[s];
+    if (ad >= 0 && a.op.rank[ad] > 0 && len > 0) n += (len + a.tile_rows - 1) / a.tile_rows;
+  }
+  a.tile_start[a.seg.n] = (int32_t)n;
+  if (n == 0) return MLORA_OK;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int rt = (rmax + 31) / 32;
+  if (rt <= 1) launch_shrink_rt<WT, 1>(a, (int)n, s);
+  else if (rt == 2) launch_shrink_rt<WT, 2>(a, (int)n, s);
+  else if (rt <= 4) launch_shrink_rt<WT, 4>(a, (int)n, s);
+  else launch_shrink_rt<WT, 8>(a, (int)n, s);
+  return launch_status();
+}
+
+static int outer_setup(OuterArgs &a, OuterPlan &pl, int64_t M, int64_t C, const int32_t *ranks, int32_t n_adapters,
+                       const int64_t *seg_offsets, const int32_t *adapter_ids, int32_t n_segments) {
+  int st = build_segtable(a.seg, M, seg_offsets, adapter_ids, n_segments, n_adapters);
+  if (st) return st;
+  if (n_adapters < 0) return MLORA_ERR_INVALID;
+  if (n_adapters > kMaxAdapters) return MLORA_ERR_LIMIT;
+  if (n_adapters > 0 && ranks == nullptr) return MLORA_ERR_INVALID;
+  if (C < 0 || C > INT32_MAX - 1024) return MLORA_ERR_INVALID;
+  for (int i = 0; i < kMaxAdapters; ++i) a.rank[i] = 0;
+  for (int i = 0; i < n_adapters; ++i) {
+    if (ranks[i] < 0 || (ranks[i] > 0 && ranks[i] < 8) || ranks[i] % 8) return MLORA_ERR_INVALID;
+    if (ranks[i] > kMaxRank) return MLORA_ERR_LIMIT;
+    a.rank[i] = ranks[i];
+  }
+  plan_outer(pl, a.seg, a.rank, C);
+  return MLORA_OK;
+}
+
+extern "C" int64_t mlora_seg_outer_workspace_bytes(int64_t M, int64_t C, const int32_t *ranks, int32_t n_adapters,
+                                                   const int64_t *seg_offsets, const int32_t *adapter_ids,
+                                                   int32_t n_segments) {
+  OuterArgs a{};
+  OuterPlan pl;
+  int st = outer_setup(a, pl, M, C, ranks, n_adapters, seg_offsets, adapter_ids, n_segments);
+  if (st) return st;
+  return (int64_t)pl.n_chunks * C * pl.rpad * (int64_t)sizeof(float);
+}
+
+extern "C" int mlora_seg_outer(const void *p, int64_t ldp, int64_t M, int64_t C, const float *qt, int64_t ldq,
+                               void *const *out_ptrs, int out_layout, int out_dtype, const int32_t *ranks,
+                               int32_t n_adapters, const int64_t *seg_offsets, const int32_t *adapter_ids,
+                               int32_t n_segments, void *workspace, int64_t workspace_bytes, void *stream) {
+  OuterArgs a{};
+  OuterPlan pl;
+  int st = outer_setup(a, pl, M, C, ranks, n_adapters, seg_offsets, adapter_ids, n_segments);
+  if (st) return st;
+  if (out_layout != 0 && out_layout != 1) return MLORA_ERR_INVALID;
+  if (out_dtype != MLORA_F32 && out_dtype != MLORA_BF16) return MLORA_ERR_UNSUPPORTED;
+  if (n_adapters > 0 && out_ptrs == nullptr) return MLORA_ERR_INVALID;
+  for (int i = 0; i < n_adapters; ++i)
+    if (a.rank[i] > 0 && C > 0 && out_ptrs[i] == nullptr) return MLORA_ERR_INVALID;
+  if (C == 0 || n_adapters == 0) return MLORA_OK;
+  const int64_t need = (int64_t)pl.n_chunks * C * pl.rpad * (int64_t)sizeof(float);
+  if (pl.n_chunks > 0) {
+    if ((st = check_bf16_matrix(p, ldp, M, C))) return st;
+    if (qt == nullptr || ldq < M) return MLORA_ERR_INVALID;
+    if (workspace == nullptr || workspace_bytes < need) return MLORA_ERR_WORKSPACE;
+    if (!aligned16(workspace)) return MLORA_ERR_UNSUPPORTED;
+  }
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (pl.n_chunks > 0) {
+    a.P = static_cast<const uint16_t *>(p);
+    a.Qt = qt;
+    a.ws = static_cast<float *>(workspace);
+    a.ldp = ldp;
+    a.ldq = ldq;
+    a.M = (int32_t)M;
+    a.C = (int32_t)C;
+    a.chunk_rows = pl.chunk_rows;
+    a.cblocks = pl.cblocks;
+    a.jblocks = pl.jblocks;
+    a.rpad = pl.rpad;
+    for (int i = 0; i <= a.seg.n; ++i) a.chunk_start[i] = pl.chunk_start[i];
+    const int64_t items = (int64_t)pl.n_chunks * pl.jblocks * pl.cblocks;
+    if (items > INT32_MAX) return MLORA_ERR_LIMIT;
+    hipLaunchKernelGGL(seg_outer_kernel, dim3((unsigned)items), dim3(256), 0, s, a);
+    if ((st = launch_status())) return st;
+  }
+  ReduceArgs ra{};
+  ra.ws = static_cast<const float *>(workspace);
+  ra.C = C;
+  ra.rpad = pl.rpad;
+  ra.out_layout = out_layout;
+  ra.out_dtype = out_dtype;
+  ra.n_adapters = n_adapters;
+  ra.seg = a.seg;
+  int rmax = 0;
+  for (int i = 0; i <= a.seg.n; ++i) ra.chunk_start[i] = pl.chunk_start[i];
+  for (int i = 0; i < kMaxAdapters; ++i) {
+    ra.rank[i] = i < n_adapters ? a.rank[i] : 0;
+    ra.out[i] = i < n_adapters ? out_ptrs[i] : nullptr;
+    rmax = ra.rank[i] > rmax ? ra.rank[i] : rmax;
+  }
+  if (rmax == 0) return MLORA_OK;
+  const int64_t blocks_x = (C * rmax + 255) / 256;
+  if (blocks_x > INT32_MAX) return MLORA_ERR_LIMIT;
+  hipLaunchKernelGGL(seg_outer_reduce_kernel, dim3((unsigned)blocks_x, (unsigned)n_adapters), dim3(256), 0, s, ra);
+  return launch_status();
+}
+
+extern "C" int mlora_abi_version(void) { return MLORA_ABI_VERSION; }
+
+extern "C" const char *mlora_status_string(int status) {
+  switch (status) {
+    case MLORA_OK: return "ok";
+    case MLORA_ERR_INVALID: return "invalid argument (null pointer, shape, stride or routing)";
+    case MLORA_ERR_UNSUPPORTED: return "unsupported dtype or alignment";
+    case MLORA_ERR_WORKSPACE: return "workspace missing or too small";
+    case MLORA_ERR_LAUNCH: return "kernel launch failed";
+    case MLORA_ERR_LIMIT: return "segment/adapter/rank limit of one call exceeded";
+    default: return "unknown status";
+  }
+}

@@ -1,0 +1,173 @@
+"""Torch-tensor front end of the C ABI: checks, output allocation, streams.
+
+Every function here launches HIP kernels from ``libmlora.so`` on the current
+stream of the tensors' device. There is no CPU path: non-ROCm tensors or a
+missing library raise.
+"""
+from __future__ import annotations
+
+import ctypes
+from typing import Sequence
+
+import torch
+
+from . import _lib
+from .routing import SegmentRouting
+
+_DT = {torch.float32: _lib.F32, torch.bfloat16: _lib.BF16}
+
+
+def _require(cond: bool, message: str) -> None:
+    if not cond:
+        raise RuntimeError("multi-LoRA kernel contract: " + message)
+
+
+def _stream(t: torch.Tensor) -> ctypes.c_void_p:
+    return ctypes.c_void_p(torch.cuda.current_stream(t.device).cuda_stream)
+
+
+def _ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def _check_rows(name: str, t: torch.Tensor, cols: int | None = None) -> None:
+    _require(t.is_cuda, f"{name} must be a ROCm device tensor")
+    _require(t.dtype == torch.bfloat16, f"{name} must be bfloat16, got {t.dtype}")
+    _require(t.dim() == 2 and t.stride(1) == 1, f"{name} must be a 2-D row-major matrix")
+    if cols is not None:
+        _require(t.shape[1] == cols, f"{name} has {t.shape[1]} columns, expected {cols}")
+
+
+def _routing_arrays(off, ids):
+    return _lib.i64_array(off), _lib.i32_array(ids), len(ids)
+
+
+def padded_rank(ranks: Sequence[int]) -> int:
+    r = max([0, *ranks])
+    return (r + 7) // 8 * 8
+
+
+def shrink(p: torch.Tensor, ops: Sequence[torch.Tensor], op_layout: int, scales: Sequence[float],
+           routing: SegmentRouting, want_cols: bool, width: int) -> tuple[torch.Tensor, torch.Tensor | None]:
+    """h = s·P·Op_aᵀ per segment -> (h_rows bf16 [M, width], h_cols fp32 [width, M] or None)."""
+    M, K = p.shape
+    _check_rows("P", p)
+    ranks = [int(o.shape[0] if op_layout == 0 else o.shape[1]) for o in ops]
+    for o, r in zip(ops, ranks):
+        _check_rows("adapter operand", o)
+        _require(o.is_contiguous(), "adapter operands must be contiguous")
+        _require(o.shape == ((r, K) if op_layout == 0 else (K, r)), "adapter operand shape")
+    h_rows = torch.empty((M, width), dtype=torch.bfloat16, device=p.device)
+    h_cols = torch.empty((width, M), dtype=torch.float32, device=p.device) if want_cols else None
+    lib = _lib.load()
+    ptrs, rk, sc = _lib.ptr_array([_ptr(o) for o in ops]), _lib.i32_array(ranks), _lib.f32_array(scales)
+    stream = _stream(p)
+    for r0, r1, off, ids in routing.groups(_lib.MAX_SEGMENTS):
+        if r1 == r0:
+            continue
+        o, i, n = _routing_arrays(off, ids)
+        hc = None if h_cols is None else h_cols.data_ptr() + r0 * 4
+        _lib.check("mlora_shrink", lib.mlora_shrink(
+            p[r0:r1].data_ptr(), p.stride(0), r1 - r0, K, ptrs, op_layout, rk, sc, len(ops),
+            o, i, n, h_rows[r0:r1].data_ptr(), width, hc, M, stream))
+    return h_rows, h_cols
+
+
+def gemm_fwd(x: torch.Tensor, w: torch.Tensor, bias: torch.Tensor | None, h_rows: torch.Tensor | None,
+             bs: Sequence[torch.Tensor], routing: SegmentRouting, out: torch.Tensor | None = None,
+             accumulate: bool = False) -> torch.Tensor:
+    """Y = X·Wᵀ + bias + per-segment h_rows·B_aᵀ, bf16 out."""
+    M, K = x.shape
+    N = w.shape[0]
+    _check_rows("X", x, K)
+    _check_rows("W", w, K)
+    if bias is not None:
+        _require(bias.is_cuda and bias.dtype in _DT and bias.is_contiguous() and bias.shape == (N,), "bias")
+    ranks = [int(b.shape[1]) for b in bs]
+    for b in bs:
+        _check_rows("lora_b", b)
+        _require(b.is_contiguous() and b.shape[0] == N, "lora_b must be contiguous [N, r]")
+    y = out if out is not None else torch.empty((M, N), dtype=torch.bfloat16, device=x.device)
+    _check_rows("Y", y, N)
+    lib = _lib.load()
+    ptrs, rk = _lib.ptr_array([_ptr(b) for b in bs]), _lib.i32_array(ranks)
+    ldh = h_rows.stride(0) if h_rows is not None else 0
+    stream = _stream(x)
+    for r0, r1, off, ids in routing.groups(_lib.MAX_SEGMENTS):
+        if r1 == r0:
+            continue
+        o, i, n = _routing_arrays(off, ids)
+        hr = None if h_rows is None else h_rows[r0:r1].data_ptr()
+        _lib.check("mlora_gemm_fwd", lib.mlora_gemm_fwd(
+            x[r0:r1].data_ptr(), x.stride(0), r1 - r0, K, w.data_ptr(), w.stride(0), N,
+            _ptr(bias), _DT[bias.dtype] if bias is not None else 0, hr, ldh,
+            ptrs, rk, len(bs), o, i, n, y[r0:r1].data_ptr(), y.stride(0), int(accumulate), stream))
+    return y
+
+
+def gemm_dx(dy: torch.Tensor, w: torch.Tensor, g_rows: torch.Tensor | None, as_: Sequence[torch.Tensor],
+            routing: SegmentRouting) -> torch.Tensor:
+    """dX = dY·W + per-segment g_rows·A_a, bf16 out."""
+    M, N = dy.shape
+    K = w.shape[1]
+    _check_rows("dY", dy, N)
+    _check_rows("W", w, K)
+    ranks = [int(a.shape[0]) for a in as_]
+    for a in as_:
+        _check_rows("lora_a", a, K)
+        _require(a.is_contiguous(), "lora_a must be contiguous [r, K]")
+    dx = torch.empty((M, K), dtype=torch.bfloat16, device=dy.device)
+    lib = _lib.load()
+    ptrs, rk = _lib.ptr_array([_ptr(a) for a in as_]), _lib.i32_array(ranks)
+    ldg = g_rows.stride(0) if g_rows is not None else 0
+    stream = _stream(dy)
+    for r0, r1, off, ids in routing.groups(_lib.MAX_SEGMENTS):
+        if r1 == r0:
+            continue
+        o, i, n = _routing_arrays(off, ids)
+        gr = None if g_rows is None else g_rows[r0:r1].data_ptr()
+        _lib.check("mlora_gemm_dx", lib.mlora_gemm_dx(
+            dy[r0:r1].data_ptr(), dy.stride(0), r1 - r0, N, w.data_ptr(), w.stride(0), K, gr, ldg,
+            ptrs, rk, len(as_), o, i, n, dx[r0:r1].data_ptr(), dx.stride(0), stream))
+    return dx
+
+
+def seg_outer(p: torch.Tensor, qt: torch.Tensor, ranks: Sequence[int], routing: SegmentRouting,
+              out_layout: int, out_dtypes: Sequence[torch.dtype]) -> list[torch.Tensor]:
+    """Per-adapter Σ_m P[m,c]·Qt[j,m] -> [C, r_a] (layout 0) or [r_a, C] (layout 1)."""
+    M, C = p.shape
+    _check_rows("P", p, C)
+    _require(qt.is_cuda and qt.dtype == torch.float32 and qt.dim() == 2 and qt.stride(1) == 1
+             and qt.shape[1] == M, "Qt must be fp32 [R, M]")
+    lib = _lib.load()
+    groups = list(routing.groups(_lib.MAX_SEGMENTS))
+    dtypes = list(out_dtypes)
+    _require(all(d in _DT for d in dtypes), "adapter gradients are float32 or bfloat16")
+    # Adapters are reduced per output dtype (normally one dtype for all).
+    outs: list[torch.Tensor | None] = [None] * len(ranks)
+    stream = _stream(p)
+    rk = _lib.i32_array(list(ranks))
+    for dt in sorted(set(dtypes), key=str):
+        sel = [a for a in range(len(ranks)) if dtypes[a] == dt]
+        mask_ranks = _lib.i32_array([r if dtypes[a] == dt else 0 for a, r in enumerate(ranks)])
+        shape = (lambda r: (C, r)) if out_layout == 0 else (lambda r: (r, C))
+        # several row groups: reduce each into fp32 scratch, then add in group order
+        single = len(groups) == 1
+        for r0, r1, off, ids in groups:
+            o, i, n = _routing_arrays(off, ids)
+            ws_bytes = lib.mlora_seg_outer_workspace_bytes(r1 - r0, C, mask_ranks, len(ranks), o, i, n)
+            _lib.check("mlora_seg_outer_workspace_bytes", ws_bytes if ws_bytes < 0 else 0)
+            ws = torch.empty((max(ws_bytes, 16) + 15) // 16 * 4, dtype=torch.float32, device=p.device)
+            part = [torch.empty(shape(ranks[a]), dtype=dt if single else torch.float32, device=p.device)
+                    if a in sel else None for a in range(len(ranks))]
+            _lib.check("mlora_seg_outer", lib.mlora_seg_outer(
+                p[r0:r1].data_ptr(), p.stride(0), r1 - r0, C, qt.data_ptr() + r0 * 4, qt.stride(0),
+                _lib.ptr_array([_ptr(t) for t in part]), out_layout, _DT[dt if single else torch.float32],
+                mask_ranks, len(ranks), o, i, n, ws.data_ptr(), ws.numel() * 4, stream))
+            for a in sel:
+                outs[a] = part[a] if outs[a] is None else outs[a] + part[a]
+        if not single:
+            for a in sel:
+                outs[a] = outs[a].to(dt)
+    del rk
+    return outs  # type: ignore[return-value]

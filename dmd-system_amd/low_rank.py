@@ -1,0 +1,135 @@
+"""Drop-in LoRA modules over a shared frozen base, backed by the HIP kernels.
+
+Mirrors the reference's native LoRA interface (training/low_rank.py):
+``TrainableLowRankLinear(base, rank=, alpha=)`` with parameters ``base``,
+``lora_a`` [r, in] (Kaiming-uniform, a=sqrt(5)), ``lora_b`` [out, r] (zeros),
+``scale = alpha / rank``, and ``trainable_scope(native, config)`` with the
+same schema and the same fail-closed ``ValueError`` messages. Checkpoint keys
+are therefore unchanged (training/checkpoint.py:177 packs named parameters).
+
+``MultiLoRALinear`` is the batched form: one frozen base, several adapters
+(``lora_a.{i}``, ``lora_b.{i}``) and a SegmentRouting per call, so that the
+generator and fake-critic roles (and base-only teacher rows) share one
+launch of the base GEMM.
+"""
+from __future__ import annotations
+
+import math
+from typing import Sequence
+
+import torch
+from torch import nn
+
+from .function import multi_lora_linear
+from .routing import SegmentRouting
+
+
+def _require(value, message):
+    if not value:
+        raise ValueError('native trainable scope: ' + message)
+
+
+def _init_pair(rank: int, base: nn.Linear, dtype=None) -> tuple[nn.Parameter, nn.Parameter]:
+    # low_rank.py:21-23: A Kaiming-uniform(a=sqrt(5)) i.e. U(±1/sqrt(in)), B zeros
+    dt = dtype or base.weight.dtype
+    a = nn.Parameter(torch.empty(rank, base.in_features, device=base.weight.device, dtype=dt))
+    b = nn.Parameter(torch.zeros(base.out_features, rank, device=base.weight.device, dtype=dt))
+    nn.init.kaiming_uniform_(a, a=5 ** .5)
+    return a, b
+
+
+class TrainableLowRankLinear(nn.Module):
+    """Frozen W*x + (alpha/rank)*B(A*x), with separately owned trainable A/B.
+
+    Same constructor contract as training/low_rank.py:13-24; forward runs the
+    HIP multi-LoRA path with one adapter over all rows.
+    """
+
+    def __init__(self, base, *, rank, alpha):
+        super().__init__()
+        _require(type(base) is nn.Linear and type(rank) is int and 0 < rank <= min(base.in_features, base.out_features)
+                 and type(alpha) in (int, float) and math.isfinite(alpha) and alpha > 0,
+                 'invalid native Linear LoRA scope/rank/alpha')
+        self.base = base.requires_grad_(False)
+        self.lora_a, self.lora_b = _init_pair(rank, base)
+        self.scale = float(alpha) / rank
+
+    def forward(self, value):
+        rows = value.numel() // value.shape[-1] if value.dim() else 0
+        return multi_lora_linear(value, self.base.weight, self.base.bias, [self.lora_a], [self.lora_b],
+                                 [self.scale], SegmentRouting.single(rows, 0))
+
+
+def trainable_scope(native, config):
+    """Install TrainableLowRankLinear on the named nn.Linear targets (training/low_rank.py:31-50)."""
+    _require(isinstance(config, dict) and config.get('mode') in ('full', 'lora'), 'explicit full or lora trainable scope required')
+    if config['mode'] == 'full':
+        _require(set(config) == {'mode'}, 'full mode accepts no ignored LoRA settings')
+        native.requires_grad_(True)
+        return
+    _require(set(config) == {'mode', 'rank', 'alpha', 'targets'} and isinstance(config['targets'], list)
+             and config['targets'] and all(isinstance(name, str) and name for name in config['targets'])
+             and len(config['targets']) == len(set(config['targets'])), 'exact nonempty native Linear LoRA targets required')
+    targets = {}
+    for name in config['targets']:
+        try:
+            targets[name] = native.get_submodule(name)
+        except AttributeError as exc:
+            raise ValueError('missing actual native LoRA target: ' + name) from exc
+        _require(type(targets[name]) is nn.Linear, 'LoRA target is not an actual native Linear: ' + name)
+    native.requires_grad_(False)
+    for name, module in targets.items():
+        native.set_submodule(name, TrainableLowRankLinear(module, rank=config['rank'], alpha=config['alpha']))
+
+
+class MultiLoRALinear(nn.Module):
+    """One frozen base nn.Linear shared by several adapters, routed by segment.
+
+    ``forward(x, routing)``: x [..., in]; routing a SegmentRouting over the
+    flattened rows (adapter id -1 = base only, the teacher role).
+    """
+
+    def __init__(self, base: nn.Linear, *, ranks: Sequence[int], alphas: Sequence[float], dtype=None):
+        super().__init__()
+        _require(type(base) is nn.Linear, 'multi-LoRA base must be an actual native Linear')
+        _require(len(ranks) == len(alphas) and len(ranks) > 0, 'one alpha per adapter rank required')
+        for r, al in zip(ranks, alphas):
+            _require(type(r) is int and 0 < r <= min(base.in_features, base.out_features)
+                     and type(al) in (int, float) and math.isfinite(al) and al > 0,
+                     'invalid native Linear LoRA scope/rank/alpha')
+        self.base = base.requires_grad_(False)
+        pairs = [_init_pair(r, base, dtype) for r in ranks]
+        self.lora_a = nn.ParameterList([a for a, _ in pairs])
+        self.lora_b = nn.ParameterList([b for _, b in pairs])
+        self.scales = [float(al) / r for r, al in zip(ranks, alphas)]
+
+    @classmethod
+    def from_roles(cls, roles: Sequence[TrainableLowRankLinear]) -> "MultiLoRALinear":
+        """Batch per-role TrainableLowRankLinear modules that alias one frozen base.
+
+        The adapters are the roles' own Parameters (not copies), so each role's
+        optimizer keeps owning exactly its trainables (open_workload/dmd.py:266-275);
+        the base must be the same Parameter object in every role, as
+        construction_sharing.place_frozen_role arranges (construction_sharing.py:105-118).
+        """
+        _require(len(roles) > 0, 'at least one role module required')
+        base = roles[0].base
+        for m in roles:
+            _require(isinstance(m, TrainableLowRankLinear), 'roles must be TrainableLowRankLinear modules')
+            _require(m.base.weight is base.weight and m.base.bias is base.bias,
+                     'roles must alias one frozen base (shared construction)')
+        obj = cls.__new__(cls)
+        nn.Module.__init__(obj)
+        obj.base = base
+        obj.lora_a = nn.ParameterList([m.lora_a for m in roles])
+        obj.lora_b = nn.ParameterList([m.lora_b for m in roles])
+        obj.scales = [m.scale for m in roles]
+        return obj
+
+    @property
+    def num_adapters(self) -> int:
+        return len(self.scales)
+
+    def forward(self, x: torch.Tensor, routing: SegmentRouting) -> torch.Tensor:
+        return multi_lora_linear(x, self.base.weight, self.base.bias, list(self.lora_a), list(self.lora_b),
+                                 self.scales, routing)

@@ -1,0 +1,158 @@
+/*
+ * mlora.h — C ABI of the MI355X (gfx950) batched multi-LoRA linear.
+ *
+ * Computes, for a frozen base W shared by several low-rank adapters,
+ *
+ *   Y = X·Wᵀ (+b) + Σ_seg s_a·(X_seg·A_aᵀ)·B_aᵀ          forward
+ *   dX = dY·W + Σ_seg (s_a·dY_seg·B_a)·A_a                backward (W frozen: no dW)
+ *   dB_a = s_a·Σ_{m∈a} dY[m]ᵀ·h[m]      dA_a = Σ_{m∈a} g[m]ᵀ·X[m]
+ *
+ * where rows of X are split into contiguous segments [seg_offsets[s],
+ * seg_offsets[s+1]) and segment s uses adapter adapter_ids[s] (-1 = base only,
+ * the teacher / "LoRA disabled" role).
+ *
+ * It replaces, for one call, the per-role modules of the reference
+ * (DMD-System, sliortega295-ops):
+ *   src/distillschedule/training/low_rank.py:26-28   TrainableLowRankLinear.forward
+ *   src/distillschedule/native/models.py:44-51       LoRALinear.forward (fp32 LoRA)
+ *   src/distillschedule/reference/livewan_wan21/wanstreamer/lora.py:22-27,65-74
+ *       LoRALinear.forward / lora_enabled(model, False) (null adapter)
+ * and the Triton LoRA kernels those modules call:
+ *   src/distillschedule/runtime/wan13b_lora_epilogue.py:55-92   (epilogue add)
+ *   src/distillschedule/runtime/helios_lora_b_gemm_kernel.py:53-131 (LoRA-B GEMM + residual)
+ *   src/distillschedule/backends/training/minimax_h3/triton_lora_epilogue.py:143-178
+ *
+ * Conventions (all entry points):
+ *   - Every tensor pointer is a device pointer; every array documented as
+ *     "host" is read on the host during the call and may be freed after it.
+ *   - Matrices are row-major with an explicit leading dimension (elements).
+ *   - Nothing is allocated, nothing synchronises the host; work is enqueued on
+ *     `stream` (a hipStream_t, passed as void* so this header needs no HIP).
+ *   - Return MLORA_OK (0) or a negative mlora_status; no exceptions cross the
+ *     ABI. Argument errors are detected before any launch.
+ *   - Reentrant: no global mutable state; safe to call from several host
+ *     threads on different streams.
+ *   - Results are deterministic: fixed-order reductions, no float atomics.
+ */
+#ifndef MLORA_H_
+#define MLORA_H_
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MLORA_ABI_VERSION 1
+
+/* Limits of one call (kernel-argument tables). Callers with more segments
+ * split the rows into several calls; the Python host layer does this. */
+#define MLORA_MAX_SEGMENTS 128
+#define MLORA_MAX_ADAPTERS 32
+#define MLORA_MAX_RANK 256
+
+typedef enum mlora_dtype {
+  MLORA_F32 = 0,
+  MLORA_BF16 = 1,
+  MLORA_FP8_E4M3 = 2 /* OCP e4m3fn, as gfx950 MFMA consumes it */
+} mlora_dtype;
+
+typedef enum mlora_status {
+  MLORA_OK = 0,
+  MLORA_ERR_INVALID = -1,     /* null pointer, bad shape, bad stride, bad routing */
+  MLORA_ERR_UNSUPPORTED = -2, /* dtype/alignment combination not implemented */
+  MLORA_ERR_WORKSPACE = -3,   /* workspace missing or too small */
+  MLORA_ERR_LAUNCH = -4,      /* hipLaunchKernel reported an error */
+  MLORA_ERR_LIMIT = -5        /* more segments/adapters/rank than one call takes */
+} mlora_status;
+
+/* Segment routing shared by all entry points (host arrays).
+ *   seg_offsets[n_segments+1]: seg_offsets[0] == 0, nondecreasing,
+ *                              seg_offsets[n_segments] == M.
+ *   adapter_ids[n_segments]:   -1 (base only) or 0 <= id < n_adapters.
+ * Adapter table (host arrays, length n_adapters):
+ *   ranks[i] in {0} ∪ [8, MLORA_MAX_RANK], multiple of 8; scales[i] = alpha_i / rank_i.
+ * The reference builds one role per module call (training/dmd.py:301-353);
+ * here each role is a segment of one call over the shared frozen base
+ * (training/construction_sharing.py:105-118). */
+
+int mlora_abi_version(void);
+const char *mlora_status_string(int status);
+
+/* Shrink: for each row m of a segment with adapter a (rank r_a),
+ *   h[m, j] = s_a · Σ_k P[m, k] · Op_a(j, k),   j < r_a
+ * and writes it twice:
+ *   h_rows  bf16 [M, ldh]   (row-major; round-to-nearest-even of the fp32 value)
+ *   h_cols  fp32 [ldh, ldhc] (transposed: h_cols[j*ldhc + m]); may be NULL.
+ * op_layout 0: Op_a stored [r_a, K] (K contiguous, e.g. lora_a, low_rank.py:21)
+ * op_layout 1: Op_a stored [K, r_a] (r contiguous, e.g. lora_b [N, r] for the
+ *              backward g = s·dY·B, low_rank.py:22)
+ * Rows of base-only segments are not written.
+ * Reference: F.linear(value, lora_a) in low_rank.py:28 (forward shrink) and the
+ * autograd LinearBackward of F.linear(h, lora_b) (dH = g·B, as written out in
+ * runtime/helios_lora_b_gemm_kernel.py:105). */
+int mlora_shrink(const void *p, int64_t ldp, int64_t M, int64_t K,
+                 const void *const *op_ptrs, int op_layout,
+                 const int32_t *ranks, const float *scales, int32_t n_adapters,
+                 const int64_t *seg_offsets, const int32_t *adapter_ids, int32_t n_segments,
+                 void *h_rows, int64_t ldh, void *h_cols, int64_t ldhc,
+                 void *stream);
+
+/* Base GEMM with the LoRA expand fused into its epilogue:
+ *   Y[m, n] = bf16( Σ_k X[m,k]·W[n,k] + bias[n] + Σ_j h_rows[m,j]·B_a[n,j] )
+ * (h_rows already carries s_a, see mlora_shrink). W is bf16 [N, K] (ldw).
+ * bias: NULL, or bias_dtype MLORA_BF16 / MLORA_F32, length N.
+ * b_ptrs[i]: bf16 [N, r_i] contiguous (lora_b). h_rows may be NULL when no
+ * segment has an adapter.
+ * If accumulate != 0, Y is read and the result added to it (Y += ...), which
+ * with K == 0 gives the standalone expand of the reference's LoRA-B GEMM +
+ * residual kernels (helios_lora_b_gemm_kernel.py:25-50).
+ * Reference: low_rank.py:28 (base(value) + scale·F.linear(F.linear(value, A), B)). */
+int mlora_gemm_fwd(const void *x, int64_t ldx, int64_t M, int64_t K,
+                   const void *w, int64_t ldw, int64_t N,
+                   const void *bias, int bias_dtype,
+                   const void *h_rows, int64_t ldh,
+                   const void *const *b_ptrs, const int32_t *ranks, int32_t n_adapters,
+                   const int64_t *seg_offsets, const int32_t *adapter_ids, int32_t n_segments,
+                   void *y, int64_t ldy, int accumulate,
+                   void *stream);
+
+/* Input gradient with the LoRA term fused into its epilogue:
+ *   dX[m, k] = bf16( Σ_n dY[m,n]·W[n,k] + Σ_j g_rows[m,j]·A_a[j,k] )
+ * g_rows = s_a·dY·B_a from mlora_shrink(op_layout=1). a_ptrs[i]: bf16 [r_i, K].
+ * Reference: autograd of low_rank.py:28 — dX = dY·W + (s·dY·B)·A. */
+int mlora_gemm_dx(const void *dy, int64_t lddy, int64_t M, int64_t N,
+                  const void *w, int64_t ldw, int64_t K,
+                  const void *g_rows, int64_t ldg,
+                  const void *const *a_ptrs, const int32_t *ranks, int32_t n_adapters,
+                  const int64_t *seg_offsets, const int32_t *adapter_ids, int32_t n_segments,
+                  void *dx, int64_t lddx,
+                  void *stream);
+
+/* Segmented outer-product reduction (adapter gradients):
+ *   D_a[c, j] = Σ_{m in segments of adapter a} P[m, c] · Qt[j, m]
+ * P bf16 [M, C] (ldp); Qt fp32 [*, ldq] transposed per-row values (h_cols /
+ * g_cols of mlora_shrink). Written as out_dtype (MLORA_F32 or MLORA_BF16) to
+ * out_ptrs[a], layout out_layout 0: [C, r_a] (dB_a = s·dYᵀ·h, lora_b shape),
+ * out_layout 1: [r_a, C] (dA_a = gᵀ·X, lora_a shape). Adapters with no rows
+ * get zeros. Deterministic two-stage reduction through `workspace`
+ * (size from mlora_seg_outer_workspace_bytes).
+ * Reference: autograd of low_rank.py:28 (dB = s·dYᵀ·h, dA = gᵀ·x);
+ * runtime/helios_lora_b_gemm_kernel.py:106 (d_b = g.T @ h). */
+int mlora_seg_outer(const void *p, int64_t ldp, int64_t M, int64_t C,
+                    const float *qt, int64_t ldq,
+                    void *const *out_ptrs, int out_layout, int out_dtype,
+                    const int32_t *ranks, int32_t n_adapters,
+                    const int64_t *seg_offsets, const int32_t *adapter_ids, int32_t n_segments,
+                    void *workspace, int64_t workspace_bytes,
+                    void *stream);
+int64_t mlora_seg_outer_workspace_bytes(int64_t M, int64_t C,
+                                        const int32_t *ranks, int32_t n_adapters,
+                                        const int64_t *seg_offsets, const int32_t *adapter_ids,
+                                        int32_t n_segments);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MLORA_H_ */

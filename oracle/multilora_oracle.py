@@ -1,0 +1,213 @@
+"""CPU oracle of the batched multi-LoRA linear — TEST INFRASTRUCTURE ONLY.
+
+Only ``tests/``, ``__graft_entry__.smoke()`` and ``bench.py``'s CPU-baseline
+leg may import this module, and only as the checker / the timed CPU baseline.
+The product path (``dmd-system_amd``) never imports it and has no CPU path.
+
+It restates, in numpy, the reference's per-adapter LoRA linear
+(sliortega295-ops/DMD-System):
+
+  * training/low_rank.py:26-28   ``base(value) + scale * F.linear(F.linear(value, lora_a), lora_b)``
+    applied to each role's rows — the roles are the segments here
+    (training/dmd.py:301-353 calls each role module on its own batch);
+  * its autograd backward (W frozen, low_rank.py:20):
+    g_u = s·dY, dB = g_uᵀ·h, g_h = g_u·B, dA = g_hᵀ·X, dX = dY·W + g_h·A;
+  * reference/livewan_wan21/wanstreamer/lora.py:22-27,65-74: a disabled
+    adapter (``lora_enabled(model, False)``) is the base alone -> adapter id -1;
+  * the rounding points of three reference variants, for comparison only:
+      - autocast bf16 (low_rank.py:28 under training/single_device.py:88):
+        every F.linear output rounded to bf16, then bf16 mul and bf16 add;
+      - fp32 LoRA update (native/models.py:44-51):
+        bf16(f32(base) + f32(update)·s);
+      - LiveWan (wanstreamer/lora.py:27): base + bf16(update)·s in bf16.
+
+How each function is pinned (tests/test_oracle.py): brute-force loops on
+tiny inputs, central finite differences for the backward, torch.autograd as
+an independent library routine, the reference's own construction fixture
+(tests/test_training_construction.py:24-38: 4x4 linears filled with 0.25,
+rank 2, alpha 2, B = 0 -> base only), invariants (segment permutation,
+concatenation of per-role calls, linearity in the scale), and torch's bf16
+conversion for ``bf16_round``.
+"""
+from __future__ import annotations
+
+from typing import Sequence
+
+import numpy as np
+
+
+# ------------------------------------------------------------------ bf16
+
+def bf16_round(a) -> np.ndarray:
+    """Round float32 values to the nearest bfloat16 (ties to even); returns float32.
+
+    Same rule as IEEE round-to-nearest-even on the top 16 bits; NaN stays NaN.
+    """
+    f = np.ascontiguousarray(np.asarray(a, dtype=np.float32))
+    u = f.view(np.uint32).astype(np.uint64)
+    rounded = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16) << 16
+    out = (rounded & 0xFFFFFFFF).astype(np.uint32).view(np.float32)
+    nan = np.isnan(f)
+    if nan.any():
+        out = np.where(nan, np.float32(np.nan), out)
+    return out.reshape(f.shape)
+
+
+# ------------------------------------------------------------------ routing
+
+def row_adapters(seg_offsets: Sequence[int], adapter_ids: Sequence[int]) -> np.ndarray:
+    """Adapter id of each row (int64), -1 for base-only rows."""
+    off = [int(v) for v in seg_offsets]
+    ids = [int(v) for v in adapter_ids]
+    if len(off) != len(ids) + 1 or off[0] != 0 or any(b < a for a, b in zip(off, off[1:])):
+        raise ValueError("oracle: malformed segment offsets")
+    out = np.empty(off[-1], dtype=np.int64)
+    for s, a in enumerate(ids):
+        out[off[s]:off[s + 1]] = a
+    return out
+
+
+def _segments(seg_offsets, adapter_ids):
+    for s, a in enumerate(adapter_ids):
+        lo, hi = int(seg_offsets[s]), int(seg_offsets[s + 1])
+        yield lo, hi, int(a)
+
+
+# ------------------------------------------------------------------ exact path
+
+def forward(x, w, b, As, Bs, scales, seg_offsets, adapter_ids, dtype=np.float64) -> np.ndarray:
+    """Y for every segment, evaluated per segment like one reference module call each."""
+    x = np.asarray(x, dtype)
+    w = np.asarray(w, dtype)
+    y = x @ w.T
+    if b is not None:
+        y = y + np.asarray(b, dtype)
+    for lo, hi, a in _segments(seg_offsets, adapter_ids):
+        if a < 0 or hi == lo:
+            continue
+        h = x[lo:hi] @ np.asarray(As[a], dtype).T
+        y[lo:hi] += dtype(scales[a]) * (h @ np.asarray(Bs[a], dtype).T)
+    return y
+
+
+def backward(x, w, As, Bs, scales, seg_offsets, adapter_ids, dy, dtype=np.float64):
+    """(dX, [dA_i], [dB_i]) of sum(Y * dY); W and bias are frozen."""
+    x = np.asarray(x, dtype)
+    w = np.asarray(w, dtype)
+    dy = np.asarray(dy, dtype)
+    dx = dy @ w
+    dAs = [np.zeros(np.shape(A), dtype) for A in As]
+    dBs = [np.zeros(np.shape(B), dtype) for B in Bs]
+    for lo, hi, a in _segments(seg_offsets, adapter_ids):
+        if a < 0 or hi == lo:
+            continue
+        A = np.asarray(As[a], dtype)
+        B = np.asarray(Bs[a], dtype)
+        s = dtype(scales[a])
+        xs, gu = x[lo:hi], s * dy[lo:hi]
+        h = xs @ A.T
+        dBs[a] += gu.T @ h
+        gh = gu @ B
+        dAs[a] += gh.T @ xs
+        dx[lo:hi] += gh @ A
+    return dx, dAs, dBs
+
+
+def forward_rows(rows, x, w, b, As, Bs, scales, seg_offsets, adapter_ids, dtype=np.float64) -> np.ndarray:
+    """Y restricted to the given row indices (rows are independent in the forward)."""
+    rows = np.asarray(rows, dtype=np.int64)
+    ad = row_adapters(seg_offsets, adapter_ids)[rows]
+    xr = np.asarray(x[rows], dtype)
+    y = xr @ np.asarray(w, dtype).T
+    if b is not None:
+        y = y + np.asarray(b, dtype)
+    for a in np.unique(ad):
+        if a < 0:
+            continue
+        sel = ad == a
+        h = xr[sel] @ np.asarray(As[a], dtype).T
+        y[sel] += dtype(scales[a]) * (h @ np.asarray(Bs[a], dtype).T)
+    return y
+
+
+def dx_rows(rows, w, As, Bs, scales, seg_offsets, adapter_ids, dy, dtype=np.float64) -> np.ndarray:
+    """dX restricted to the given rows (rows are independent in dX)."""
+    rows = np.asarray(rows, dtype=np.int64)
+    ad = row_adapters(seg_offsets, adapter_ids)[rows]
+    dyr = np.asarray(dy[rows], dtype)
+    dx = dyr @ np.asarray(w, dtype)
+    for a in np.unique(ad):
+        if a < 0:
+            continue
+        sel = ad == a
+        gh = dtype(scales[a]) * (dyr[sel] @ np.asarray(Bs[a], dtype))
+        dx[sel] += gh @ np.asarray(As[a], dtype)
+    return dx
+
+
+# ------------------------------------------------------------------ reference rounding variants
+
+def _mm_f32(a, b_t):
+    """fp32-accumulated product a @ b_tᵀ of float32 operands."""
+    return np.asarray(a, np.float32) @ np.asarray(b_t, np.float32).T
+
+
+def forward_autocast_bf16(x, w, b, As, Bs, scales, seg_offsets, adapter_ids) -> np.ndarray:
+    """low_rank.py:28 under bf16 autocast: operands and every op result rounded to bf16."""
+    xq, wq = bf16_round(x), bf16_round(w)
+    base = _mm_f32(xq, wq)
+    if b is not None:
+        base = base + bf16_round(b)
+    base = bf16_round(base)
+    y = base.copy()
+    for lo, hi, a in _segments(seg_offsets, adapter_ids):
+        if a < 0 or hi == lo:
+            continue
+        h = bf16_round(_mm_f32(xq[lo:hi], bf16_round(As[a])))
+        u = bf16_round(_mm_f32(h, bf16_round(Bs[a])))
+        su = bf16_round(np.float32(scales[a]) * u)
+        y[lo:hi] = bf16_round(base[lo:hi] + su)
+    return y
+
+
+def forward_fp32_update(x, w, b, As, Bs, scales, seg_offsets, adapter_ids) -> np.ndarray:
+    """native/models.py:44-51: bf16 base, fp32 update, (base.float() + update*s).to(bf16)."""
+    xq, wq = bf16_round(x), bf16_round(w)
+    base = _mm_f32(xq, wq)
+    if b is not None:
+        base = base + bf16_round(b)
+    base = bf16_round(base)
+    y = base.copy()
+    x32 = np.asarray(xq, np.float32)
+    for lo, hi, a in _segments(seg_offsets, adapter_ids):
+        if a < 0 or hi == lo:
+            continue
+        upd = _mm_f32(_mm_f32(x32[lo:hi], As[a]), Bs[a])
+        y[lo:hi] = bf16_round(base[lo:hi] + (upd * np.float32(scales[a])).astype(np.float32))
+    return y
+
+
+def forward_livewan(x, w, b, As, Bs, scales, seg_offsets, adapter_ids) -> np.ndarray:
+    """wanstreamer/lora.py:22-27: y + linear(linear(x.f32, a), b).to(bf16) * scale, in bf16."""
+    xq, wq = bf16_round(x), bf16_round(w)
+    base = _mm_f32(xq, wq)
+    if b is not None:
+        base = base + bf16_round(b)
+    base = bf16_round(base)
+    y = base.copy()
+    for lo, hi, a in _segments(seg_offsets, adapter_ids):
+        if a < 0 or hi == lo:
+            continue
+        upd = bf16_round(_mm_f32(_mm_f32(xq[lo:hi], As[a]), Bs[a]))
+        y[lo:hi] = bf16_round(base[lo:hi] + bf16_round(upd * np.float32(scales[a])))
+    return y
+
+
+# ------------------------------------------------------------------ metrics
+
+def rel_l2(got, want) -> float:
+    got = np.asarray(got, np.float64)
+    want = np.asarray(want, np.float64)
+    den = np.linalg.norm(want.ravel())
+    num = np.linalg.norm((got - want).ravel())
+    return float(num / den) if den > 0 else float(num)

@@ -1,0 +1,109 @@
+"""The C-ABI library loads, exports every symbol include/mlora.h declares, and
+rejects bad arguments with the documented status codes before any launch
+(so these run without a GPU)."""
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+ROOT = Path(__file__).resolve().parents[1]
+HEADER = ROOT / "include" / "mlora.h"
+
+
+@pytest.fixture(scope="module")
+def lib(pkg):
+    return pkg._lib.load()
+
+
+def declared_symbols():
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    return sorted(set(re.findall(r"\b(mlora_\w+)\s*\(", text)))
+
+
+def test_header_declares_expected_entry_points():
+    syms = declared_symbols()
+    for name in ("mlora_abi_version", "mlora_status_string", "mlora_shrink", "mlora_gemm_fwd", "mlora_gemm_dx",
+                 "mlora_seg_outer", "mlora_seg_outer_workspace_bytes"):
+        assert name in syms
+
+
+def test_library_exports_every_declared_symbol(lib, pkg):
+    for name in declared_symbols():
+        assert hasattr(lib, name), name
+        assert name in pkg._lib.SIGNATURES, f"{name} has no ctypes signature"
+
+
+def test_abi_version_and_status_strings(lib, pkg):
+    assert lib.mlora_abi_version() == pkg._lib.ABI_VERSION == 1
+    for code in (0, -1, -2, -3, -4, -5):
+        assert lib.mlora_status_string(code)
+    assert b"unknown" in lib.mlora_status_string(-99)
+
+
+def test_header_limits_match_python(pkg):
+    text = HEADER.read_text()
+    for name, val in (("MLORA_MAX_SEGMENTS", pkg._lib.MAX_SEGMENTS), ("MLORA_MAX_ADAPTERS", pkg._lib.MAX_ADAPTERS),
+                      ("MLORA_MAX_RANK", pkg._lib.MAX_RANK), ("MLORA_ABI_VERSION", pkg._lib.ABI_VERSION)):
+        assert re.search(rf"#define {name} {val}\b", text), name
+
+
+def _gemm_fwd(lib, L, *, M=64, K=64, N=64, x=0x1000, w=0x2000, y=0x3000, ldx=None, off=None, ids=None,
+              ranks=(8,), bptr=(0x4000,), h=0x5000, ldh=8, bias=None, bias_dtype=1):
+    off = off if off is not None else [0, M]
+    ids = ids if ids is not None else [0]
+    return lib.mlora_gemm_fwd(x, ldx or K, M, K, w, K, N, bias, bias_dtype, h, ldh,
+                              L.ptr_array(list(bptr)), L.i32_array(list(ranks)), len(ranks),
+                              L.i64_array(off), L.i32_array(ids), len(ids), y, N, 0, None)
+
+
+def test_gemm_fwd_rejects_bad_routing_and_layout(lib, pkg):
+    L = pkg._lib
+    assert _gemm_fwd(lib, L, off=[0, 32]) == L.ERR_INVALID            # offsets do not cover M
+    assert _gemm_fwd(lib, L, off=[1, 64]) == L.ERR_INVALID            # does not start at 0
+    assert _gemm_fwd(lib, L, off=[0, 40, 30, 64], ids=[0, 0, 0]) == L.ERR_INVALID  # decreasing
+    assert _gemm_fwd(lib, L, ids=[1]) == L.ERR_INVALID                # adapter id out of range
+    assert _gemm_fwd(lib, L, ids=[-2]) == L.ERR_INVALID
+    assert _gemm_fwd(lib, L, x=0x1008) == L.ERR_UNSUPPORTED           # misaligned X
+    assert _gemm_fwd(lib, L, K=60, ldx=60) == L.ERR_UNSUPPORTED       # K not a multiple of 8
+    assert _gemm_fwd(lib, L, ranks=(5,)) == L.ERR_INVALID             # rank not a multiple of 8
+    assert _gemm_fwd(lib, L, ranks=(264,)) == L.ERR_LIMIT             # rank above the limit
+    assert _gemm_fwd(lib, L, bptr=(0,)) == L.ERR_INVALID              # used adapter without B
+    assert _gemm_fwd(lib, L, h=0) == L.ERR_INVALID                    # adapter rows without h
+    assert _gemm_fwd(lib, L, bias=0x6000, bias_dtype=2) == L.ERR_UNSUPPORTED
+    n = L.MAX_SEGMENTS + 1
+    assert _gemm_fwd(lib, L, M=n, off=list(range(n + 1)), ids=[0] * n) == L.ERR_LIMIT
+
+
+def test_gemm_fwd_empty_problem_is_a_no_op(lib, pkg):
+    L = pkg._lib
+    assert _gemm_fwd(lib, L, M=0, off=[0, 0], x=0, y=0, h=0) == L.OK
+
+
+def test_seg_outer_workspace_and_validation(lib, pkg):
+    L = pkg._lib
+    off, ids = L.i64_array([0, 1000, 3000]), L.i32_array([0, 1])
+    ranks = L.i32_array([64, 128])
+    ws = lib.mlora_seg_outer_workspace_bytes(3000, 1536, ranks, 2, off, ids, 2)
+    assert ws > 0 and ws % (1536 * 4) == 0
+    # adapters without rows need no workspace
+    assert lib.mlora_seg_outer_workspace_bytes(3000, 1536, ranks, 2, L.i64_array([0, 3000]),
+                                               L.i32_array([-1]), 1) == 0
+    outs = L.ptr_array([0x7000, 0x8000])
+    st = lib.mlora_seg_outer(0x1000, 1536, 3000, 1536, 0x2000, 3000, outs, 0, L.F32, ranks, 2, off, ids, 2,
+                             0x9000, ws - 16, None)
+    assert st == L.ERR_WORKSPACE
+    st = lib.mlora_seg_outer(0x1000, 1536, 3000, 1536, 0x2000, 3000, outs, 2, L.F32, ranks, 2, off, ids, 2,
+                             0x9000, ws, None)
+    assert st == L.ERR_INVALID  # bad layout
+
+
+def test_shrink_validation(lib, pkg):
+    L = pkg._lib
+    off, ids = L.i64_array([0, 64]), L.i32_array([0])
+    args = lambda layout, ranks, h: lib.mlora_shrink(  # noqa: E731
+        0x1000, 64, 64, 64, L.ptr_array([0x2000]), layout, L.i32_array(ranks), L.f32_array([1.0]), 1,
+        off, ids, 1, h, 64, None, 0, None)
+    assert args(3, [8], 0x3000) == L.ERR_INVALID
+    assert args(0, [12], 0x3000) == L.ERR_INVALID
+    assert args(0, [8], 0) == L.ERR_INVALID

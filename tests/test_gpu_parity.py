@@ -1,0 +1,242 @@
+"""HIP path vs the CPU oracle (and torch fp32 on the GPU at full size).
+
+Tolerance: bf16 outputs (Y, dX) and the adapter gradients within
+rel-L2 <= 2e-3 of the exact (fp64) per-adapter result on the same bf16
+inputs; routing (which rows get which adapter) must be bit-exact, checked by
+comparing base-only rows with an adapter-free launch.
+"""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import multilora_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+TOL = 2e-3
+
+
+def f64(t):
+    return t.detach().double().cpu().numpy()
+
+
+def make_case(M, K, N, ranks, lengths, ids, seed, bias=True, dtype=torch.bfloat16, b_std=0.02):
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn(M, K, generator=g).to(torch.bfloat16)
+    w = (torch.randn(N, K, generator=g) / math.sqrt(K)).to(torch.bfloat16)
+    b = (torch.randn(N, generator=g) / math.sqrt(K)).to(torch.bfloat16) if bias else None
+    As = [((torch.rand(r, K, generator=g) * 2 - 1) / math.sqrt(K)).to(dtype) for r in ranks]
+    Bs = [(torch.randn(N, r, generator=g) * b_std).to(dtype) for r in ranks]
+    dy = torch.randn(M, N, generator=g).to(torch.bfloat16)
+    return x, w, b, As, Bs, dy
+
+
+def run_hip(pkg, dev, x, w, b, As, Bs, dy, scales, routing, need_x=True):
+    xg = x.to(dev).requires_grad_(need_x)
+    Ag = [a.to(dev).requires_grad_(True) for a in As]
+    Bg = [v.to(dev).requires_grad_(True) for v in Bs]
+    y = pkg.multi_lora_linear(xg, w.to(dev), None if b is None else b.to(dev), Ag, Bg, scales, routing)
+    y.backward(dy.to(dev))
+    torch.cuda.synchronize()
+    return y, (xg.grad if need_x else None), [a.grad for a in Ag], [v.grad for v in Bg]
+
+
+def check_against_oracle(pkg, dev, case, scales, routing, tol=TOL):
+    x, w, b, As, Bs, dy = case
+    y, dx, dAs, dBs = run_hip(pkg, dev, *case, scales, routing)
+    off, ids = routing.seg_offsets, routing.adapter_ids
+    Af, Bf = [f64(a) for a in As], [f64(v) for v in Bs]
+    y_ref = O.forward(f64(x), f64(w), None if b is None else f64(b), Af, Bf, scales, off, ids)
+    dx_ref, dA_ref, dB_ref = O.backward(f64(x), f64(w), Af, Bf, scales, off, ids, f64(dy))
+    errs = {"y": O.rel_l2(f64(y), y_ref), "dx": O.rel_l2(f64(dx), dx_ref)}
+    for i in range(len(As)):
+        if np.abs(dA_ref[i]).max() == 0:
+            assert not dAs[i].any() and not dBs[i].any(), "adapter without rows must get zero gradient"
+            continue
+        errs[f"dA{i}"] = O.rel_l2(f64(dAs[i]), dA_ref[i])
+        errs[f"dB{i}"] = O.rel_l2(f64(dBs[i]), dB_ref[i])
+    print("rel-L2", {k: f"{v:.2e}" for k, v in errs.items()}, flush=True)
+    assert all(v <= tol for v in errs.values()), errs
+    assert y.dtype == torch.bfloat16 and dx.dtype == torch.bfloat16
+    for a, g in zip(As, dAs):
+        assert g.dtype == a.dtype and g.shape == a.shape
+    return y, dx, dAs, dBs
+
+
+@pytest.mark.parametrize("bias", [True, False])
+@pytest.mark.parametrize("lengths,ids", [((256, 256), (0, 1)), ((200, 56, 256), (0, -1, 1)),
+                                         ((0, 300, 212), (1, 0, -1))])
+def test_tiny_config_vs_oracle(pkg, dev, bias, lengths, ids):
+    """BASELINE config 1 shape: 512 tokens, 256 -> 256, two rank-8 adapters."""
+    case = make_case(512, 256, 256, (8, 8), lengths, ids, seed=11, bias=bias)
+    routing = pkg.SegmentRouting.from_lengths(lengths, ids)
+    check_against_oracle(pkg, dev, case, [1.0, 1.0], routing)
+
+
+def test_ragged_shapes_and_ranks(pkg, dev):
+    """M, K, N not multiples of any tile; ranks 8/24/40 and a rank-5 adapter (padded to 8)."""
+    lengths, ids = (77, 301, 1, 250, 371), (2, 0, 3, -1, 1)
+    case = make_case(1000, 136, 200, (24, 8, 40, 5), lengths, ids, seed=12)
+    routing = pkg.SegmentRouting.from_lengths(lengths, ids)
+    check_against_oracle(pkg, dev, case, [0.5, 2.0, 1.0, 3.0], routing)
+
+
+def test_heterogeneous_ranks_many_adapters(pkg, dev):
+    """16 adapters of ranks {16,32,64,128} plus a rank-256 adapter, one segment each (config 4 pattern)."""
+    rng = np.random.default_rng(13)
+    ranks = [int(rng.choice([16, 32, 64, 128])) for _ in range(16)] + [256]
+    lengths = [int(v) for v in rng.integers(50, 400, size=17)]
+    ids = list(range(17))
+    case = make_case(sum(lengths), 512, 384, ranks, lengths, ids, seed=13)
+    routing = pkg.SegmentRouting.from_lengths(lengths, ids)
+    check_against_oracle(pkg, dev, case, [2.0] * 17, routing)
+
+
+def test_more_segments_than_one_call(pkg, dev):
+    """300 segments: the host splits the rows into calls of <= 128 segments."""
+    rng = np.random.default_rng(14)
+    lengths = [int(v) for v in rng.integers(0, 12, size=300)]
+    ids = [int(v) for v in rng.integers(-1, 3, size=300)]
+    case = make_case(sum(lengths), 64, 72, (8, 16, 8), lengths, ids, seed=14)
+    routing = pkg.SegmentRouting.from_lengths(lengths, ids)
+    check_against_oracle(pkg, dev, case, [1.0, 0.5, 2.0], routing)
+
+
+def test_routing_is_bit_exact(pkg, dev):
+    """Rows of base-only segments equal an adapter-free launch bit for bit, and
+    adapter rows equal the launch with that adapter on all rows."""
+    lengths, ids = (130, 70, 200, 112), (0, -1, 1, -1)
+    x, w, b, As, Bs, dy = make_case(512, 256, 256, (16, 16), lengths, ids, seed=15, b_std=0.2)
+    routing = pkg.SegmentRouting.from_lengths(lengths, ids)
+    with torch.no_grad():
+        args = lambda r: pkg.multi_lora_linear(x.to(dev), w.to(dev), b.to(dev), [a.to(dev) for a in As],  # noqa
+                                               [v.to(dev) for v in Bs], [1.0, 1.0], r)
+        y = args(routing)
+        y_base = args(pkg.SegmentRouting.single(512, -1))
+        y0 = args(pkg.SegmentRouting.single(512, 0))
+        y1 = args(pkg.SegmentRouting.single(512, 1))
+    row = torch.tensor(routing.row_adapter(), device=dev)
+    assert torch.equal(y[row == -1], y_base[row == -1])
+    assert torch.equal(y[row == 0], y0[row == 0])
+    assert torch.equal(y[row == 1], y1[row == 1])
+    assert not torch.equal(y[row == 0], y_base[row == 0])
+
+
+def test_deterministic(pkg, dev):
+    lengths, ids = (300, 212), (0, 1)
+    case = make_case(512, 256, 256, (8, 8), lengths, ids, seed=16)
+    routing = pkg.SegmentRouting.from_lengths(lengths, ids)
+    r1 = run_hip(pkg, dev, *case, [1.0, 1.0], routing)
+    r2 = run_hip(pkg, dev, *case, [1.0, 1.0], routing)
+    assert torch.equal(r1[0], r2[0]) and torch.equal(r1[1], r2[1])
+    for a, b in zip(r1[2] + r1[3], r2[2] + r2[3]):
+        assert torch.equal(a, b)
+
+
+def test_fp32_masters_get_fp32_grads(pkg, dev):
+    """fp32 LoRA masters (native/models.py:38-39) are cast to bf16 for the kernels
+    (autocast semantics); gradients come back fp32. Oracle on the bf16-rounded values."""
+    lengths, ids = (256, 256), (0, 1)
+    x, w, b, As, Bs, dy = make_case(512, 256, 256, (8, 8), lengths, ids, seed=17, dtype=torch.float32)
+    routing = pkg.SegmentRouting.from_lengths(lengths, ids)
+    y, dx, dAs, dBs = run_hip(pkg, dev, x, w, b, As, Bs, dy, [1.0, 1.0], routing)
+    assert all(g.dtype == torch.float32 for g in dAs + dBs)
+    q = lambda t: f64(t.to(torch.bfloat16))  # noqa: E731
+    dx_ref, dA_ref, dB_ref = O.backward(f64(x), f64(w), [q(a) for a in As], [q(v) for v in Bs], [1.0, 1.0],
+                                        routing.seg_offsets, routing.adapter_ids, f64(dy))
+    for i in range(2):
+        assert O.rel_l2(f64(dAs[i]), dA_ref[i]) <= TOL
+        assert O.rel_l2(f64(dBs[i]), dB_ref[i]) <= TOL
+
+
+def test_drop_in_trainable_scope_under_autocast(pkg, dev):
+    """The reference's trainable_scope contract on a small fp32 model run under bf16 autocast."""
+    torch.manual_seed(18)
+    model = torch.nn.Sequential(torch.nn.Linear(64, 128), torch.nn.GELU(), torch.nn.Linear(128, 64))
+    pkg.trainable_scope(model, {'mode': 'lora', 'rank': 8, 'alpha': 16., 'targets': ['0', '2']})
+    with torch.no_grad():
+        for m in (model[0], model[2]):
+            m.lora_b.normal_(0, 0.05)
+    model = model.to(dev)
+    x = torch.randn(3, 40, 64, device=dev)
+    with torch.autocast("cuda", dtype=torch.bfloat16):
+        y = model(x)
+    assert y.dtype == torch.bfloat16 and y.shape == (3, 40, 64)
+    y.float().square().mean().backward()
+    for m in (model[0], model[2]):
+        assert m.lora_a.grad is not None and m.lora_a.grad.dtype == torch.float32
+        assert m.base.weight.grad is None
+    # compare the first layer against the oracle on autocast-rounded inputs
+    m0 = model[0]
+    q = lambda t: f64(t.to(torch.bfloat16))  # noqa: E731
+    h = O.forward(q(x.reshape(-1, 64)), q(m0.base.weight), f64(m0.base.bias), [q(m0.lora_a)], [q(m0.lora_b)],
+                  [2.0], [0, 120], [0])
+    with torch.no_grad(), torch.autocast("cuda", dtype=torch.bfloat16):
+        got = m0(x).reshape(-1, 128)
+    assert O.rel_l2(f64(got), h) <= TOL
+
+
+def test_expand_standalone_accumulates(pkg, dev):
+    """K = 0 + accumulate: Y += h·Bᵀ, the reference's LoRA-B GEMM + residual
+    (runtime/helios_lora_b_gemm_kernel.py:25-50) as one launch."""
+    M, N, r = 300, 192, 32
+    g = torch.Generator().manual_seed(19)
+    base = torch.randn(M, N, generator=g).to(torch.bfloat16)
+    h = torch.randn(M, r, generator=g).to(torch.bfloat16)
+    B = (torch.randn(N, r, generator=g) * 0.1).to(torch.bfloat16)
+    routing = pkg.SegmentRouting.single(M, 0)
+    y = base.to(dev).clone()
+    x0 = torch.empty(M, 0, dtype=torch.bfloat16, device=dev)
+    w0 = torch.empty(N, 0, dtype=torch.bfloat16, device=dev)
+    pkg.kernels.gemm_fwd(x0, w0, None, h.to(dev), [B.to(dev)], routing, out=y, accumulate=True)
+    want = f64(base) + f64(h) @ f64(B).T
+    assert O.rel_l2(f64(y), want) <= TOL
+
+
+@pytest.mark.parametrize("name,K,N", [("q", 1536, 1536), ("ffn.0", 1536, 8960), ("ffn.2", 8960, 1536)])
+def test_wan13b_full_shape(pkg, dev, name, K, N):
+    """BASELINE config 2 (65520 tokens, 2 adapters rank 64) at full size:
+    Y and dX on 512 sampled rows vs the fp64 oracle, adapter gradients vs torch
+    fp32 on the GPU, frozen W untouched."""
+    from dmd_system_amd import workloads as W
+    cfg = W.CONFIGS["wan13b"]
+    x, w, b, As, Bs, dy = W.make_linear(cfg, K, N, dev, seed=cfg.seed)
+    w_sum = w.float().sum().item()
+    routing = cfg.routing
+    y, dx, dAs, dBs = run_hip(pkg, dev, x, w, b, As, Bs, dy, [cfg.scale] * 2, routing)
+    rows = np.sort(np.random.default_rng(20).choice(cfg.tokens, 512, replace=False))
+    rows[0], rows[-1] = 0, cfg.tokens - 1
+    Af, Bf = [f64(a) for a in As], [f64(v) for v in Bs]
+    off, ids = routing.seg_offsets, routing.adapter_ids
+    y_ref = O.forward_rows(np.arange(len(rows)), f64(x[rows]), f64(w), f64(b), Af, Bf, [cfg.scale] * 2,
+                           *_local_routing(rows, off, ids))
+    assert O.rel_l2(f64(y[rows]), y_ref) <= TOL
+    dx_ref = O.dx_rows(np.arange(len(rows)), f64(w), Af, Bf, [cfg.scale] * 2, *_local_routing(rows, off, ids),
+                       f64(dy[rows]))
+    assert O.rel_l2(f64(dx[rows]), dx_ref) <= TOL
+    # adapter gradients: torch fp32 matmuls on the same device
+    for a, (lo, hi) in enumerate(zip(off, off[1:])):
+        xs, dys = x[lo:hi].float(), dy[lo:hi].float()
+        h = xs @ As[a].float().T
+        dB_ref = cfg.scale * dys.T @ h
+        gh = cfg.scale * dys @ Bs[a].float()
+        dA_ref = gh.T @ xs
+        assert O.rel_l2(f64(dBs[a]), f64(dB_ref)) <= TOL
+        assert O.rel_l2(f64(dAs[a]), f64(dA_ref)) <= TOL
+    assert w.float().sum().item() == w_sum
+    assert torch.isfinite(y).all() and torch.isfinite(dx).all()
+
+
+def _local_routing(rows, off, ids):
+    """Routing of the sampled rows (kept in order) as consecutive segments."""
+    ad = O.row_adapters(off, ids)[rows]
+    loff, lids = [0], []
+    for i, a in enumerate(ad):
+        if not lids or lids[-1] != a:
+            if lids:
+                loff.append(i)
+            lids.append(int(a))
+    loff.append(len(ad))
+    return loff, lids

@@ -1,0 +1,223 @@
+"""Pins the CPU oracle before it is trusted as the checker of the HIP path.
+
+Each check is chosen so that a plausible mistake in the oracle (a dropped
+term, a transposed operand, a misplaced scale, a wrong segment index) fails:
+brute-force loops, finite differences, torch.autograd on an independent
+restatement, the reference's own construction fixture, and invariants.
+"""
+import itertools
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import multilora_oracle as O
+from oracle import torch_reference as TR
+
+
+def _case(rng, M=9, K=6, N=5, ranks=(2, 3), lengths=(3, 0, 2, 4), ids=(0, 1, -1, 1), bias=True):
+    x = rng.standard_normal((M, K))
+    w = rng.standard_normal((N, K))
+    b = rng.standard_normal(N) if bias else None
+    As = [rng.standard_normal((r, K)) for r in ranks]
+    Bs = [rng.standard_normal((N, r)) for r in ranks]
+    off = np.concatenate([[0], np.cumsum(lengths)]).astype(int).tolist()
+    assert off[-1] == M
+    return x, w, b, As, Bs, off, list(ids)
+
+
+# ---------------------------------------------------------------- bf16 rounding
+
+def test_bf16_round_known_values():
+    one = 1.0
+    ulp = 2.0 ** -7  # bf16 spacing in [1, 2)
+    vals = np.array([one, one + ulp / 2, one + 1.5 * ulp, one + 0.75 * ulp, -one - ulp / 2, 0.0, -0.0,
+                     np.inf, -np.inf, 3.0e38], dtype=np.float32)
+    want = np.array([one, one, one + 2 * ulp, one + ulp, -one, 0.0, -0.0, np.inf, -np.inf, 2.0 ** 128], dtype=np.float64)
+    got = O.bf16_round(vals).astype(np.float64)
+    # 3e38 rounds up past the largest bf16 (~3.39e38) only if above; check it stays finite-or-inf consistently
+    assert got[:9].tolist() == want[:9].tolist()
+    assert np.signbit(got[6])
+    assert np.isnan(O.bf16_round(np.array([np.nan], np.float32)))[0]
+
+
+def test_bf16_round_matches_torch_conversion():
+    rng = np.random.default_rng(0)
+    v = np.concatenate([rng.standard_normal(100000).astype(np.float32) * 10.0 ** rng.integers(-30, 30, 100000),
+                        rng.standard_normal(1000).astype(np.float32)]).astype(np.float32)
+    want = torch.from_numpy(v).to(torch.bfloat16).float().numpy()
+    np.testing.assert_array_equal(O.bf16_round(v), want)
+
+
+# ---------------------------------------------------------------- forward
+
+def _brute_forward(x, w, b, As, Bs, scales, off, ids):
+    M, K = x.shape
+    N = w.shape[0]
+    y = [[0.0] * N for _ in range(M)]
+    for s, a in enumerate(ids):
+        for m in range(off[s], off[s + 1]):
+            for n in range(N):
+                acc = sum(x[m][k] * w[n][k] for k in range(K)) + (b[n] if b is not None else 0.0)
+                if a >= 0:
+                    r = As[a].shape[0]
+                    h = [sum(x[m][k] * As[a][j][k] for k in range(K)) for j in range(r)]
+                    acc += scales[a] * sum(h[j] * Bs[a][n][j] for j in range(r))
+                y[m][n] = acc
+    return np.array(y)
+
+
+@pytest.mark.parametrize("bias", [True, False])
+def test_forward_matches_brute_force(bias):
+    rng = np.random.default_rng(1)
+    x, w, b, As, Bs, off, ids = _case(rng, bias=bias)
+    scales = [0.5, 2.0]
+    got = O.forward(x, w, b, As, Bs, scales, off, ids)
+    np.testing.assert_allclose(got, _brute_forward(x, w, b, As, Bs, scales, off, ids), rtol=1e-12, atol=1e-12)
+
+
+def test_forward_rows_and_dx_rows_agree_with_full():
+    rng = np.random.default_rng(2)
+    x, w, b, As, Bs, off, ids = _case(rng)
+    dy = rng.standard_normal((x.shape[0], w.shape[0]))
+    rows = [8, 0, 3, 5]
+    np.testing.assert_allclose(O.forward_rows(rows, x, w, b, As, Bs, [1.5, 0.25], off, ids),
+                               O.forward(x, w, b, As, Bs, [1.5, 0.25], off, ids)[rows], rtol=1e-13)
+    dx = O.backward(x, w, As, Bs, [1.5, 0.25], off, ids, dy)[0]
+    np.testing.assert_allclose(O.dx_rows(rows, w, As, Bs, [1.5, 0.25], off, ids, dy), dx[rows], rtol=1e-13)
+
+
+def test_reference_construction_fixture_known_answer():
+    """tests/test_training_construction.py:24-38 of the reference: 4x4 Linear filled
+    with 0.25, LoRA rank 2 alpha 2 (scale 1), lora_b initialised to zeros -> the
+    LoRA linear equals its base: y_n = 0.25 * sum(x) + 0.25."""
+    x = np.arange(12, dtype=np.float64).reshape(3, 4) / 7.0
+    w = np.full((4, 4), 0.25)
+    b = np.full(4, 0.25)
+    A = np.random.default_rng(3).uniform(-0.5, 0.5, (2, 4))
+    B = np.zeros((4, 2))
+    y = O.forward(x, w, b, [A], [B], [2.0 / 2], [0, 3], [0])
+    want = np.repeat((0.25 * x.sum(1) + 0.25)[:, None], 4, axis=1)
+    np.testing.assert_allclose(y, want, rtol=1e-14)
+
+
+def test_null_adapter_rows_are_base_only_and_scale_is_linear():
+    rng = np.random.default_rng(4)
+    x, w, b, As, Bs, off, ids = _case(rng)
+    y1 = O.forward(x, w, b, As, Bs, [1.0, 1.0], off, ids)
+    y0 = O.forward(x, w, b, As, Bs, [0.0, 0.0], off, ids)
+    y3 = O.forward(x, w, b, As, Bs, [3.0, 3.0], off, ids)
+    np.testing.assert_allclose(y3 - y0, 3.0 * (y1 - y0), rtol=1e-12, atol=1e-12)
+    base = x @ w.T + b
+    np.testing.assert_allclose(y0, base, rtol=1e-14)
+    lo, hi = off[2], off[3]  # the -1 segment
+    np.testing.assert_array_equal(y1[lo:hi], base[lo:hi])
+
+
+def test_segment_permutation_and_per_role_concatenation():
+    rng = np.random.default_rng(5)
+    x, w, b, As, Bs, off, ids = _case(rng)
+    scales = [0.7, 1.3]
+    y = O.forward(x, w, b, As, Bs, scales, off, ids)
+    # one call per role (the reference's per-module calls) == the batched call
+    for s, a in enumerate(ids):
+        lo, hi = off[s], off[s + 1]
+        ys = O.forward(x[lo:hi], w, b, As, Bs, scales, [0, hi - lo], [a])
+        np.testing.assert_allclose(ys, y[lo:hi], rtol=1e-13)
+    # reversing segment order permutes the rows accordingly
+    segs = [(off[s], off[s + 1], a) for s, a in enumerate(ids)][::-1]
+    order = np.concatenate([np.arange(lo, hi) for lo, hi, _ in segs]).astype(int)
+    off2 = np.concatenate([[0], np.cumsum([hi - lo for lo, hi, _ in segs])]).tolist()
+    y2 = O.forward(x[order], w, b, As, Bs, scales, off2, [a for _, _, a in segs])
+    np.testing.assert_allclose(y2, y[order], rtol=1e-13)
+
+
+# ---------------------------------------------------------------- backward
+
+def test_backward_matches_finite_differences():
+    rng = np.random.default_rng(6)
+    x, w, b, As, Bs, off, ids = _case(rng, M=7, K=4, N=3, ranks=(2, 1), lengths=(2, 3, 2, 0), ids=(1, 0, -1, 0))
+    scales = [0.9, -1.7]
+    dy = rng.standard_normal((7, 3))
+    dx, dAs, dBs = O.backward(x, w, As, Bs, scales, off, ids, dy)
+
+    def loss(x_, As_, Bs_):
+        return float((O.forward(x_, w, b, As_, Bs_, scales, off, ids) * dy).sum())
+
+    eps = 1e-6
+
+    def numgrad(arr, fn):
+        g = np.zeros_like(arr)
+        for idx in itertools.product(*map(range, arr.shape)):
+            old = arr[idx]
+            arr[idx] = old + eps
+            fp = fn()
+            arr[idx] = old - eps
+            fm = fn()
+            arr[idx] = old
+            g[idx] = (fp - fm) / (2 * eps)
+        return g
+
+    np.testing.assert_allclose(dx, numgrad(x, lambda: loss(x, As, Bs)), rtol=1e-6, atol=1e-7)
+    for i in range(2):
+        np.testing.assert_allclose(dAs[i], numgrad(As[i], lambda: loss(x, As, Bs)), rtol=1e-6, atol=1e-7)
+        np.testing.assert_allclose(dBs[i], numgrad(Bs[i], lambda: loss(x, As, Bs)), rtol=1e-6, atol=1e-7)
+
+
+def test_backward_matches_torch_autograd_of_per_adapter_path():
+    rng = np.random.default_rng(7)
+    x, w, b, As, Bs, off, ids = _case(rng, M=40, K=16, N=12, ranks=(4, 8), lengths=(10, 12, 8, 10), ids=(1, -1, 0, 1))
+    scales = [1.25, 0.5]
+    dy = rng.standard_normal((40, 12))
+    t = lambda a: torch.from_numpy(np.asarray(a, np.float64))  # noqa: E731
+    y, dx, dAs, dBs = TR.per_adapter_step(t(x), t(w), t(b), [t(a) for a in As], [t(v) for v in Bs], scales,
+                                          off, ids, t(dy))
+    np.testing.assert_allclose(O.forward(x, w, b, As, Bs, scales, off, ids), y.numpy(), rtol=1e-12)
+    odx, odAs, odBs = O.backward(x, w, As, Bs, scales, off, ids, dy)
+    np.testing.assert_allclose(odx, dx.numpy(), rtol=1e-12)
+    for i in range(2):
+        np.testing.assert_allclose(odAs[i], dAs[i].numpy(), rtol=1e-12)
+        np.testing.assert_allclose(odBs[i], dBs[i].numpy(), rtol=1e-12)
+
+
+def test_adapter_without_rows_gets_zero_gradient():
+    rng = np.random.default_rng(8)
+    x, w, b, As, Bs, off, ids = _case(rng, ranks=(2, 3, 2), ids=(0, 1, -1, 1))
+    dy = rng.standard_normal((x.shape[0], w.shape[0]))
+    _, dAs, dBs = O.backward(x, w, As, Bs, [1, 1, 1], off, ids, dy)
+    assert not dAs[2].any() and not dBs[2].any()
+
+
+# ---------------------------------------------------------------- reference rounding variants
+
+def test_autocast_restatement_matches_torch_cpu_autocast():
+    """low_rank.py:28 under bf16 autocast, evaluated by torch's CPU autocast."""
+    rng = np.random.default_rng(9)
+    M, K, N = 64, 32, 24
+    x, w, b, As, Bs, off, ids = _case(rng, M=M, K=K, N=N, ranks=(8, 8), lengths=(30, 34), ids=(0, 1))
+    scales = [1.0, 2.0]
+    t = lambda a: torch.from_numpy(np.asarray(a, np.float32))  # noqa: E731
+    with torch.autocast("cpu", dtype=torch.bfloat16):
+        yt = TR.per_adapter_forward(t(x), t(w), t(b), [t(a) for a in As], [t(v) for v in Bs], scales, off, ids)
+    assert yt.dtype == torch.bfloat16
+    ours = O.forward_autocast_bf16(x, w, b, As, Bs, scales, off, ids)
+    # same rounding points; only the fp32 accumulation order inside each product may differ
+    assert O.rel_l2(ours, yt.float().numpy()) < 2e-3
+    truth = O.forward(O.bf16_round(x), O.bf16_round(w), O.bf16_round(b), [O.bf16_round(a) for a in As],
+                      [O.bf16_round(v) for v in Bs], scales, off, ids)
+    assert O.rel_l2(ours, truth) < 1e-2
+
+
+def test_fp32_update_and_livewan_variants_are_close_to_exact():
+    rng = np.random.default_rng(10)
+    x, w, b, As, Bs, off, ids = _case(rng, M=64, K=32, N=24, ranks=(8, 8), lengths=(30, 34), ids=(0, 1))
+    q = O.bf16_round
+    truth = O.forward(q(x), q(w), q(b), As, Bs, [1.0, 1.0], off, ids)
+    for fn in (O.forward_fp32_update, O.forward_livewan):
+        assert O.rel_l2(fn(x, w, b, As, Bs, [1.0, 1.0], off, ids), truth) < 1e-2
+
+
+def test_rel_l2_definition():
+    assert O.rel_l2([3.0, 4.0], [3.0, 4.0]) == 0.0
+    assert math.isclose(O.rel_l2([3.0, 4.0], [0.0, 5.0]), math.hypot(3, 1) / 5.0)
