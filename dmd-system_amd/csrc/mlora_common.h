@@ -2,7 +2,7 @@
 //
 // Conventions used by every kernel in this library:
 //   * bf16 values travel as raw uint16_t bit patterns; MFMA operands are
-//     8 x bf16 = 16 bytes per lane, loaded as one uint4.
+//     8 x bf16 = 16 bytes per lane, loaded as one u32x4.
 //   * An LDS tile row holds 64 contraction elements = 8 chunks of 16 bytes.
 //     Chunk c of row r is stored at chunk position c ^ swz(r) so that the 32
 //     (or 16) lanes of one fragment read hit distinct banks.
@@ -18,8 +18,43 @@
 namespace mlora {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+// Explicit address spaces: LDS pointers stay ds_* instructions and global
+// traffic goes through buffer resources (never generic flat accesses).
+#define MLORA_LDS __attribute__((address_space(3)))
+#define MLORA_GLOBAL __attribute__((address_space(1)))
+typedef MLORA_LDS u32x4 lds_u4;
+typedef MLORA_LDS f32x4 lds_f4;
+
+template <class T>
+__device__ __forceinline__ MLORA_GLOBAL T *gp(T *p) {
+  return (MLORA_GLOBAL T *)p;
+}
+
+// Raw buffer resource over [base, base + bytes); loads at offsets >= bytes
+// return zeros, which is how every loader masks rows/columns out of range.
+constexpr uint32_t kBufFlags = 0x00020000u;  // gfx9 raw buffer, dword data format
+constexpr int32_t kOOB = 0x7ffffff0;         // an offset past every buffer we build
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void *base, int64_t bytes) {
+  const int32_t n = bytes > (int64_t)kOOB ? kOOB : (bytes < 0 ? 0 : (int32_t)bytes);
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, n, (int)kBufFlags);
+}
+
+__device__ __forceinline__ u32x4 buf_load16(__amdgpu_buffer_rsrc_t r, int32_t off) {
+  return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
+}
+
+__device__ __forceinline__ float buf_load4f(__amdgpu_buffer_rsrc_t r, int32_t off) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0));
+}
+
+__device__ __forceinline__ void buf_store8(__amdgpu_buffer_rsrc_t r, int32_t off, uint2 v) {
+  __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(__attribute__((ext_vector_type(2))) unsigned, v), r, off, 0, 0);
+}
 
 constexpr int kMaxSeg = MLORA_MAX_SEGMENTS;
 constexpr int kMaxAdapters = MLORA_MAX_ADAPTERS;
@@ -54,12 +89,12 @@ __device__ __forceinline__ uint32_t pack2_bf16(float lo, float hi) {
   return (uint32_t)f32_to_bf16_rne(lo) | ((uint32_t)f32_to_bf16_rne(hi) << 16);
 }
 
-__device__ __forceinline__ bf16x8 as_bf16x8(uint4 v) { return __builtin_bit_cast(bf16x8, v); }
+__device__ __forceinline__ bf16x8 as_bf16x8(u32x4 v) { return __builtin_bit_cast(bf16x8, v); }
 
 // Split 8 fp32 values into hi = bf16(v) and lo = bf16(v - hi): hi + lo carries
 // ~16 significant bits, so one bf16 MFMA per part keeps fp32-class accuracy
 // for the adapter-gradient reductions.
-__device__ __forceinline__ void split_hi_lo(const float (&v)[8], uint4 &hi, uint4 &lo) {
+__device__ __forceinline__ void split_hi_lo(const float (&v)[8], u32x4 &hi, u32x4 &lo) {
   uint32_t h[4], l[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
@@ -70,18 +105,18 @@ __device__ __forceinline__ void split_hi_lo(const float (&v)[8], uint4 &hi, uint
     h[i] = (uint32_t)h0 | ((uint32_t)h1 << 16);
     l[i] = pack2_bf16(r0, r1);
   }
-  hi = make_uint4(h[0], h[1], h[2], h[3]);
-  lo = make_uint4(l[0], l[1], l[2], l[3]);
+  hi = u32x4{h[0], h[1], h[2], h[3]};
+  lo = u32x4{l[0], l[1], l[2], l[3]};
 }
 
-// Transpose an 8x8 block of 16-bit values held as 8 rows of uint4
+// Transpose an 8x8 block of 16-bit values held as 8 rows of u32x4
 // (row e = 8 consecutive columns). Output t holds column t as 8 values
 // (element e = row e).
-__device__ __forceinline__ uint32_t word_of(const uint4 &v, int i) {
+__device__ __forceinline__ uint32_t word_of(const u32x4 &v, int i) {
   return i == 0 ? v.x : (i == 1 ? v.y : (i == 2 ? v.z : v.w));
 }
 
-__device__ __forceinline__ void transpose8x8_b16(const uint4 (&in)[8], uint4 (&out)[8]) {
+__device__ __forceinline__ void transpose8x8_b16(const u32x4 (&in)[8], u32x4 (&out)[8]) {
 #pragma unroll
   for (int t = 0; t < 8; ++t) {
     uint32_t o[4];
@@ -92,7 +127,7 @@ __device__ __forceinline__ void transpose8x8_b16(const uint4 (&in)[8], uint4 (&o
       // element t of rows 2q (low half) and 2q+1 (high half)
       o[q] = (t & 1) ? ((a >> 16) | (b & 0xffff0000u)) : ((a & 0xffffu) | (b << 16));
     }
-    out[t] = make_uint4(o[0], o[1], o[2], o[3]);
+    out[t] = u32x4{o[0], o[1], o[2], o[3]};
   }
 }
 

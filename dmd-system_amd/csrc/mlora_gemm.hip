@@ -8,14 +8,17 @@
 // "NN" ([Kc, Ncols]: W and A_a in dX). The LoRA term is more contraction: after
 // the main loop over Kc, every segment that overlaps the tile's rows and has
 // an adapter runs ceil(r/64) extra k-tiles with P = Hs rows of that segment
-// (other rows zero) and Q = that adapter's B_a / A_a. Y is written once.
+// (other rows read as zero) and Q = that adapter's B_a / A_a. Y is written once.
 //
 // gfx950 mapping: v_mfma_f32_32x32x16_bf16, wave64. A workgroup of WM x WN
-// waves owns a BM x BN tile; every wave a (BM/WM) x (BN/WN) sub-tile. Operand
-// tiles of 64 contraction elements are double-buffered in LDS (one barrier per
-// k-tile); the global loads for tile k+1 are in flight while tile k is
-// multiplied. NN operands are transposed in registers (8x8 blocks of bf16) on
-// their way into LDS, so both layouts are read from LDS the same way.
+// waves owns a BM x BN tile; each wave a (BM/WM) x (BN/WN) sub-tile whose fp32
+// accumulators live in AGPRs. Operand tiles of 64 contraction elements are
+// double-buffered in LDS (one barrier per k-tile): the buffer loads of tile k+1
+// are in flight while tile k is multiplied. Global reads use raw buffer
+// resources; out-of-range rows/columns are given an offset past the buffer and
+// read as zero, so tails need no branches. NN operands are transposed in
+// registers (8x8 blocks of bf16) on their way into LDS, so both layouts are
+// read from LDS the same way (16-byte fragments, XOR-swizzled chunks).
 // Reference semantics: training/low_rank.py:26-28 (and its autograd backward).
 #include "mlora_common.h"
 #include "mlora_host.h"
@@ -48,13 +51,15 @@ struct GemmCfg {
   static constexpr int A_CH = BM * 8 / THREADS;  // 16-byte chunks of the P tile per thread
   static constexpr int B_CH = BN * 8 / THREADS;  // NT: chunks of the Q tile per thread
   static constexpr int B_BLK = (BN + THREADS - 1) / THREADS;  // NN: 8x8 blocks per thread
+  static constexpr int ROWS_PER_PASS = THREADS / 8;
+  static constexpr int STAGE = (BM + BN) * 8;  // u32x4 per LDS stage
   static_assert(A_CH * THREADS == BM * 8, "P tile must split evenly over threads");
   static_assert(NN || B_CH * THREADS == BN * 8, "Q tile must split evenly over threads");
   static constexpr int GROUP_M = 8;
 };
 
-// One contraction source: P rows valid in [row_lo, row_hi), contraction valid
-// below klim for both operands.
+// One contraction source (wave-uniform): P rows valid in [row_lo, row_hi),
+// contraction valid below klim for both operands.
 struct KSource {
   const uint16_t *P;
   const uint16_t *Q;
@@ -64,59 +69,74 @@ struct KSource {
 };
 
 template <class C>
-struct GemmTile {
-  uint4 a_regs[C::A_CH];
-  uint4 b_regs[C::NN ? 8 * C::B_BLK : C::B_CH];
+struct Pipe {
+  __amdgpu_buffer_rsrc_t rp, rq;
+  int32_t p_off[C::A_CH];  // byte offset of each P chunk at k = 0, or kOOB
+  int32_t q_off[C::NN ? 1 : C::B_CH];
+  int32_t kchunk;          // 8 * (tid & 7): contraction index of this thread's chunks
+  int32_t ldq_b;
+  int32_t nn_col_ok;
+  int32_t klim;
+  u32x4 a_regs[C::A_CH];
+  u32x4 b_regs[C::NN ? 8 * C::B_BLK : C::B_CH];
 
-  __device__ __forceinline__ void load(const KSource &src, int m0, int n0, int Ncols, int k0, int tid) {
-    const uint4 zero = make_uint4(0, 0, 0, 0);
+  __device__ __forceinline__ void init(const KSource &s, int m0, int n0, int Ncols, int tid) {
+    klim = s.klim;
+    kchunk = 8 * (tid & 7);
+    const int base_row = max(s.row_lo, m0);
+    const int64_t ldp_b = s.ldp * 2;
+    rp = make_rsrc(s.P + (int64_t)base_row * s.ldp, (int64_t)(s.row_hi - base_row) * ldp_b);
 #pragma unroll
     for (int i = 0; i < C::A_CH; ++i) {
-      const int q = tid + i * C::THREADS;
-      const int r = q >> 3, c = q & 7;
-      const int grow = m0 + r, kk = k0 + c * 8;
-      a_regs[i] = (grow >= src.row_lo && grow < src.row_hi && kk < src.klim)
-                      ? *reinterpret_cast<const uint4 *>(src.P + (int64_t)grow * src.ldp + kk)
-                      : zero;
+      const int grow = m0 + (tid >> 3) + i * C::ROWS_PER_PASS;
+      p_off[i] = (grow >= base_row && grow < s.row_hi) ? (int32_t)((grow - base_row) * ldp_b + kchunk * 2) : kOOB;
     }
+    ldq_b = (int32_t)(s.ldq * 2);
+    if constexpr (!C::NN) {
+      rq = make_rsrc(s.Q + (int64_t)n0 * s.ldq, (int64_t)(Ncols - n0) * s.ldq * 2);
+#pragma unroll
+      for (int i = 0; i < C::B_CH; ++i) q_off[i] = ((tid >> 3) + i * C::ROWS_PER_PASS) * ldq_b + kchunk * 2;
+    } else {
+      rq = make_rsrc(s.Q + n0, (int64_t)s.klim * s.ldq * 2);
+      const int bc = tid % (C::BN / 8);
+      nn_col_ok = (n0 + 8 * bc < Ncols) ? 1 : 0;
+    }
+  }
+
+  __device__ __forceinline__ void load(int k0, int tid) {
+    const bool kok = k0 + kchunk < klim;
+#pragma unroll
+    for (int i = 0; i < C::A_CH; ++i) a_regs[i] = buf_load16(rp, kok ? p_off[i] + k0 * 2 : kOOB);
     if constexpr (!C::NN) {
 #pragma unroll
-      for (int i = 0; i < C::B_CH; ++i) {
-        const int q = tid + i * C::THREADS;
-        const int r = q >> 3, c = q & 7;
-        const int gcol = n0 + r, kk = k0 + c * 8;
-        b_regs[i] = (gcol < Ncols && kk < src.klim)
-                        ? *reinterpret_cast<const uint4 *>(src.Q + (int64_t)gcol * src.ldq + kk)
-                        : zero;
-      }
+      for (int i = 0; i < C::B_CH; ++i) b_regs[i] = buf_load16(rq, kok ? q_off[i] + k0 * 2 : kOOB);
     } else {
 #pragma unroll
       for (int i = 0; i < C::B_BLK; ++i) {
         const int b = tid + i * C::THREADS;
         const int a = b / (C::BN / 8), bc = b % (C::BN / 8);
-        const int gcol = n0 + bc * 8;
+        const bool ok = b < C::BN && nn_col_ok;
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
           const int kr = k0 + a * 8 + e;
-          b_regs[i * 8 + e] = (b < C::BN && gcol < Ncols && kr < src.klim)
-                                  ? *reinterpret_cast<const uint4 *>(src.Q + (int64_t)kr * src.ldq + gcol)
-                                  : zero;
+          b_regs[i * 8 + e] = buf_load16(rq, (ok && kr < klim) ? kr * ldq_b + bc * 16 : kOOB);
         }
       }
     }
   }
 
-  __device__ __forceinline__ void store(uint4 *ldsA, uint4 *ldsB, int tid) {
+  __device__ __forceinline__ void store(lds_u4 *ldsA, lds_u4 *ldsB, int tid) const {
+    const int c = tid & 7;
 #pragma unroll
     for (int i = 0; i < C::A_CH; ++i) {
-      const int q = tid + i * C::THREADS;
-      ldsA[lds_chunk_offset(q >> 3, q & 7)] = a_regs[i];
+      const int r = (tid >> 3) + i * C::ROWS_PER_PASS;
+      ldsA[lds_chunk_offset(r, c)] = a_regs[i];
     }
     if constexpr (!C::NN) {
 #pragma unroll
       for (int i = 0; i < C::B_CH; ++i) {
-        const int q = tid + i * C::THREADS;
-        ldsB[lds_chunk_offset(q >> 3, q & 7)] = b_regs[i];
+        const int r = (tid >> 3) + i * C::ROWS_PER_PASS;
+        ldsB[lds_chunk_offset(r, c)] = b_regs[i];
       }
     } else {
 #pragma unroll
@@ -124,7 +144,7 @@ struct GemmTile {
         const int b = tid + i * C::THREADS;
         if (b < C::BN) {
           const int a = b / (C::BN / 8), bc = b % (C::BN / 8);
-          uint4 blk[8], tr[8];
+          u32x4 blk[8], tr[8];
 #pragma unroll
           for (int e = 0; e < 8; ++e) blk[e] = b_regs[i * 8 + e];
           transpose8x8_b16(blk, tr);
@@ -137,7 +157,7 @@ struct GemmTile {
 };
 
 template <class C>
-__device__ __forceinline__ void mma_stage(f32x16 (&acc)[C::TM][C::TN], const uint4 *ldsA, const uint4 *ldsB,
+__device__ __forceinline__ void mma_stage(f32x16 (&acc)[C::TM][C::TN], const lds_u4 *ldsA, const lds_u4 *ldsB,
                                           int wm0, int wn0, int lane) {
 #pragma unroll
   for (int s = 0; s < 4; ++s) {
@@ -157,31 +177,37 @@ __device__ __forceinline__ void mma_stage(f32x16 (&acc)[C::TM][C::TN], const uin
   }
 }
 
-// Contraction over one source, pipelined through the two LDS buffers.
+// Contraction over one source, pipelined through the two LDS stages.
 template <class C>
-__device__ __forceinline__ void run_source(f32x16 (&acc)[C::TM][C::TN], const KSource &src, uint4 *lds, int m0, int n0,
-                                           int Ncols, int wm0, int wn0, int tid, int lane) {
+__device__ __forceinline__ void run_source(f32x16 (&acc)[C::TM][C::TN], const KSource &src, lds_u4 *lds, int m0,
+                                           int n0, int Ncols, int wm0, int wn0, int tid, int lane) {
   const int nk = (src.klim + C::BK - 1) / C::BK;
   if (nk <= 0) return;
-  uint4 *ldsA[2] = {lds, lds + (C::BM + C::BN) * 8};
-  uint4 *ldsB[2] = {lds + C::BM * 8, lds + (C::BM + C::BN) * 8 + C::BM * 8};
-  GemmTile<C> tile;
-  tile.load(src, m0, n0, Ncols, 0, tid);
+  Pipe<C> pipe;
+  pipe.init(src, m0, n0, Ncols, tid);
+  pipe.load(0, tid);
   __syncthreads();  // LDS may still be read by a previous source's last stage
-  tile.store(ldsA[0], ldsB[0], tid);
+  pipe.store(lds, lds + C::BM * 8, tid);
   __syncthreads();
   for (int kt = 0; kt < nk; ++kt) {
-    const bool more = kt + 1 < nk;
-    if (more) tile.load(src, m0, n0, Ncols, (kt + 1) * C::BK, tid);
-    mma_stage<C>(acc, ldsA[kt & 1], ldsB[kt & 1], wm0, wn0, lane);
-    if (more) tile.store(ldsA[(kt + 1) & 1], ldsB[(kt + 1) & 1], tid);
+    // the load past the last tile reads zeros (offsets out of range) and is never used
+    pipe.load((kt + 1) * C::BK, tid);
+    // keep the loads issued ahead of the MFMAs (the scheduler would sink them
+    // next to their LDS stores and expose the full memory latency)
+    __builtin_amdgcn_sched_barrier(0);
+    lds_u4 *cur = lds + (kt & 1) * C::STAGE;
+    lds_u4 *nxt = lds + ((kt + 1) & 1) * C::STAGE;
+    mma_stage<C>(acc, cur, cur + C::BM * 8, wm0, wn0, lane);
+    __builtin_amdgcn_sched_barrier(0);
+    pipe.store(nxt, nxt + C::BM * 8, tid);
     __syncthreads();
   }
 }
 
 template <class C>
 __global__ __launch_bounds__(C::THREADS) void gemm_kernel(const GemmArgs args) {
-  __shared__ uint4 lds[2 * (C::BM + C::BN) * 8];
+  __shared__ u32x4 smem[2 * C::STAGE];
+  lds_u4 *lds = (lds_u4 *)smem;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm0 = (wave / C::WN) * (C::BM / C::WM);
   const int wn0 = (wave % C::WN) * (C::BN / C::WN);
@@ -226,10 +252,13 @@ __global__ __launch_bounds__(C::THREADS) void gemm_kernel(const GemmArgs args) {
   }
 
   // epilogue: + bias, (+ Y), round to bf16, 8-byte stores of 4 consecutive n
+  const int rows_here = min(C::BM, args.M - m0);
+  const int64_t ldy_b = args.ldy * 2;
+  const __amdgpu_buffer_rsrc_t ry = make_rsrc(args.Y + (int64_t)m0 * args.ldy, rows_here * ldy_b);
 #pragma unroll
   for (int i = 0; i < C::TM; ++i) {
-    const int m = m0 + wm0 + 32 * i + (lane & 31);
-    if (m >= args.M) continue;
+    const int ml = wm0 + 32 * i + (lane & 31);
+    if (ml >= rows_here) continue;
 #pragma unroll
     for (int j = 0; j < C::TN; ++j) {
 #pragma unroll
@@ -247,13 +276,13 @@ __global__ __launch_bounds__(C::THREADS) void gemm_kernel(const GemmArgs args) {
           v[0] += bf16_to_f32(b.x & 0xffff); v[1] += bf16_to_f32(b.x >> 16);
           v[2] += bf16_to_f32(b.y & 0xffff); v[3] += bf16_to_f32(b.y >> 16);
         }
-        uint16_t *dst = args.Y + (int64_t)m * args.ldy + n;
+        const int32_t off = (int32_t)(ml * ldy_b + n * 2);
         if (args.accumulate) {
-          const uint2 o = *reinterpret_cast<const uint2 *>(dst);
+          const uint2 o = *reinterpret_cast<const uint2 *>(args.Y + (int64_t)(m0 + ml) * args.ldy + n);
           v[0] += bf16_to_f32(o.x & 0xffff); v[1] += bf16_to_f32(o.x >> 16);
           v[2] += bf16_to_f32(o.y & 0xffff); v[3] += bf16_to_f32(o.y >> 16);
         }
-        *reinterpret_cast<uint2 *>(dst) = make_uint2(pack2_bf16(v[0], v[1]), pack2_bf16(v[2], v[3]));
+        buf_store8(ry, off, make_uint2(pack2_bf16(v[0], v[1]), pack2_bf16(v[2], v[3])));
       }
     }
   }
@@ -275,10 +304,11 @@ static int launch_gemm(GemmArgs &a, hipStream_t stream) {
   return launch_status();
 }
 
-// Tile choice: 128x128 (4 waves of 64x64, no register spills).
+// Tile choice: 256x256 when that still gives every CU at least one tile, else 128x128.
 template <class Big, class Small>
 static int dispatch_gemm(GemmArgs &a, hipStream_t stream) {
-  (void)sizeof(Big);
+  const int64_t big_tiles = (int64_t)((a.M + 255) / 256) * ((a.Ncols + 255) / 256);
+  if (big_tiles >= 256) return launch_gemm<Big>(a, stream);
   return launch_gemm<Small>(a, stream);
 }
 
@@ -304,6 +334,10 @@ static int fill_common(GemmArgs &a, int64_t M, int64_t Kc, int64_t Ncols, const 
   return MLORA_OK;
 }
 
+// Byte offsets inside one buffer resource are 31-bit: a tile's rows of P and Y,
+// and all of an NN operand, must stay below that.
+static bool offsets_fit(int64_t ld, int64_t rows) { return ld * 2 * rows < (int64_t)kOOB; }
+
 }  // namespace mlora
 
 using namespace mlora;
@@ -325,6 +359,7 @@ extern "C" int mlora_gemm_fwd(const void *x, int64_t ldx, int64_t M, int64_t K, 
     if (bias_dtype != MLORA_F32 && bias_dtype != MLORA_BF16) return MLORA_ERR_UNSUPPORTED;
     if (!aligned16(bias)) return MLORA_ERR_UNSUPPORTED;
   }
+  if (!offsets_fit(ldx, 256) || !offsets_fit(ldy, 256) || !offsets_fit(ldw, 256)) return MLORA_ERR_LIMIT;
   a.P = static_cast<const uint16_t *>(x);
   a.Q = static_cast<const uint16_t *>(w);
   a.ldp = ldx;
@@ -350,6 +385,8 @@ extern "C" int mlora_gemm_dx(const void *dy, int64_t lddy, int64_t M, int64_t N,
   if ((st = check_bf16_matrix(dx, lddx, M, K))) return st;
   if (M == 0 || K == 0) return MLORA_OK;
   if (dx == nullptr) return MLORA_ERR_INVALID;
+  if (!offsets_fit(lddy, 256) || !offsets_fit(lddx, 256) || !offsets_fit(ldw, N) || !offsets_fit(K, kMaxRank))
+    return MLORA_ERR_LIMIT;
   a.P = static_cast<const uint16_t *>(dy);
   a.Q = static_cast<const uint16_t *>(w);
   a.ldp = lddy;

@@ -41,7 +41,8 @@ template <int WT, int RT, int OPL>
 __global__ __launch_bounds__(256) void shrink_kernel(const ShrinkArgs args) {
   constexpr int BMS = 4 * WT * 32;
   constexpr int OPROWS = 32 * RT;
-  __shared__ uint4 lds[2 * OPROWS * 8];
+  __shared__ u32x4 smem[2 * OPROWS * 8];
+  lds_u4 *lds = (lds_u4 *)smem;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
 
   // workgroup -> (segment, tile)
@@ -51,16 +52,21 @@ __global__ __launch_bounds__(256) void shrink_kernel(const ShrinkArgs args) {
   const int a = args.seg.aid[s];
   const int r = args.op.rank[a];
   const float scale = args.op.scale[a];
-  const uint16_t *op = args.op.ptr[a];
   const int m0 = args.seg.off[s] + (bid - args.tile_start[s]) * BMS;
   const int mend = args.seg.off[s + 1];
   const int K = args.K;
   const int nk = (K + 63) / 64;
+  const int64_t ldp_b = args.ldp * 2;
+  const __amdgpu_buffer_rsrc_t rop = make_rsrc(args.op.ptr[a], (int64_t)r * K * 2);
+  // rows past the segment end fall outside this resource and read as zero
+  const __amdgpu_buffer_rsrc_t rp = make_rsrc(args.P + (int64_t)m0 * args.ldp, (int64_t)(mend - m0) * ldp_b);
+  int32_t prow[WT];
+#pragma unroll
+  for (int i = 0; i < WT; ++i) prow[i] = (int32_t)((32 * (wave * WT + i) + (lane & 31)) * ldp_b);
 
   // ---- operand loaders
-  const uint4 zero = make_uint4(0, 0, 0, 0);
   constexpr int OP_CH = (OPROWS * 8 + 255) / 256;  // layout 0: chunks per thread
-  uint4 opr[OPL == 0 ? OP_CH : 8];
+  u32x4 opr[OPL == 0 ? OP_CH : 8];
   auto load_op = [&](int kc) {
     const int k0 = kc * 64;
     if constexpr (OPL == 0) {
@@ -69,21 +75,20 @@ __global__ __launch_bounds__(256) void shrink_kernel(const ShrinkArgs args) {
         const int q = tid + i * 256;
         const int j = q >> 3, c = q & 7;
         const int kk = k0 + 8 * c;
-        opr[i] = (q < OPROWS * 8 && j < r && kk < K) ? *reinterpret_cast<const uint4 *>(op + (int64_t)j * K + kk) : zero;
+        opr[i] = buf_load16(rop, (q < OPROWS * 8 && j < r && kk < K) ? (j * K + kk) * 2 : kOOB);
       }
     } else {
-      // [K, r]: thread b < 8*(OPROWS/8) loads an 8x8 block (8 k rows x 8 j)
+      // [K, r]: thread b < OPROWS loads an 8x8 block (8 k rows x 8 j)
       const int b = tid;
       const int kb = b / (OPROWS / 8), jb = b % (OPROWS / 8);
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         const int kk = k0 + 8 * kb + e;
-        opr[e] = (b < OPROWS && 8 * jb < r && kk < K) ? *reinterpret_cast<const uint4 *>(op + (int64_t)kk * r + 8 * jb)
-                                                        : zero;
+        opr[e] = buf_load16(rop, (b < OPROWS && 8 * jb < r && kk < K) ? (kk * r + 8 * jb) * 2 : kOOB);
       }
     }
   };
-  auto store_op = [&](uint4 *dst) {
+  auto store_op = [&](lds_u4 *dst) {
     if constexpr (OPL == 0) {
 #pragma unroll
       for (int i = 0; i < OP_CH; ++i) {
@@ -94,23 +99,21 @@ __global__ __launch_bounds__(256) void shrink_kernel(const ShrinkArgs args) {
       const int b = tid;
       if (b < OPROWS) {
         const int kb = b / (OPROWS / 8), jb = b % (OPROWS / 8);
-        uint4 tr[8];
+        u32x4 tr[8];
         transpose8x8_b16(opr, tr);
 #pragma unroll
         for (int t = 0; t < 8; ++t) dst[lds_chunk_offset(8 * jb + t, kb)] = tr[t];
       }
     }
   };
-  uint4 pc[WT][4], pn[WT][4];
-  auto load_p = [&](uint4 (&dst)[WT][4], int kc) {
+  u32x4 pc[WT][4], pn[WT][4];
+  auto load_p = [&](u32x4 (&dst)[WT][4], int kc) {
 #pragma unroll
     for (int i = 0; i < WT; ++i) {
-      const int row = m0 + 32 * (wave * WT + i) + (lane & 31);
-      const bool ok = row < mend;
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         const int kk = kc * 64 + 32 * (lane >> 5) + 8 * q;
-        dst[i][q] = (ok && kk < K) ? *reinterpret_cast<const uint4 *>(args.P + (int64_t)row * args.ldp + kk) : zero;
+        dst[i][q] = buf_load16(rp, kk < K ? prow[i] + kk * 2 : kOOB);
       }
     }
   };
@@ -128,12 +131,11 @@ __global__ __launch_bounds__(256) void shrink_kernel(const ShrinkArgs args) {
   store_op(lds);
   __syncthreads();
   for (int kc = 0; kc < nk; ++kc) {
-    const bool more = kc + 1 < nk;
-    if (more) {
-      load_op(kc + 1);
-      load_p(pn, kc + 1);
-    }
-    const uint4 *cur = lds + (kc & 1) * OPROWS * 8;
+    // loads past the last chunk read zeros and are not used
+    load_op(kc + 1);
+    load_p(pn, kc + 1);
+    __builtin_amdgcn_sched_barrier(0);  // keep the next chunk's loads ahead of the MFMAs
+    const lds_u4 *cur = lds + (kc & 1) * OPROWS * 8;
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
       const int c = 4 * (lane >> 5) + q;
@@ -146,17 +148,18 @@ __global__ __launch_bounds__(256) void shrink_kernel(const ShrinkArgs args) {
         for (int j = 0; j < RT; ++j)
           acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(pc[i][q]), of[j], acc[i][j], 0, 0, 0);
     }
-    if (more) store_op(lds + ((kc + 1) & 1) * OPROWS * 8);
+    __builtin_amdgcn_sched_barrier(0);
+    store_op(lds + ((kc + 1) & 1) * OPROWS * 8);
     __syncthreads();
-    if (more) {
 #pragma unroll
-      for (int i = 0; i < WT; ++i)
+    for (int i = 0; i < WT; ++i)
 #pragma unroll
-        for (int q = 0; q < 4; ++q) pc[i][q] = pn[i][q];
-    }
+      for (int q = 0; q < 4; ++q) pc[i][q] = pn[i][q];
   }
 
   // ---- epilogue: scale, bf16 row-major copy and fp32 transposed copy
+  MLORA_GLOBAL uint16_t *hr = gp(args.Hr);
+  MLORA_GLOBAL float *hc = args.Hc ? gp(args.Hc) : nullptr;
 #pragma unroll
   for (int i = 0; i < WT; ++i) {
 #pragma unroll
@@ -168,8 +171,8 @@ __global__ __launch_bounds__(256) void shrink_kernel(const ShrinkArgs args) {
         const int row = m0 + 32 * (wave * WT + i) + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
         if (row >= mend) continue;
         const float h = acc[i][j][v] * scale;
-        args.Hr[(int64_t)row * args.ldh + col] = f32_to_bf16_rne(h);
-        if (args.Hc) args.Hc[(int64_t)col * args.ldhc + row] = h;
+        hr[(int64_t)row * args.ldh + col] = f32_to_bf16_rne(h);
+        if (hc) hc[(int64_t)col * args.ldhc + row] = h;
       }
     }
   }
@@ -197,6 +200,7 @@ static void launch_shrink_rt(const ShrinkArgs &a, int nblocks, hipStream_t strea
 // fragment t), columns <- j, contraction <- m.
 
 constexpr int OUT_C = 128;  // c per workgroup
+constexpr int kMaxChunkRows = 32768;
 constexpr int OUT_J = 64;   // j per workgroup
 
 struct OuterArgs {
@@ -214,7 +218,8 @@ struct OuterArgs {
 };
 
 __global__ __launch_bounds__(256) void seg_outer_kernel(const OuterArgs args) {
-  __shared__ f32x4 red[3][32][64];  // waves 1..3: 32 f32x4 accumulators x 64 lanes
+  __shared__ f32x4 red_smem[3 * 32 * 64];  // waves 1..3: 32 f32x4 accumulators x 64 lanes
+  lds_f4 *red = (lds_f4 *)red_smem;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int item = blockIdx.x;
   const int cb = item % args.cblocks;
@@ -232,7 +237,10 @@ __global__ __launch_bounds__(256) void seg_outer_kernel(const OuterArgs args) {
   const int li = lane & 15, lq = lane >> 4;
   const int ccol = c0 + 8 * li;  // this lane's 8 columns
   const bool col_ok = ccol < args.C;
-  const uint4 zero = make_uint4(0, 0, 0, 0);
+  const int64_t ldp_b = args.ldp * 2;
+  // rows past the chunk end fall outside this resource and read as zero
+  const __amdgpu_buffer_rsrc_t rp = make_rsrc(args.P + (int64_t)row0 * args.ldp, (int64_t)(rend - row0) * ldp_b);
+  const __amdgpu_buffer_rsrc_t rq = make_rsrc(args.Qt, (int64_t)args.ldq * kMaxRank * 4);
 
   f32x4 acc[8][4];
 #pragma unroll
@@ -241,13 +249,13 @@ __global__ __launch_bounds__(256) void seg_outer_kernel(const OuterArgs args) {
     for (int q = 0; q < 4; ++q) acc[t][q] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   for (int m0 = row0 + 32 * wave; m0 < rend; m0 += 128) {
-    uint4 blk[8];
+    u32x4 blk[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
       const int m = m0 + 8 * lq + e;
-      blk[e] = (col_ok && m < rend) ? *reinterpret_cast<const uint4 *>(args.P + (int64_t)m * args.ldp + ccol) : zero;
+      blk[e] = buf_load16(rp, col_ok ? (int32_t)((m - row0) * ldp_b + ccol * 2) : kOOB);
     }
-    uint4 qhi[4], qlo[4];
+    u32x4 qhi[4], qlo[4];
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
       const int j = j0 + 16 * q + li;
@@ -255,11 +263,11 @@ __global__ __launch_bounds__(256) void seg_outer_kernel(const OuterArgs args) {
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         const int m = m0 + 8 * lq + e;
-        v[e] = (j < r && m < rend) ? args.Qt[(int64_t)j * args.ldq + m] : 0.f;
+        v[e] = buf_load4f(rq, (j < r && m < rend) ? (int32_t)(((int64_t)j * args.ldq + m) * 4) : kOOB);
       }
       split_hi_lo(v, qhi[q], qlo[q]);
     }
-    uint4 frag[8];
+    u32x4 frag[8];
     transpose8x8_b16(blk, frag);
 #pragma unroll
     for (int t = 0; t < 8; ++t)
@@ -275,7 +283,7 @@ __global__ __launch_bounds__(256) void seg_outer_kernel(const OuterArgs args) {
 #pragma unroll
     for (int t = 0; t < 8; ++t)
 #pragma unroll
-      for (int q = 0; q < 4; ++q) red[wave - 1][t * 4 + q][lane] = acc[t][q];
+      for (int q = 0; q < 4; ++q) red[((wave - 1) * 32 + t * 4 + q) * 64 + lane] = acc[t][q];
   }
   __syncthreads();
   if (wave != 0) return;
@@ -284,10 +292,10 @@ __global__ __launch_bounds__(256) void seg_outer_kernel(const OuterArgs args) {
 #pragma unroll
     for (int t = 0; t < 8; ++t)
 #pragma unroll
-      for (int q = 0; q < 4; ++q) acc[t][q] += red[w][t * 4 + q][lane];
+      for (int q = 0; q < 4; ++q) acc[t][q] += red[(w * 32 + t * 4 + q) * 64 + lane];
 
   // partial layout: ws[chunk][c][rpad]; lane holds c = c0 + 8*(4*lq + v) + t, j = j0 + 16*q + li
-  float *dst = args.ws + (int64_t)chunk * args.C * args.rpad;
+  MLORA_GLOBAL float *dst = gp(args.ws) + (int64_t)chunk * args.C * args.rpad;
 #pragma unroll
   for (int t = 0; t < 8; ++t)
 #pragma unroll
@@ -326,13 +334,13 @@ __global__ __launch_bounds__(256) void seg_outer_reduce_kernel(const ReduceArgs 
   for (int s = 0; s < args.seg.n; ++s) {
     if (args.seg.aid[s] != a) continue;
     for (int ch = args.chunk_start[s]; ch < args.chunk_start[s + 1]; ++ch)
-      sum += args.ws[((int64_t)ch * args.C + c) * args.rpad + j];
+      sum += gp(args.ws)[((int64_t)ch * args.C + c) * args.rpad + j];
   }
   const int64_t o = args.out_layout == 0 ? c * r + j : (int64_t)j * args.C + c;
   if (args.out_dtype == MLORA_F32)
-    static_cast<float *>(args.out[a])[o] = sum;
+    gp(static_cast<float *>(args.out[a]))[o] = sum;
   else
-    static_cast<uint16_t *>(args.out[a])[o] = f32_to_bf16_rne(sum);
+    gp(static_cast<uint16_t *>(args.out[a]))[o] = f32_to_bf16_rne(sum);
 }
 
 // Chunking shared by the entry point and the workspace query.
@@ -360,7 +368,7 @@ static void plan_outer(OuterPlan &pl, const SegTable &st, const int32_t *rank, i
   int64_t cr = rows * pl.cblocks * (pl.jblocks > 0 ? pl.jblocks : 1) / target_items;
   cr = cr < 512 ? 512 : cr;
   cr = (cr + 127) / 128 * 128;
-  pl.chunk_rows = (int32_t)(cr > INT32_MAX / 2 ? INT32_MAX / 2 : cr);
+  pl.chunk_rows = (int32_t)(cr > kMaxChunkRows ? kMaxChunkRows : cr);
   int32_t n = 0;
   for (int s = 0; s < st.n; ++s) {
     pl.chunk_start[s] = n;
@@ -390,6 +398,8 @@ extern "C" int mlora_shrink(const void *p, int64_t ldp, int64_t M, int64_t K, co
   if (rmax == 0 || M == 0) return MLORA_OK;
   if ((st = check_bf16_matrix(p, ldp, M, K))) return st;
   if ((st = check_bf16_matrix(h_rows, ldh, M, rmax))) return st;
+  // 31-bit byte offsets inside the buffer resources of one tile / one operand
+  if (ldp * 2 * 128 >= kOOB || K * 2 * (int64_t)kMaxRank >= kOOB) return MLORA_ERR_LIMIT;
   if (h_cols != nullptr) {
     if (ldhc < M) return MLORA_ERR_INVALID;
     if (ldh < rmax) return MLORA_ERR_INVALID;
@@ -469,6 +479,7 @@ extern "C" int mlora_seg_outer(const void *p, int64_t ldp, int64_t M, int64_t C,
   if (pl.n_chunks > 0) {
     if ((st = check_bf16_matrix(p, ldp, M, C))) return st;
     if (qt == nullptr || ldq < M) return MLORA_ERR_INVALID;
+    if (ldp * 2 * kMaxChunkRows >= kOOB || ldq * 4 * (int64_t)kMaxRank >= kOOB) return MLORA_ERR_LIMIT;
     if (workspace == nullptr || workspace_bytes < need) return MLORA_ERR_WORKSPACE;
     if (!aligned16(workspace)) return MLORA_ERR_UNSUPPORTED;
   }
