@@ -124,8 +124,8 @@ def main():
             A_ops = [_as_operand(a) for a in L["As"]]
             B_ops = [_as_operand(v) for v in L["Bs"]]
             x, dy = L["x"].detach(), L["dy"]
-            h_rows, h_cols = kernels.shrink(x, A_ops, 0, scales, routing, True, R)
-            g_rows, g_cols = kernels.shrink(dy, B_ops, 1, scales, routing, True, R)
+            h_rows, h_frag = kernels.shrink(x, A_ops, 0, scales, routing, True, R)
+            g_rows, g_frag = kernels.shrink(dy, B_ops, 1, scales, routing, True, R)
             lora_mr = sum(m * cfg.ranks[a] for m, a in seg if a >= 0)
             r_sum = sum(cfg.ranks)
             runs = {
@@ -137,10 +137,10 @@ def main():
                              2 * lora_mr * K, M * K * 2 + r_sum * K * 2 + lora_mr * (2 + 4)),
                 "shrink_dy": (lambda: kernels.shrink(dy, B_ops, 1, scales, routing, True, R),
                               2 * lora_mr * N, M * N * 2 + r_sum * N * 2 + lora_mr * (2 + 4)),
-                "seg_outer_dB": (lambda: kernels.seg_outer(dy, h_cols, cfg.ranks, routing, 0,
+                "seg_outer_dB": (lambda: kernels.seg_outer(dy, h_frag, R, cfg.ranks, routing, 0,
                                                            [torch.bfloat16] * len(cfg.ranks)),
                                  2 * lora_mr * N, M * N * 2 + lora_mr * 4 + r_sum * N * 2),
-                "seg_outer_dA": (lambda: kernels.seg_outer(x, g_cols, cfg.ranks, routing, 1,
+                "seg_outer_dA": (lambda: kernels.seg_outer(x, g_frag, R, cfg.ranks, routing, 1,
                                                            [torch.bfloat16] * len(cfg.ranks)),
                                  2 * lora_mr * K, M * K * 2 + lora_mr * 4 + r_sum * K * 2),
             }
@@ -150,7 +150,7 @@ def main():
                 fam[k]["flops"] += fl
                 fam[k]["bytes"] += by
                 fam[k]["launches"] += 1
-            del h_rows, h_cols, g_rows, g_cols
+            del h_rows, h_frag, g_rows, g_frag
     kern = {}
     for k, v in fam.items():
         avg = v["time"] / v["launches"]

@@ -31,12 +31,13 @@ SIGNATURES = {
     "mlora_abi_version": (_int, []),
     "mlora_status_string": (ctypes.c_char_p, [_int]),
     "mlora_shrink": (_int, [_vp, _i64, _i64, _i64, _pvp, _int, _pi32, _pf32, _i32,
-                            _pi64, _pi32, _i32, _vp, _i64, _vp, _i64, _vp]),
+                            _pi64, _pi32, _i32, _vp, _i64, _vp, _i32, _vp]),
+    "mlora_frag_bytes": (_i64, [_i64, _i32, _pi64, _pi32, _i32]),
     "mlora_gemm_fwd": (_int, [_vp, _i64, _i64, _i64, _vp, _i64, _i64, _vp, _int, _vp, _i64,
                               _pvp, _pi32, _i32, _pi64, _pi32, _i32, _vp, _i64, _int, _vp]),
     "mlora_gemm_dx": (_int, [_vp, _i64, _i64, _i64, _vp, _i64, _i64, _vp, _i64,
                              _pvp, _pi32, _i32, _pi64, _pi32, _i32, _vp, _i64, _vp]),
-    "mlora_seg_outer": (_int, [_vp, _i64, _i64, _i64, _vp, _i64, _pvp, _int, _int, _pi32, _i32,
+    "mlora_seg_outer": (_int, [_vp, _i64, _i64, _i64, _vp, _i32, _pvp, _int, _int, _pi32, _i32,
                                _pi64, _pi32, _i32, _vp, _i64, _vp]),
     "mlora_seg_outer_workspace_bytes": (_i64, [_i64, _i64, _pi32, _i32, _pi64, _pi32, _i32]),
 }

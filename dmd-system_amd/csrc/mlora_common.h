@@ -19,6 +19,7 @@ namespace mlora {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
@@ -131,10 +132,19 @@ __device__ __forceinline__ void transpose8x8_b16(const u32x4 (&in)[8], u32x4 (&o
   }
 }
 
+// Wave index within the workgroup, as a value the compiler knows is uniform
+// (threadIdx.x >> 6 alone is treated as divergent, which would force
+// waterfall loops around scalar buffer operands and M0 writes).
+__device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane(threadIdx.x >> 6); }
+
 // ---------------------------------------------------------------- LDS layout
 
-// Chunk swizzle for a tile with 8 chunks (128 bytes) per row.
-__device__ __forceinline__ int swz(int row) { return (row ^ (row >> 3)) & 7; }
+// Chunk swizzle for a tile with 8 chunks (128 bytes) per row: chunk c of row r
+// sits at slot c ^ swz(r). Any 16 consecutive rows read at one chunk then cover
+// 16 distinct 16-byte bank groups (slot bits from r%8, parity from r/8), and
+// the swizzle of row r depends only on r mod 16, so every MFMA fragment row
+// (32-aligned base + lane) has a lane-constant swizzle.
+__device__ __forceinline__ int swz(int row) { return (row & 7) ^ ((row >> 3) & 1); }
 __device__ __forceinline__ int lds_chunk_offset(int row, int chunk) { return row * 8 + (chunk ^ swz(row)); }
 
 // ---------------------------------------------------------------- routing

@@ -45,16 +45,22 @@ struct GemmCfg {
   static constexpr int BM = BM_, BN = BN_, WM = WM_, WN = WN_;
   static constexpr bool NN = NN_;
   static constexpr int BK = 64;
-  static constexpr int THREADS = 64 * WM * WN;
+  static constexpr int NW = WM * WN;
+  static constexpr int THREADS = 64 * NW;
   static constexpr int TM = BM / WM / 32;  // 32x32 MFMA tiles per wave along m
   static constexpr int TN = BN / WN / 32;  // ... along n
-  static constexpr int A_CH = BM * 8 / THREADS;  // 16-byte chunks of the P tile per thread
-  static constexpr int B_CH = BN * 8 / THREADS;  // NT: chunks of the Q tile per thread
-  static constexpr int B_BLK = (BN + THREADS - 1) / THREADS;  // NN: 8x8 blocks per thread
-  static constexpr int ROWS_PER_PASS = THREADS / 8;
-  static constexpr int STAGE = (BM + BN) * 8;  // u32x4 per LDS stage
-  static_assert(A_CH * THREADS == BM * 8, "P tile must split evenly over threads");
-  static_assert(NN || B_CH * THREADS == BN * 8, "Q tile must split evenly over threads");
+  static constexpr int A_DMA = BM / 8 / NW;  // 1 KB direct-to-LDS loads per wave for the P tile
+  static constexpr int B_DMA = BN / 8 / NW;  // NT: the same for the Q tile
+  static constexpr int NN_BLK = 2 * BN / THREADS;  // NN: 8x4 blocks (8 k x 4 n) per thread
+  static_assert(A_DMA * NW * 8 == BM, "P tile rows must split into 8-row loads over the waves");
+  static_assert(NN || B_DMA * NW * 8 == BN, "Q tile rows must split into 8-row loads over the waves");
+  static_assert(!NN || NN_BLK == 1, "NN tile must split into one 8x4 block per thread");
+  static_assert(A_DMA % 2 == 0 && (NN || B_DMA % 2 == 0), "even 8-row load counts per wave");
+  // LDS (bytes): P stage 0 | P stage 1 | Q stage 0 | Q stage 1
+  static constexpr int A_BYTES = BM * 128, B_BYTES = BN * 128;
+  static constexpr int B_BASE = 2 * A_BYTES;
+  static constexpr int LDS_BYTES = 2 * (A_BYTES + B_BYTES);
+  static_assert(A_BYTES < 65536 && B_BYTES < 65536, "stage offsets must fit the ds_read offset field");
   static constexpr int GROUP_M = 8;
 };
 
@@ -68,147 +74,244 @@ struct KSource {
   int32_t klim;
 };
 
+// Per-thread state of one contraction source. Global tiles go to LDS with the
+// gfx950 direct-to-LDS buffer load: one wave instruction fills 1 KB (8 rows of
+// 8 chunks); lane L lands at chunk slot L of that KB, so it fetches the
+// logical chunk (L%8) ^ swz(row) that the XOR-swizzled layout keeps there.
+// With swz depending on row%16 only, the 1 KB loads of one wave differ by a
+// whole number of rows plus one of two lane patterns (even / odd 8-row block),
+// so the per-load row step and the tile's k offset travel in soffset.
 template <class C>
 struct Pipe {
   __amdgpu_buffer_rsrc_t rp, rq;
-  int32_t p_off[C::A_CH];  // byte offset of each P chunk at k = 0, or kOOB
-  int32_t q_off[C::NN ? 1 : C::B_CH];
-  int32_t kchunk;          // 8 * (tid & 7): contraction index of this thread's chunks
-  int32_t ldq_b;
-  int32_t nn_col_ok;
-  int32_t klim;
-  u32x4 a_regs[C::A_CH];
-  u32x4 b_regs[C::NN ? 8 * C::B_BLK : C::B_CH];
+  int32_t a_off[2];     // even / odd 8-row block: this lane's P chunk offset at k = 0 (rows past the tile: kOOB)
+  int32_t a_kc[2];      // contraction index of that chunk
+  int32_t a_row0;       // first P row (tile-local) of this wave's loads
+  int32_t b_off[2], b_kc[2];
+  int32_t b_row0;
+  int32_t klim, ldp_b, ldq_b, p_rows;
+  uint2 nn_regs[C::NN ? 8 * C::NN_BLK : 1];
 
   __device__ __forceinline__ void init(const KSource &s, int m0, int n0, int Ncols, int tid) {
+    const int lane = tid & 63, wave = wave_id();
     klim = s.klim;
-    kchunk = 8 * (tid & 7);
     const int base_row = max(s.row_lo, m0);
-    const int64_t ldp_b = s.ldp * 2;
-    rp = make_rsrc(s.P + (int64_t)base_row * s.ldp, (int64_t)(s.row_hi - base_row) * ldp_b);
-#pragma unroll
-    for (int i = 0; i < C::A_CH; ++i) {
-      const int grow = m0 + (tid >> 3) + i * C::ROWS_PER_PASS;
-      p_off[i] = (grow >= base_row && grow < s.row_hi) ? (int32_t)((grow - base_row) * ldp_b + kchunk * 2) : kOOB;
-    }
+    ldp_b = (int32_t)(s.ldp * 2);
     ldq_b = (int32_t)(s.ldq * 2);
+    // P rows of the tile are read relative to m0; rows outside [row_lo, row_hi) read zero
+    rp = make_rsrc(s.P + (int64_t)m0 * s.ldp, (int64_t)(s.row_hi - m0) * ldp_b);
+    p_rows = base_row - m0;  // tile rows below this index belong to another segment
+    a_row0 = 8 * wave * C::A_DMA;
+#pragma unroll
+    for (int par = 0; par < 2; ++par) {
+      const int c = (lane & 7) ^ (lane >> 3) ^ par;
+      a_kc[par] = 8 * c;
+      a_off[par] = (lane >> 3) * ldp_b + 16 * c;
+    }
     if constexpr (!C::NN) {
       rq = make_rsrc(s.Q + (int64_t)n0 * s.ldq, (int64_t)(Ncols - n0) * s.ldq * 2);
+      b_row0 = 8 * wave * C::B_DMA;
 #pragma unroll
-      for (int i = 0; i < C::B_CH; ++i) q_off[i] = ((tid >> 3) + i * C::ROWS_PER_PASS) * ldq_b + kchunk * 2;
+      for (int par = 0; par < 2; ++par) {
+        const int c = (lane & 7) ^ (lane >> 3) ^ par;
+        b_kc[par] = 8 * c;
+        b_off[par] = (lane >> 3) * ldq_b + 16 * c;  // rows past Ncols fall outside rq
+      }
     } else {
       rq = make_rsrc(s.Q + n0, (int64_t)s.klim * s.ldq * 2);
-      const int bc = tid % (C::BN / 8);
-      nn_col_ok = (n0 + 8 * bc < Ncols) ? 1 : 0;
+      const int kb = tid / (C::BN / 4), nb = tid % (C::BN / 4);
+      b_kc[0] = 8 * kb;
+      b_off[0] = (n0 + 4 * nb < Ncols) ? 8 * kb * ldq_b + 8 * nb : kOOB;
     }
   }
 
-  __device__ __forceinline__ void load(int k0, int tid) {
-    const bool kok = k0 + kchunk < klim;
+  // Issue the loads of the k-tile starting at k0 (P and NT Q straight into LDS stage `st`).
+  __device__ __forceinline__ void issue(MLORA_LDS char *lds, int st, int k0, int wave, int lane, bool KMASK) {
 #pragma unroll
-    for (int i = 0; i < C::A_CH; ++i) a_regs[i] = buf_load16(rp, kok ? p_off[i] + k0 * 2 : kOOB);
+    for (int q = 0; q < C::A_DMA; ++q) {
+      MLORA_LDS void *dst = lds + st * C::A_BYTES + (wave * C::A_DMA + q) * 1024;
+      const int row = a_row0 + 8 * q;  // wave-uniform
+      const int par = q & 1;
+      int32_t off = a_off[par];
+      if (p_rows > 0 && row + (lane >> 3) < p_rows) off = kOOB;  // rows of an earlier segment
+      if (KMASK && k0 + a_kc[par] >= klim) off = kOOB;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rp, dst, 16, off, row * ldp_b + k0 * 2, 0, 0);
+    }
     if constexpr (!C::NN) {
 #pragma unroll
-      for (int i = 0; i < C::B_CH; ++i) b_regs[i] = buf_load16(rq, kok ? q_off[i] + k0 * 2 : kOOB);
+      for (int q = 0; q < C::B_DMA; ++q) {
+        MLORA_LDS void *dst = lds + C::B_BASE + st * C::B_BYTES + (wave * C::B_DMA + q) * 1024;
+        const int row = b_row0 + 8 * q;
+        const int par = q & 1;
+        const int32_t off = (KMASK && k0 + b_kc[par] >= klim) ? kOOB : b_off[par];
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rq, dst, 16, off, row * ldq_b + k0 * 2, 0, 0);
+      }
     } else {
 #pragma unroll
-      for (int i = 0; i < C::B_BLK; ++i) {
-        const int b = tid + i * C::THREADS;
-        const int a = b / (C::BN / 8), bc = b % (C::BN / 8);
-        const bool ok = b < C::BN && nn_col_ok;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const int kr = k0 + a * 8 + e;
-          b_regs[i * 8 + e] = buf_load16(rq, (ok && kr < klim) ? kr * ldq_b + bc * 16 : kOOB);
-        }
+      for (int e = 0; e < 8; ++e) {
+        const int32_t off = (KMASK && k0 + b_kc[0] + e >= klim) ? kOOB : b_off[0];
+        nn_regs[e] = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(rq, off, (k0 + e) * ldq_b, 0));
       }
     }
   }
 
-  __device__ __forceinline__ void store(lds_u4 *ldsA, lds_u4 *ldsB, int tid) const {
-    const int c = tid & 7;
+  // NN only: transpose the staged 8x4 block and write it to LDS stage `st`.
+  __device__ __forceinline__ void store_nn(MLORA_LDS char *lds, int st, int tid) const {
+    if constexpr (C::NN) {
+      lds_u4 *dstB = (lds_u4 *)(lds + C::B_BASE + st * C::B_BYTES);
+      const int kb = tid / (C::BN / 4), nb = tid % (C::BN / 4);
 #pragma unroll
-    for (int i = 0; i < C::A_CH; ++i) {
-      const int r = (tid >> 3) + i * C::ROWS_PER_PASS;
-      ldsA[lds_chunk_offset(r, c)] = a_regs[i];
-    }
-    if constexpr (!C::NN) {
+      for (int t = 0; t < 4; ++t) {
+        uint32_t o[4];
+        const int word = t >> 1;
 #pragma unroll
-      for (int i = 0; i < C::B_CH; ++i) {
-        const int r = (tid >> 3) + i * C::ROWS_PER_PASS;
-        ldsB[lds_chunk_offset(r, c)] = b_regs[i];
-      }
-    } else {
-#pragma unroll
-      for (int i = 0; i < C::B_BLK; ++i) {
-        const int b = tid + i * C::THREADS;
-        if (b < C::BN) {
-          const int a = b / (C::BN / 8), bc = b % (C::BN / 8);
-          u32x4 blk[8], tr[8];
-#pragma unroll
-          for (int e = 0; e < 8; ++e) blk[e] = b_regs[i * 8 + e];
-          transpose8x8_b16(blk, tr);
-#pragma unroll
-          for (int t = 0; t < 8; ++t) ldsB[lds_chunk_offset(bc * 8 + t, a)] = tr[t];
+        for (int q = 0; q < 4; ++q) {
+          const uint2 ra = nn_regs[2 * q], rb = nn_regs[2 * q + 1];
+          const uint32_t a = word ? ra.y : ra.x, bw = word ? rb.y : rb.x;
+          o[q] = (t & 1) ? ((a >> 16) | (bw & 0xffff0000u)) : ((a & 0xffffu) | (bw << 16));
         }
+        dstB[lds_chunk_offset(4 * nb + t, kb)] = u32x4{o[0], o[1], o[2], o[3]};
       }
     }
   }
 };
 
+// Byte addresses (stage 0, first 32-row tile) of this lane's fragments per
+// substep; further tiles are +4096 bytes and stage 1 is +A_BYTES / +B_BYTES,
+// all folded into the ds_read offset field.
 template <class C>
-__device__ __forceinline__ void mma_stage(f32x16 (&acc)[C::TM][C::TN], const lds_u4 *ldsA, const lds_u4 *ldsB,
-                                          int wm0, int wn0, int lane) {
+struct FragAddr {
+  int32_t a[4], b[4];
+  __device__ __forceinline__ void init(int wm0, int wn0, int lane) {
+    const int z = swz(lane & 31);  // lane-constant: fragment rows are 32-aligned + lane
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      const int slot = (2 * s + (lane >> 5)) ^ z;
+      a[s] = (wm0 + (lane & 31)) * 128 + 16 * slot;
+      b[s] = C::B_BASE + (wn0 + (lane & 31)) * 128 + 16 * slot;
+    }
+  }
+};
+
+template <class C, int ST>
+__device__ __forceinline__ void read_frags(bf16x8 (&af)[C::TM], bf16x8 (&bf)[C::TN], const MLORA_LDS char *lds,
+                                           const FragAddr<C> &fa, int s) {
+#pragma unroll
+  for (int i = 0; i < C::TM; ++i)
+    af[i] = as_bf16x8(*(const lds_u4 *)(lds + fa.a[s] + (4096 * i + ST * C::A_BYTES)));
+#pragma unroll
+  for (int j = 0; j < C::TN; ++j)
+    bf[j] = as_bf16x8(*(const lds_u4 *)(lds + fa.b[s] + (4096 * j + ST * C::B_BYTES)));
+}
+
+// One 64-deep k-tile from LDS stage ST: 4 substeps of 16. The fragments of
+// substep s+1 are read while the TM*TN MFMAs of substep s run.
+template <class C, int ST>
+__device__ __forceinline__ void mma_stage(f32x16 (&acc)[C::TM][C::TN], const MLORA_LDS char *lds,
+                                          const FragAddr<C> &fa) {
+  bf16x8 af[2][C::TM], bf[2][C::TN];
+  read_frags<C, ST>(af[0], bf[0], lds, fa, 0);
 #pragma unroll
   for (int s = 0; s < 4; ++s) {
-    const int c = 2 * s + (lane >> 5);
-    bf16x8 af[C::TM], bf[C::TN];
-#pragma unroll
-    for (int i = 0; i < C::TM; ++i) af[i] = as_bf16x8(ldsA[lds_chunk_offset(wm0 + 32 * i + (lane & 31), c)]);
-#pragma unroll
-    for (int j = 0; j < C::TN; ++j) bf[j] = as_bf16x8(ldsB[lds_chunk_offset(wn0 + 32 * j + (lane & 31), c)]);
+    const int cur = s & 1;
+    if (s < 3) read_frags<C, ST>(af[cur ^ 1], bf[cur ^ 1], lds, fa, s + 1);
 #pragma unroll
     for (int i = 0; i < C::TM; ++i)
 #pragma unroll
       for (int j = 0; j < C::TN; ++j)
         // MFMA rows <- Q (n), columns <- P (m): each lane ends up with 4
         // consecutive n of one row m, stored as one 8-byte write.
-        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bf[j], af[i], acc[i][j], 0, 0, 0);
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bf[cur][j], af[cur][i], acc[i][j], 0, 0, 0);
+    if (s < 3) {
+#pragma unroll
+      for (int g = 0; g < C::TM + C::TN; ++g) {
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // one DS read
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+      }
+    }
   }
 }
 
-// Contraction over one source, pipelined through the two LDS stages.
-template <class C>
-__device__ __forceinline__ void run_source(f32x16 (&acc)[C::TM][C::TN], const KSource &src, lds_u4 *lds, int m0,
-                                           int n0, int Ncols, int wm0, int wn0, int tid, int lane) {
-  const int nk = (src.klim + C::BK - 1) / C::BK;
-  if (nk <= 0) return;
-  Pipe<C> pipe;
-  pipe.init(src, m0, n0, Ncols, tid);
-  pipe.load(0, tid);
-  __syncthreads();  // LDS may still be read by a previous source's last stage
-  pipe.store(lds, lds + C::BM * 8, tid);
+// Wait for this wave's direct-to-LDS loads, then publish the stage to all waves.
+__device__ __forceinline__ void stage_barrier() {
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
   __syncthreads();
-  for (int kt = 0; kt < nk; ++kt) {
-    // the load past the last tile reads zeros (offsets out of range) and is never used
-    pipe.load((kt + 1) * C::BK, tid);
-    // keep the loads issued ahead of the MFMAs (the scheduler would sink them
-    // next to their LDS stores and expose the full memory latency)
-    __builtin_amdgcn_sched_barrier(0);
-    lds_u4 *cur = lds + (kt & 1) * C::STAGE;
-    lds_u4 *nxt = lds + ((kt + 1) & 1) * C::STAGE;
-    mma_stage<C>(acc, cur, cur + C::BM * 8, wm0, wn0, lane);
-    __builtin_amdgcn_sched_barrier(0);
-    pipe.store(nxt, nxt + C::BM * 8, tid);
-    __syncthreads();
+}
+
+// Finds the next LoRA source of this tile: the next segment from `seg` on that
+// overlaps rows [m0, row_end) and has an adapter. Wave-uniform scalar code.
+__device__ __forceinline__ bool next_lora_source(const GemmArgs &args, bool nn, int m0, int row_end, int &seg,
+                                                 KSource &src) {
+  while (seg < args.seg.n && args.seg.off[seg] < row_end) {
+    const int a = args.seg.aid[seg];
+    const int lo = max(args.seg.off[seg], m0), hi = min(args.seg.off[seg + 1], row_end);
+    ++seg;
+    if (a >= 0 && args.ext.rank[a] > 0 && lo < hi) {
+      const int r = args.ext.rank[a];
+      src = KSource{args.E, args.ext.ptr[a], args.lde, nn ? (int64_t)args.Ncols : (int64_t)r, lo, hi, r};
+      return true;
+    }
+  }
+  return false;
+}
+
+// All contraction of one tile in a single pipelined loop over "virtual"
+// k-tiles: first the main X·Wᵀ (or dY·W) tiles, then ceil(r/64) tiles per LoRA
+// segment overlapping the tile. At a source boundary the loader is re-pointed
+// (a few scalars and two offsets); the LDS stages and the MFMA code are shared,
+// so the accumulators stay in place. Tiles past a source's contraction length
+// mask their chunks.
+template <class C>
+__device__ __forceinline__ void contract_tile(f32x16 (&acc)[C::TM][C::TN], const GemmArgs &args, MLORA_LDS char *lds,
+                                              const FragAddr<C> &fa, int m0, int n0, int tid) {
+  const int wave = wave_id(), lane = tid & 63;
+  const int row_end = min(m0 + C::BM, args.M);
+  int seg = args.E != nullptr ? seg_of_row(args.seg, m0) : args.seg.n;
+  Pipe<C> pipe;
+  KSource src{args.P, args.Q, args.ldp, args.ldq, 0, args.M, args.Kc};
+  int ntile = (src.klim + C::BK - 1) / C::BK;
+  if (ntile == 0) {
+    if (!next_lora_source(args, C::NN, m0, row_end, seg, src)) return;
+    ntile = (src.klim + C::BK - 1) / C::BK;
+  }
+  bool kmask = src.klim % C::BK != 0;
+  pipe.init(src, m0, n0, args.Ncols, tid);
+  int t_in_src = 0;  // index of the tile being loaded within its source
+  pipe.issue(lds, 0, 0, wave, lane, kmask);
+  pipe.store_nn(lds, 0, tid);
+  stage_barrier();
+  // `more`: whether a tile after the current one exists (and was loaded)
+  auto advance = [&]() -> bool {
+    if (++t_in_src < ntile) return true;
+    if (!next_lora_source(args, C::NN, m0, row_end, seg, src)) return false;
+    ntile = (src.klim + C::BK - 1) / C::BK;
+    kmask = src.klim % C::BK != 0;
+    pipe.init(src, m0, n0, args.Ncols, tid);
+    t_in_src = 0;
+    return true;
+  };
+  while (true) {
+    // stage 0 holds the current tile; the next one (if any) goes to stage 1
+    bool more = advance();
+    if (more) pipe.issue(lds, 1, t_in_src * C::BK, wave, lane, kmask);
+    mma_stage<C, 0>(acc, lds, fa);
+    if (more) pipe.store_nn(lds, 1, tid);
+    stage_barrier();
+    if (!more) break;
+    more = advance();
+    if (more) pipe.issue(lds, 0, t_in_src * C::BK, wave, lane, kmask);
+    mma_stage<C, 1>(acc, lds, fa);
+    if (more) pipe.store_nn(lds, 0, tid);
+    stage_barrier();
+    if (!more) break;
   }
 }
 
 template <class C>
 __global__ __launch_bounds__(C::THREADS) void gemm_kernel(const GemmArgs args) {
-  __shared__ u32x4 smem[2 * C::STAGE];
-  lds_u4 *lds = (lds_u4 *)smem;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  __shared__ u32x4 smem[C::LDS_BYTES / 16];
+  MLORA_LDS char *lds = (MLORA_LDS char *)smem;
+  const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
   const int wm0 = (wave / C::WN) * (C::BM / C::WM);
   const int wn0 = (wave % C::WN) * (C::BN / C::WN);
 
@@ -224,61 +327,56 @@ __global__ __launch_bounds__(C::THREADS) void gemm_kernel(const GemmArgs args) {
   const int tn = (id % per_group) / gsize;
   const int m0 = tm * C::BM, n0 = tn * C::BN;
 
+  // accumulators start at the bias of their column (lane holds n = n0 + wn0 +
+  // 32j + 8g + 4(lane/32) + e for register 4g + e of tile (i, j))
   f32x16 acc[C::TM][C::TN];
 #pragma unroll
-  for (int i = 0; i < C::TM; ++i)
+  for (int j = 0; j < C::TN; ++j) {
+    f32x16 b0;
 #pragma unroll
-    for (int j = 0; j < C::TN; ++j)
+    for (int g = 0; g < 4; ++g) {
+      const int n = n0 + wn0 + 32 * j + 8 * g + 4 * (lane >> 5);
+      float v[4] = {0.f, 0.f, 0.f, 0.f};
+      if (n < args.Ncols) {
+        if (args.bias_dtype == MLORA_F32) {
+          const f32x4 b = *(const MLORA_GLOBAL f32x4 *)(static_cast<const float *>(args.bias) + n);
+          v[0] = b[0]; v[1] = b[1]; v[2] = b[2]; v[3] = b[3];
+        } else if (args.bias_dtype == MLORA_BF16) {
+          const u32x2 b = *(const MLORA_GLOBAL u32x2 *)(static_cast<const uint16_t *>(args.bias) + n);
+          v[0] = bf16_to_f32(b.x & 0xffff); v[1] = bf16_to_f32(b.x >> 16);
+          v[2] = bf16_to_f32(b.y & 0xffff); v[3] = bf16_to_f32(b.y >> 16);
+        }
+      }
 #pragma unroll
-      for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
-
-  // main contraction
-  {
-    KSource src{args.P, args.Q, args.ldp, args.ldq, 0, args.M, args.Kc};
-    run_source<C>(acc, src, lds, m0, n0, args.Ncols, wm0, wn0, tid, lane);
-  }
-  // LoRA term: one pass per overlapping segment that has an adapter
-  if (args.E != nullptr) {
-    const int row_end = min(m0 + C::BM, args.M);
-    for (int s = seg_of_row(args.seg, m0); s < args.seg.n && args.seg.off[s] < row_end; ++s) {
-      const int a = args.seg.aid[s];
-      if (a < 0) continue;
-      const int r = args.ext.rank[a];
-      const int lo = max(args.seg.off[s], m0), hi = min(args.seg.off[s + 1], row_end);
-      if (r == 0 || lo >= hi) continue;
-      KSource src{args.E, args.ext.ptr[a], args.lde, C::NN ? (int64_t)args.Ncols : (int64_t)r, lo, hi, r};
-      run_source<C>(acc, src, lds, m0, n0, args.Ncols, wm0, wn0, tid, lane);
+      for (int e = 0; e < 4; ++e) b0[4 * g + e] = v[e];
     }
+#pragma unroll
+    for (int i = 0; i < C::TM; ++i) acc[i][j] = b0;
   }
+  FragAddr<C> fa;
+  fa.init(wm0, wn0, lane);
 
-  // epilogue: + bias, (+ Y), round to bf16, 8-byte stores of 4 consecutive n
+  contract_tile<C>(acc, args, lds, fa, m0, n0, tid);
+
+  // epilogue: (+ Y), round to bf16, 8-byte stores of 4 consecutive n
   const int rows_here = min(C::BM, args.M - m0);
   const int64_t ldy_b = args.ldy * 2;
   const __amdgpu_buffer_rsrc_t ry = make_rsrc(args.Y + (int64_t)m0 * args.ldy, rows_here * ldy_b);
 #pragma unroll
   for (int i = 0; i < C::TM; ++i) {
     const int ml = wm0 + 32 * i + (lane & 31);
-    if (ml >= rows_here) continue;
 #pragma unroll
     for (int j = 0; j < C::TN; ++j) {
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
         const int n = n0 + wn0 + 32 * j + 8 * g + 4 * (lane >> 5);
-        if (n >= args.Ncols) continue;
         float v[4];
 #pragma unroll
         for (int e = 0; e < 4; ++e) v[e] = acc[i][j][4 * g + e];
-        if (args.bias_dtype == MLORA_F32) {
-          const float4 b = *reinterpret_cast<const float4 *>(static_cast<const float *>(args.bias) + n);
-          v[0] += b.x; v[1] += b.y; v[2] += b.z; v[3] += b.w;
-        } else if (args.bias_dtype == MLORA_BF16) {
-          const uint2 b = *reinterpret_cast<const uint2 *>(static_cast<const uint16_t *>(args.bias) + n);
-          v[0] += bf16_to_f32(b.x & 0xffff); v[1] += bf16_to_f32(b.x >> 16);
-          v[2] += bf16_to_f32(b.y & 0xffff); v[3] += bf16_to_f32(b.y >> 16);
-        }
-        const int32_t off = (int32_t)(ml * ldy_b + n * 2);
-        if (args.accumulate) {
-          const uint2 o = *reinterpret_cast<const uint2 *>(args.Y + (int64_t)(m0 + ml) * args.ldy + n);
+        // rows past M / columns past Ncols fall outside ry or are dropped
+        const int32_t off = (ml < rows_here && n < args.Ncols) ? (int32_t)(ml * ldy_b + n * 2) : kOOB;
+        if (args.accumulate && off != kOOB) {
+          const u32x2 o = *(const MLORA_GLOBAL u32x2 *)(args.Y + (int64_t)(m0 + ml) * args.ldy + n);
           v[0] += bf16_to_f32(o.x & 0xffff); v[1] += bf16_to_f32(o.x >> 16);
           v[2] += bf16_to_f32(o.y & 0xffff); v[3] += bf16_to_f32(o.y >> 16);
         }
@@ -288,8 +386,8 @@ __global__ __launch_bounds__(C::THREADS) void gemm_kernel(const GemmArgs args) {
   }
 }
 
-using CfgNT256 = GemmCfg<256, 256, 2, 2, false>;
-using CfgNN256 = GemmCfg<256, 256, 2, 2, true>;
+using CfgNT256 = GemmCfg<256, 256, 4, 2, false>;
+using CfgNN256 = GemmCfg<256, 256, 4, 2, true>;
 using CfgNT128 = GemmCfg<128, 128, 2, 2, false>;
 using CfgNN128 = GemmCfg<128, 128, 2, 2, true>;
 
@@ -304,7 +402,8 @@ static int launch_gemm(GemmArgs &a, hipStream_t stream) {
   return launch_status();
 }
 
-// Tile choice: 256x256 when that still gives every CU at least one tile, else 128x128.
+// Tile choice (measured on MI355X at the Wan shapes): the 8-wave 256x256 tile
+// whenever it still gives every CU a tile; the 4-wave 128x128 tile otherwise.
 template <class Big, class Small>
 static int dispatch_gemm(GemmArgs &a, hipStream_t stream) {
   const int64_t big_tiles = (int64_t)((a.M + 255) / 256) * ((a.Ncols + 255) / 256);

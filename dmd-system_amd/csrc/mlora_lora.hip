@@ -2,48 +2,75 @@
 // reductions.
 //
 // shrink     h[m, j]   = s_a · Σ_k P[m,k]·Op_a(j,k)           (X·Aᵀ forward, s·dY·B backward)
-// seg_outer  D_a[c, j] = Σ_{m ∈ rows of a} P[m,c]·Qt[j,m]      (dB_a = s·dYᵀ·h, dA_a = gᵀ·X)
+// seg_outer  D_a[c, j] = Σ_{m ∈ rows of a} P[m,c]·h[m,j]       (dB_a = s·dYᵀ·h, dA_a = gᵀ·X)
 //
 // Both stream the big operand P (X or dY) exactly once at full width and keep
 // the adapter operands, which are small, in LDS or L2. Work is organised per
 // segment, so a workgroup never mixes adapters. Reference semantics:
 // training/low_rank.py:26-28 and its autograd backward.
+//
+// The shrink writes h twice: bf16 rows [M, ldh] for the fused GEMM epilogues,
+// and "fragments" for seg_outer: h split into bf16 hi + lo (hi + lo carries
+// ~16 significant bits) and stored in the exact per-lane order of the B
+// operand of v_mfma_f32_16x16x32_bf16. Fragment blocks cover 32 rows counted
+// from each segment's first row (segment s starts at padded row
+// pad_start[s] = Σ_{s'<s} roundup(len_s', 32)), so every block belongs to one
+// segment; rows past a segment's end inside its last block hold zeros.
+//   fragment (block B, j-tile t, part p in {hi, lo}), lane L, element e:
+//     h[row = 32·B' + 8·(L/16) + e][j = 16·t + L%16]   (B' = block within segment)
+//   stored at u32x4 index ((B·jtiles + t)·2 + p)·64 + L.
 #include "mlora_common.h"
 #include "mlora_host.h"
 
 namespace mlora {
 
+// Padded-row start of every segment (shared by shrink and seg_outer).
+struct PadTable {
+  int32_t start[kMaxSeg + 1];
+};
+
+static int64_t build_pad(PadTable &pt, const SegTable &st) {
+  int64_t p = 0;
+  for (int s = 0; s < st.n; ++s) {
+    pt.start[s] = (int32_t)p;
+    p += (int64_t)(st.off[s + 1] - st.off[s] + 31) / 32 * 32;
+  }
+  pt.start[st.n] = (int32_t)p;
+  return p;
+}
+
 // ============================================================== shrink
 //
-// Workgroup: 4 waves x WT row-tiles of 32 rows of one segment, all r <= 32*RT
-// columns of its adapter. P fragments go straight from HBM to registers
-// (each lane streams 64 contiguous bytes of one row per 64-wide k-chunk; the
-// k order inside a chunk is permuted identically for both operands). The
-// adapter operand chunk [32*RT x 64] is shared through double-buffered LDS.
-// v_mfma_f32_32x32x16_bf16: rows <- P (m), columns <- Op (j), so each lane
-// holds 4 consecutive m of one j: the transposed fp32 copy is written as
-// 4 consecutive floats.
+// Workgroup: 4 waves x 32 rows of one segment, all r <= 32*RT columns of its
+// adapter. P fragments go straight from HBM to registers (each lane streams
+// 64 contiguous bytes of one row per 64-wide k-chunk; the k order inside a
+// chunk is permuted identically for both operands). The adapter operand chunk
+// [32*RT x 64] is shared through double-buffered LDS.
+// v_mfma_f32_32x32x16_bf16: rows <- P (m), columns <- Op (j).
 
 struct ShrinkArgs {
   const uint16_t *P;
   uint16_t *Hr;  // bf16 [M, ldh]
-  float *Hc;     // fp32 [ldh, ldhc] or null
-  int64_t ldp, ldh, ldhc;
+  u32x4 *Hf;     // fragments (see above) or null
+  int64_t ldp, ldh;
   int32_t M, K;
   int32_t op_layout;  // 0: [r, K]; 1: [K, r]
-  int32_t tile_rows;
+  int32_t jtiles;     // fragment j-tiles per block
   int32_t tile_start[kMaxSeg + 1];
+  PadTable pad;
   AdapterTable op;
   SegTable seg;
 };
 
-template <int WT, int RT, int OPL>
+template <int RT, int OPL>
 __global__ __launch_bounds__(256) void shrink_kernel(const ShrinkArgs args) {
-  constexpr int BMS = 4 * WT * 32;
+  constexpr int BMS = 128;
   constexpr int OPROWS = 32 * RT;
   __shared__ u32x4 smem[2 * OPROWS * 8];
+  __shared__ float ebuf_smem[4 * 32 * 33];  // epilogue: per wave 32 rows x 32 j (+1 pad)
   lds_u4 *lds = (lds_u4 *)smem;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  MLORA_LDS float *ebuf = (MLORA_LDS float *)ebuf_smem;
+  const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
 
   // workgroup -> (segment, tile)
   const int bid = blockIdx.x;
@@ -52,7 +79,8 @@ __global__ __launch_bounds__(256) void shrink_kernel(const ShrinkArgs args) {
   const int a = args.seg.aid[s];
   const int r = args.op.rank[a];
   const float scale = args.op.scale[a];
-  const int m0 = args.seg.off[s] + (bid - args.tile_start[s]) * BMS;
+  const int rel0 = (bid - args.tile_start[s]) * BMS;  // tile start relative to the segment
+  const int m0 = args.seg.off[s] + rel0;
   const int mend = args.seg.off[s + 1];
   const int K = args.K;
   const int nk = (K + 63) / 64;
@@ -60,9 +88,7 @@ __global__ __launch_bounds__(256) void shrink_kernel(const ShrinkArgs args) {
   const __amdgpu_buffer_rsrc_t rop = make_rsrc(args.op.ptr[a], (int64_t)r * K * 2);
   // rows past the segment end fall outside this resource and read as zero
   const __amdgpu_buffer_rsrc_t rp = make_rsrc(args.P + (int64_t)m0 * args.ldp, (int64_t)(mend - m0) * ldp_b);
-  int32_t prow[WT];
-#pragma unroll
-  for (int i = 0; i < WT; ++i) prow[i] = (int32_t)((32 * (wave * WT + i) + (lane & 31)) * ldp_b);
+  const int32_t prow = (int32_t)((32 * wave + (lane & 31)) * ldp_b);
 
   // ---- operand loaders
   constexpr int OP_CH = (OPROWS * 8 + 255) / 256;  // layout 0: chunks per thread
@@ -106,25 +132,20 @@ __global__ __launch_bounds__(256) void shrink_kernel(const ShrinkArgs args) {
       }
     }
   };
-  u32x4 pc[WT][4], pn[WT][4];
-  auto load_p = [&](u32x4 (&dst)[WT][4], int kc) {
+  u32x4 pc[4], pn[4];
+  auto load_p = [&](u32x4 (&dst)[4], int kc) {
 #pragma unroll
-    for (int i = 0; i < WT; ++i) {
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int kk = kc * 64 + 32 * (lane >> 5) + 8 * q;
-        dst[i][q] = buf_load16(rp, kk < K ? prow[i] + kk * 2 : kOOB);
-      }
+    for (int q = 0; q < 4; ++q) {
+      const int kk = kc * 64 + 32 * (lane >> 5) + 8 * q;
+      dst[q] = buf_load16(rp, kk < K ? prow + kk * 2 : kOOB);
     }
   };
 
-  f32x16 acc[WT][RT];
+  f32x16 acc[RT];
 #pragma unroll
-  for (int i = 0; i < WT; ++i)
+  for (int j = 0; j < RT; ++j)
 #pragma unroll
-    for (int j = 0; j < RT; ++j)
-#pragma unroll
-      for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
+    for (int v = 0; v < 16; ++v) acc[j][v] = 0.f;
 
   load_op(0);
   load_p(pc, 0);
@@ -143,84 +164,113 @@ __global__ __launch_bounds__(256) void shrink_kernel(const ShrinkArgs args) {
 #pragma unroll
       for (int j = 0; j < RT; ++j) of[j] = as_bf16x8(cur[lds_chunk_offset(32 * j + (lane & 31), c)]);
 #pragma unroll
-      for (int i = 0; i < WT; ++i)
-#pragma unroll
-        for (int j = 0; j < RT; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(pc[i][q]), of[j], acc[i][j], 0, 0, 0);
+      for (int j = 0; j < RT; ++j)
+        acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(pc[q]), of[j], acc[j], 0, 0, 0);
     }
     __builtin_amdgcn_sched_barrier(0);
     store_op(lds + ((kc + 1) & 1) * OPROWS * 8);
     __syncthreads();
 #pragma unroll
-    for (int i = 0; i < WT; ++i)
-#pragma unroll
-      for (int q = 0; q < 4; ++q) pc[i][q] = pn[i][q];
+    for (int q = 0; q < 4; ++q) pc[q] = pn[q];
   }
 
-  // ---- epilogue: scale, bf16 row-major copy and fp32 transposed copy
+  // ---- epilogue 1: scaled bf16 rows (lane holds j = l%32, m = 8(v/4) + 4(l/32) + v%4)
   MLORA_GLOBAL uint16_t *hr = gp(args.Hr);
-  MLORA_GLOBAL float *hc = args.Hc ? gp(args.Hc) : nullptr;
+  const int wrow = m0 + 32 * wave;  // first row of this wave
 #pragma unroll
-  for (int i = 0; i < WT; ++i) {
+  for (int j = 0; j < RT; ++j) {
+    const int col = 32 * j + (lane & 31);
+    if (col >= r) continue;
 #pragma unroll
-    for (int j = 0; j < RT; ++j) {
-      const int col = 32 * j + (lane & 31);
-      if (col >= r) continue;
+    for (int v = 0; v < 16; ++v) {
+      const int row = wrow + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
+      if (row < mend) hr[(int64_t)row * args.ldh + col] = f32_to_bf16_rne(acc[j][v] * scale);
+    }
+  }
+  // ---- epilogue 2: hi/lo fragments, re-laid out through LDS one 32-wide j tile at a time
+  if (args.Hf == nullptr) return;  // uniform over the workgroup
+  const bool wave_rows = wrow < mend;  // a wave past the segment end owns no block
+  const int64_t block = (args.pad.start[s] + rel0 + 32 * wave) / 32;
+  MLORA_LDS float *wb = ebuf + wave * 32 * 33;
+  MLORA_GLOBAL u32x4 *hf = gp(args.Hf);
 #pragma unroll
-      for (int v = 0; v < 16; ++v) {
-        const int row = m0 + 32 * (wave * WT + i) + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
-        if (row >= mend) continue;
-        const float h = acc[i][j][v] * scale;
-        hr[(int64_t)row * args.ldh + col] = f32_to_bf16_rne(h);
-        if (hc) hc[(int64_t)col * args.ldhc + row] = h;
+  for (int j = 0; j < RT; ++j) {
+    if (32 * j >= r) break;  // uniform
+#pragma unroll
+    for (int v = 0; v < 16; ++v) {
+      const int ml = 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
+      wb[ml * 33 + (lane & 31)] = acc[j][v] * scale;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int sub = 0; sub < 2; ++sub) {
+      const int t = 2 * j + sub;
+      if (16 * t < r && wave_rows) {
+        float v8[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v8[e] = wb[(8 * (lane >> 4) + e) * 33 + 16 * sub + (lane & 15)];
+        u32x4 hi, lo;
+        split_hi_lo(v8, hi, lo);
+        const int64_t base = ((block * args.jtiles + t) * 2) * 64 + lane;
+        hf[base] = hi;
+        hf[base + 64] = lo;
       }
     }
+    __syncthreads();
   }
 }
 
-template <int WT, int RT>
+template <int RT>
 static void launch_shrink_rt(const ShrinkArgs &a, int nblocks, hipStream_t stream) {
   if (a.op_layout == 0)
-    hipLaunchKernelGGL((shrink_kernel<WT, RT, 0>), dim3(nblocks), dim3(256), 0, stream, a);
+    hipLaunchKernelGGL((shrink_kernel<RT, 0>), dim3(nblocks), dim3(256), 0, stream, a);
   else
-    hipLaunchKernelGGL((shrink_kernel<WT, RT, 1>), dim3(nblocks), dim3(256), 0, stream, a);
+    hipLaunchKernelGGL((shrink_kernel<RT, 1>), dim3(nblocks), dim3(256), 0, stream, a);
 }
 
 // ============================================================== seg_outer
 //
-// Work item = (row chunk of one segment, 64-wide j block, 128-wide c block).
+// Work item = (row chunk of one segment, 64-wide j block, 64-wide c block).
 // The 4 waves of a workgroup take interleaved 32-row steps of the chunk and
 // are summed through LDS at the end (fixed order), so each item leaves one
-// fp32 partial [128 c x 64 j]. A second kernel adds an adapter's partials in
+// fp32 partial [64 c x 64 j]. A second kernel adds an adapter's partials in
 // chunk order.
-// Per 32-row step a lane loads an 8x8 block of P (8 rows x 8 columns),
-// transposes it in registers into 8 MFMA A-fragments (one per column), and
-// loads 8 consecutive m of Qt per j, split into bf16 hi + lo parts.
-// v_mfma_f32_16x16x32_bf16: rows <- c (stride 8: c = c0 + 8*i + t for
-// fragment t), columns <- j, contraction <- m.
+// Per 32-row step a lane loads an 8x4 block of P (8 rows x 4 columns) and
+// transposes it in registers into 4 MFMA A-fragments (one per column); the
+// h fragments (hi and lo) are read ready-made. The next step's loads are in
+// flight while the current step's 32 MFMAs run; two waves share each SIMD.
+// v_mfma_f32_16x16x32_bf16: rows <- c (c = c0 + 4*i + t for fragment t),
+// columns <- j, contraction <- m.
 
-constexpr int OUT_C = 128;  // c per workgroup
-constexpr int kMaxChunkRows = 32768;
+constexpr int OUT_C = 64;   // c per workgroup
 constexpr int OUT_J = 64;   // j per workgroup
+constexpr int kMaxChunkRows = 32768;
 
 struct OuterArgs {
   const uint16_t *P;
-  const float *Qt;
+  const u32x4 *Hf;
   float *ws;
-  int64_t ldp, ldq;
+  int64_t ldp;
   int32_t M, C;
   int32_t chunk_rows;
   int32_t cblocks, jblocks;  // jblocks = ceil(max rank / 64)
   int32_t rpad;              // 64 * jblocks: partial row length
+  int32_t jtiles;            // fragment j-tiles per block
   int32_t chunk_start[kMaxSeg + 1];
   int32_t rank[kMaxAdapters];
+  PadTable pad;
   SegTable seg;
 };
 
-__global__ __launch_bounds__(256) void seg_outer_kernel(const OuterArgs args) {
-  __shared__ f32x4 red_smem[3 * 32 * 64];  // waves 1..3: 32 f32x4 accumulators x 64 lanes
+struct OuterStep {
+  uint2 blk[8];
+  u32x4 hi[4], lo[4];
+};
+
+__global__ __launch_bounds__(256, 2) void seg_outer_kernel(const OuterArgs args) {
+  __shared__ f32x4 red_smem[3 * 16 * 64];  // waves 1..3: 16 f32x4 accumulators x 64 lanes
   lds_f4 *red = (lds_f4 *)red_smem;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
   const int item = blockIdx.x;
   const int cb = item % args.cblocks;
   const int jb = (item / args.cblocks) % args.jblocks;
@@ -231,76 +281,111 @@ __global__ __launch_bounds__(256) void seg_outer_kernel(const OuterArgs args) {
   const int r = args.rank[a];
   const int j0 = jb * OUT_J;
   if (j0 >= r) return;  // whole workgroup exits together
-  const int row0 = args.seg.off[s] + (chunk - args.chunk_start[s]) * args.chunk_rows;
+  const int rel0 = (chunk - args.chunk_start[s]) * args.chunk_rows;  // multiple of 32
+  const int row0 = args.seg.off[s] + rel0;
   const int rend = min(row0 + args.chunk_rows, args.seg.off[s + 1]);
+  const int nsteps = (rend - row0 + 31) / 32;
+  const int64_t block0 = (args.pad.start[s] + rel0) / 32;
   const int c0 = cb * OUT_C;
   const int li = lane & 15, lq = lane >> 4;
-  const int ccol = c0 + 8 * li;  // this lane's 8 columns
-  const bool col_ok = ccol < args.C;
-  const int64_t ldp_b = args.ldp * 2;
+  const int ccol = c0 + 4 * li;  // this lane's 4 columns
+  const int32_t ldp_b = (int32_t)(args.ldp * 2);
   // rows past the chunk end fall outside this resource and read as zero
   const __amdgpu_buffer_rsrc_t rp = make_rsrc(args.P + (int64_t)row0 * args.ldp, (int64_t)(rend - row0) * ldp_b);
-  const __amdgpu_buffer_rsrc_t rq = make_rsrc(args.Qt, (int64_t)args.ldq * kMaxRank * 4);
-
-  f32x4 acc[8][4];
+  const __amdgpu_buffer_rsrc_t rh =
+      make_rsrc(args.Hf + (block0 * args.jtiles) * 128, (int64_t)nsteps * args.jtiles * 2048);
+  // per-lane offsets at step 0; a step adds 32 rows of P and one fragment block
+  const int32_t p_off = ccol < args.C ? (8 * lq) * ldp_b + ccol * 2 : kOOB;
+  const int32_t p_step = 32 * ldp_b;
+  const int32_t h_step = args.jtiles * 2048;
+  int32_t h_off[4];
 #pragma unroll
-  for (int t = 0; t < 8; ++t)
+  for (int q = 0; q < 4; ++q) {
+    const int t = (j0 >> 4) + q;
+    h_off[q] = 16 * t < r ? (t * 2 * 64 + lane) * 16 : kOOB;
+  }
+
+  auto load = [&](OuterStep &st, int step) {
+    // a step past the end reads zeros (soffset beyond both resources)
+    const int32_t sp = step < nsteps ? step * p_step : kOOB;
+    const int32_t sh = step < nsteps ? step * h_step : kOOB;
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+      st.blk[e] = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(rp, p_off + e * ldp_b, sp, 0));
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      st.hi[q] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rh, h_off[q], sh, 0));
+      st.lo[q] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rh, h_off[q] + 1024, sh, 0));
+    }
+  };
+
+  f32x4 acc[4][4];
+#pragma unroll
+  for (int t = 0; t < 4; ++t)
 #pragma unroll
     for (int q = 0; q < 4; ++q) acc[t][q] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  for (int m0 = row0 + 32 * wave; m0 < rend; m0 += 128) {
-    u32x4 blk[8];
+  auto compute = [&](const OuterStep &st) {
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const int m = m0 + 8 * lq + e;
-      blk[e] = buf_load16(rp, col_ok ? (int32_t)((m - row0) * ldp_b + ccol * 2) : kOOB);
-    }
-    u32x4 qhi[4], qlo[4];
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const int j = j0 + 16 * q + li;
-      float v[8];
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const int m = m0 + 8 * lq + e;
-        v[e] = buf_load4f(rq, (j < r && m < rend) ? (int32_t)(((int64_t)j * args.ldq + m) * 4) : kOOB);
-      }
-      split_hi_lo(v, qhi[q], qlo[q]);
-    }
-    u32x4 frag[8];
-    transpose8x8_b16(blk, frag);
-#pragma unroll
-    for (int t = 0; t < 8; ++t)
+    for (int t = 0; t < 4; ++t) {
+      // column t of the 8x4 block: element t of rows 2q (low half) and 2q+1 (high half)
+      uint32_t o[4];
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
-        acc[t][q] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(frag[t]), as_bf16x8(qhi[q]), acc[t][q], 0, 0, 0);
-        acc[t][q] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(frag[t]), as_bf16x8(qlo[q]), acc[t][q], 0, 0, 0);
+        const uint32_t x = (t >> 1) ? st.blk[2 * q].y : st.blk[2 * q].x;
+        const uint32_t y = (t >> 1) ? st.blk[2 * q + 1].y : st.blk[2 * q + 1].x;
+        o[q] = (t & 1) ? ((x >> 16) | (y & 0xffff0000u)) : ((x & 0xffffu) | (y << 16));
       }
+      const bf16x8 frag = as_bf16x8(u32x4{o[0], o[1], o[2], o[3]});
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        acc[t][q] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(frag, as_bf16x8(st.hi[q]), acc[t][q], 0, 0, 0);
+        acc[t][q] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(frag, as_bf16x8(st.lo[q]), acc[t][q], 0, 0, 0);
+      }
+    }
+  };
+
+  // two register stages, unrolled so no copies are needed between them
+  OuterStep s0, s1;
+  int step = wave;
+  load(s0, step);
+  while (step < nsteps) {
+    load(s1, step + 4);
+    __builtin_amdgcn_sched_barrier(0);
+    compute(s0);
+    __builtin_amdgcn_sched_barrier(0);
+    step += 4;
+    if (step >= nsteps) break;
+    load(s0, step + 4);
+    __builtin_amdgcn_sched_barrier(0);
+    compute(s1);
+    __builtin_amdgcn_sched_barrier(0);
+    step += 4;
   }
 
   // fixed-order cross-wave sum: wave0 + wave1 + wave2 + wave3
   if (wave > 0) {
 #pragma unroll
-    for (int t = 0; t < 8; ++t)
+    for (int t = 0; t < 4; ++t)
 #pragma unroll
-      for (int q = 0; q < 4; ++q) red[((wave - 1) * 32 + t * 4 + q) * 64 + lane] = acc[t][q];
+      for (int q = 0; q < 4; ++q) red[((wave - 1) * 16 + t * 4 + q) * 64 + lane] = acc[t][q];
   }
   __syncthreads();
   if (wave != 0) return;
 #pragma unroll
   for (int w = 0; w < 3; ++w)
 #pragma unroll
-    for (int t = 0; t < 8; ++t)
+    for (int t = 0; t < 4; ++t)
 #pragma unroll
-      for (int q = 0; q < 4; ++q) acc[t][q] += red[(w * 32 + t * 4 + q) * 64 + lane];
+      for (int q = 0; q < 4; ++q) acc[t][q] += red[(w * 16 + t * 4 + q) * 64 + lane];
 
-  // partial layout: ws[chunk][c][rpad]; lane holds c = c0 + 8*(4*lq + v) + t, j = j0 + 16*q + li
+  // partial layout: ws[chunk][c][rpad]; lane holds c = c0 + 4*(4*lq + v) + t, j = j0 + 16*q + li
   MLORA_GLOBAL float *dst = gp(args.ws) + (int64_t)chunk * args.C * args.rpad;
 #pragma unroll
-  for (int t = 0; t < 8; ++t)
+  for (int t = 0; t < 4; ++t)
 #pragma unroll
     for (int v = 0; v < 4; ++v) {
-      const int c = c0 + 8 * (4 * lq + v) + t;
+      const int c = c0 + 4 * (4 * lq + v) + t;
       if (c >= args.C) continue;
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
@@ -380,14 +465,28 @@ static void plan_outer(OuterPlan &pl, const SegTable &st, const int32_t *rank, i
   pl.n_chunks = n;
 }
 
+static int64_t frag_bytes(const SegTable &st, int jtiles) {
+  PadTable pt;
+  return build_pad(pt, st) / 32 * jtiles * 2048;
+}
+
 }  // namespace mlora
 
 using namespace mlora;
 
+extern "C" int64_t mlora_frag_bytes(int64_t M, int32_t frag_jtiles, const int64_t *seg_offsets,
+                                    const int32_t *adapter_ids, int32_t n_segments) {
+  SegTable st;
+  int s = build_segtable(st, M, seg_offsets, adapter_ids, n_segments, kMaxAdapters);
+  if (s) return s;
+  if (frag_jtiles < 0 || frag_jtiles > kMaxRank / 16) return MLORA_ERR_INVALID;
+  return frag_bytes(st, frag_jtiles);
+}
+
 extern "C" int mlora_shrink(const void *p, int64_t ldp, int64_t M, int64_t K, const void *const *op_ptrs, int op_layout,
                             const int32_t *ranks, const float *scales, int32_t n_adapters, const int64_t *seg_offsets,
-                            const int32_t *adapter_ids, int32_t n_segments, void *h_rows, int64_t ldh, void *h_cols,
-                            int64_t ldhc, void *stream) {
+                            const int32_t *adapter_ids, int32_t n_segments, void *h_rows, int64_t ldh, void *h_frag,
+                            int32_t frag_jtiles, void *stream) {
   ShrinkArgs a{};
   int st = build_segtable(a.seg, M, seg_offsets, adapter_ids, n_segments, n_adapters);
   if (st) return st;
@@ -400,36 +499,36 @@ extern "C" int mlora_shrink(const void *p, int64_t ldp, int64_t M, int64_t K, co
   if ((st = check_bf16_matrix(h_rows, ldh, M, rmax))) return st;
   // 31-bit byte offsets inside the buffer resources of one tile / one operand
   if (ldp * 2 * 128 >= kOOB || K * 2 * (int64_t)kMaxRank >= kOOB) return MLORA_ERR_LIMIT;
-  if (h_cols != nullptr) {
-    if (ldhc < M) return MLORA_ERR_INVALID;
-    if (ldh < rmax) return MLORA_ERR_INVALID;
+  if (h_frag != nullptr) {
+    if (frag_jtiles * 16 < rmax || frag_jtiles > kMaxRank / 16) return MLORA_ERR_INVALID;
+    if (!aligned16(h_frag)) return MLORA_ERR_UNSUPPORTED;
   }
   a.P = static_cast<const uint16_t *>(p);
   a.Hr = static_cast<uint16_t *>(h_rows);
-  a.Hc = static_cast<float *>(h_cols);
+  a.Hf = static_cast<u32x4 *>(h_frag);
   a.ldp = ldp;
   a.ldh = ldh;
-  a.ldhc = ldhc;
   a.M = (int32_t)M;
   a.K = (int32_t)K;
   a.op_layout = op_layout;
-  constexpr int WT = 1;
-  a.tile_rows = 4 * WT * 32;
+  a.jtiles = frag_jtiles;
+  build_pad(a.pad, a.seg);
+  constexpr int kTileRows = 128;
   int64_t n = 0;
   for (int s = 0; s < a.seg.n; ++s) {
     a.tile_start[s] = (int32_t)n;
     const int ad = a.seg.aid[s];
     const int len = a.seg.off[s + 1] - a.seg.off[s];
-    if (ad >= 0 && a.op.rank[ad] > 0 && len > 0) n += (len + a.tile_rows - 1) / a.tile_rows;
+    if (ad >= 0 && a.op.rank[ad] > 0 && len > 0) n += (len + kTileRows - 1) / kTileRows;
   }
   a.tile_start[a.seg.n] = (int32_t)n;
   if (n == 0) return MLORA_OK;
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int rt = (rmax + 31) / 32;
-  if (rt <= 1) launch_shrink_rt<WT, 1>(a, (int)n, s);
-  else if (rt == 2) launch_shrink_rt<WT, 2>(a, (int)n, s);
-  else if (rt <= 4) launch_shrink_rt<WT, 4>(a, (int)n, s);
-  else launch_shrink_rt<WT, 8>(a, (int)n, s);
+  if (rt <= 1) launch_shrink_rt<1>(a, (int)n, s);
+  else if (rt == 2) launch_shrink_rt<2>(a, (int)n, s);
+  else if (rt <= 4) launch_shrink_rt<4>(a, (int)n, s);
+  else launch_shrink_rt<8>(a, (int)n, s);
   return launch_status();
 }
 
@@ -461,10 +560,11 @@ extern "C" int64_t mlora_seg_outer_workspace_bytes(int64_t M, int64_t C, const i
   return (int64_t)pl.n_chunks * C * pl.rpad * (int64_t)sizeof(float);
 }
 
-extern "C" int mlora_seg_outer(const void *p, int64_t ldp, int64_t M, int64_t C, const float *qt, int64_t ldq,
-                               void *const *out_ptrs, int out_layout, int out_dtype, const int32_t *ranks,
-                               int32_t n_adapters, const int64_t *seg_offsets, const int32_t *adapter_ids,
-                               int32_t n_segments, void *workspace, int64_t workspace_bytes, void *stream) {
+extern "C" int mlora_seg_outer(const void *p, int64_t ldp, int64_t M, int64_t C, const void *h_frag,
+                               int32_t frag_jtiles, void *const *out_ptrs, int out_layout, int out_dtype,
+                               const int32_t *ranks, int32_t n_adapters, const int64_t *seg_offsets,
+                               const int32_t *adapter_ids, int32_t n_segments, void *workspace,
+                               int64_t workspace_bytes, void *stream) {
   OuterArgs a{};
   OuterPlan pl;
   int st = outer_setup(a, pl, M, C, ranks, n_adapters, seg_offsets, adapter_ids, n_segments);
@@ -476,26 +576,29 @@ extern "C" int mlora_seg_outer(const void *p, int64_t ldp, int64_t M, int64_t C,
     if (a.rank[i] > 0 && C > 0 && out_ptrs[i] == nullptr) return MLORA_ERR_INVALID;
   if (C == 0 || n_adapters == 0) return MLORA_OK;
   const int64_t need = (int64_t)pl.n_chunks * C * pl.rpad * (int64_t)sizeof(float);
-  if (pl.n_chunks > 0) {
-    if ((st = check_bf16_matrix(p, ldp, M, C))) return st;
-    if (qt == nullptr || ldq < M) return MLORA_ERR_INVALID;
-    if (ldp * 2 * kMaxChunkRows >= kOOB || ldq * 4 * (int64_t)kMaxRank >= kOOB) return MLORA_ERR_LIMIT;
-    if (workspace == nullptr || workspace_bytes < need) return MLORA_ERR_WORKSPACE;
-    if (!aligned16(workspace)) return MLORA_ERR_UNSUPPORTED;
-  }
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (pl.n_chunks > 0) {
+    if ((st = check_bf16_matrix(p, ldp, M, C))) return st;
+    if (h_frag == nullptr || !aligned16(h_frag)) return MLORA_ERR_INVALID;
+    if (frag_jtiles < 1 || frag_jtiles > kMaxRank / 16) return MLORA_ERR_INVALID;
+    for (int i = 0; i < n_adapters; ++i)
+      if (a.rank[i] > frag_jtiles * 16) return MLORA_ERR_INVALID;
+    if (workspace == nullptr || workspace_bytes < need) return MLORA_ERR_WORKSPACE;
+    if (!aligned16(workspace)) return MLORA_ERR_UNSUPPORTED;
+    if (ldp * 2 * kMaxChunkRows >= kOOB || (int64_t)(kMaxChunkRows / 32) * frag_jtiles * 2048 >= kOOB)
+      return MLORA_ERR_LIMIT;
     a.P = static_cast<const uint16_t *>(p);
-    a.Qt = qt;
+    a.Hf = static_cast<const u32x4 *>(h_frag);
     a.ws = static_cast<float *>(workspace);
     a.ldp = ldp;
-    a.ldq = ldq;
     a.M = (int32_t)M;
     a.C = (int32_t)C;
     a.chunk_rows = pl.chunk_rows;
     a.cblocks = pl.cblocks;
     a.jblocks = pl.jblocks;
     a.rpad = pl.rpad;
+    a.jtiles = frag_jtiles;
+    build_pad(a.pad, a.seg);
     for (int i = 0; i <= a.seg.n; ++i) a.chunk_start[i] = pl.chunk_start[i];
     const int64_t items = (int64_t)pl.n_chunks * pl.jblocks * pl.cblocks;
     if (items > INT32_MAX) return MLORA_ERR_LIMIT;

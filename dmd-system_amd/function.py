@@ -65,21 +65,23 @@ class MultiLoRAFunction(torch.autograd.Function):
         B_ops = [_as_operand(b, cols_pad=p) for b, p in zip(Bs, pranks)]
         width = kernels.padded_rank(pranks)
         need_b_grad = any(ctx.needs_input_grad[5 + n + i] for i in range(n))
-        h_rows, h_cols = (None, None)
+        h_rows, h_frag = (None, None)
         if width > 0:
-            h_rows, h_cols = kernels.shrink(x, A_ops, 0, scales, routing, want_cols=need_b_grad, width=width)
+            h_rows, h_frag = kernels.shrink(x, A_ops, 0, scales, routing, want_frag=need_b_grad, width=width)
         y = kernels.gemm_fwd(x, weight, bias, h_rows, B_ops, routing)
         ctx.routing, ctx.scales, ctx.n = routing, tuple(float(s) for s in scales), n
         ctx.ranks, ctx.pranks, ctx.width = ranks, pranks, width
         ctx.a_dtypes = [a.dtype for a in As]
         ctx.b_dtypes = [b.dtype for b in Bs]
-        ctx.save_for_backward(x, weight, h_cols, *A_ops, *B_ops)
+        ctx.h_frag = h_frag  # per call group; plain tensors produced and consumed here
+        ctx.save_for_backward(x, weight, *A_ops, *B_ops)
         return y
 
     @staticmethod
     def backward(ctx, dy):
         n = ctx.n
-        x, weight, h_cols, *ops = ctx.saved_tensors
+        x, weight, *ops = ctx.saved_tensors
+        h_frag = ctx.h_frag
         A_ops, B_ops = ops[:n], ops[n:]
         routing = ctx.routing
         need_x = ctx.needs_input_grad[0]
@@ -87,19 +89,19 @@ class MultiLoRAFunction(torch.autograd.Function):
         need_b = [ctx.needs_input_grad[5 + n + i] for i in range(n)]
         dy = dy.to(torch.bfloat16).contiguous()
         dx = None
-        g_rows = g_cols = None
+        g_rows = g_frag = None
         if ctx.width > 0 and (need_x or any(need_a)):
-            g_rows, g_cols = kernels.shrink(dy, B_ops, 1, ctx.scales, routing, want_cols=any(need_a), width=ctx.width)
+            g_rows, g_frag = kernels.shrink(dy, B_ops, 1, ctx.scales, routing, want_frag=any(need_a), width=ctx.width)
         if need_x:
             dx = kernels.gemm_dx(dy, weight, g_rows, A_ops, routing)
         dAs: list = [None] * n
         dBs: list = [None] * n
         if any(need_b):
-            outs = kernels.seg_outer(dy, h_cols, ctx.pranks, routing, 0,
+            outs = kernels.seg_outer(dy, h_frag, ctx.width, ctx.pranks, routing, 0,
                                      [ctx.b_dtypes[i] for i in range(n)])
             dBs = [o[:, :r] if nb else None for o, r, nb in zip(outs, ctx.ranks, need_b)]
         if any(need_a):
-            outs = kernels.seg_outer(x, g_cols, ctx.pranks, routing, 1,
+            outs = kernels.seg_outer(x, g_frag, ctx.width, ctx.pranks, routing, 1,
                                      [ctx.a_dtypes[i] for i in range(n)])
             dAs = [o[:r] if na else None for o, r, na in zip(outs, ctx.ranks, need_a)]
         return (dx, None, None, None, None, *dAs, *dBs)

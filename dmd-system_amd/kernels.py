@@ -47,9 +47,14 @@ def padded_rank(ranks: Sequence[int]) -> int:
     return (r + 7) // 8 * 8
 
 
+def frag_jtiles(width: int) -> int:
+    """j-tiles (16 ranks each) of the hi/lo fragment layout for row width `width`."""
+    return (width + 15) // 16
+
+
 def shrink(p: torch.Tensor, ops: Sequence[torch.Tensor], op_layout: int, scales: Sequence[float],
-           routing: SegmentRouting, want_cols: bool, width: int) -> tuple[torch.Tensor, torch.Tensor | None]:
-    """h = s·P·Op_aᵀ per segment -> (h_rows bf16 [M, width], h_cols fp32 [width, M] or None)."""
+           routing: SegmentRouting, want_frag: bool, width: int) -> tuple[torch.Tensor, list | None]:
+    """h = s·P·Op_aᵀ per segment -> (h_rows bf16 [M, width], per-call-group hi/lo fragments or None)."""
     M, K = p.shape
     _check_rows("P", p)
     ranks = [int(o.shape[0] if op_layout == 0 else o.shape[1]) for o in ops]
@@ -58,19 +63,25 @@ def shrink(p: torch.Tensor, ops: Sequence[torch.Tensor], op_layout: int, scales:
         _require(o.is_contiguous(), "adapter operands must be contiguous")
         _require(o.shape == ((r, K) if op_layout == 0 else (K, r)), "adapter operand shape")
     h_rows = torch.empty((M, width), dtype=torch.bfloat16, device=p.device)
-    h_cols = torch.empty((width, M), dtype=torch.float32, device=p.device) if want_cols else None
     lib = _lib.load()
     ptrs, rk, sc = _lib.ptr_array([_ptr(o) for o in ops]), _lib.i32_array(ranks), _lib.f32_array(scales)
+    jt = frag_jtiles(width)
     stream = _stream(p)
+    frags = [] if want_frag else None
     for r0, r1, off, ids in routing.groups(_lib.MAX_SEGMENTS):
+        o, i, n = _routing_arrays(off, ids)
+        frag = None
+        if want_frag:
+            nbytes = lib.mlora_frag_bytes(r1 - r0, jt, o, i, n)
+            _lib.check("mlora_frag_bytes", nbytes if nbytes < 0 else 0)
+            frag = torch.empty(max(nbytes, 16) // 2, dtype=torch.bfloat16, device=p.device)
+            frags.append(frag)
         if r1 == r0:
             continue
-        o, i, n = _routing_arrays(off, ids)
-        hc = None if h_cols is None else h_cols.data_ptr() + r0 * 4
         _lib.check("mlora_shrink", lib.mlora_shrink(
             p[r0:r1].data_ptr(), p.stride(0), r1 - r0, K, ptrs, op_layout, rk, sc, len(ops),
-            o, i, n, h_rows[r0:r1].data_ptr(), width, hc, M, stream))
-    return h_rows, h_cols
+            o, i, n, h_rows[r0:r1].data_ptr(), width, _ptr(frag), jt, stream))
+    return h_rows, frags
 
 
 def gemm_fwd(x: torch.Tensor, w: torch.Tensor, bias: torch.Tensor | None, h_rows: torch.Tensor | None,
@@ -132,28 +143,30 @@ def gemm_dx(dy: torch.Tensor, w: torch.Tensor, g_rows: torch.Tensor | None, as_:
     return dx
 
 
-def seg_outer(p: torch.Tensor, qt: torch.Tensor, ranks: Sequence[int], routing: SegmentRouting,
+def seg_outer(p: torch.Tensor, frags: list, width: int, ranks: Sequence[int], routing: SegmentRouting,
               out_layout: int, out_dtypes: Sequence[torch.dtype]) -> list[torch.Tensor]:
-    """Per-adapter Σ_m P[m,c]·Qt[j,m] -> [C, r_a] (layout 0) or [r_a, C] (layout 1)."""
+    """Per-adapter Σ_m P[m,c]·h[m,j] -> [C, r_a] (layout 0) or [r_a, C] (layout 1).
+
+    `frags` are the hi/lo fragments written by `shrink` for the same routing and width.
+    """
     M, C = p.shape
     _check_rows("P", p, C)
-    _require(qt.is_cuda and qt.dtype == torch.float32 and qt.dim() == 2 and qt.stride(1) == 1
-             and qt.shape[1] == M, "Qt must be fp32 [R, M]")
     lib = _lib.load()
     groups = list(routing.groups(_lib.MAX_SEGMENTS))
+    _require(frags is not None and len(frags) == len(groups), "h fragments from shrink() of the same routing")
     dtypes = list(out_dtypes)
     _require(all(d in _DT for d in dtypes), "adapter gradients are float32 or bfloat16")
-    # Adapters are reduced per output dtype (normally one dtype for all).
+    jt = frag_jtiles(width)
     outs: list[torch.Tensor | None] = [None] * len(ranks)
     stream = _stream(p)
-    rk = _lib.i32_array(list(ranks))
+    shape = (lambda r: (C, r)) if out_layout == 0 else (lambda r: (r, C))
+    single = len(groups) == 1
+    # Adapters are reduced per output dtype (normally one dtype for all).
     for dt in sorted(set(dtypes), key=str):
         sel = [a for a in range(len(ranks)) if dtypes[a] == dt]
         mask_ranks = _lib.i32_array([r if dtypes[a] == dt else 0 for a, r in enumerate(ranks)])
-        shape = (lambda r: (C, r)) if out_layout == 0 else (lambda r: (r, C))
-        # several row groups: reduce each into fp32 scratch, then add in group order
-        single = len(groups) == 1
-        for r0, r1, off, ids in groups:
+        # several row groups: reduce each into fp32, then add in group order
+        for (r0, r1, off, ids), frag in zip(groups, frags):
             o, i, n = _routing_arrays(off, ids)
             ws_bytes = lib.mlora_seg_outer_workspace_bytes(r1 - r0, C, mask_ranks, len(ranks), o, i, n)
             _lib.check("mlora_seg_outer_workspace_bytes", ws_bytes if ws_bytes < 0 else 0)
@@ -161,7 +174,7 @@ def seg_outer(p: torch.Tensor, qt: torch.Tensor, ranks: Sequence[int], routing: 
             part = [torch.empty(shape(ranks[a]), dtype=dt if single else torch.float32, device=p.device)
                     if a in sel else None for a in range(len(ranks))]
             _lib.check("mlora_seg_outer", lib.mlora_seg_outer(
-                p[r0:r1].data_ptr(), p.stride(0), r1 - r0, C, qt.data_ptr() + r0 * 4, qt.stride(0),
+                p[r0:r1].data_ptr(), p.stride(0), r1 - r0, C, _ptr(frag), jt,
                 _lib.ptr_array([_ptr(t) for t in part]), out_layout, _DT[dt if single else torch.float32],
                 mask_ranks, len(ranks), o, i, n, ws.data_ptr(), ws.numel() * 4, stream))
             for a in sel:
@@ -169,5 +182,4 @@ def seg_outer(p: torch.Tensor, qt: torch.Tensor, ranks: Sequence[int], routing: 
         if not single:
             for a in sel:
                 outs[a] = outs[a].to(dt)
-    del rk
     return outs  # type: ignore[return-value]

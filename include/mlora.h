@@ -83,7 +83,14 @@ const char *mlora_status_string(int status);
  *   h[m, j] = s_a · Σ_k P[m, k] · Op_a(j, k),   j < r_a
  * and writes it twice:
  *   h_rows  bf16 [M, ldh]   (row-major; round-to-nearest-even of the fp32 value)
- *   h_cols  fp32 [ldh, ldhc] (transposed: h_cols[j*ldhc + m]); may be NULL.
+ *   h_frag  (may be NULL)   h split into bf16 hi + lo parts (hi = bf16(h),
+ *           lo = bf16(h - hi)) in the per-lane operand order of the gfx950
+ *           16x16x32 bf16 MFMA, for mlora_seg_outer. Blocks of 32 rows are
+ *           counted from each segment's first row; segment s starts at padded
+ *           row Σ_{s'<s} roundup(len_s', 32). Block B, j-tile t (16 j), part p
+ *           (0 hi, 1 lo), lane L, element e holds h[32·B' + 8·(L/16) + e][16·t + L%16]
+ *           (B' = block within its segment) at 16-byte index ((B·frag_jtiles + t)·2 + p)·64 + L.
+ *           Size: mlora_frag_bytes(). frag_jtiles >= ceil(max rank / 16).
  * op_layout 0: Op_a stored [r_a, K] (K contiguous, e.g. lora_a, low_rank.py:21)
  * op_layout 1: Op_a stored [K, r_a] (r contiguous, e.g. lora_b [N, r] for the
  *              backward g = s·dY·B, low_rank.py:22)
@@ -95,8 +102,11 @@ int mlora_shrink(const void *p, int64_t ldp, int64_t M, int64_t K,
                  const void *const *op_ptrs, int op_layout,
                  const int32_t *ranks, const float *scales, int32_t n_adapters,
                  const int64_t *seg_offsets, const int32_t *adapter_ids, int32_t n_segments,
-                 void *h_rows, int64_t ldh, void *h_cols, int64_t ldhc,
+                 void *h_rows, int64_t ldh, void *h_frag, int32_t frag_jtiles,
                  void *stream);
+/* Bytes of the h_frag buffer for this routing and frag_jtiles (< 0: status). */
+int64_t mlora_frag_bytes(int64_t M, int32_t frag_jtiles, const int64_t *seg_offsets,
+                         const int32_t *adapter_ids, int32_t n_segments);
 
 /* Base GEMM with the LoRA expand fused into its epilogue:
  *   Y[m, n] = bf16( Σ_k X[m,k]·W[n,k] + bias[n] + Σ_j h_rows[m,j]·B_a[n,j] )
@@ -130,9 +140,9 @@ int mlora_gemm_dx(const void *dy, int64_t lddy, int64_t M, int64_t N,
                   void *stream);
 
 /* Segmented outer-product reduction (adapter gradients):
- *   D_a[c, j] = Σ_{m in segments of adapter a} P[m, c] · Qt[j, m]
- * P bf16 [M, C] (ldp); Qt fp32 [*, ldq] transposed per-row values (h_cols /
- * g_cols of mlora_shrink). Written as out_dtype (MLORA_F32 or MLORA_BF16) to
+ *   D_a[c, j] = Σ_{m in segments of adapter a} P[m, c] · h[m, j]
+ * P bf16 [M, C] (ldp); h given as the h_frag fragments of mlora_shrink (same
+ * routing and frag_jtiles), used as hi + lo, so h enters at ~16-bit precision. Written as out_dtype (MLORA_F32 or MLORA_BF16) to
  * out_ptrs[a], layout out_layout 0: [C, r_a] (dB_a = s·dYᵀ·h, lora_b shape),
  * out_layout 1: [r_a, C] (dA_a = gᵀ·X, lora_a shape). Adapters with no rows
  * get zeros. Deterministic two-stage reduction through `workspace`
@@ -140,7 +150,7 @@ int mlora_gemm_dx(const void *dy, int64_t lddy, int64_t M, int64_t N,
  * Reference: autograd of low_rank.py:28 (dB = s·dYᵀ·h, dA = gᵀ·x);
  * runtime/helios_lora_b_gemm_kernel.py:106 (d_b = g.T @ h). */
 int mlora_seg_outer(const void *p, int64_t ldp, int64_t M, int64_t C,
-                    const float *qt, int64_t ldq,
+                    const void *h_frag, int32_t frag_jtiles,
                     void *const *out_ptrs, int out_layout, int out_dtype,
                     const int32_t *ranks, int32_t n_adapters,
                     const int64_t *seg_offsets, const int32_t *adapter_ids, int32_t n_segments,

@@ -90,12 +90,23 @@ def test_seg_outer_workspace_and_validation(lib, pkg):
     assert lib.mlora_seg_outer_workspace_bytes(3000, 1536, ranks, 2, L.i64_array([0, 3000]),
                                                L.i32_array([-1]), 1) == 0
     outs = L.ptr_array([0x7000, 0x8000])
-    st = lib.mlora_seg_outer(0x1000, 1536, 3000, 1536, 0x2000, 3000, outs, 0, L.F32, ranks, 2, off, ids, 2,
+    st = lib.mlora_seg_outer(0x1000, 1536, 3000, 1536, 0x2000, 8, outs, 0, L.F32, ranks, 2, off, ids, 2,
                              0x9000, ws - 16, None)
     assert st == L.ERR_WORKSPACE
-    st = lib.mlora_seg_outer(0x1000, 1536, 3000, 1536, 0x2000, 3000, outs, 2, L.F32, ranks, 2, off, ids, 2,
+    st = lib.mlora_seg_outer(0x1000, 1536, 3000, 1536, 0x2000, 8, outs, 2, L.F32, ranks, 2, off, ids, 2,
                              0x9000, ws, None)
     assert st == L.ERR_INVALID  # bad layout
+    st = lib.mlora_seg_outer(0x1000, 1536, 3000, 1536, 0x2000, 4, outs, 0, L.F32, ranks, 2, off, ids, 2,
+                             0x9000, ws, None)
+    assert st == L.ERR_INVALID  # fragments narrower than rank 128
+
+
+def test_frag_bytes(lib, pkg):
+    L = pkg._lib
+    # segments of 40 and 0 and 70 rows -> padded 64 + 0 + 96 rows = 5 blocks of 32
+    n = lib.mlora_frag_bytes(110, 4, L.i64_array([0, 40, 40, 110]), L.i32_array([0, -1, 1]), 3)
+    assert n == 5 * 4 * 2048
+    assert lib.mlora_frag_bytes(110, 99, L.i64_array([0, 110]), L.i32_array([0]), 1) == L.ERR_INVALID
 
 
 def test_shrink_validation(lib, pkg):
