@@ -38,7 +38,36 @@ def parse():
     p.add_argument("--kernel-reps", type=int, default=10)
     p.add_argument("--cpu-seconds", type=float, default=12.0, help="bounded CPU-baseline sample budget")
     p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--copy-calibration", action="store_true",
+                   help="only run a plain 1 GiB device copy 4 times (scale for rocprofv3 FETCH_SIZE/WRITE_SIZE)")
     return p.parse_args()
+
+
+TRAFFIC_FILE = ROOT / "profiles" / "gemm_fwd_wan13b_traffic.md"
+
+
+def recorded_traffic():
+    """HBM bytes per launch of the fused forward GEMM, as measured by the rocprofv3
+    FETCH_SIZE / WRITE_SIZE passes summarised in profiles/ (None if absent)."""
+    if not TRAFFIC_FILE.exists():
+        return None
+    for line in TRAFFIC_FILE.read_text().splitlines():
+        if line.startswith("traffic_bytes_per_launch:"):
+            return int(float(line.split(":", 1)[1]))
+    return None
+
+
+def copy_calibration():
+    import torch
+    n = 1 << 30
+    src = torch.empty(n, dtype=torch.uint8, device="cuda:0")
+    dst = torch.empty_like(src)
+    src.fill_(1)
+    torch.cuda.synchronize()
+    for _ in range(4):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_calibration_bytes": n, "copies": 4}), flush=True)
 
 
 def main():
@@ -51,6 +80,9 @@ def main():
         sys.exit(2)
 
     import torch
+    if args.copy_calibration:
+        copy_calibration()
+        return
     import __graft_entry__
     pkg = __graft_entry__.load_package()
     pkg.load_library()
@@ -161,7 +193,7 @@ def main():
     gem_ach = gem["flops"] / gem["time"] / 1e12
     roofline = {"kernel": "gemm_kernel NT (base GEMM + fused LoRA expand), avg over the 6 block linears",
                 "bound": "mfma", "achieved": round(gem_ach, 1), "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
-                "frac": round(gem_ach / MFMA_BF16_PEAK_TFLOPS, 4), "traffic": None,
+                "frac": round(gem_ach / MFMA_BF16_PEAK_TFLOPS, 4), "traffic": recorded_traffic(),
                 "avg_launch_us": round(gem["time"] / gem["launches"] * 1e6, 2),
                 "flops_per_launch": gem["flops"] // gem["launches"]}
     lora = {}

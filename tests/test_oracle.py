@@ -209,6 +209,52 @@ def test_autocast_restatement_matches_torch_cpu_autocast():
     assert O.rel_l2(ours, truth) < 1e-2
 
 
+def _torch_variant_inputs(seed):
+    rng = np.random.default_rng(seed)
+    x, w, b, As, Bs, off, ids = _case(rng, M=64, K=32, N=24, ranks=(8, 8), lengths=(30, 34), ids=(0, 1))
+    return x, w, b, As, Bs, off, ids
+
+
+def test_fp32_update_variant_matches_torch_restatement():
+    """native/models.py:44-51: bf16 base module, fp32 update, (base.float() + update*s).to(bf16)."""
+    x, w, b, As, Bs, off, ids = _torch_variant_inputs(11)
+    scales = [0.5, 2.0]
+    xb = torch.from_numpy(np.asarray(x, np.float32)).to(torch.bfloat16)
+    wb = torch.from_numpy(np.asarray(w, np.float32)).to(torch.bfloat16)
+    bb = torch.from_numpy(np.asarray(b, np.float32)).to(torch.bfloat16)
+    outs = []
+    for s_, a in enumerate(ids):
+        lo, hi = off[s_], off[s_ + 1]
+        base = torch.nn.functional.linear(xb[lo:hi], wb, bb)
+        A = torch.from_numpy(np.asarray(As[a], np.float32))
+        B = torch.from_numpy(np.asarray(Bs[a], np.float32))
+        upd = torch.nn.functional.linear(torch.nn.functional.linear(xb[lo:hi].float(), A), B)
+        outs.append((base.float() + upd * scales[a]).to(torch.bfloat16))
+    want = torch.cat(outs).float().numpy()
+    got = O.forward_fp32_update(x, w, b, As, Bs, scales, off, ids)
+    assert O.rel_l2(got, want) < 2e-3
+
+
+def test_livewan_variant_matches_torch_restatement():
+    """wanstreamer/lora.py:22-27: y + linear(linear(x.to(fp32), a), b).to(y.dtype) * scale."""
+    x, w, b, As, Bs, off, ids = _torch_variant_inputs(12)
+    scales = [1.0, 3.0]
+    xb = torch.from_numpy(np.asarray(x, np.float32)).to(torch.bfloat16)
+    wb = torch.from_numpy(np.asarray(w, np.float32)).to(torch.bfloat16)
+    bb = torch.from_numpy(np.asarray(b, np.float32)).to(torch.bfloat16)
+    outs = []
+    for s_, a in enumerate(ids):
+        lo, hi = off[s_], off[s_ + 1]
+        y = torch.nn.functional.linear(xb[lo:hi], wb, bb)
+        A = torch.from_numpy(np.asarray(As[a], np.float32))
+        B = torch.from_numpy(np.asarray(Bs[a], np.float32))
+        h = torch.nn.functional.linear(xb[lo:hi].to(torch.float32), A)
+        outs.append(y + torch.nn.functional.linear(h, B).to(y.dtype) * scales[a])
+    want = torch.cat(outs).float().numpy()
+    got = O.forward_livewan(x, w, b, As, Bs, scales, off, ids)
+    assert O.rel_l2(got, want) < 2e-3
+
+
 def test_fp32_update_and_livewan_variants_are_close_to_exact():
     rng = np.random.default_rng(10)
     x, w, b, As, Bs, off, ids = _case(rng, M=64, K=32, N=24, ranks=(8, 8), lengths=(30, 34), ids=(0, 1))
