@@ -12,13 +12,14 @@
 //
 // gfx950 mapping: v_mfma_f32_32x32x16_bf16, wave64. A workgroup of WM x WN
 // waves owns a BM x BN tile; each wave a (BM/WM) x (BN/WN) sub-tile whose fp32
-// accumulators live in AGPRs. Operand tiles of 64 contraction elements are
-// double-buffered in LDS (one barrier per k-tile): the buffer loads of tile k+1
-// are in flight while tile k is multiplied. Global reads use raw buffer
+// accumulators stay in registers. Operand tiles of 64 contraction elements are
+// double-buffered in LDS (one barrier per k-tile): the direct-to-LDS loads of
+// tile k+1 are issued one by one between the MFMAs of tile k. Global reads use raw buffer
 // resources; out-of-range rows/columns are given an offset past the buffer and
-// read as zero, so tails need no branches. NN operands are transposed in
-// registers (8x8 blocks of bf16) on their way into LDS, so both layouts are
-// read from LDS the same way (16-byte fragments, XOR-swizzled chunks).
+// read as zero, so tails need no branches. NN operands stay in their natural
+// layout in LDS and are read with the gfx950 transposing LDS read
+// (ds_read_b64_tr_b16), which turns 4 rows x 4 columns into per-column
+// contraction runs, i.e. MFMA B fragments.
 // Reference semantics: training/low_rank.py:26-28 (and its autograd backward).
 #include "mlora_common.h"
 #include "mlora_host.h"
@@ -50,12 +51,22 @@ struct GemmCfg {
   static constexpr int TM = BM / WM / 32;  // 32x32 MFMA tiles per wave along m
   static constexpr int TN = BN / WN / 32;  // ... along n
   static constexpr int A_DMA = BM / 8 / NW;  // 1 KB direct-to-LDS loads per wave for the P tile
-  static constexpr int B_DMA = BN / 8 / NW;  // NT: the same for the Q tile
-  static constexpr int NN_BLK = 2 * BN / THREADS;  // NN: 8x4 blocks (8 k x 4 n) per thread
+  static constexpr int B_DMA = BN / 8 / NW;  // the same for the Q tile (both layouts hold 64 x BN)
+  // NN Q tile: natural layout, one row of BN output columns per contraction index
+  static constexpr int QROW = BN * 2;       // bytes per NN row
+  static constexpr int QCPR = BN / 8;       // 16-byte chunks per NN row
+  static constexpr int QRPD = 1024 / QROW;  // NN rows per 1 KB load
   static_assert(A_DMA * NW * 8 == BM, "P tile rows must split into 8-row loads over the waves");
-  static_assert(NN || B_DMA * NW * 8 == BN, "Q tile rows must split into 8-row loads over the waves");
-  static_assert(!NN || NN_BLK == 1, "NN tile must split into one 8x4 block per thread");
-  static_assert(A_DMA % 2 == 0 && (NN || B_DMA % 2 == 0), "even 8-row load counts per wave");
+  static_assert(B_DMA * NW * 8 == BN, "Q tile must split into 1 KB loads over the waves");
+  static_assert(A_DMA % 2 == 0 && B_DMA % 2 == 0, "even 1 KB load counts per wave");
+  static_assert(!NN || (QCPR >= 16 && QRPD >= 1), "NN rows hold at least 16 chunks");
+  static constexpr int NDMA = A_DMA + B_DMA;  // 1 KB loads per wave and k-tile
+  static constexpr int TMN = TM * TN;         // MFMAs per wave and 16-deep substep
+  // The next tile's loads are spread over the MFMAs of this tile's first two
+  // substeps, one after every DMA_EVERY-th MFMA (the stage barrier after the
+  // last substep waits for them).
+  static constexpr int DMA_EVERY = 2 * TMN / NDMA > 1 ? 2 * TMN / NDMA : 1;
+  static_assert(NDMA * DMA_EVERY <= 4 * TMN, "every load is issued within the k-tile");
   // LDS (bytes): P stage 0 | P stage 1 | Q stage 0 | Q stage 1
   static constexpr int A_BYTES = BM * 128, B_BYTES = BN * 128;
   static constexpr int B_BASE = 2 * A_BYTES;
@@ -90,7 +101,6 @@ struct Pipe {
   int32_t b_off[2], b_kc[2];
   int32_t b_row0;
   int32_t klim, ldp_b, ldq_b, p_rows;
-  uint2 nn_regs[C::NN ? 8 * C::NN_BLK : 1];
 
   __device__ __forceinline__ void init(const KSource &s, int m0, int n0, int Ncols, int tid) {
     const int lane = tid & 63, wave = wave_id();
@@ -118,116 +128,152 @@ struct Pipe {
         b_off[par] = (lane >> 3) * ldq_b + 16 * c;  // rows past Ncols fall outside rq
       }
     } else {
+      // NN: rows are contraction indices, chunk c of row k at slot c ^ (4 * (k & 3))
       rq = make_rsrc(s.Q + n0, (int64_t)s.klim * s.ldq * 2);
-      const int kb = tid / (C::BN / 4), nb = tid % (C::BN / 4);
-      b_kc[0] = 8 * kb;
-      b_off[0] = (n0 + 4 * nb < Ncols) ? 8 * kb * ldq_b + 8 * nb : kOOB;
+      const int p = lane % C::QCPR, rl = lane / C::QCPR;
+#pragma unroll
+      for (int par = 0; par < 2; ++par) {
+        const int c = p ^ (4 * ((C::QRPD * par + rl) & 3));
+        b_off[par] = (n0 + 8 * c < Ncols) ? rl * ldq_b + 16 * c : kOOB;
+      }
+      b_kc[0] = rl;  // row of this lane within its 1 KB load
     }
   }
 
-  // Issue the loads of the k-tile starting at k0 (P and NT Q straight into LDS stage `st`).
-  __device__ __forceinline__ void issue(MLORA_LDS char *lds, int st, int k0, int wave, int lane, bool KMASK) {
-#pragma unroll
-    for (int q = 0; q < C::A_DMA; ++q) {
+  // Issue 1 KB load number q (of NDMA per wave) of the k-tile starting at k0
+  // into LDS stage `st`: q < A_DMA are P rows, the rest Q. live == false turns
+  // every lane's offset out of range: the instruction then moves no data.
+  __device__ __forceinline__ void issue_one(MLORA_LDS char *lds, int q, int st, int k0, int wave, int lane, bool KMASK,
+                                            bool live) const {
+    if (q < C::A_DMA) {
       MLORA_LDS void *dst = lds + st * C::A_BYTES + (wave * C::A_DMA + q) * 1024;
       const int row = a_row0 + 8 * q;  // wave-uniform
       const int par = q & 1;
       int32_t off = a_off[par];
       if (p_rows > 0 && row + (lane >> 3) < p_rows) off = kOOB;  // rows of an earlier segment
       if (KMASK && k0 + a_kc[par] >= klim) off = kOOB;
+      if (!live) off = kOOB;
       __builtin_amdgcn_raw_ptr_buffer_load_lds(rp, dst, 16, off, row * ldp_b + k0 * 2, 0, 0);
-    }
-    if constexpr (!C::NN) {
-#pragma unroll
-      for (int q = 0; q < C::B_DMA; ++q) {
-        MLORA_LDS void *dst = lds + C::B_BASE + st * C::B_BYTES + (wave * C::B_DMA + q) * 1024;
-        const int row = b_row0 + 8 * q;
-        const int par = q & 1;
-        const int32_t off = (KMASK && k0 + b_kc[par] >= klim) ? kOOB : b_off[par];
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(rq, dst, 16, off, row * ldq_b + k0 * 2, 0, 0);
-      }
+    } else if constexpr (!C::NN) {
+      const int qb = q - C::A_DMA;
+      MLORA_LDS void *dst = lds + C::B_BASE + st * C::B_BYTES + (wave * C::B_DMA + qb) * 1024;
+      const int row = b_row0 + 8 * qb;
+      const int par = qb & 1;
+      int32_t off = (KMASK && k0 + b_kc[par] >= klim) ? kOOB : b_off[par];
+      if (!live) off = kOOB;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rq, dst, 16, off, row * ldq_b + k0 * 2, 0, 0);
     } else {
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const int32_t off = (KMASK && k0 + b_kc[0] + e >= klim) ? kOOB : b_off[0];
-        nn_regs[e] = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(rq, off, (k0 + e) * ldq_b, 0));
-      }
+      const int blk = wave * C::B_DMA + (q - C::A_DMA);  // wave-uniform
+      MLORA_LDS void *dst = lds + C::B_BASE + st * C::B_BYTES + blk * 1024;
+      const int row = C::QRPD * blk;
+      int32_t off = (KMASK && k0 + row + b_kc[0] >= klim) ? kOOB : b_off[blk & 1];
+      if (!live) off = kOOB;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rq, dst, 16, off, (k0 + row) * ldq_b, 0, 0);
     }
   }
 
-  // NN only: transpose the staged 8x4 block and write it to LDS stage `st`.
-  __device__ __forceinline__ void store_nn(MLORA_LDS char *lds, int st, int tid) const {
-    if constexpr (C::NN) {
-      lds_u4 *dstB = (lds_u4 *)(lds + C::B_BASE + st * C::B_BYTES);
-      const int kb = tid / (C::BN / 4), nb = tid % (C::BN / 4);
+  // All loads of the k-tile starting at k0, back to back (pipeline prologue).
+  __device__ __forceinline__ void issue(MLORA_LDS char *lds, int st, int k0, int wave, int lane, bool KMASK) const {
 #pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        uint32_t o[4];
-        const int word = t >> 1;
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const uint2 ra = nn_regs[2 * q], rb = nn_regs[2 * q + 1];
-          const uint32_t a = word ? ra.y : ra.x, bw = word ? rb.y : rb.x;
-          o[q] = (t & 1) ? ((a >> 16) | (bw & 0xffff0000u)) : ((a & 0xffffu) | (bw << 16));
-        }
-        dstB[lds_chunk_offset(4 * nb + t, kb)] = u32x4{o[0], o[1], o[2], o[3]};
-      }
-    }
+    for (int q = 0; q < C::NDMA; ++q) issue_one(lds, q, st, k0, wave, lane, KMASK, true);
   }
 };
 
 // Byte addresses (stage 0, first 32-row tile) of this lane's fragments per
 // substep; further tiles are +4096 bytes and stage 1 is +A_BYTES / +B_BYTES,
 // all folded into the ds_read offset field.
+// NN: b[j] is the first of the two transposing reads of tile j at substep 0
+// (substep s adds 16 rows, the second read 4 rows). ds_read_b64_tr_b16 gives
+// lane j of a 16-lane group element e = element (j & 3) of the 8 bytes
+// addressed by lane 4e + (j >> 2); lane i pointing at row k0 + (i >> 2),
+// column c0 + 4(i & 3) therefore yields 4 consecutive contraction values of
+// column c0 + j: half of the B fragment of v_mfma_f32_32x32x16_bf16.
 template <class C>
 struct FragAddr {
-  int32_t a[4], b[4];
+  int32_t a[4], b[C::NN ? C::TN : 4];
   __device__ __forceinline__ void init(int wm0, int wn0, int lane) {
     const int z = swz(lane & 31);  // lane-constant: fragment rows are 32-aligned + lane
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
       const int slot = (2 * s + (lane >> 5)) ^ z;
       a[s] = (wm0 + (lane & 31)) * 128 + 16 * slot;
-      b[s] = C::B_BASE + (wn0 + (lane & 31)) * 128 + 16 * slot;
+      if constexpr (!C::NN) b[s] = C::B_BASE + (wn0 + (lane & 31)) * 128 + 16 * slot;
+    }
+    if constexpr (C::NN) {
+      const int i = lane & 15, h = lane >> 5, g1 = (lane >> 4) & 1;
+      const int m = (i >> 2) & 3;  // k & 3 of every row this lane reads
+#pragma unroll
+      for (int j = 0; j < C::TN; ++j) {
+        const int c = (wn0 + 32 * j + 16 * g1) / 8 + ((i & 3) >> 1);
+        b[j] = C::B_BASE + (8 * h + (i >> 2)) * C::QROW + 16 * (c ^ (4 * m)) + 8 * (i & 1);
+      }
     }
   }
 };
 
+// Fragment read r of substep s from LDS stage ST: r < TM reads P tile r
+// (af[r]), the others Q tile r - TM (bf[r - TM]).
 template <class C, int ST>
-__device__ __forceinline__ void read_frags(bf16x8 (&af)[C::TM], bf16x8 (&bf)[C::TN], const MLORA_LDS char *lds,
-                                           const FragAddr<C> &fa, int s) {
-#pragma unroll
-  for (int i = 0; i < C::TM; ++i)
-    af[i] = as_bf16x8(*(const lds_u4 *)(lds + fa.a[s] + (4096 * i + ST * C::A_BYTES)));
-#pragma unroll
-  for (int j = 0; j < C::TN; ++j)
+__device__ __forceinline__ void read_frag(int r, bf16x8 (&af)[C::TM], bf16x8 (&bf)[C::TN], const MLORA_LDS char *lds,
+                                          const FragAddr<C> &fa, int s) {
+  if (r < C::TM) {
+    af[r] = as_bf16x8(*(const lds_u4 *)(lds + fa.a[s] + (4096 * r + ST * C::A_BYTES)));
+    return;
+  }
+  const int j = r - C::TM;
+  if constexpr (!C::NN) {
     bf[j] = as_bf16x8(*(const lds_u4 *)(lds + fa.b[s] + (4096 * j + ST * C::B_BYTES)));
+  } else {
+    typedef short v4i16 __attribute__((ext_vector_type(4)));
+    const MLORA_LDS char *p = lds + fa.b[j] + (ST * C::B_BYTES + 16 * C::QROW * s);
+    const v4i16 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((MLORA_LDS v4i16 *)p);
+    const v4i16 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((MLORA_LDS v4i16 *)(p + 4 * C::QROW));
+    const u32x2 l2 = __builtin_bit_cast(u32x2, lo), h2 = __builtin_bit_cast(u32x2, hi);
+    bf[j] = as_bf16x8(u32x4{l2[0], l2[1], h2[0], h2[1]});
+  }
 }
 
-// One 64-deep k-tile from LDS stage ST: 4 substeps of 16. The fragments of
-// substep s+1 are read while the TM*TN MFMAs of substep s run.
+// One 64-deep k-tile from LDS stage ST: 4 substeps of 16, entered with the
+// substep-0 fragments in af0/bf0 (and leaving the next stage's there). The
+// fragments of substep s+1 are read while the TM*TN MFMAs of substep s run,
+// and the loads of the next k-tile (into the other stage) are issued between
+// the MFMAs, one after every DMA_EVERY-th MFMA: issued back to back they fill
+// the texture unit's queue and stall the waves' MFMA issue behind them.
 template <class C, int ST>
-__device__ __forceinline__ void mma_stage(f32x16 (&acc)[C::TM][C::TN], const MLORA_LDS char *lds,
-                                          const FragAddr<C> &fa) {
+__device__ __forceinline__ void mma_stage(f32x16 (&acc)[C::TM][C::TN], MLORA_LDS char *lds, const FragAddr<C> &fa,
+                                          const Pipe<C> &pipe, int k0, bool kmask, bool live, int wave, int lane) {
+  constexpr int NR = C::TM + C::TN;                      // fragment reads per substep
+  constexpr int DSR = C::TM + (C::NN ? 2 : 1) * C::TN;  // DS read instructions per substep
   bf16x8 af[2][C::TM], bf[2][C::TN];
-  read_frags<C, ST>(af[0], bf[0], lds, fa, 0);
+#pragma unroll
+  for (int r = 0; r < NR; ++r) read_frag<C, ST>(r, af[0], bf[0], lds, fa, 0);
 #pragma unroll
   for (int s = 0; s < 4; ++s) {
     const int cur = s & 1;
-    if (s < 3) read_frags<C, ST>(af[cur ^ 1], bf[cur ^ 1], lds, fa, s + 1);
-#pragma unroll
-    for (int i = 0; i < C::TM; ++i)
-#pragma unroll
-      for (int j = 0; j < C::TN; ++j)
-        // MFMA rows <- Q (n), columns <- P (m): each lane ends up with 4
-        // consecutive n of one row m, stored as one 8-byte write.
-        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bf[cur][j], af[cur][i], acc[i][j], 0, 0, 0);
     if (s < 3) {
 #pragma unroll
-      for (int g = 0; g < C::TM + C::TN; ++g) {
-        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // one DS read
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
-      }
+      for (int r = 0; r < NR; ++r) read_frag<C, ST>(r, af[cur ^ 1], bf[cur ^ 1], lds, fa, s + 1);
+    }
+#pragma unroll
+    for (int g = 0; g < C::TMN; ++g) {
+      const int i = g / C::TN, j = g % C::TN;
+      // MFMA rows <- Q (n), columns <- P (m): each lane ends up with 4
+      // consecutive n of one row m, stored as one 8-byte write.
+      acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bf[cur][j], af[cur][i], acc[i][j], 0, 0, 0);
+      const int idx = s * C::TMN + g;
+      if (idx % C::DMA_EVERY == 0 && idx / C::DMA_EVERY < C::NDMA)
+        pipe.issue_one(lds, idx / C::DMA_EVERY, ST ^ 1, k0, wave, lane, kmask, live);
+    }
+    // scheduling hints: DS reads spread evenly over the MFMAs, each load right after its MFMA
+#pragma unroll
+    for (int g = 0; g < C::TMN; ++g) {
+      const int nr = s < 3 ? ((g + 1) * DSR) / C::TMN - (g * DSR) / C::TMN : 0;
+#pragma unroll
+      for (int r = 0; r < nr; ++r) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // one DS read
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                                // one MFMA
+      const int idx = s * C::TMN + g;
+      if (idx % C::DMA_EVERY == 0 && idx / C::DMA_EVERY < C::NDMA)
+        __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // one load
     }
   }
 }
@@ -278,7 +324,6 @@ __device__ __forceinline__ void contract_tile(f32x16 (&acc)[C::TM][C::TN], const
   pipe.init(src, m0, n0, args.Ncols, tid);
   int t_in_src = 0;  // index of the tile being loaded within its source
   pipe.issue(lds, 0, 0, wave, lane, kmask);
-  pipe.store_nn(lds, 0, tid);
   stage_barrier();
   // `more`: whether a tile after the current one exists (and was loaded)
   auto advance = [&]() -> bool {
@@ -293,15 +338,11 @@ __device__ __forceinline__ void contract_tile(f32x16 (&acc)[C::TM][C::TN], const
   while (true) {
     // stage 0 holds the current tile; the next one (if any) goes to stage 1
     bool more = advance();
-    if (more) pipe.issue(lds, 1, t_in_src * C::BK, wave, lane, kmask);
-    mma_stage<C, 0>(acc, lds, fa);
-    if (more) pipe.store_nn(lds, 1, tid);
+    mma_stage<C, 0>(acc, lds, fa, pipe, t_in_src * C::BK, kmask, more, wave, lane);
     stage_barrier();
     if (!more) break;
     more = advance();
-    if (more) pipe.issue(lds, 0, t_in_src * C::BK, wave, lane, kmask);
-    mma_stage<C, 1>(acc, lds, fa);
-    if (more) pipe.store_nn(lds, 0, tid);
+    mma_stage<C, 1>(acc, lds, fa, pipe, t_in_src * C::BK, kmask, more, wave, lane);
     stage_barrier();
     if (!more) break;
   }
