@@ -3,6 +3,7 @@
 Public API:
     SegmentRouting, BASE_ONLY            row-segment -> adapter routing
     MultiLoRAFunction, multi_lora_linear autograd op
+    MultiLoRAFP8Function, multi_lora_linear_fp8   the same with an e4m3 frozen base
     TrainableLowRankLinear, trainable_scope, MultiLoRALinear   drop-in modules
     kernels                              torch front end of each C-ABI entry point
     load_library()                       load libmlora.so (raises if missing)
@@ -12,7 +13,7 @@ The directory name is not a Python identifier; importers load it as
 ``__graft_entry__.py``).
 """
 from . import _lib, kernels
-from .function import MultiLoRAFunction, multi_lora_linear
+from .function import MultiLoRAFP8Function, MultiLoRAFunction, multi_lora_linear, multi_lora_linear_fp8
 from .low_rank import MultiLoRALinear, TrainableLowRankLinear, trainable_scope
 from .routing import BASE_ONLY, SegmentRouting
 
@@ -22,6 +23,7 @@ def load_library():
 
 
 __all__ = [
-    "BASE_ONLY", "SegmentRouting", "MultiLoRAFunction", "multi_lora_linear", "MultiLoRALinear",
+    "BASE_ONLY", "SegmentRouting", "MultiLoRAFunction", "multi_lora_linear", "MultiLoRAFP8Function",
+    "multi_lora_linear_fp8", "MultiLoRALinear",
     "TrainableLowRankLinear", "trainable_scope", "kernels", "load_library",
 ]

@@ -40,6 +40,10 @@ SIGNATURES = {
     "mlora_seg_outer": (_int, [_vp, _i64, _i64, _i64, _vp, _i32, _pvp, _int, _int, _pi32, _i32,
                                _pi64, _pi32, _i32, _vp, _i64, _vp]),
     "mlora_seg_outer_workspace_bytes": (_i64, [_i64, _i64, _pi32, _i32, _pi64, _pi32, _i32]),
+    "mlora_quantize_rows_fp8": (_int, [_vp, _i64, _i64, _i64, _vp, _i64, _vp, _vp]),
+    "mlora_dequant_rows_fp8": (_int, [_vp, _i64, _vp, _i64, _i64, _vp, _i64, _vp]),
+    "mlora_gemm_fwd_fp8": (_int, [_vp, _i64, _vp, _i64, _i64, _vp, _i64, _vp, _i64, _vp, _int, _vp, _i64,
+                                  _pvp, _pi32, _i32, _pi64, _pi32, _i32, _vp, _i64, _int, _vp]),
 }
 
 _LIB = None

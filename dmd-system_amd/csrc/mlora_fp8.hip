@@ -1,0 +1,144 @@
+// e4m3 (OCP E4M3FN: bias 7, max 448, no infinities) conversions for the
+// quantised-base variant of the multi-LoRA linear:
+//
+//   mlora_quantize_rows_fp8 : per-row absmax scaling of a bf16 matrix to e4m3
+//                             (activations X before the fp8 base GEMM)
+//   mlora_dequant_rows_fp8  : e4m3 rows times a per-row fp32 scale back to bf16
+//                             (the frozen base W for the bf16 dX GEMM)
+//
+// Quantisation of row m: amax = max_k |x[m,k]|; scale[m] = amax / 448 and
+// q = e4m3_rne(x * (448 / amax)) (both divisions IEEE fp32; an all-zero row
+// gets scale 1). The conversion is written out (round to nearest even on the
+// 3 mantissa bits, subnormals in steps of 2^-9, saturation at 448) so that
+// the bytes are reproducible from the definition of the format.
+//
+// One wave per row: pass 1 reduces the absmax over 16-byte loads, pass 2
+// re-reads the row (an L2 hit) and writes 8 bytes per lane. Memory-bound:
+// 3 bytes of HBM traffic per element.
+#include "mlora_common.h"
+#include "mlora_host.h"
+
+namespace mlora {
+
+__device__ __forceinline__ uint32_t f32_to_e4m3(float f) {
+  const uint32_t sign = (__float_as_uint(f) >> 24) & 0x80u;
+  const float a = fabsf(f);
+  if (!(a < 464.f)) return sign | 0x7Eu;  // rounds past 448 (or NaN): saturate
+  if (a < 0.015625f) {                     // below 2^-6: subnormal grid 2^-9
+    return sign | (uint32_t)rintf(a * 512.f);  // 8 lands on 0x08 = 2^-6
+  }
+  uint32_t v = __float_as_uint(a);
+  v += 0x7FFFFu + ((v >> 20) & 1u);  // round the fp32 mantissa to 3 bits, ties to even
+  const uint32_t e = (v >> 23) - 120u;  // rebias 127 -> 7
+  return sign | (e << 3) | ((v >> 20) & 7u);
+}
+
+__device__ __forceinline__ float e4m3_to_f32(uint32_t c) {
+  const uint32_t sign = (c & 0x80u) << 24, e = (c >> 3) & 15u, m = c & 7u;
+  if (e == 0) return __uint_as_float(sign | __float_as_uint((float)m * 0.001953125f));  // m * 2^-9
+  return __uint_as_float(sign | ((e + 120u) << 23) | (m << 20));
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+  return v;
+}
+
+struct QuantArgs {
+  const uint16_t *x;
+  uint8_t *q;
+  float *scale;
+  int64_t ldx, ldq;
+  int32_t M, K;
+};
+
+__global__ __launch_bounds__(256) void quantize_rows_kernel(const QuantArgs a) {
+  const int lane = threadIdx.x & 63;
+  const int m = blockIdx.x * 4 + wave_id();
+  if (m >= a.M) return;
+  const __amdgpu_buffer_rsrc_t rx = make_rsrc(a.x + (int64_t)m * a.ldx, (int64_t)a.K * 2);
+  float amax = 0.f;
+  for (int k = 8 * lane; k < a.K; k += 512) {
+    const u32x4 v = buf_load16(rx, 2 * k);
+#pragma unroll
+    for (int w = 0; w < 4; ++w)
+      amax = fmaxf(amax, fmaxf(fabsf(bf16_to_f32(v[w] & 0xffff)), fabsf(bf16_to_f32(v[w] >> 16))));
+  }
+  amax = wave_max(amax);
+  const float inv = amax > 0.f ? 448.f / amax : 1.f;
+  if (lane == 0) a.scale[m] = amax > 0.f ? amax / 448.f : 1.f;
+  uint8_t *qrow = a.q + (int64_t)m * a.ldq;
+  for (int k = 8 * lane; k < a.K; k += 512) {
+    const u32x4 v = buf_load16(rx, 2 * k);
+    uint32_t o[2] = {0u, 0u};
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      const uint32_t lo = f32_to_e4m3(bf16_to_f32(v[w] & 0xffff) * inv);
+      const uint32_t hi = f32_to_e4m3(bf16_to_f32(v[w] >> 16) * inv);
+      o[w >> 1] |= (lo | (hi << 8)) << (16 * (w & 1));
+    }
+    *(MLORA_GLOBAL u32x2 *)(qrow + k) = u32x2{o[0], o[1]};
+  }
+}
+
+struct DequantArgs {
+  const uint8_t *q;
+  const float *scale;
+  uint16_t *y;
+  int64_t ldq, ldy;
+  int32_t M, K;
+};
+
+__global__ __launch_bounds__(256) void dequant_rows_kernel(const DequantArgs a) {
+  const int lane = threadIdx.x & 63;
+  const int m = blockIdx.x * 4 + wave_id();
+  if (m >= a.M) return;
+  const float s = a.scale[m];
+  const uint8_t *qrow = a.q + (int64_t)m * a.ldq;
+  uint16_t *yrow = a.y + (int64_t)m * a.ldy;
+  for (int k = 8 * lane; k < a.K; k += 512) {
+    const u32x2 v = *(const MLORA_GLOBAL u32x2 *)(qrow + k);
+    uint32_t o[4];
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      const uint32_t word = v[w >> 1] >> (16 * (w & 1));
+      o[w] = pack2_bf16(e4m3_to_f32(word & 0xff) * s, e4m3_to_f32((word >> 8) & 0xff) * s);
+    }
+    *(MLORA_GLOBAL u32x4 *)(yrow + k) = u32x4{o[0], o[1], o[2], o[3]};
+  }
+}
+
+}  // namespace mlora
+
+using namespace mlora;
+
+extern "C" int mlora_quantize_rows_fp8(const void *x, int64_t ldx, int64_t M, int64_t K, void *xq, int64_t ldq,
+                                       float *scale, void *stream) {
+  if (M < 0 || K < 0) return MLORA_ERR_INVALID;
+  if (M > INT32_MAX - 4 || K > INT32_MAX / 2) return MLORA_ERR_LIMIT;
+  int st = check_bf16_matrix(x, ldx, M, K);
+  if (st) return st;
+  if ((st = check_fp8_matrix(xq, ldq, M, K))) return st;
+  if (M == 0 || K == 0) return MLORA_OK;
+  if (scale == nullptr) return MLORA_ERR_INVALID;
+  QuantArgs a{static_cast<const uint16_t *>(x), static_cast<uint8_t *>(xq), scale, ldx, ldq, (int32_t)M, (int32_t)K};
+  hipLaunchKernelGGL(quantize_rows_kernel, dim3((unsigned)((M + 3) / 4)), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), a);
+  return launch_status();
+}
+
+extern "C" int mlora_dequant_rows_fp8(const void *q, int64_t ldq, const float *scale, int64_t M, int64_t K, void *y,
+                                      int64_t ldy, void *stream) {
+  if (M < 0 || K < 0) return MLORA_ERR_INVALID;
+  if (M > INT32_MAX - 4 || K > INT32_MAX / 2) return MLORA_ERR_LIMIT;
+  int st = check_fp8_matrix(q, ldq, M, K);
+  if (st) return st;
+  if ((st = check_bf16_matrix(y, ldy, M, K))) return st;
+  if (M == 0 || K == 0) return MLORA_OK;
+  if (scale == nullptr) return MLORA_ERR_INVALID;
+  DequantArgs a{static_cast<const uint8_t *>(q), scale, static_cast<uint16_t *>(y), ldq, ldy, (int32_t)M, (int32_t)K};
+  hipLaunchKernelGGL(dequant_rows_kernel, dim3((unsigned)((M + 3) / 4)), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), a);
+  return launch_status();
+}

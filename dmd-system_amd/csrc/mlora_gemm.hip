@@ -24,12 +24,16 @@
 #include "mlora_common.h"
 #include "mlora_host.h"
 
+#include <type_traits>
+
 namespace mlora {
 
 struct GemmArgs {
-  const uint16_t *P;
-  const uint16_t *Q;
-  const uint16_t *E;  // extension rows (Hs / Gs), [M, lde]
+  const void *P;       // bf16, or e4m3 in the fp8 forward
+  const void *Q;       // bf16, or e4m3 in the fp8 forward
+  const uint16_t *E;   // extension rows (Hs / Gs), [M, lde]
+  const float *psc;    // fp8 forward: per-row scale of P [M]
+  const float *qsc;    // fp8 forward: per-row scale of Q [Ncols]
   const void *bias;
   uint16_t *Y;
   int64_t ldp, ldq, lde, ldy;
@@ -41,11 +45,12 @@ struct GemmArgs {
   SegTable seg;
 };
 
-template <int BM_, int BN_, int WM_, int WN_, bool NN_>
+template <int BM_, int BN_, int WM_, int WN_, bool NN_, bool F8_ = false>
 struct GemmCfg {
   static constexpr int BM = BM_, BN = BN_, WM = WM_, WN = WN_;
   static constexpr bool NN = NN_;
-  static constexpr int BK = 64;
+  static constexpr bool F8 = F8_;  // main contraction in e4m3 (v_mfma_scale_f32_32x32x64_f8f6f4)
+  static_assert(!(NN && F8), "the fp8 main contraction is NT only");
   static constexpr int NW = WM * WN;
   static constexpr int THREADS = 64 * NW;
   static constexpr int TM = BM / WM / 32;  // 32x32 MFMA tiles per wave along m
@@ -66,7 +71,7 @@ struct GemmCfg {
   // substeps, one after every DMA_EVERY-th MFMA (the stage barrier after the
   // last substep waits for them).
   static constexpr int DMA_EVERY = 2 * TMN / NDMA > 1 ? 2 * TMN / NDMA : 1;
-  static_assert(NDMA * DMA_EVERY <= 4 * TMN, "every load is issued within the k-tile");
+  static_assert(NDMA * DMA_EVERY <= (F8 ? 2 : 4) * TMN, "every load is issued within the k-tile");
   // LDS (bytes): P stage 0 | P stage 1 | Q stage 0 | Q stage 1
   static constexpr int A_BYTES = BM * 128, B_BYTES = BN * 128;
   static constexpr int B_BASE = 2 * A_BYTES;
@@ -76,13 +81,16 @@ struct GemmCfg {
 };
 
 // One contraction source (wave-uniform): P rows valid in [row_lo, row_hi),
-// contraction valid below klim for both operands.
+// contraction valid below klim (elements) for both operands. esz is the
+// element size (2: bf16, 1: e4m3); an LDS k-tile always holds 128 bytes of
+// contraction per row, i.e. 128 / esz elements.
 struct KSource {
-  const uint16_t *P;
-  const uint16_t *Q;
-  int64_t ldp, ldq;
+  const char *P;
+  const char *Q;
+  int64_t ldp_b, ldq_b;  // row pitches in bytes
   int32_t row_lo, row_hi;
   int32_t klim;
+  int32_t esz;
 };
 
 // Per-thread state of one contraction source. Global tiles go to LDS with the
@@ -100,36 +108,38 @@ struct Pipe {
   int32_t a_row0;       // first P row (tile-local) of this wave's loads
   int32_t b_off[2], b_kc[2];
   int32_t b_row0;
-  int32_t klim, ldp_b, ldq_b, p_rows;
+  int32_t klim, ldp_b, ldq_b, p_rows, esz;
 
   __device__ __forceinline__ void init(const KSource &s, int m0, int n0, int Ncols, int tid) {
     const int lane = tid & 63, wave = wave_id();
     klim = s.klim;
+    esz = s.esz;
     const int base_row = max(s.row_lo, m0);
-    ldp_b = (int32_t)(s.ldp * 2);
-    ldq_b = (int32_t)(s.ldq * 2);
+    ldp_b = (int32_t)s.ldp_b;
+    ldq_b = (int32_t)s.ldq_b;
+    const int chunk_elems = 16 / s.esz;
     // P rows of the tile are read relative to m0; rows outside [row_lo, row_hi) read zero
-    rp = make_rsrc(s.P + (int64_t)m0 * s.ldp, (int64_t)(s.row_hi - m0) * ldp_b);
+    rp = make_rsrc(s.P + (int64_t)m0 * s.ldp_b, (int64_t)(s.row_hi - m0) * ldp_b);
     p_rows = base_row - m0;  // tile rows below this index belong to another segment
     a_row0 = 8 * wave * C::A_DMA;
 #pragma unroll
     for (int par = 0; par < 2; ++par) {
       const int c = (lane & 7) ^ (lane >> 3) ^ par;
-      a_kc[par] = 8 * c;
+      a_kc[par] = chunk_elems * c;
       a_off[par] = (lane >> 3) * ldp_b + 16 * c;
     }
     if constexpr (!C::NN) {
-      rq = make_rsrc(s.Q + (int64_t)n0 * s.ldq, (int64_t)(Ncols - n0) * s.ldq * 2);
+      rq = make_rsrc(s.Q + (int64_t)n0 * s.ldq_b, (int64_t)(Ncols - n0) * s.ldq_b);
       b_row0 = 8 * wave * C::B_DMA;
 #pragma unroll
       for (int par = 0; par < 2; ++par) {
         const int c = (lane & 7) ^ (lane >> 3) ^ par;
-        b_kc[par] = 8 * c;
+        b_kc[par] = chunk_elems * c;
         b_off[par] = (lane >> 3) * ldq_b + 16 * c;  // rows past Ncols fall outside rq
       }
     } else {
-      // NN: rows are contraction indices, chunk c of row k at slot c ^ (4 * (k & 3))
-      rq = make_rsrc(s.Q + n0, (int64_t)s.klim * s.ldq * 2);
+      // NN (bf16 only): rows are contraction indices, chunk c of row k at slot c ^ (4 * (k & 3))
+      rq = make_rsrc(s.Q + 2 * n0, (int64_t)s.klim * s.ldq_b);
       const int p = lane % C::QCPR, rl = lane / C::QCPR;
 #pragma unroll
       for (int par = 0; par < 2; ++par) {
@@ -153,7 +163,7 @@ struct Pipe {
       if (p_rows > 0 && row + (lane >> 3) < p_rows) off = kOOB;  // rows of an earlier segment
       if (KMASK && k0 + a_kc[par] >= klim) off = kOOB;
       if (!live) off = kOOB;
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rp, dst, 16, off, row * ldp_b + k0 * 2, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rp, dst, 16, off, row * ldp_b + k0 * esz, 0, 0);
     } else if constexpr (!C::NN) {
       const int qb = q - C::A_DMA;
       MLORA_LDS void *dst = lds + C::B_BASE + st * C::B_BYTES + (wave * C::B_DMA + qb) * 1024;
@@ -161,7 +171,7 @@ struct Pipe {
       const int par = qb & 1;
       int32_t off = (KMASK && k0 + b_kc[par] >= klim) ? kOOB : b_off[par];
       if (!live) off = kOOB;
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rq, dst, 16, off, row * ldq_b + k0 * 2, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rq, dst, 16, off, row * ldq_b + k0 * esz, 0, 0);
     } else {
       const int blk = wave * C::B_DMA + (q - C::A_DMA);  // wave-uniform
       MLORA_LDS void *dst = lds + C::B_BASE + st * C::B_BYTES + blk * 1024;
@@ -278,6 +288,57 @@ __device__ __forceinline__ void mma_stage(f32x16 (&acc)[C::TM][C::TN], MLORA_LDS
   }
 }
 
+// The fp8 form of mma_stage: one 128-element (128-byte) k-tile of e4m3 in 2
+// substeps of v_mfma_scale_f32_32x32x64_f8f6f4 (unit block scales). That MFMA
+// gives lane l the 32 contraction bytes of row (A) / column (B) l%32 at
+// positions 32*(l/32) + e; any assignment of k to (l/32, e) works as long as A
+// and B agree, so each operand fragment is simply the two 16-byte chunks that
+// the bf16 substeps 2s and 2s+1 read: the LDS layout and addresses are shared.
+template <class C, int ST>
+__device__ __forceinline__ void mma_stage_fp8(f32x16 (&acc)[C::TM][C::TN], MLORA_LDS char *lds, const FragAddr<C> &fa,
+                                              const Pipe<C> &pipe, int k0, bool kmask, bool live, int wave, int lane) {
+  typedef int i32x8 __attribute__((ext_vector_type(8)));
+  // one 32-byte fragment: P tile r (r < TM) or Q tile r - TM, fp8 substep s
+  auto frag = [&](int r, int s) -> i32x8 {
+    bf16x8 a[C::TM], b[C::TN];
+    read_frag<C, ST>(r, a, b, lds, fa, 2 * s);
+    const u32x4 lo = __builtin_bit_cast(u32x4, r < C::TM ? a[r] : b[r - C::TM]);
+    read_frag<C, ST>(r, a, b, lds, fa, 2 * s + 1);
+    const u32x4 hi = __builtin_bit_cast(u32x4, r < C::TM ? a[r] : b[r - C::TM]);
+    return i32x8{(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3], (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
+  };
+  i32x8 ac[C::TM], bc[C::TN], an[C::TM];
+#pragma unroll
+  for (int i = 0; i < C::TM; ++i) ac[i] = frag(i, 0);
+#pragma unroll
+  for (int j = 0; j < C::TN; ++j) bc[j] = frag(C::TM + j, 0);
+#pragma unroll
+  for (int s = 0; s < 2; ++s) {
+    if (s == 0) {
+#pragma unroll
+      for (int i = 0; i < C::TM; ++i) an[i] = frag(i, 1);
+    }
+    // j-major order: once tile j's MFMAs are issued its fragment is dead and
+    // the next substep's fragment of tile j can take its registers
+#pragma unroll
+    for (int j = 0; j < C::TN; ++j) {
+#pragma unroll
+      for (int i = 0; i < C::TM; ++i) {
+        // MFMA rows <- Q (n), columns <- P (m), as in the bf16 form
+        acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(bc[j], ac[i], acc[i][j], 0, 0, 0, 127, 0, 127);
+        const int idx = s * C::TMN + j * C::TM + i;
+        if (idx % C::DMA_EVERY == 0 && idx / C::DMA_EVERY < C::NDMA)
+          pipe.issue_one(lds, idx / C::DMA_EVERY, ST ^ 1, k0, wave, lane, kmask, live);
+      }
+      if (s == 0) bc[j] = frag(C::TM + j, 1);
+    }
+    if (s == 0) {
+#pragma unroll
+      for (int i = 0; i < C::TM; ++i) ac[i] = an[i];
+    }
+  }
+}
+
 // Wait for this wave's direct-to-LDS loads, then publish the stage to all waves.
 __device__ __forceinline__ void stage_barrier() {
   __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
@@ -294,7 +355,8 @@ __device__ __forceinline__ bool next_lora_source(const GemmArgs &args, bool nn, 
     ++seg;
     if (a >= 0 && args.ext.rank[a] > 0 && lo < hi) {
       const int r = args.ext.rank[a];
-      src = KSource{args.E, args.ext.ptr[a], args.lde, nn ? (int64_t)args.Ncols : (int64_t)r, lo, hi, r};
+      src = KSource{reinterpret_cast<const char *>(args.E), reinterpret_cast<const char *>(args.ext.ptr[a]), 2 * args.lde,
+                    2 * (nn ? (int64_t)args.Ncols : (int64_t)r), lo, hi, r, 2};
       return true;
     }
   }
@@ -307,20 +369,24 @@ __device__ __forceinline__ bool next_lora_source(const GemmArgs &args, bool nn, 
 // (a few scalars and two offsets); the LDS stages and the MFMA code are shared,
 // so the accumulators stay in place. Tiles past a source's contraction length
 // mask their chunks.
-template <class C>
+template <class C, class Dequant>
 __device__ __forceinline__ void contract_tile(f32x16 (&acc)[C::TM][C::TN], const GemmArgs &args, MLORA_LDS char *lds,
-                                              const FragAddr<C> &fa, int m0, int n0, int tid) {
+                                              const FragAddr<C> &fa, int m0, int n0, int tid, const Dequant &dequant) {
   const int wave = wave_id(), lane = tid & 63;
   const int row_end = min(m0 + C::BM, args.M);
   int seg = args.E != nullptr ? seg_of_row(args.seg, m0) : args.seg.n;
   Pipe<C> pipe;
-  KSource src{args.P, args.Q, args.ldp, args.ldq, 0, args.M, args.Kc};
-  int ntile = (src.klim + C::BK - 1) / C::BK;
+  constexpr int esz0 = C::F8 ? 1 : 2;
+  KSource src{static_cast<const char *>(args.P), static_cast<const char *>(args.Q), esz0 * args.ldp, esz0 * args.ldq,
+              0, args.M, args.Kc, esz0};
+  int bk = 128 / src.esz;  // contraction elements per k-tile of the current source
+  int ntile = (src.klim + bk - 1) / bk;
   if (ntile == 0) {
     if (!next_lora_source(args, C::NN, m0, row_end, seg, src)) return;
-    ntile = (src.klim + C::BK - 1) / C::BK;
+    bk = 128 / src.esz;
+    ntile = (src.klim + bk - 1) / bk;
   }
-  bool kmask = src.klim % C::BK != 0;
+  bool kmask = src.klim % bk != 0;
   pipe.init(src, m0, n0, args.Ncols, tid);
   int t_in_src = 0;  // index of the tile being loaded within its source
   pipe.issue(lds, 0, 0, wave, lane, kmask);
@@ -329,22 +395,47 @@ __device__ __forceinline__ void contract_tile(f32x16 (&acc)[C::TM][C::TN], const
   auto advance = [&]() -> bool {
     if (++t_in_src < ntile) return true;
     if (!next_lora_source(args, C::NN, m0, row_end, seg, src)) return false;
-    ntile = (src.klim + C::BK - 1) / C::BK;
-    kmask = src.klim % C::BK != 0;
+    bk = 128 / src.esz;
+    ntile = (src.klim + bk - 1) / bk;
+    kmask = src.klim % bk != 0;
     pipe.init(src, m0, n0, args.Ncols, tid);
     t_in_src = 0;
     return true;
   };
+  // One step: multiply the tile in LDS stage ST while the next tile (if any)
+  // loads into the other stage; returns whether there is a next tile.
+  auto step = [&](auto st_c, auto f8_c) -> bool {
+    constexpr int ST = decltype(st_c)::value;
+    const bool more = advance();
+    if constexpr (decltype(f8_c)::value) mma_stage_fp8<C, ST>(acc, lds, fa, pipe, t_in_src * bk, kmask, more, wave, lane);
+    else mma_stage<C, ST>(acc, lds, fa, pipe, t_in_src * bk, kmask, more, wave, lane);
+    stage_barrier();
+    return more;
+  };
+  using S0 = std::integral_constant<int, 0>;
+  using S1 = std::integral_constant<int, 1>;
+  using E4 = std::true_type;
+  using B16 = std::false_type;
+  if constexpr (C::F8) {
+    // the e4m3 main contraction (at least one tile), then one dequantize, then
+    // the bf16 LoRA tiles starting from whichever stage holds the next one
+    bool more;
+    int st;
+    while (true) {
+      more = step(S0{}, E4{});
+      st = 1;
+      if (!more || src.esz != 1) break;
+      more = step(S1{}, E4{});
+      st = 0;
+      if (!more || src.esz != 1) break;
+    }
+    dequant(acc);
+    if (!more) return;
+    if (st == 1 && !step(S1{}, B16{})) return;
+  }
   while (true) {
-    // stage 0 holds the current tile; the next one (if any) goes to stage 1
-    bool more = advance();
-    mma_stage<C, 0>(acc, lds, fa, pipe, t_in_src * C::BK, kmask, more, wave, lane);
-    stage_barrier();
-    if (!more) break;
-    more = advance();
-    mma_stage<C, 1>(acc, lds, fa, pipe, t_in_src * C::BK, kmask, more, wave, lane);
-    stage_barrier();
-    if (!more) break;
+    if (!step(S0{}, B16{})) break;
+    if (!step(S1{}, B16{})) break;
   }
 }
 
@@ -368,36 +459,75 @@ __global__ __launch_bounds__(C::THREADS) void gemm_kernel(const GemmArgs args) {
   const int tn = (id % per_group) / gsize;
   const int m0 = tm * C::BM, n0 = tn * C::BN;
 
-  // accumulators start at the bias of their column (lane holds n = n0 + wn0 +
-  // 32j + 8g + 4(lane/32) + e for register 4g + e of tile (i, j))
+  // Register 4g + e of tile (i, j) holds row m = m0 + wm0 + 32i + lane%32 and
+  // column n = n0 + wn0 + 32j + 8g + 4(lane/32) + e.
+  auto bias_of = [&](int n, float (&v)[4]) {
+    v[0] = v[1] = v[2] = v[3] = 0.f;
+    if (n < args.Ncols) {
+      if (args.bias_dtype == MLORA_F32) {
+        const f32x4 b = *(const MLORA_GLOBAL f32x4 *)(static_cast<const float *>(args.bias) + n);
+        v[0] = b[0]; v[1] = b[1]; v[2] = b[2]; v[3] = b[3];
+      } else if (args.bias_dtype == MLORA_BF16) {
+        const u32x2 b = *(const MLORA_GLOBAL u32x2 *)(static_cast<const uint16_t *>(args.bias) + n);
+        v[0] = bf16_to_f32(b.x & 0xffff); v[1] = bf16_to_f32(b.x >> 16);
+        v[2] = bf16_to_f32(b.y & 0xffff); v[3] = bf16_to_f32(b.y >> 16);
+      }
+    }
+  };
   f32x16 acc[C::TM][C::TN];
+  if constexpr (!C::F8) {
+    // bf16: accumulators start at the bias of their column
 #pragma unroll
-  for (int j = 0; j < C::TN; ++j) {
-    f32x16 b0;
+    for (int j = 0; j < C::TN; ++j) {
+      f32x16 b0;
 #pragma unroll
-    for (int g = 0; g < 4; ++g) {
-      const int n = n0 + wn0 + 32 * j + 8 * g + 4 * (lane >> 5);
-      float v[4] = {0.f, 0.f, 0.f, 0.f};
-      if (n < args.Ncols) {
-        if (args.bias_dtype == MLORA_F32) {
-          const f32x4 b = *(const MLORA_GLOBAL f32x4 *)(static_cast<const float *>(args.bias) + n);
-          v[0] = b[0]; v[1] = b[1]; v[2] = b[2]; v[3] = b[3];
-        } else if (args.bias_dtype == MLORA_BF16) {
-          const u32x2 b = *(const MLORA_GLOBAL u32x2 *)(static_cast<const uint16_t *>(args.bias) + n);
-          v[0] = bf16_to_f32(b.x & 0xffff); v[1] = bf16_to_f32(b.x >> 16);
-          v[2] = bf16_to_f32(b.y & 0xffff); v[3] = bf16_to_f32(b.y >> 16);
-        }
+      for (int g = 0; g < 4; ++g) {
+        float v[4];
+        bias_of(n0 + wn0 + 32 * j + 8 * g + 4 * (lane >> 5), v);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) b0[4 * g + e] = v[e];
       }
 #pragma unroll
-      for (int e = 0; e < 4; ++e) b0[4 * g + e] = v[e];
+      for (int i = 0; i < C::TM; ++i) acc[i][j] = b0;
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < C::TM; ++i)
+#pragma unroll
+      for (int j = 0; j < C::TN; ++j)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
+  }
+  // fp8: after the e4m3 contraction, acc = acc * psc[m] * qsc[n] + bias[n]
+  // (then the bf16 LoRA k-tiles accumulate on top)
+  auto dequant = [&](f32x16 (&a)[C::TM][C::TN]) {
+    float ps[C::TM];
+#pragma unroll
+    for (int i = 0; i < C::TM; ++i) {
+      const int m = m0 + wm0 + 32 * i + (lane & 31);
+      ps[i] = m < args.M ? args.psc[m] : 0.f;
     }
 #pragma unroll
-    for (int i = 0; i < C::TM; ++i) acc[i][j] = b0;
-  }
+    for (int j = 0; j < C::TN; ++j)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int n = n0 + wn0 + 32 * j + 8 * g + 4 * (lane >> 5);
+        float v[4], qs[4] = {0.f, 0.f, 0.f, 0.f};
+        bias_of(n, v);
+        if (n < args.Ncols) {
+          const f32x4 q = *(const MLORA_GLOBAL f32x4 *)(args.qsc + n);
+          qs[0] = q[0]; qs[1] = q[1]; qs[2] = q[2]; qs[3] = q[3];
+        }
+#pragma unroll
+        for (int i = 0; i < C::TM; ++i)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) a[i][j][4 * g + e] = a[i][j][4 * g + e] * (ps[i] * qs[e]) + v[e];
+      }
+  };
   FragAddr<C> fa;
   fa.init(wm0, wn0, lane);
 
-  contract_tile<C>(acc, args, lds, fa, m0, n0, tid);
+  contract_tile<C>(acc, args, lds, fa, m0, n0, tid, dequant);
 
   // epilogue: (+ Y), round to bf16, 8-byte stores of 4 consecutive n
   const int rows_here = min(C::BM, args.M - m0);
@@ -428,6 +558,8 @@ __global__ __launch_bounds__(C::THREADS) void gemm_kernel(const GemmArgs args) {
 }
 
 using CfgNT256 = GemmCfg<256, 256, 4, 2, false>;
+using CfgF8256 = GemmCfg<256, 256, 4, 2, false, true>;
+using CfgF8128 = GemmCfg<128, 128, 2, 2, false, true>;
 using CfgNN256 = GemmCfg<256, 256, 4, 2, true>;
 using CfgNT128 = GemmCfg<128, 128, 2, 2, false>;
 using CfgNN128 = GemmCfg<128, 128, 2, 2, true>;
@@ -537,4 +669,39 @@ extern "C" int mlora_gemm_dx(const void *dy, int64_t lddy, int64_t M, int64_t N,
   a.ldy = lddx;
   a.accumulate = 0;
   return dispatch_gemm<CfgNN256, CfgNN128>(a, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int mlora_gemm_fwd_fp8(const void *xq, int64_t ldx, const float *x_scale, int64_t M, int64_t K,
+                                  const void *wq, int64_t ldw, const float *w_scale, int64_t N, const void *bias,
+                                  int bias_dtype, const void *h_rows, int64_t ldh, const void *const *b_ptrs,
+                                  const int32_t *ranks, int32_t n_adapters, const int64_t *seg_offsets,
+                                  const int32_t *adapter_ids, int32_t n_segments, void *y, int64_t ldy, int accumulate,
+                                  void *stream) {
+  GemmArgs a{};
+  int st = fill_common(a, M, K, N, h_rows, ldh, b_ptrs, ranks, n_adapters, seg_offsets, adapter_ids, n_segments);
+  if (st) return st;
+  if ((st = check_fp8_matrix(xq, ldx, M, K))) return st;
+  if ((st = check_fp8_matrix(wq, ldw, N, K))) return st;
+  if ((st = check_bf16_matrix(y, ldy, M, N))) return st;
+  if (M == 0 || N == 0) return MLORA_OK;
+  if (y == nullptr || xq == nullptr || wq == nullptr || x_scale == nullptr || w_scale == nullptr) return MLORA_ERR_INVALID;
+  if (K == 0) return MLORA_ERR_UNSUPPORTED;  // the dequantize step follows the first e4m3 k-tile
+  if (!aligned16(w_scale)) return MLORA_ERR_UNSUPPORTED;
+  if (bias != nullptr) {
+    if (bias_dtype != MLORA_F32 && bias_dtype != MLORA_BF16) return MLORA_ERR_UNSUPPORTED;
+    if (!aligned16(bias)) return MLORA_ERR_UNSUPPORTED;
+  }
+  if (ldx * 256 >= (int64_t)kOOB || ldw * 256 >= (int64_t)kOOB || !offsets_fit(ldy, 256)) return MLORA_ERR_LIMIT;
+  a.P = xq;
+  a.Q = wq;
+  a.psc = x_scale;
+  a.qsc = w_scale;
+  a.ldp = ldx;
+  a.ldq = ldw;
+  a.bias = bias;
+  a.bias_dtype = bias ? bias_dtype : -1;
+  a.Y = static_cast<uint16_t *>(y);
+  a.ldy = ldy;
+  a.accumulate = accumulate ? 1 : 0;
+  return dispatch_gemm<CfgF8256, CfgF8128>(a, static_cast<hipStream_t>(stream));
 }

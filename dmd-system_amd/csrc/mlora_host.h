@@ -81,6 +81,14 @@ inline int check_bf16_matrix(const void *p, int64_t ld, int64_t rows, int64_t co
   return MLORA_OK;
 }
 
+// e4m3 matrices: rows of 16-byte chunks (ld and cols multiples of 16).
+inline int check_fp8_matrix(const void *p, int64_t ld, int64_t rows, int64_t cols) {
+  if (rows == 0 || cols == 0) return MLORA_OK;
+  if (p == nullptr || ld < cols) return MLORA_ERR_INVALID;
+  if (!aligned16(p) || (ld % 16) != 0 || (cols % 16) != 0) return MLORA_ERR_UNSUPPORTED;
+  return MLORA_OK;
+}
+
 inline int launch_status() {
   hipError_t e = hipGetLastError();
   return e == hipSuccess ? MLORA_OK : MLORA_ERR_LAUNCH;

@@ -36,6 +36,65 @@ def _as_operand(t: torch.Tensor, rows_pad: int | None = None, cols_pad: int | No
     return t
 
 
+def _prepare(ctx, x, N: int, ab, scales, routing: SegmentRouting, grad0: int):
+    """Validate adapters, build padded bf16 operands and run the forward shrink.
+
+    grad0 is the index of the first lora_a among the autograd inputs.
+    Returns (A_ops, B_ops, h_rows); records what backward needs on ctx.
+    """
+    n = len(ab) // 2
+    if len(ab) != 2 * n or len(scales) != n:
+        raise ValueError("multi-LoRA: one lora_a, one lora_b and one scale per adapter")
+    As, Bs = ab[:n], ab[n:]
+    M, K = x.shape
+    routing.validate_for(M, n)
+    ranks = [int(a.shape[0]) for a in As]
+    for a, b, r in zip(As, Bs, ranks):
+        if a.shape != (r, K) or b.shape != (N, r):
+            raise ValueError(f"multi-LoRA: lora_a {tuple(a.shape)} / lora_b {tuple(b.shape)} do not match "
+                             f"rank {r}, in {K}, out {N}")
+    pranks = [(r + 7) // 8 * 8 for r in ranks]
+    A_ops = [_as_operand(a, rows_pad=p) for a, p in zip(As, pranks)]
+    B_ops = [_as_operand(b, cols_pad=p) for b, p in zip(Bs, pranks)]
+    width = kernels.padded_rank(pranks)
+    need_b_grad = any(ctx.needs_input_grad[grad0 + n + i] for i in range(n))
+    h_rows, h_frag = (None, None)
+    if width > 0:
+        h_rows, h_frag = kernels.shrink(x, A_ops, 0, scales, routing, want_frag=need_b_grad, width=width)
+    ctx.routing, ctx.scales, ctx.n, ctx.grad0 = routing, tuple(float(s) for s in scales), n, grad0
+    ctx.ranks, ctx.pranks, ctx.width = ranks, pranks, width
+    ctx.a_dtypes = [a.dtype for a in As]
+    ctx.b_dtypes = [b.dtype for b in Bs]
+    ctx.h_frag = h_frag  # per call group; plain tensors produced and consumed here
+    return A_ops, B_ops, h_rows
+
+
+def _backward(ctx, dy, x, weight, A_ops, B_ops):
+    """dX (bf16 base `weight`), dA_i, dB_i; returns (dx, dAs, dBs)."""
+    n, g0, routing = ctx.n, ctx.grad0, ctx.routing
+    need_x = ctx.needs_input_grad[0]
+    need_a = [ctx.needs_input_grad[g0 + i] for i in range(n)]
+    need_b = [ctx.needs_input_grad[g0 + n + i] for i in range(n)]
+    dy = dy.to(torch.bfloat16).contiguous()
+    dx = None
+    g_rows = g_frag = None
+    if ctx.width > 0 and (need_x or any(need_a)):
+        g_rows, g_frag = kernels.shrink(dy, B_ops, 1, ctx.scales, routing, want_frag=any(need_a), width=ctx.width)
+    if need_x:
+        dx = kernels.gemm_dx(dy, weight(), g_rows, A_ops, routing)
+    dAs: list = [None] * n
+    dBs: list = [None] * n
+    if any(need_b):
+        outs = kernels.seg_outer(dy, ctx.h_frag, ctx.width, ctx.pranks, routing, 0,
+                                 [ctx.b_dtypes[i] for i in range(n)])
+        dBs = [o[:, :r] if nb else None for o, r, nb in zip(outs, ctx.ranks, need_b)]
+    if any(need_a):
+        outs = kernels.seg_outer(x, g_frag, ctx.width, ctx.pranks, routing, 1,
+                                 [ctx.a_dtypes[i] for i in range(n)])
+        dAs = [o[:r] if na else None for o, r, na in zip(outs, ctx.ranks, need_a)]
+    return dx, dAs, dBs
+
+
 class MultiLoRAFunction(torch.autograd.Function):
     """``apply(x, weight, bias, routing, scales, *lora_as, *lora_bs)``.
 
@@ -46,34 +105,10 @@ class MultiLoRAFunction(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, x, weight, bias, routing: SegmentRouting, scales: Sequence[float], *ab):
-        n = len(ab) // 2
-        if len(ab) != 2 * n or len(scales) != n:
-            raise ValueError("multi-LoRA: one lora_a, one lora_b and one scale per adapter")
         if ctx.needs_input_grad[1] or ctx.needs_input_grad[2]:
             raise RuntimeError("multi-LoRA: the base weight and bias are frozen (requires_grad=False)")
-        As, Bs = ab[:n], ab[n:]
-        M, K = x.shape
-        N = weight.shape[0]
-        routing.validate_for(M, n)
-        ranks = [int(a.shape[0]) for a in As]
-        for a, b, r in zip(As, Bs, ranks):
-            if a.shape != (r, K) or b.shape != (N, r):
-                raise ValueError(f"multi-LoRA: lora_a {tuple(a.shape)} / lora_b {tuple(b.shape)} do not match "
-                                 f"rank {r}, in {K}, out {N}")
-        pranks = [(r + 7) // 8 * 8 for r in ranks]
-        A_ops = [_as_operand(a, rows_pad=p) for a, p in zip(As, pranks)]
-        B_ops = [_as_operand(b, cols_pad=p) for b, p in zip(Bs, pranks)]
-        width = kernels.padded_rank(pranks)
-        need_b_grad = any(ctx.needs_input_grad[5 + n + i] for i in range(n))
-        h_rows, h_frag = (None, None)
-        if width > 0:
-            h_rows, h_frag = kernels.shrink(x, A_ops, 0, scales, routing, want_frag=need_b_grad, width=width)
+        A_ops, B_ops, h_rows = _prepare(ctx, x, weight.shape[0], ab, scales, routing, grad0=5)
         y = kernels.gemm_fwd(x, weight, bias, h_rows, B_ops, routing)
-        ctx.routing, ctx.scales, ctx.n = routing, tuple(float(s) for s in scales), n
-        ctx.ranks, ctx.pranks, ctx.width = ranks, pranks, width
-        ctx.a_dtypes = [a.dtype for a in As]
-        ctx.b_dtypes = [b.dtype for b in Bs]
-        ctx.h_frag = h_frag  # per call group; plain tensors produced and consumed here
         ctx.save_for_backward(x, weight, *A_ops, *B_ops)
         return y
 
@@ -81,30 +116,37 @@ class MultiLoRAFunction(torch.autograd.Function):
     def backward(ctx, dy):
         n = ctx.n
         x, weight, *ops = ctx.saved_tensors
-        h_frag = ctx.h_frag
-        A_ops, B_ops = ops[:n], ops[n:]
-        routing = ctx.routing
-        need_x = ctx.needs_input_grad[0]
-        need_a = [ctx.needs_input_grad[5 + i] for i in range(n)]
-        need_b = [ctx.needs_input_grad[5 + n + i] for i in range(n)]
-        dy = dy.to(torch.bfloat16).contiguous()
-        dx = None
-        g_rows = g_frag = None
-        if ctx.width > 0 and (need_x or any(need_a)):
-            g_rows, g_frag = kernels.shrink(dy, B_ops, 1, ctx.scales, routing, want_frag=any(need_a), width=ctx.width)
-        if need_x:
-            dx = kernels.gemm_dx(dy, weight, g_rows, A_ops, routing)
-        dAs: list = [None] * n
-        dBs: list = [None] * n
-        if any(need_b):
-            outs = kernels.seg_outer(dy, h_frag, ctx.width, ctx.pranks, routing, 0,
-                                     [ctx.b_dtypes[i] for i in range(n)])
-            dBs = [o[:, :r] if nb else None for o, r, nb in zip(outs, ctx.ranks, need_b)]
-        if any(need_a):
-            outs = kernels.seg_outer(x, g_frag, ctx.width, ctx.pranks, routing, 1,
-                                     [ctx.a_dtypes[i] for i in range(n)])
-            dAs = [o[:r] if na else None for o, r, na in zip(outs, ctx.ranks, need_a)]
+        dx, dAs, dBs = _backward(ctx, dy, x, lambda: weight, ops[:n], ops[n:])
         return (dx, None, None, None, None, *dAs, *dBs)
+
+
+class MultiLoRAFP8Function(torch.autograd.Function):
+    """``apply(x, wq, w_scale, bias, routing, scales, *lora_as, *lora_bs)``: the
+    same linear with the frozen base stored as e4m3 ``wq`` [N, K] and one fp32
+    scale per output channel ``w_scale`` [N] (base weight = w_scale[n]·wq[n, k]).
+
+    Forward: X is quantised per token to e4m3 (mlora_quantize_rows_fp8) and the
+    base product runs on the e4m3 MFMA with fp32 accumulation; the LoRA shrink
+    and expand stay bf16 on the unquantised X. Backward: dX runs the bf16 dX
+    GEMM over the dequantised W (dY is not quantised); dA, dB as in the bf16 path.
+    """
+
+    @staticmethod
+    def forward(ctx, x, wq, w_scale, bias, routing: SegmentRouting, scales: Sequence[float], *ab):
+        if any(ctx.needs_input_grad[1:4]):
+            raise RuntimeError("multi-LoRA: the base weight, its scale and the bias are frozen")
+        A_ops, B_ops, h_rows = _prepare(ctx, x, wq.shape[0], ab, scales, routing, grad0=6)
+        xq, x_scale = kernels.quantize_rows_fp8(x)
+        y = kernels.gemm_fwd_fp8(xq, x_scale, wq, w_scale, bias, h_rows, B_ops, routing)
+        ctx.save_for_backward(x, wq, w_scale, *A_ops, *B_ops)
+        return y
+
+    @staticmethod
+    def backward(ctx, dy):
+        n = ctx.n
+        x, wq, w_scale, *ops = ctx.saved_tensors
+        dx, dAs, dBs = _backward(ctx, dy, x, lambda: kernels.dequant_rows_fp8(wq, w_scale), ops[:n], ops[n:])
+        return (dx, None, None, None, None, None, *dAs, *dBs)
 
 
 def multi_lora_linear(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None,
@@ -125,3 +167,23 @@ def multi_lora_linear(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor 
     with torch.autocast("cuda", enabled=False):
         y = MultiLoRAFunction.apply(x2.contiguous(), weight, bias, routing, tuple(scales), *lora_as, *lora_bs)
     return y.reshape(*lead, weight.shape[0])
+
+
+def multi_lora_linear_fp8(x: torch.Tensor, wq: torch.Tensor, w_scale: torch.Tensor, bias: torch.Tensor | None,
+                          lora_as: Sequence[torch.Tensor], lora_bs: Sequence[torch.Tensor],
+                          scales: Sequence[float], routing: SegmentRouting) -> torch.Tensor:
+    """Functional form with an e4m3 base (wq [N, K] float8_e4m3fn, w_scale [N] fp32); bf16 out."""
+    K = x.shape[-1]
+    lead = x.shape[:-1]
+    x2 = x.reshape(-1, K)
+    if torch.is_autocast_enabled("cuda") and torch.get_autocast_dtype("cuda") == torch.bfloat16:
+        x2 = x2.to(torch.bfloat16)
+    if x2.dtype != torch.bfloat16:
+        raise RuntimeError("multi-LoRA linear computes in bfloat16: pass a bf16 input, "
+                           "or call it under torch.autocast('cuda', dtype=torch.bfloat16)")
+    if not x2.is_cuda:
+        raise RuntimeError("multi-LoRA linear runs on the ROCm device only (HIP kernels, no CPU path)")
+    with torch.autocast("cuda", enabled=False):
+        y = MultiLoRAFP8Function.apply(x2.contiguous(), wq, w_scale, bias, routing, tuple(scales),
+                                       *lora_as, *lora_bs)
+    return y.reshape(*lead, wq.shape[0])

@@ -183,3 +183,79 @@ def seg_outer(p: torch.Tensor, frags: list, width: int, ranks: Sequence[int], ro
             for a in sel:
                 outs[a] = outs[a].to(dt)
     return outs  # type: ignore[return-value]
+
+
+# ------------------------------------------------------------ quantised base (e4m3)
+
+_FP8_STORAGE = (torch.uint8, torch.float8_e4m3fn)
+
+
+def _check_fp8_rows(name: str, t: torch.Tensor, cols: int | None = None) -> None:
+    _require(t.is_cuda, f"{name} must be a ROCm device tensor")
+    _require(t.dtype in _FP8_STORAGE, f"{name} must be float8_e4m3fn (or its uint8 bytes), got {t.dtype}")
+    _require(t.dim() == 2 and t.stride(1) == 1, f"{name} must be a 2-D row-major matrix")
+    if cols is not None:
+        _require(t.shape[1] == cols, f"{name} has {t.shape[1]} columns, expected {cols}")
+
+
+def _check_scale(name: str, s: torch.Tensor, n: int) -> None:
+    _require(s.is_cuda and s.dtype == torch.float32 and s.is_contiguous() and s.shape == (n,),
+             f"{name} must be a contiguous float32 vector of length {n}")
+
+
+def quantize_rows_fp8(x: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """Per-row absmax e4m3 quantisation: (q float8_e4m3fn [M, K], scale float32 [M]), x ≈ q·scale."""
+    M, K = x.shape
+    _check_rows("X", x, K)
+    q = torch.empty((M, K), dtype=torch.float8_e4m3fn, device=x.device)
+    scale = torch.empty((M,), dtype=torch.float32, device=x.device)
+    lib = _lib.load()
+    _lib.check("mlora_quantize_rows_fp8", lib.mlora_quantize_rows_fp8(
+        x.data_ptr(), x.stride(0), M, K, q.data_ptr(), q.stride(0), scale.data_ptr(), _stream(x)))
+    return q, scale
+
+
+def dequant_rows_fp8(q: torch.Tensor, scale: torch.Tensor) -> torch.Tensor:
+    """bf16(e4m3(q[m, k]) · scale[m])."""
+    M, K = q.shape
+    _check_fp8_rows("q", q, K)
+    _check_scale("scale", scale, M)
+    y = torch.empty((M, K), dtype=torch.bfloat16, device=q.device)
+    lib = _lib.load()
+    _lib.check("mlora_dequant_rows_fp8", lib.mlora_dequant_rows_fp8(
+        q.data_ptr(), q.stride(0), scale.data_ptr(), M, K, y.data_ptr(), y.stride(0), _stream(q)))
+    return y
+
+
+def gemm_fwd_fp8(xq: torch.Tensor, x_scale: torch.Tensor, wq: torch.Tensor, w_scale: torch.Tensor,
+                 bias: torch.Tensor | None, h_rows: torch.Tensor | None, bs: Sequence[torch.Tensor],
+                 routing: SegmentRouting) -> torch.Tensor:
+    """Y = (Xq·Wqᵀ)·x_scale[m]·w_scale[n] + bias + per-segment h_rows·B_aᵀ, bf16 out (e4m3 MFMA base)."""
+    M, K = xq.shape
+    N = wq.shape[0]
+    _check_fp8_rows("Xq", xq, K)
+    _check_fp8_rows("Wq", wq, K)
+    _check_scale("x_scale", x_scale, M)
+    _check_scale("w_scale", w_scale, N)
+    if bias is not None:
+        _require(bias.is_cuda and bias.dtype in _DT and bias.is_contiguous() and bias.shape == (N,), "bias")
+    ranks = [int(b.shape[1]) for b in bs]
+    for b in bs:
+        _check_rows("lora_b", b)
+        _require(b.is_contiguous() and b.shape[0] == N, "lora_b must be contiguous [N, r]")
+    y = torch.empty((M, N), dtype=torch.bfloat16, device=xq.device)
+    lib = _lib.load()
+    ptrs, rk = _lib.ptr_array([_ptr(b) for b in bs]), _lib.i32_array(ranks)
+    ldh = h_rows.stride(0) if h_rows is not None else 0
+    stream = _stream(xq)
+    for r0, r1, off, ids in routing.groups(_lib.MAX_SEGMENTS):
+        if r1 == r0:
+            continue
+        o, i, n = _routing_arrays(off, ids)
+        hr = None if h_rows is None else h_rows[r0:r1].data_ptr()
+        _lib.check("mlora_gemm_fwd_fp8", lib.mlora_gemm_fwd_fp8(
+            xq[r0:r1].data_ptr(), xq.stride(0), x_scale[r0:r1].data_ptr(), r1 - r0, K,
+            wq.data_ptr(), wq.stride(0), w_scale.data_ptr(), N,
+            _ptr(bias), _DT[bias.dtype] if bias is not None else 0, hr, ldh,
+            ptrs, rk, len(bs), o, i, n, y[r0:r1].data_ptr(), y.stride(0), 0, stream))
+    return y

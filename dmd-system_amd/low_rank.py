@@ -20,7 +20,8 @@ from typing import Sequence
 import torch
 from torch import nn
 
-from .function import multi_lora_linear
+from .function import multi_lora_linear, multi_lora_linear_fp8
+from .kernels import quantize_rows_fp8
 from .routing import SegmentRouting
 
 
@@ -130,6 +131,20 @@ class MultiLoRALinear(nn.Module):
     def num_adapters(self) -> int:
         return len(self.scales)
 
+    def quantize_base_fp8(self) -> "MultiLoRALinear":
+        """Store the frozen base weight as e4m3 with one fp32 scale per output
+        channel (buffers ``base_wq`` [out, in], ``base_wscale`` [out]); forward
+        then runs the e4m3 base GEMM. The bf16/fp32 ``base.weight`` is left in
+        place for its other users (shared construction aliases it)."""
+        w = self.base.weight.detach().to(torch.bfloat16).contiguous()
+        wq, ws = quantize_rows_fp8(w)
+        self.register_buffer("base_wq", wq, persistent=True)
+        self.register_buffer("base_wscale", ws, persistent=True)
+        return self
+
     def forward(self, x: torch.Tensor, routing: SegmentRouting) -> torch.Tensor:
+        if getattr(self, "base_wq", None) is not None:
+            return multi_lora_linear_fp8(x, self.base_wq, self.base_wscale, self.base.bias, list(self.lora_a),
+                                         list(self.lora_b), self.scales, routing)
         return multi_lora_linear(x, self.base.weight, self.base.bias, list(self.lora_a), list(self.lora_b),
                                  self.scales, routing)

@@ -161,6 +161,38 @@ int64_t mlora_seg_outer_workspace_bytes(int64_t M, int64_t C,
                                         const int64_t *seg_offsets, const int32_t *adapter_ids,
                                         int32_t n_segments);
 
+/* ---- Quantised frozen base (OCP e4m3 / float8_e4m3fn, per-row fp32 scale).
+ * The reference keeps its frozen base in bf16/fp32 (low_rank.py:20, native/models.py:150-156);
+ * these three entry points serve the variant whose frozen W is stored as e4m3 with one fp32
+ * scale per output channel, with the same LoRA semantics (low_rank.py:28) on top. */
+
+/* Per-row absmax quantisation of a bf16 matrix: scale[m] = max_k |x[m,k]| / 448 (1 for an
+ * all-zero row), q[m,k] = e4m3_rne(x[m,k] · (448 / max_k |x[m,k]|)), saturating at 448.
+ * q: [M, K] bytes (ldq and K multiples of 16, 16-byte aligned). Used for activations (per
+ * token) and to produce the per-output-channel weight format. */
+int mlora_quantize_rows_fp8(const void *x, int64_t ldx, int64_t M, int64_t K,
+                            void *q, int64_t ldq, float *scale,
+                            void *stream);
+
+/* y[m, k] = bf16( e4m3(q[m,k]) · scale[m] ): the frozen e4m3 W back in bf16 for the dX GEMM. */
+int mlora_dequant_rows_fp8(const void *q, int64_t ldq, const float *scale, int64_t M, int64_t K,
+                           void *y, int64_t ldy,
+                           void *stream);
+
+/* mlora_gemm_fwd with an e4m3 base contraction (v_mfma_scale_f32_32x32x64_f8f6f4):
+ *   Y[m, n] = bf16( x_scale[m]·w_scale[n]·Σ_k xq[m,k]·wq[n,k] + bias[n] + Σ_j h_rows[m,j]·B_a[n,j] )
+ * xq [M, K] and wq [N, K] e4m3 bytes (mlora_quantize_rows_fp8 layout, K >= 16); x_scale [M],
+ * w_scale [N] fp32 (w_scale 16-byte aligned). The LoRA term stays bf16 (h_rows, b_ptrs as in
+ * mlora_gemm_fwd). Reference semantics: low_rank.py:28 with base weight w_scale[n]·wq[n,k]. */
+int mlora_gemm_fwd_fp8(const void *xq, int64_t ldx, const float *x_scale, int64_t M, int64_t K,
+                       const void *wq, int64_t ldw, const float *w_scale, int64_t N,
+                       const void *bias, int bias_dtype,
+                       const void *h_rows, int64_t ldh,
+                       const void *const *b_ptrs, const int32_t *ranks, int32_t n_adapters,
+                       const int64_t *seg_offsets, const int32_t *adapter_ids, int32_t n_segments,
+                       void *y, int64_t ldy, int accumulate,
+                       void *stream);
+
 #ifdef __cplusplus
 }
 #endif

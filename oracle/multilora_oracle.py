@@ -53,6 +53,92 @@ def bf16_round(a) -> np.ndarray:
     return out.reshape(f.shape)
 
 
+# ------------------------------------------------------------------ e4m3 (OCP E4M3FN)
+#
+# The quantised-base variant stores the frozen W as OCP 8-bit E4M3 (bias 7,
+# 3 mantissa bits, subnormals 2^-9 apart, max 448, 0x7F/0xFF NaN, no
+# infinities; the format torch calls float8_e4m3fn) with one fp32 scale per
+# output channel, and quantises activations per row. The reference has no
+# such path (its base is bf16/fp32, low_rank.py:20); these functions define
+# the variant's arithmetic. Pinned in tests/test_oracle.py against torch's
+# float8_e4m3fn conversions (all 256 codes; random, tie and subnormal values)
+# and against a brute-force nearest-representable search.
+
+def e4m3_decode(q) -> np.ndarray:
+    """float32 value of each e4m3 byte (NaN for 0x7F / 0xFF)."""
+    q = np.asarray(q, dtype=np.uint8).astype(np.int64)
+    sign = np.where(q & 0x80, -1.0, 1.0)
+    e = (q >> 3) & 15
+    m = q & 7
+    mag = np.where(e == 0, m * 2.0 ** -9, (1.0 + m / 8.0) * np.exp2(e - 7.0))
+    out = (sign * mag).astype(np.float32)
+    return np.where((q & 0x7F) == 0x7F, np.float32(np.nan), out)
+
+
+def e4m3_encode(a) -> np.ndarray:
+    """Nearest e4m3 byte of float32 values (ties to even), saturating at ±448.
+
+    Normal range (|a| >= 2^-6): round the fp32 mantissa to 3 bits; below it,
+    round |a|·2^9 to an integer (the subnormal grid); |a| >= 464 (which rounds
+    past 448) and NaN give 0x7E with the sign of a.
+    """
+    f = np.ascontiguousarray(np.asarray(a, dtype=np.float32))
+    bits = f.view(np.uint32).astype(np.uint64)
+    sign = (bits >> 24) & 0x80
+    mag = np.abs(f)
+    v = mag.view(np.uint32).astype(np.uint64)
+    v = v + 0x7FFFF + ((v >> 20) & 1)
+    normal = ((((v >> 23) - 120) << 3) | ((v >> 20) & 7)) & 0xFF
+    with np.errstate(invalid="ignore"):
+        sub = np.rint(mag * np.float32(512)).astype(np.float64)
+        code = np.where(mag < np.float32(2.0 ** -6), np.nan_to_num(sub), normal)
+        code = np.where(mag < np.float32(464), code, 0x7E)
+    code = np.where(np.isnan(f), 0x7E, code)
+    return (code.astype(np.uint64) | sign).astype(np.uint8).reshape(f.shape)
+
+
+def quantize_rows_e4m3(x):
+    """Per-row absmax quantisation -> (q uint8 [M, K], scale float32 [M]).
+
+    scale = amax / 448 and q = e4m3(x · (448 / amax)), both quotients in fp32;
+    an all-zero row gets scale 1 (and q = 0).
+    """
+    x = np.asarray(x, dtype=np.float32)
+    amax = np.abs(x).max(axis=1) if x.shape[1] else np.zeros(x.shape[0], np.float32)
+    pos = amax > 0
+    safe = np.where(pos, amax, np.float32(1)).astype(np.float32)
+    inv = np.where(pos, np.float32(448) / safe, np.float32(1)).astype(np.float32)
+    scale = np.where(pos, safe / np.float32(448), np.float32(1)).astype(np.float32)
+    q = e4m3_encode((x * inv[:, None]).astype(np.float32))
+    return q, scale
+
+
+def dequant_rows_e4m3(q, scale) -> np.ndarray:
+    """fp32 e4m3(q)·scale per row (before any bf16 rounding)."""
+    return (e4m3_decode(q) * np.asarray(scale, np.float32)[:, None]).astype(np.float32)
+
+
+def forward_fp8_base(x, wq, w_scale, b, As, Bs, scales, seg_offsets, adapter_ids) -> np.ndarray:
+    """Reference semantics with the e4m3 base: forward() with W = w_scale[n]·e4m3(wq[n, k]), exact."""
+    w = e4m3_decode(wq).astype(np.float64) * np.asarray(w_scale, np.float64)[:, None]
+    return forward(x, w, b, As, Bs, scales, seg_offsets, adapter_ids)
+
+
+def forward_fp8_quantized_x(x, wq, w_scale, b, As, Bs, scales, seg_offsets, adapter_ids) -> np.ndarray:
+    """The e4m3 kernel's arithmetic, exactly: the base product uses X quantised
+    per row (quantize_rows_e4m3), the LoRA term the unquantised X; fp64 sums
+    (the kernel's e4m3 products are exact in fp32, only the summation order
+    and the final bf16 rounding differ)."""
+    x = np.asarray(x, np.float64)
+    xq, xs = quantize_rows_e4m3(x.astype(np.float32))
+    base = (e4m3_decode(xq).astype(np.float64) @ e4m3_decode(wq).astype(np.float64).T)
+    base = base * xs.astype(np.float64)[:, None] * np.asarray(w_scale, np.float64)[None, :]
+    if b is not None:
+        base = base + np.asarray(b, np.float64)[None, :]
+    lora = forward(x, np.zeros((base.shape[1], x.shape[1])), None, As, Bs, scales, seg_offsets, adapter_ids)
+    return base + lora
+
+
 # ------------------------------------------------------------------ routing
 
 def row_adapters(seg_offsets: Sequence[int], adapter_ids: Sequence[int]) -> np.ndarray:

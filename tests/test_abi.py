@@ -118,3 +118,29 @@ def test_shrink_validation(lib, pkg):
     assert args(3, [8], 0x3000) == L.ERR_INVALID
     assert args(0, [12], 0x3000) == L.ERR_INVALID
     assert args(0, [8], 0) == L.ERR_INVALID
+
+
+def test_fp8_entry_points_validate_before_launch(lib, pkg):
+    L = pkg._lib
+    # quantize: K must be a multiple of 16 for the e4m3 rows, ld >= K, non-null scale
+    assert lib.mlora_quantize_rows_fp8(0x1000, 40, 4, 40, 0x2000, 48, 0x3000, None) == L.ERR_UNSUPPORTED
+    assert lib.mlora_quantize_rows_fp8(0x1000, 32, 4, 32, 0x2000, 16, 0x3000, None) == L.ERR_INVALID
+    assert lib.mlora_quantize_rows_fp8(0x1000, 32, 4, 32, 0x2000, 32, None, None) == L.ERR_INVALID
+    assert lib.mlora_quantize_rows_fp8(0x1000, 32, 0, 32, 0x2000, 32, None, None) == L.OK
+    assert lib.mlora_dequant_rows_fp8(0x1001, 32, 0x3000, 4, 32, 0x2000, 32, None) == L.ERR_UNSUPPORTED
+    assert lib.mlora_dequant_rows_fp8(0x1000, 32, None, 4, 32, 0x2000, 32, None) == L.ERR_INVALID
+
+    def fwd8(M=64, K=64, N=64, ldx=64, xs=0x6000, ws=0x7000, off=None, ids=None):
+        off = off if off is not None else [0, M]
+        ids = ids if ids is not None else [-1]
+        return lib.mlora_gemm_fwd_fp8(0x1000, ldx, xs, M, K, 0x2000, K, ws, N, None, 1, None, 0,
+                                      L.ptr_array([0x4000]), L.i32_array([8]), 1,
+                                      L.i64_array(off), L.i32_array(ids), len(ids), 0x3000, N, 0, None)
+    assert fwd8(K=40, ldx=48) == L.ERR_UNSUPPORTED       # K not a multiple of 16
+    assert fwd8(ldx=72) == L.ERR_UNSUPPORTED             # ld not a multiple of 16
+    assert fwd8(ldx=32) == L.ERR_INVALID                 # ld < K
+    assert fwd8(xs=None) == L.ERR_INVALID                # scales required
+    assert fwd8(ws=0x7004) == L.ERR_UNSUPPORTED          # w_scale 16-byte aligned
+    assert fwd8(K=0, ldx=0) == L.ERR_UNSUPPORTED         # an e4m3 contraction is required
+    assert fwd8(off=[0, 60]) == L.ERR_INVALID            # routing must cover M rows
+    assert fwd8(M=0, off=[0, 0]) == L.OK

@@ -1,0 +1,220 @@
+"""Quantised-base (e4m3) variant on the GPU vs the CPU oracle.
+
+Bit-exact: the per-row e4m3 quantisation (bytes and scales) and the dequantisation.
+Kernel arithmetic: the e4m3 GEMM vs ``forward_fp8_quantized_x`` (X quantised per
+row exactly as the kernel does, exact sums) within rel-L2 <= 2e-3, the bf16 bound.
+End to end: Y of MultiLoRAFP8Function vs the exact reference semantics with the
+e4m3 base (``forward_fp8_base``) within the fp8 tolerance 3e-2; dX, dA, dB (no
+quantised operand in their arithmetic) within 2e-3 of the kernel arithmetic and
+3e-2 of the exact reference.
+"""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import multilora_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+TOL = 2e-3
+TOL_FP8 = 3e-2
+
+
+def f64(t):
+    return t.detach().double().cpu().numpy()
+
+
+def u8(t):
+    return t.detach().view(torch.uint8).cpu().numpy()
+
+
+def _rows_with_features(M, K, seed):
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn(M, K, generator=g)
+    x *= torch.exp(torch.randn(M, 1, generator=g) * 3)       # row magnitudes over many binades
+    if M > 3:
+        x[1] = 0.0                                           # all-zero row
+        x[2] = torch.randn(K, generator=g) * 1e-3
+        x[2, 0] = 50.0                                       # one large value: the rest on the subnormal grid
+        x[3, : K // 2] = -0.0
+    return x.to(torch.bfloat16)
+
+
+@pytest.mark.parametrize("M,K", [(5, 16), (130, 48), (257, 1536), (64, 8960)])
+def test_quantize_rows_bit_exact(pkg, dev, M, K):
+    x = _rows_with_features(M, K, seed=M + K)
+    q, s = pkg.kernels.quantize_rows_fp8(x.to(dev))
+    torch.cuda.synchronize()
+    q_ref, s_ref = O.quantize_rows_e4m3(x.float().numpy())
+    assert q.dtype == torch.float8_e4m3fn and s.dtype == torch.float32
+    assert np.array_equal(s.cpu().numpy(), s_ref)
+    assert np.array_equal(u8(q), q_ref)
+
+
+def test_dequant_rows_bit_exact(pkg, dev):
+    g = np.random.default_rng(5)
+    codes = g.integers(0, 256, size=(96, 272)).astype(np.uint8)
+    codes[(codes & 0x7F) == 0x7F] = 0x7E                     # no NaN codes
+    codes[0, :256] = np.arange(256, dtype=np.uint8)
+    codes[0, 127], codes[0, 255] = 0x00, 0x80
+    scale = (np.exp(g.standard_normal(96)) * 0.01).astype(np.float32)
+    q = torch.from_numpy(codes).view(torch.float8_e4m3fn).to(dev)
+    y = pkg.kernels.dequant_rows_fp8(q, torch.from_numpy(scale).to(dev))
+    torch.cuda.synchronize()
+    want = O.bf16_round(O.dequant_rows_e4m3(codes, scale))
+    assert np.array_equal(y.float().cpu().numpy(), want)
+
+
+def _case(M, K, N, ranks, seed, bias=True):
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn(M, K, generator=g).to(torch.bfloat16)
+    w = (torch.randn(N, K, generator=g) / math.sqrt(K)).to(torch.bfloat16)
+    b = (torch.randn(N, generator=g) / math.sqrt(K)).to(torch.bfloat16) if bias else None
+    As = [((torch.rand(r, K, generator=g) * 2 - 1) / math.sqrt(K)).to(torch.bfloat16) for r in ranks]
+    Bs = [(torch.randn(N, r, generator=g) * 0.02).to(torch.bfloat16) for r in ranks]
+    dy = torch.randn(M, N, generator=g).to(torch.bfloat16)
+    return x, w, b, As, Bs, dy
+
+
+@pytest.mark.parametrize("bias", [True, False])
+@pytest.mark.parametrize("M,K,N,lengths,ids", [
+    (512, 256, 256, (256, 256), (0, 1)),
+    (1249, 272, 200, (77, 600, 1, 571), (1, -1, 0, 1)),
+    (300, 1536, 1536, (300,), (-1,)),
+])
+def test_gemm_fwd_fp8_kernel_arithmetic(pkg, dev, bias, M, K, N, lengths, ids):
+    x, w, b, As, Bs, _ = _case(M, K, N, (8, 24), seed=M + N, bias=bias)
+    routing = pkg.SegmentRouting.from_lengths(lengths, ids)
+    xd = x.to(dev)
+    wq, ws = pkg.kernels.quantize_rows_fp8(w.to(dev))
+    xq, xs = pkg.kernels.quantize_rows_fp8(xd)
+    scales = [1.0, 2.0]
+    A_ops = [a.to(dev) for a in As]
+    B_ops = [v.to(dev) for v in Bs]
+    h_rows, _ = pkg.kernels.shrink(xd, A_ops, 0, scales, routing, want_frag=False, width=24)
+    bd = None if b is None else b.to(dev)
+    y = pkg.kernels.gemm_fwd_fp8(xq, xs, wq, ws, bd, h_rows, B_ops, routing)
+    torch.cuda.synchronize()
+    off, ids_ = routing.seg_offsets, routing.adapter_ids
+    Af, Bf = [f64(a) for a in As], [f64(v) for v in Bs]
+    want = O.forward_fp8_quantized_x(f64(x), u8(wq), ws.cpu().numpy(), None if b is None else f64(b),
+                                     Af, Bf, scales, off, ids_)
+    assert O.rel_l2(f64(y), want) <= TOL
+    # routing is bit-exact: base-only rows equal a launch without any adapter
+    y0 = pkg.kernels.gemm_fwd_fp8(xq, xs, wq, ws, bd, None, [], pkg.SegmentRouting.single(M, -1))
+    torch.cuda.synchronize()
+    base_rows = O.row_adapters(off, ids_) < 0
+    assert torch.equal(y[torch.from_numpy(base_rows).to(dev)], y0[torch.from_numpy(base_rows).to(dev)])
+
+
+def _module_case(pkg, dev, M, K, N, ranks, lengths, ids, seed, scales):
+    x, w, b, As, Bs, dy = _case(M, K, N, ranks, seed)
+    wq, ws = pkg.kernels.quantize_rows_fp8(w.to(dev))
+    routing = pkg.SegmentRouting.from_lengths(lengths, ids)
+    xg = x.to(dev).requires_grad_(True)
+    Ag = [a.to(dev).float().requires_grad_(True) for a in As]
+    Bg = [v.to(dev).float().requires_grad_(True) for v in Bs]
+    y = pkg.multi_lora_linear_fp8(xg, wq, ws, b.to(dev), Ag, Bg, scales, routing)
+    y.backward(dy.to(dev))
+    torch.cuda.synchronize()
+    return (x, b, As, Bs, dy, u8(wq), ws.cpu().numpy(), routing), (y, xg.grad, [a.grad for a in Ag],
+                                                                  [v.grad for v in Bg])
+
+
+def test_fp8_module_fwd_bwd_vs_reference(pkg, dev):
+    scales = [1.0, 0.5, 2.0, 1.0]
+    (x, b, As, Bs, dy, wq, ws, routing), (y, dx, dAs, dBs) = _module_case(
+        pkg, dev, 777, 320, 272, (8, 16, 24, 8), (100, 0, 300, 77, 300), (2, 0, 1, -1, 3), 31, scales)
+    off, ids = routing.seg_offsets, routing.adapter_ids
+    Af, Bf = [f64(a) for a in As], [f64(v) for v in Bs]
+    y_exact = O.forward_fp8_base(f64(x), wq, ws, f64(b), Af, Bf, scales, off, ids)
+    y_kern = O.forward_fp8_quantized_x(f64(x), wq, ws, f64(b), Af, Bf, scales, off, ids)
+    assert O.rel_l2(f64(y), y_exact) <= TOL_FP8
+    assert O.rel_l2(f64(y), y_kern) <= TOL
+    w_exact = O.e4m3_decode(wq).astype(np.float64) * ws.astype(np.float64)[:, None]
+    w_bf16 = O.bf16_round(O.dequant_rows_e4m3(wq, ws)).astype(np.float64)
+    for w_ref, tol in ((w_exact, TOL_FP8), (w_bf16, TOL)):
+        dx_ref, dA_ref, dB_ref = O.backward(f64(x), w_ref, Af, Bf, scales, off, ids, f64(dy))
+        assert O.rel_l2(f64(dx), dx_ref) <= tol
+        for i in range(4):
+            assert O.rel_l2(f64(dAs[i]), dA_ref[i]) <= TOL
+            assert O.rel_l2(f64(dBs[i]), dB_ref[i]) <= TOL
+    assert dAs[0].dtype == torch.float32
+
+
+def test_module_quantize_base_fp8(pkg, dev):
+    """MultiLoRALinear.quantize_base_fp8(): forward under bf16 autocast uses the
+    e4m3 base; Y vs the exact reference with that e4m3 base, adapters train."""
+    torch.manual_seed(3)
+    base = torch.nn.Linear(256, 128).to(dev)
+    lin = pkg.MultiLoRALinear(base, ranks=[8, 16], alphas=[8.0, 32.0]).to(dev)
+    with torch.no_grad():
+        for bp in lin.lora_b:
+            bp.normal_(0, 0.02)
+    x = torch.randn(300, 256, device=dev)
+    routing = pkg.SegmentRouting.from_lengths((100, 200), (1, 0))
+    lin.quantize_base_fp8()
+    assert lin.base_wq.dtype == torch.float8_e4m3fn and lin.base_wscale.shape == (128,)
+    with torch.autocast("cuda", dtype=torch.bfloat16):
+        y8 = lin(x, routing)
+    y8.float().sum().backward()
+    torch.cuda.synchronize()
+    bf = lambda t: f64(t.to(torch.bfloat16))  # noqa: E731  (operands as the kernels see them)
+    want = O.forward_fp8_base(bf(x), u8(lin.base_wq), lin.base_wscale.cpu().numpy(), f64(base.bias),
+                              [bf(a) for a in lin.lora_a], [bf(v) for v in lin.lora_b], lin.scales,
+                              routing.seg_offsets, routing.adapter_ids)
+    assert O.rel_l2(f64(y8), want) <= TOL_FP8
+    assert all(p.grad is not None for p in lin.lora_a) and base.weight.grad is None
+
+
+def test_wan13b_fp8_full_shape(pkg, dev):
+    """Config 5 at full size (65520 tokens, 4 rank-64 adapters on seeded segments, q/k/v/o shape):
+    Y and dX on 512 sampled rows vs the oracle, adapter gradients vs torch fp32 on the GPU."""
+    from dmd_system_amd import workloads as W
+    cfg = W.CONFIGS["wan13b_fp8"]
+    K = N = cfg.hidden
+    x, w, b, As, Bs, dy = W.make_linear(cfg, K, N, dev, seed=cfg.seed)
+    wq, ws = pkg.kernels.quantize_rows_fp8(w)
+    routing = cfg.routing
+    n = len(cfg.ranks)
+    xg = x.clone().requires_grad_(True)
+    Ag = [a.clone().requires_grad_(True) for a in As]
+    Bg = [v.clone().requires_grad_(True) for v in Bs]
+    y = pkg.multi_lora_linear_fp8(xg, wq, ws, b, Ag, Bg, [cfg.scale] * n, routing)
+    y.backward(dy)
+    torch.cuda.synchronize()
+    rows = np.sort(np.random.default_rng(50).choice(cfg.tokens, 512, replace=False))
+    rows[0], rows[-1] = 0, cfg.tokens - 1
+    Af, Bf = [f64(a) for a in As], [f64(v) for v in Bs]
+    off, ids = routing.seg_offsets, routing.adapter_ids
+    loff, lids = _local_routing(rows, off, ids)
+    wq_np, ws_np = u8(wq), ws.cpu().numpy()
+    xs = f64(x[rows])
+    y_kern = O.forward_fp8_quantized_x(xs, wq_np, ws_np, f64(b), Af, Bf, [cfg.scale] * n, loff, lids)
+    y_exact = O.forward_fp8_base(xs, wq_np, ws_np, f64(b), Af, Bf, [cfg.scale] * n, loff, lids)
+    print("rel-L2 y vs kernel arithmetic %.2e, vs exact %.2e" % (O.rel_l2(f64(y[rows]), y_kern),
+                                                                  O.rel_l2(f64(y[rows]), y_exact)), flush=True)
+    assert O.rel_l2(f64(y[rows]), y_kern) <= TOL
+    assert O.rel_l2(f64(y[rows]), y_exact) <= TOL_FP8
+    w_bf16 = O.bf16_round(O.dequant_rows_e4m3(wq_np, ws_np)).astype(np.float64)
+    dx_ref = O.dx_rows(np.arange(len(rows)), w_bf16, Af, Bf, [cfg.scale] * n, loff, lids, f64(dy[rows]))
+    assert O.rel_l2(f64(xg.grad[rows]), dx_ref) <= TOL
+    for a, (lo, hi) in enumerate(zip(off, off[1:])):
+        xs_, dys = x[lo:hi].float(), dy[lo:hi].float()
+        h = xs_ @ As[a].float().T
+        assert O.rel_l2(f64(Bg[a].grad), f64(cfg.scale * dys.T @ h)) <= TOL
+        assert O.rel_l2(f64(Ag[a].grad), f64((cfg.scale * dys @ Bs[a].float()).T @ xs_)) <= TOL
+
+
+def _local_routing(rows, off, ids):
+    ad = O.row_adapters(off, ids)[rows]
+    loff, lids = [0], []
+    for i, a in enumerate(ad):
+        if not lids or lids[-1] != a:
+            if lids:
+                loff.append(i)
+            lids.append(int(a))
+    loff.append(len(ad))
+    return loff, lids

@@ -267,3 +267,91 @@ def test_fp32_update_and_livewan_variants_are_close_to_exact():
 def test_rel_l2_definition():
     assert O.rel_l2([3.0, 4.0], [3.0, 4.0]) == 0.0
     assert math.isclose(O.rel_l2([3.0, 4.0], [0.0, 5.0]), math.hypot(3, 1) / 5.0)
+
+
+# ------------------------------------------------------------------ e4m3 (quantised base)
+
+def _torch_e4m3_bytes(v):
+    return torch.from_numpy(np.asarray(v, np.float32)).to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+
+
+def _nearest_e4m3(v):
+    """Brute force: the finite positive code nearest to |v| (ties to the even code), with v's sign."""
+    codes = np.arange(0x7F, dtype=np.uint8)
+    vals = O.e4m3_decode(codes).astype(np.float64)
+    out = []
+    for x in np.asarray(v, np.float64):
+        d = np.abs(vals - abs(x))
+        best = np.flatnonzero(d == d.min())
+        c = int(best[0]) if len(best) == 1 else int(best[(codes[best] & 1) == 0][0])
+        out.append(c | (0x80 if math.copysign(1.0, x) < 0 else 0))
+    return np.array(out, dtype=np.uint8)
+
+
+def test_e4m3_decode_matches_torch_for_all_codes():
+    codes = np.arange(256, dtype=np.uint8)
+    got = O.e4m3_decode(codes)
+    want = torch.from_numpy(codes).view(torch.float8_e4m3fn).float().numpy()
+    assert np.array_equal(np.isnan(got), np.isnan(want))
+    assert np.array_equal(got[~np.isnan(got)], want[~np.isnan(want)])
+    assert O.e4m3_decode([0x7E])[0] == 448.0 and O.e4m3_decode([0x01])[0] == 2.0 ** -9
+    assert O.e4m3_decode([0x08])[0] == 2.0 ** -6 and O.e4m3_decode([0x38])[0] == 1.0
+
+
+def test_e4m3_encode_matches_torch_and_nearest_value():
+    rng = np.random.default_rng(21)
+    v = np.concatenate([rng.standard_normal(20000).astype(np.float32) * s for s in (1e-4, 1e-2, 1, 30, 150)])
+    v = v[np.abs(v) <= 448]
+    pos = O.e4m3_decode(np.arange(0, 0x7F, dtype=np.uint8)).astype(np.float64)
+    ties = ((pos[:-1] + pos[1:]) / 2).astype(np.float32)  # exact midpoints, incl. the subnormal grid
+    v = np.concatenate([v, ties, -ties, [0.0, -0.0, 448.0, -448.0, 2.0 ** -10, 2.0 ** -6]]).astype(np.float32)
+    got = O.e4m3_encode(v)
+    assert np.array_equal(got, _torch_e4m3_bytes(v))
+    sample = np.concatenate([v[::97], ties])
+    assert np.array_equal(O.e4m3_encode(sample), _nearest_e4m3(sample))
+
+
+def test_e4m3_encode_saturates_past_448():
+    v = np.array([448.5, 463.9, 464.0, 500.0, 1e6, -470.0, np.nan], np.float32)
+    assert list(O.e4m3_encode(v)) == [0x7E, 0x7E, 0x7E, 0x7E, 0x7E, 0xFE, 0x7E]
+
+
+def test_quantize_rows_e4m3_properties():
+    rng = np.random.default_rng(22)
+    x = O.bf16_round(rng.standard_normal((7, 96)) * np.array([1e-3, 1, 1, 50, 1, 1, 1])[:, None])
+    x[2] = 0.0
+    q, s = O.quantize_rows_e4m3(x)
+    assert q.dtype == np.uint8 and s.dtype == np.float32
+    assert s[2] == 1.0 and not q[2].any()
+    for m in (0, 1, 3, 4, 5, 6):
+        amax = np.abs(x[m]).max()
+        assert s[m] == np.float32(amax) / np.float32(448)
+        assert (q[m] & 0x7F).max() == 0x7E  # the absmax element lands on ±448
+        back = O.dequant_rows_e4m3(q[m:m + 1], s[m:m + 1])[0]
+        # half an e4m3 ulp: relative 2^-4 in the normal range, absolute 2^-10·s below it
+        tol = np.maximum(np.abs(x[m]) * 2.0 ** -4, s[m] * 2.0 ** -10) * (1 + 1e-6)
+        assert np.all(np.abs(back - x[m]) <= tol)
+
+
+def test_fp8_forward_variants_match_brute_force():
+    rng = np.random.default_rng(23)
+    x, w, b, As, Bs, off, ids = _case(rng, M=9, K=32, N=5, ranks=(2, 3), lengths=(3, 0, 2, 4), ids=(0, 1, -1, 1))
+    wq, ws = O.quantize_rows_e4m3(w)
+    scales = [0.5, 2.0]
+    W = np.array([[float(O.e4m3_decode([wq[n, k]])[0]) * float(ws[n]) for k in range(32)] for n in range(5)])
+    xq, xs = O.quantize_rows_e4m3(x)
+    Xq = np.array([[float(O.e4m3_decode([xq[m, k]])[0]) * float(xs[m]) for k in range(32)] for m in range(9)])
+    aid = O.row_adapters(off, ids)
+    want_base, want_q = np.zeros((9, 5)), np.zeros((9, 5))
+    for m in range(9):
+        for n in range(5):
+            lora = 0.0
+            if aid[m] >= 0:
+                A, B = As[aid[m]], Bs[aid[m]]
+                h = [sum(float(x[m, k]) * float(A[j, k]) for k in range(32)) for j in range(A.shape[0])]
+                lora = scales[aid[m]] * sum(h[j] * float(B[n, j]) for j in range(A.shape[0]))
+            want_base[m, n] = sum(float(x[m, k]) * W[n, k] for k in range(32)) + float(b[n]) + lora
+            want_q[m, n] = sum(Xq[m, k] * W[n, k] for k in range(32)) + float(b[n]) + lora
+    np.testing.assert_allclose(O.forward_fp8_base(x, wq, ws, b, As, Bs, scales, off, ids), want_base, rtol=1e-12, atol=1e-12)
+    np.testing.assert_allclose(O.forward_fp8_quantized_x(x, wq, ws, b, As, Bs, scales, off, ids), want_q,
+                               rtol=1e-12, atol=1e-12)
