@@ -11,7 +11,11 @@ of the dominant kernel measured with HIP events, the LoRA kernels' HBM GB/s,
 and a CPU baseline (the reference per-adapter path in fp32 torch on host
 cores, timed on a bounded sample of the same workload).
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--config wan13b]
+Other configurations (parity-test cases, measured on request): --config
+tiny | wan22_5b | flux | wan13b_fp8 (frozen base stored e4m3 with a per-output-
+channel scale: forward on the e4m3 MFMA), and --fwd-only for a forward-only step.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--config wan13b] [--fwd-only]
 """
 from __future__ import annotations
 
@@ -27,6 +31,7 @@ sys.path.insert(0, str(ROOT))
 
 HBM_PEAK_GBS = 8000.0          # MI355X HBM3E
 MFMA_BF16_PEAK_TFLOPS = 2500.0  # dense bf16
+MFMA_FP8_PEAK_TFLOPS = 5000.0   # dense fp8
 
 
 def parse():
@@ -35,6 +40,7 @@ def parse():
     p.add_argument("--steps", type=int, default=10)
     p.add_argument("--warmup", type=int, default=3)
     p.add_argument("--config", default="wan13b")
+    p.add_argument("--fwd-only", action="store_true", help="time forward passes only (no autograd)")
     p.add_argument("--kernel-reps", type=int, default=10)
     p.add_argument("--cpu-seconds", type=float, default=12.0, help="bounded CPU-baseline sample budget")
     p.add_argument("--no-cpu-baseline", action="store_true")
@@ -96,22 +102,35 @@ def main():
     routing = cfg.routing
     scales = [cfg.scale] * len(cfg.ranks)
 
-    # ---------------- inputs (resident in HBM)
+    fp8 = cfg.base_fp8
+    # ---------------- inputs (resident in HBM); an e4m3 base is stored quantised
     lins = []
     for i, (name, K, N) in enumerate(cfg.linears()):
         x, w, b, As, Bs, dy = workloads.make_linear(cfg, K, N, dev, seed=cfg.seed * 100 + i)
-        x.requires_grad_(True)
+        x.requires_grad_(not args.fwd_only)
         for t in As + Bs:
-            t.requires_grad_(True)
-        lins.append(dict(name=name, K=K, N=N, x=x, w=w, b=b, As=As, Bs=Bs, dy=dy))
+            t.requires_grad_(not args.fwd_only)
+        L = dict(name=name, K=K, N=N, x=x, w=w, b=b, As=As, Bs=Bs, dy=dy)
+        if fp8:
+            L["wq"], L["ws"] = kernels.quantize_rows_fp8(w)
+        lins.append(L)
     torch.cuda.synchronize()
 
+    def forward(L):
+        if fp8:
+            return pkg.multi_lora_linear_fp8(L["x"], L["wq"], L["ws"], L["b"], L["As"], L["Bs"], scales, routing)
+        return pkg.multi_lora_linear(L["x"], L["w"], L["b"], L["As"], L["Bs"], scales, routing)
+
     def step():
+        if args.fwd_only:
+            with torch.no_grad():
+                for L in lins:
+                    forward(L)
+            return
         for L in lins:
             for t in [L["x"], *L["As"], *L["Bs"]]:
                 t.grad = None
-            y = pkg.multi_lora_linear(L["x"], L["w"], L["b"], L["As"], L["Bs"], scales, routing)
-            y.backward(L["dy"])
+            forward(L).backward(L["dy"])
 
     for _ in range(args.warmup):
         step()
@@ -126,7 +145,8 @@ def main():
     wall = time.perf_counter() - t0
     gpu_ms = ev0.elapsed_time(ev1)
     ms_per_step = max(gpu_ms, wall * 1e3) / args.steps
-    flops_step = sum(cfg.flops_fwd_bwd(L["K"], L["N"]) for L in lins)
+    flops_fn = cfg.flops_fwd if args.fwd_only else cfg.flops_fwd_bwd
+    flops_step = sum(flops_fn(L["K"], L["N"]) for L in lins)
     tflops = flops_step / (ms_per_step * 1e-3) / 1e12
     print(f"# step {ms_per_step:.3f} ms, {tflops:.1f} TFLOP/s", file=sys.stderr, flush=True)
 
@@ -148,8 +168,10 @@ def main():
     from dmd_system_amd.function import _as_operand
     seg = list(zip(cfg.seg_lengths, cfg.seg_adapters))
     R = kernels.padded_rank(cfg.ranks)
-    fam = {k: {"time": 0.0, "flops": 0, "bytes": 0, "launches": 0}
-           for k in ("gemm_fwd", "gemm_dx", "shrink_x", "shrink_dy", "seg_outer_dB", "seg_outer_dA")}
+    fams = ["gemm_fwd", "gemm_dx", "shrink_x", "shrink_dy", "seg_outer_dB", "seg_outer_dA"]
+    if fp8:
+        fams += ["quantize_x", "dequant_w"]
+    fam = {k: {"time": 0.0, "flops": 0, "bytes": 0, "launches": 0} for k in fams}
     with torch.no_grad():
         for L in lins:
             M, K, N = cfg.tokens, L["K"], L["N"]
@@ -176,6 +198,12 @@ def main():
                                                            [torch.bfloat16] * len(cfg.ranks)),
                                  2 * lora_mr * K, M * K * 2 + lora_mr * 4 + r_sum * K * 2),
             }
+            if fp8:
+                xq, xs = kernels.quantize_rows_fp8(x)
+                runs["gemm_fwd"] = (lambda: kernels.gemm_fwd_fp8(xq, xs, L["wq"], L["ws"], L["b"], h_rows, B_ops,
+                                                                 routing), 2 * M * K * N + 2 * lora_mr * N, 0)
+                runs["quantize_x"] = (lambda: kernels.quantize_rows_fp8(x), 0, M * K * 3 + M * 4)
+                runs["dequant_w"] = (lambda: kernels.dequant_rows_fp8(L["wq"], L["ws"]), 0, N * K * 3 + N * 4)
             for k, (fn, fl, by) in runs.items():
                 t = timed(fn)
                 fam[k]["time"] += t
@@ -191,13 +219,17 @@ def main():
                    "gbs": round(v["bytes"] / v["time"] / 1e9, 1) if v["bytes"] else None}
     gem = fam["gemm_fwd"]
     gem_ach = gem["flops"] / gem["time"] / 1e12
-    roofline = {"kernel": "gemm_kernel NT (base GEMM + fused LoRA expand), avg over the 6 block linears",
-                "bound": "mfma", "achieved": round(gem_ach, 1), "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
-                "frac": round(gem_ach / MFMA_BF16_PEAK_TFLOPS, 4), "traffic": recorded_traffic(),
+    gem_peak = MFMA_FP8_PEAK_TFLOPS if fp8 else MFMA_BF16_PEAK_TFLOPS
+    roofline = {"kernel": ("gemm_kernel NT e4m3 base (fp8 MFMA) + fused dequantise and bf16 LoRA expand"
+                           if fp8 else "gemm_kernel NT (base GEMM + fused LoRA expand)")
+                + ", avg over the 6 block linears",
+                "bound": "mfma", "achieved": round(gem_ach, 1), "peak": gem_peak, "unit": "TFLOP/s",
+                "frac": round(gem_ach / gem_peak, 4),
+                "traffic": recorded_traffic() if cfg.name == "wan13b" else None,
                 "avg_launch_us": round(gem["time"] / gem["launches"] * 1e6, 2),
                 "flops_per_launch": gem["flops"] // gem["launches"]}
     lora = {}
-    for k in ("shrink_x", "shrink_dy", "seg_outer_dB", "seg_outer_dA"):
+    for k in ("shrink_x", "shrink_dy", "seg_outer_dB", "seg_outer_dA") + (("quantize_x", "dequant_w") if fp8 else ()):
         v = fam[k]
         gbs = v["bytes"] / v["time"] / 1e9
         lora[k] = {"achieved_gbs": round(gbs, 1), "frac_hbm": round(gbs / HBM_PEAK_GBS, 4),
@@ -214,10 +246,12 @@ def main():
     # ---------------- CPU baseline: reference per-adapter path, fp32 torch, bounded sample
     cpu = None
     if not args.no_cpu_baseline:
-        cpu = cpu_baseline(cfg, args.cpu_seconds)
+        cpu = cpu_baseline(cfg, args.cpu_seconds, args.fwd_only)
 
+    pass_name = "fwd" if args.fwd_only else "fwd+bwd"
+    shape_name = "Wan-1.3B shape" if cfg.name == "wan13b" else f"{cfg.name} shape"
     out = {
-        "metric": "multi-LoRA linear fwd+bwd TFLOP/s at Wan-1.3B shape",
+        "metric": f"multi-LoRA linear {pass_name} TFLOP/s at {shape_name}",
         "value": round(tflops, 2),
         "unit": "TFLOP/s",
         "n_gpus": 1,
@@ -227,13 +261,14 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "bf16",
+        "dtype": ("e4m3 base forward (fp32 accumulate), bf16 LoRA and backward" if fp8 else "bf16")
+        + ("" if cfg.dtype == "bf16" else f" (config specifies {cfg.dtype}; computed in bf16)"),
         "data": "synthetic (seeded N(0,1) activations, N(0,1/in) frozen base, Kaiming-uniform A, N(0,0.02) B)",
-        "config": {"workload": f"{cfg.name}: fwd+bwd of the 6 DiT block linears "
+        "config": {"workload": f"{cfg.name}: {pass_name} of the 6 DiT block linears "
                                f"(q,k,v,o {cfg.hidden}->{cfg.hidden}; ffn {cfg.hidden}->{cfg.ffn}->{cfg.hidden}), "
                                f"{cfg.tokens} tokens in segments {list(cfg.seg_lengths)}, ranks {list(cfg.ranks)}, "
-                               f"scale {cfg.scale}, bias on",
-                   "tokens": cfg.tokens, "flops_per_step": flops_step, "pct_mfma_peak": round(
+                               f"scale {cfg.scale}, bias on" + (", frozen base e4m3 + per-channel scale" if fp8 else ""),
+                   "tokens": cfg.tokens, "flops_per_step": flops_step, "pct_bf16_mfma_peak": round(
                        tflops / MFMA_BF16_PEAK_TFLOPS * 100, 2)},
         "roofline": roofline,
         "cpu_baseline": cpu,
@@ -246,13 +281,14 @@ def main():
     print(json.dumps(out), flush=True)
 
 
-def cpu_baseline(cfg, budget_s: float):
-    """Reference per-adapter path (training/low_rank.py:26-28 per segment + autograd) in fp32 on host cores."""
+def cpu_baseline(cfg, budget_s: float, fwd_only: bool = False):
+    """Reference per-adapter path (training/low_rank.py:26-28 per segment + autograd) in fp32 on host cores
+    (an e4m3 base is evaluated as its fp32 dequantisation: the reference has no fp8 path)."""
     import torch
     from oracle import torch_reference as TR
     from dmd_system_amd import workloads
 
-    rows_per_seg = 1024
+    rows_per_seg = max(128, 2048 // len(cfg.seg_lengths))
     sample = workloads.LoraConfig(
         name="cpu-sample", tokens=rows_per_seg * len(cfg.seg_lengths), hidden=cfg.hidden, ffn=cfg.ffn,
         ranks=cfg.ranks, seg_lengths=(rows_per_seg,) * len(cfg.seg_lengths), seg_adapters=cfg.seg_adapters,
@@ -268,7 +304,11 @@ def cpu_baseline(cfg, budget_s: float):
 
     def one_block():
         for K, N, x, w, b, As, Bs, dy in lin:
-            TR.per_adapter_step(x, w, b, As, Bs, scales, off, ids, dy)
+            if fwd_only:
+                with torch.no_grad():
+                    TR.per_adapter_forward(x, w, b, As, Bs, scales, off, ids)
+            else:
+                TR.per_adapter_step(x, w, b, As, Bs, scales, off, ids, dy)
 
     one_block()  # warmup
     t0 = time.perf_counter()
@@ -279,10 +319,10 @@ def cpu_baseline(cfg, budget_s: float):
         el = time.perf_counter() - t0
         if el >= budget_s or reps >= 50:
             break
-    flops = sum(sample.flops_fwd_bwd(K, N) for _, K, N in sample.linears())
+    flops = sum((sample.flops_fwd if fwd_only else sample.flops_fwd_bwd)(K, N) for _, K, N in sample.linears())
     return {"value": round(flops * reps / el / 1e12, 4), "unit": "TFLOP/s", "cores": torch.get_num_threads(),
             "kind": "port",
-            "sample": f"{reps} x fwd+bwd of the 6 block linears at {sample.tokens} tokens "
+            "sample": f"{reps} x {'fwd' if fwd_only else 'fwd+bwd'} of the 6 block linears at {sample.tokens} tokens "
                       f"({rows_per_seg} per segment), fp32 torch per-adapter path, {el:.1f} s; "
                       f"host os.cpu_count()={os.cpu_count()}"}
 

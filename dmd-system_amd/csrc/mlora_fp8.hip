@@ -5,6 +5,8 @@
 //                             (activations X before the fp8 base GEMM)
 //   mlora_dequant_rows_fp8  : e4m3 rows times a per-row fp32 scale back to bf16
 //                             (the frozen base W for the bf16 dX GEMM)
+//   mlora_div_rows_bf16     : bf16 rows divided by a per-row fp32 value
+//                             (lora_b / w_scale for the e4m3 forward)
 //
 // Quantisation of row m: amax = max_k |x[m,k]|; scale[m] = amax / 448 and
 // q = e4m3_rne(x * (448 / amax)) (both divisions IEEE fp32; an all-zero row
@@ -109,6 +111,30 @@ __global__ __launch_bounds__(256) void dequant_rows_kernel(const DequantArgs a) 
   }
 }
 
+struct DivArgs {
+  const uint16_t *x;
+  const float *div;
+  uint16_t *y;
+  int64_t ldx, ldy;
+  int32_t M, K;
+};
+
+__global__ __launch_bounds__(256) void div_rows_kernel(const DivArgs a) {
+  const int lane = threadIdx.x & 63;
+  const int m = blockIdx.x * 4 + wave_id();
+  if (m >= a.M) return;
+  const float d = a.div[m];
+  const uint16_t *xrow = a.x + (int64_t)m * a.ldx;
+  uint16_t *yrow = a.y + (int64_t)m * a.ldy;
+  for (int k = 8 * lane; k < a.K; k += 512) {
+    const u32x4 v = *(const MLORA_GLOBAL u32x4 *)(xrow + k);
+    uint32_t o[4];
+#pragma unroll
+    for (int w = 0; w < 4; ++w) o[w] = pack2_bf16(bf16_to_f32(v[w] & 0xffff) / d, bf16_to_f32(v[w] >> 16) / d);
+    *(MLORA_GLOBAL u32x4 *)(yrow + k) = u32x4{o[0], o[1], o[2], o[3]};
+  }
+}
+
 }  // namespace mlora
 
 using namespace mlora;
@@ -140,5 +166,20 @@ extern "C" int mlora_dequant_rows_fp8(const void *q, int64_t ldq, const float *s
   DequantArgs a{static_cast<const uint8_t *>(q), scale, static_cast<uint16_t *>(y), ldq, ldy, (int32_t)M, (int32_t)K};
   hipLaunchKernelGGL(dequant_rows_kernel, dim3((unsigned)((M + 3) / 4)), dim3(256), 0,
                      static_cast<hipStream_t>(stream), a);
+  return launch_status();
+}
+
+extern "C" int mlora_div_rows_bf16(const void *x, int64_t ldx, const float *div, int64_t M, int64_t K, void *y,
+                                   int64_t ldy, void *stream) {
+  if (M < 0 || K < 0) return MLORA_ERR_INVALID;
+  if (M > INT32_MAX - 4 || K > INT32_MAX / 2) return MLORA_ERR_LIMIT;
+  int st = check_bf16_matrix(x, ldx, M, K);
+  if (st) return st;
+  if ((st = check_bf16_matrix(y, ldy, M, K))) return st;
+  if (M == 0 || K == 0) return MLORA_OK;
+  if (div == nullptr) return MLORA_ERR_INVALID;
+  DivArgs a{static_cast<const uint16_t *>(x), div, static_cast<uint16_t *>(y), ldx, ldy, (int32_t)M, (int32_t)K};
+  hipLaunchKernelGGL(div_rows_kernel, dim3((unsigned)((M + 3) / 4)), dim3(256), 0, static_cast<hipStream_t>(stream),
+                     a);
   return launch_status();
 }

@@ -369,9 +369,9 @@ __device__ __forceinline__ bool next_lora_source(const GemmArgs &args, bool nn, 
 // (a few scalars and two offsets); the LDS stages and the MFMA code are shared,
 // so the accumulators stay in place. Tiles past a source's contraction length
 // mask their chunks.
-template <class C, class Dequant>
+template <class C>
 __device__ __forceinline__ void contract_tile(f32x16 (&acc)[C::TM][C::TN], const GemmArgs &args, MLORA_LDS char *lds,
-                                              const FragAddr<C> &fa, int m0, int n0, int tid, const Dequant &dequant) {
+                                              const FragAddr<C> &fa, int m0, int n0, int tid) {
   const int wave = wave_id(), lane = tid & 63;
   const int row_end = min(m0 + C::BM, args.M);
   int seg = args.E != nullptr ? seg_of_row(args.seg, m0) : args.seg.n;
@@ -417,8 +417,8 @@ __device__ __forceinline__ void contract_tile(f32x16 (&acc)[C::TM][C::TN], const
   using E4 = std::true_type;
   using B16 = std::false_type;
   if constexpr (C::F8) {
-    // the e4m3 main contraction (at least one tile), then one dequantize, then
-    // the bf16 LoRA tiles starting from whichever stage holds the next one
+    // the e4m3 main contraction (at least one tile), then the bf16 LoRA tiles
+    // (operands pre-divided by the scales) from whichever stage holds the next one
     bool more;
     int st;
     while (true) {
@@ -429,7 +429,6 @@ __device__ __forceinline__ void contract_tile(f32x16 (&acc)[C::TM][C::TN], const
       st = 0;
       if (!more || src.esz != 1) break;
     }
-    dequant(acc);
     if (!more) return;
     if (st == 1 && !step(S1{}, B16{})) return;
   }
@@ -498,44 +497,20 @@ __global__ __launch_bounds__(C::THREADS) void gemm_kernel(const GemmArgs args) {
 #pragma unroll
         for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
   }
-  // fp8: after the e4m3 contraction, acc = acc * psc[m] * qsc[n] + bias[n]
-  // (then the bf16 LoRA k-tiles accumulate on top)
-  auto dequant = [&](f32x16 (&a)[C::TM][C::TN]) {
-    float ps[C::TM];
-#pragma unroll
-    for (int i = 0; i < C::TM; ++i) {
-      const int m = m0 + wm0 + 32 * i + (lane & 31);
-      ps[i] = m < args.M ? args.psc[m] : 0.f;
-    }
-#pragma unroll
-    for (int j = 0; j < C::TN; ++j)
-#pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const int n = n0 + wn0 + 32 * j + 8 * g + 4 * (lane >> 5);
-        float v[4], qs[4] = {0.f, 0.f, 0.f, 0.f};
-        bias_of(n, v);
-        if (n < args.Ncols) {
-          const f32x4 q = *(const MLORA_GLOBAL f32x4 *)(args.qsc + n);
-          qs[0] = q[0]; qs[1] = q[1]; qs[2] = q[2]; qs[3] = q[3];
-        }
-#pragma unroll
-        for (int i = 0; i < C::TM; ++i)
-#pragma unroll
-          for (int e = 0; e < 4; ++e) a[i][j][4 * g + e] = a[i][j][4 * g + e] * (ps[i] * qs[e]) + v[e];
-      }
-  };
   FragAddr<C> fa;
   fa.init(wm0, wn0, lane);
 
-  contract_tile<C>(acc, args, lds, fa, m0, n0, tid, dequant);
+  contract_tile<C>(acc, args, lds, fa, m0, n0, tid);
 
-  // epilogue: (+ Y), round to bf16, 8-byte stores of 4 consecutive n
+  // epilogue: (fp8: scale and bias), (+ Y), round to bf16, 8-byte stores of 4 consecutive n
   const int rows_here = min(C::BM, args.M - m0);
   const int64_t ldy_b = args.ldy * 2;
   const __amdgpu_buffer_rsrc_t ry = make_rsrc(args.Y + (int64_t)m0 * args.ldy, rows_here * ldy_b);
 #pragma unroll
   for (int i = 0; i < C::TM; ++i) {
     const int ml = wm0 + 32 * i + (lane & 31);
+    float ps = 1.f;
+    if constexpr (C::F8) ps = m0 + ml < args.M ? args.psc[m0 + ml] : 0.f;
 #pragma unroll
     for (int j = 0; j < C::TN; ++j) {
 #pragma unroll
@@ -544,6 +519,17 @@ __global__ __launch_bounds__(C::THREADS) void gemm_kernel(const GemmArgs args) {
         float v[4];
 #pragma unroll
         for (int e = 0; e < 4; ++e) v[e] = acc[i][j][4 * g + e];
+        if constexpr (C::F8) {
+          // acc = Σ xq·wq + Σ (h/x_scale)·(B/w_scale): one scaling restores both, then the bias
+          float b[4], qs[4] = {0.f, 0.f, 0.f, 0.f};
+          bias_of(n, b);
+          if (n < args.Ncols) {
+            const f32x4 q = *(const MLORA_GLOBAL f32x4 *)(args.qsc + n);
+            qs[0] = q[0]; qs[1] = q[1]; qs[2] = q[2]; qs[3] = q[3];
+          }
+#pragma unroll
+          for (int e = 0; e < 4; ++e) v[e] = v[e] * (ps * qs[e]) + b[e];
+        }
         // rows past M / columns past Ncols fall outside ry or are dropped
         const int32_t off = (ml < rows_here && n < args.Ncols) ? (int32_t)(ml * ldy_b + n * 2) : kOOB;
         if (args.accumulate && off != kOOB) {
@@ -685,7 +671,7 @@ extern "C" int mlora_gemm_fwd_fp8(const void *xq, int64_t ldx, const float *x_sc
   if ((st = check_bf16_matrix(y, ldy, M, N))) return st;
   if (M == 0 || N == 0) return MLORA_OK;
   if (y == nullptr || xq == nullptr || wq == nullptr || x_scale == nullptr || w_scale == nullptr) return MLORA_ERR_INVALID;
-  if (K == 0) return MLORA_ERR_UNSUPPORTED;  // the dequantize step follows the first e4m3 k-tile
+  if (K == 0) return MLORA_ERR_UNSUPPORTED;  // the contraction loop starts with an e4m3 k-tile
   if (!aligned16(w_scale)) return MLORA_ERR_UNSUPPORTED;
   if (bias != nullptr) {
     if (bias_dtype != MLORA_F32 && bias_dtype != MLORA_BF16) return MLORA_ERR_UNSUPPORTED;

@@ -52,6 +52,7 @@ struct ShrinkArgs {
   const uint16_t *P;
   uint16_t *Hr;  // bf16 [M, ldh]
   u32x4 *Hf;     // fragments (see above) or null
+  const float *row_div;  // per-row divisors of Hr, or null
   int64_t ldp, ldh;
   int32_t M, K;
   int32_t op_layout;  // 0: [r, K]; 1: [K, r]
@@ -184,7 +185,10 @@ __global__ __launch_bounds__(256) void shrink_kernel(const ShrinkArgs args) {
 #pragma unroll
     for (int v = 0; v < 16; ++v) {
       const int row = wrow + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
-      if (row < mend) hr[(int64_t)row * args.ldh + col] = f32_to_bf16_rne(acc[j][v] * scale);
+      if (row < mend) {
+        const float h = acc[j][v] * scale;
+        hr[(int64_t)row * args.ldh + col] = f32_to_bf16_rne(args.row_div ? h / args.row_div[row] : h);
+      }
     }
   }
   // ---- epilogue 2: hi/lo fragments, re-laid out through LDS one 32-wide j tile at a time
@@ -486,7 +490,7 @@ extern "C" int64_t mlora_frag_bytes(int64_t M, int32_t frag_jtiles, const int64_
 extern "C" int mlora_shrink(const void *p, int64_t ldp, int64_t M, int64_t K, const void *const *op_ptrs, int op_layout,
                             const int32_t *ranks, const float *scales, int32_t n_adapters, const int64_t *seg_offsets,
                             const int32_t *adapter_ids, int32_t n_segments, void *h_rows, int64_t ldh, void *h_frag,
-                            int32_t frag_jtiles, void *stream) {
+                            int32_t frag_jtiles, const float *row_div, void *stream) {
   ShrinkArgs a{};
   int st = build_segtable(a.seg, M, seg_offsets, adapter_ids, n_segments, n_adapters);
   if (st) return st;
@@ -506,6 +510,7 @@ extern "C" int mlora_shrink(const void *p, int64_t ldp, int64_t M, int64_t K, co
   a.P = static_cast<const uint16_t *>(p);
   a.Hr = static_cast<uint16_t *>(h_rows);
   a.Hf = static_cast<u32x4 *>(h_frag);
+  a.row_div = row_div;
   a.ldp = ldp;
   a.ldh = ldh;
   a.M = (int32_t)M;

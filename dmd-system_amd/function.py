@@ -36,7 +36,7 @@ def _as_operand(t: torch.Tensor, rows_pad: int | None = None, cols_pad: int | No
     return t
 
 
-def _prepare(ctx, x, N: int, ab, scales, routing: SegmentRouting, grad0: int):
+def _prepare(ctx, x, N: int, ab, scales, routing: SegmentRouting, grad0: int, row_div=None):
     """Validate adapters, build padded bf16 operands and run the forward shrink.
 
     grad0 is the index of the first lora_a among the autograd inputs.
@@ -60,7 +60,8 @@ def _prepare(ctx, x, N: int, ab, scales, routing: SegmentRouting, grad0: int):
     need_b_grad = any(ctx.needs_input_grad[grad0 + n + i] for i in range(n))
     h_rows, h_frag = (None, None)
     if width > 0:
-        h_rows, h_frag = kernels.shrink(x, A_ops, 0, scales, routing, want_frag=need_b_grad, width=width)
+        h_rows, h_frag = kernels.shrink(x, A_ops, 0, scales, routing, want_frag=need_b_grad, width=width,
+                                        row_div=row_div)
     ctx.routing, ctx.scales, ctx.n, ctx.grad0 = routing, tuple(float(s) for s in scales), n, grad0
     ctx.ranks, ctx.pranks, ctx.width = ranks, pranks, width
     ctx.a_dtypes = [a.dtype for a in As]
@@ -135,9 +136,12 @@ class MultiLoRAFP8Function(torch.autograd.Function):
     def forward(ctx, x, wq, w_scale, bias, routing: SegmentRouting, scales: Sequence[float], *ab):
         if any(ctx.needs_input_grad[1:4]):
             raise RuntimeError("multi-LoRA: the base weight, its scale and the bias are frozen")
-        A_ops, B_ops, h_rows = _prepare(ctx, x, wq.shape[0], ab, scales, routing, grad0=6)
         xq, x_scale = kernels.quantize_rows_fp8(x)
-        y = kernels.gemm_fwd_fp8(xq, x_scale, wq, w_scale, bias, h_rows, B_ops, routing)
+        # the LoRA operands enter the e4m3 accumulators divided by the scales the
+        # epilogue multiplies back: h / x_scale[m] (shrink) and lora_b / w_scale[n]
+        A_ops, B_ops, h_rows = _prepare(ctx, x, wq.shape[0], ab, scales, routing, grad0=6, row_div=x_scale)
+        B_div = [kernels.div_rows_bf16(b, w_scale) for b in B_ops]
+        y = kernels.gemm_fwd_fp8(xq, x_scale, wq, w_scale, bias, h_rows, B_div, routing)
         ctx.save_for_backward(x, wq, w_scale, *A_ops, *B_ops)
         return y
 

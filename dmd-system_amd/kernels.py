@@ -53,8 +53,12 @@ def frag_jtiles(width: int) -> int:
 
 
 def shrink(p: torch.Tensor, ops: Sequence[torch.Tensor], op_layout: int, scales: Sequence[float],
-           routing: SegmentRouting, want_frag: bool, width: int) -> tuple[torch.Tensor, list | None]:
-    """h = s·P·Op_aᵀ per segment -> (h_rows bf16 [M, width], per-call-group hi/lo fragments or None)."""
+           routing: SegmentRouting, want_frag: bool, width: int,
+           row_div: torch.Tensor | None = None) -> tuple[torch.Tensor, list | None]:
+    """h = s·P·Op_aᵀ per segment -> (h_rows bf16 [M, width], per-call-group hi/lo fragments or None).
+
+    row_div [M] fp32 (optional) divides the rows of h_rows only (the e4m3 forward's activation scales).
+    """
     M, K = p.shape
     _check_rows("P", p)
     ranks = [int(o.shape[0] if op_layout == 0 else o.shape[1]) for o in ops]
@@ -62,6 +66,8 @@ def shrink(p: torch.Tensor, ops: Sequence[torch.Tensor], op_layout: int, scales:
         _check_rows("adapter operand", o)
         _require(o.is_contiguous(), "adapter operands must be contiguous")
         _require(o.shape == ((r, K) if op_layout == 0 else (K, r)), "adapter operand shape")
+    if row_div is not None:
+        _check_scale("row_div", row_div, M)
     h_rows = torch.empty((M, width), dtype=torch.bfloat16, device=p.device)
     lib = _lib.load()
     ptrs, rk, sc = _lib.ptr_array([_ptr(o) for o in ops]), _lib.i32_array(ranks), _lib.f32_array(scales)
@@ -80,7 +86,8 @@ def shrink(p: torch.Tensor, ops: Sequence[torch.Tensor], op_layout: int, scales:
             continue
         _lib.check("mlora_shrink", lib.mlora_shrink(
             p[r0:r1].data_ptr(), p.stride(0), r1 - r0, K, ptrs, op_layout, rk, sc, len(ops),
-            o, i, n, h_rows[r0:r1].data_ptr(), width, _ptr(frag), jt, stream))
+            o, i, n, h_rows[r0:r1].data_ptr(), width, _ptr(frag), jt,
+            None if row_div is None else row_div[r0:r1].data_ptr(), stream))
     return h_rows, frags
 
 
@@ -227,10 +234,26 @@ def dequant_rows_fp8(q: torch.Tensor, scale: torch.Tensor) -> torch.Tensor:
     return y
 
 
+def div_rows_bf16(x: torch.Tensor, div: torch.Tensor) -> torch.Tensor:
+    """bf16(x[m, k] / div[m])."""
+    M, K = x.shape
+    _check_rows("x", x, K)
+    _check_scale("div", div, M)
+    y = torch.empty((M, K), dtype=torch.bfloat16, device=x.device)
+    lib = _lib.load()
+    _lib.check("mlora_div_rows_bf16", lib.mlora_div_rows_bf16(
+        x.data_ptr(), x.stride(0), div.data_ptr(), M, K, y.data_ptr(), y.stride(0), _stream(x)))
+    return y
+
+
 def gemm_fwd_fp8(xq: torch.Tensor, x_scale: torch.Tensor, wq: torch.Tensor, w_scale: torch.Tensor,
                  bias: torch.Tensor | None, h_rows: torch.Tensor | None, bs: Sequence[torch.Tensor],
                  routing: SegmentRouting) -> torch.Tensor:
-    """Y = (Xq·Wqᵀ)·x_scale[m]·w_scale[n] + bias + per-segment h_rows·B_aᵀ, bf16 out (e4m3 MFMA base)."""
+    """Y = (Xq·Wqᵀ + per-segment h_rows·B_aᵀ)·x_scale[m]·w_scale[n] + bias, bf16 out (e4m3 MFMA base).
+
+    h_rows and bs are the LoRA operands divided by the scales: shrink(..., row_div=x_scale) and
+    div_rows_bf16(lora_b, w_scale).
+    """
     M, K = xq.shape
     N = wq.shape[0]
     _check_fp8_rows("Xq", xq, K)

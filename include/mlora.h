@@ -43,7 +43,7 @@
 extern "C" {
 #endif
 
-#define MLORA_ABI_VERSION 1
+#define MLORA_ABI_VERSION 2
 
 /* Limits of one call (kernel-argument tables). Callers with more segments
  * split the rows into several calls; the Python host layer does this. */
@@ -94,6 +94,9 @@ const char *mlora_status_string(int status);
  * op_layout 0: Op_a stored [r_a, K] (K contiguous, e.g. lora_a, low_rank.py:21)
  * op_layout 1: Op_a stored [K, r_a] (r contiguous, e.g. lora_b [N, r] for the
  *              backward g = s·dY·B, low_rank.py:22)
+ * row_div (may be NULL): per-row divisors [M]; h_rows (not h_frag) then holds
+ *           h[m, j] / row_div[m]. The e4m3 forward passes its activation scales
+ *           here (see mlora_gemm_fwd_fp8).
  * Rows of base-only segments are not written.
  * Reference: F.linear(value, lora_a) in low_rank.py:28 (forward shrink) and the
  * autograd LinearBackward of F.linear(h, lora_b) (dH = g·B, as written out in
@@ -103,6 +106,7 @@ int mlora_shrink(const void *p, int64_t ldp, int64_t M, int64_t K,
                  const int32_t *ranks, const float *scales, int32_t n_adapters,
                  const int64_t *seg_offsets, const int32_t *adapter_ids, int32_t n_segments,
                  void *h_rows, int64_t ldh, void *h_frag, int32_t frag_jtiles,
+                 const float *row_div,
                  void *stream);
 /* Bytes of the h_frag buffer for this routing and frag_jtiles (< 0: status). */
 int64_t mlora_frag_bytes(int64_t M, int32_t frag_jtiles, const int64_t *seg_offsets,
@@ -179,11 +183,19 @@ int mlora_dequant_rows_fp8(const void *q, int64_t ldq, const float *scale, int64
                            void *y, int64_t ldy,
                            void *stream);
 
+/* y[m, k] = bf16( x[m,k] / div[m] ) for a bf16 matrix (the lora_b operand of the e4m3 forward). */
+int mlora_div_rows_bf16(const void *x, int64_t ldx, const float *div, int64_t M, int64_t K,
+                        void *y, int64_t ldy,
+                        void *stream);
+
 /* mlora_gemm_fwd with an e4m3 base contraction (v_mfma_scale_f32_32x32x64_f8f6f4):
- *   Y[m, n] = bf16( x_scale[m]·w_scale[n]·Σ_k xq[m,k]·wq[n,k] + bias[n] + Σ_j h_rows[m,j]·B_a[n,j] )
+ *   Y[m, n] = bf16( x_scale[m]·w_scale[n]·( Σ_k xq[m,k]·wq[n,k] + Σ_j h_rows[m,j]·B_a[n,j] ) + bias[n] )
  * xq [M, K] and wq [N, K] e4m3 bytes (mlora_quantize_rows_fp8 layout, K >= 16); x_scale [M],
- * w_scale [N] fp32 (w_scale 16-byte aligned). The LoRA term stays bf16 (h_rows, b_ptrs as in
- * mlora_gemm_fwd). Reference semantics: low_rank.py:28 with base weight w_scale[n]·wq[n,k]. */
+ * w_scale [N] fp32 (w_scale 16-byte aligned). The LoRA operands are bf16 and enter the same
+ * fp32 accumulators as the e4m3 products, so the caller passes them divided by the scales:
+ * h_rows = h / x_scale[m] (mlora_shrink with row_div = x_scale) and B_a = lora_b / w_scale[n]
+ * (mlora_div_rows_bf16); one scaling in the epilogue then restores both terms.
+ * Reference semantics: low_rank.py:28 with base weight w_scale[n]·wq[n,k]. */
 int mlora_gemm_fwd_fp8(const void *xq, int64_t ldx, const float *x_scale, int64_t M, int64_t K,
                        const void *wq, int64_t ldw, const float *w_scale, int64_t N,
                        const void *bias, int bias_dtype,

@@ -35,7 +35,7 @@ def test_library_exports_every_declared_symbol(lib, pkg):
 
 
 def test_abi_version_and_status_strings(lib, pkg):
-    assert lib.mlora_abi_version() == pkg._lib.ABI_VERSION == 1
+    assert lib.mlora_abi_version() == pkg._lib.ABI_VERSION == 2
     for code in (0, -1, -2, -3, -4, -5):
         assert lib.mlora_status_string(code)
     assert b"unknown" in lib.mlora_status_string(-99)
@@ -114,7 +114,7 @@ def test_shrink_validation(lib, pkg):
     off, ids = L.i64_array([0, 64]), L.i32_array([0])
     args = lambda layout, ranks, h: lib.mlora_shrink(  # noqa: E731
         0x1000, 64, 64, 64, L.ptr_array([0x2000]), layout, L.i32_array(ranks), L.f32_array([1.0]), 1,
-        off, ids, 1, h, 64, None, 0, None)
+        off, ids, 1, h, 64, None, 0, None, None)
     assert args(3, [8], 0x3000) == L.ERR_INVALID
     assert args(0, [12], 0x3000) == L.ERR_INVALID
     assert args(0, [8], 0) == L.ERR_INVALID
@@ -129,6 +129,8 @@ def test_fp8_entry_points_validate_before_launch(lib, pkg):
     assert lib.mlora_quantize_rows_fp8(0x1000, 32, 0, 32, 0x2000, 32, None, None) == L.OK
     assert lib.mlora_dequant_rows_fp8(0x1001, 32, 0x3000, 4, 32, 0x2000, 32, None) == L.ERR_UNSUPPORTED
     assert lib.mlora_dequant_rows_fp8(0x1000, 32, None, 4, 32, 0x2000, 32, None) == L.ERR_INVALID
+    assert lib.mlora_div_rows_bf16(0x1000, 32, None, 4, 32, 0x2000, 32, None) == L.ERR_INVALID
+    assert lib.mlora_div_rows_bf16(0x1000, 4, 0x3000, 4, 8, 0x2000, 8, None) == L.ERR_INVALID
 
     def fwd8(M=64, K=64, N=64, ldx=64, xs=0x6000, ws=0x7000, off=None, ids=None):
         off = off if off is not None else [0, M]

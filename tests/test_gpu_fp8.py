@@ -93,9 +93,10 @@ def test_gemm_fwd_fp8_kernel_arithmetic(pkg, dev, bias, M, K, N, lengths, ids):
     scales = [1.0, 2.0]
     A_ops = [a.to(dev) for a in As]
     B_ops = [v.to(dev) for v in Bs]
-    h_rows, _ = pkg.kernels.shrink(xd, A_ops, 0, scales, routing, want_frag=False, width=24)
+    h_rows, _ = pkg.kernels.shrink(xd, A_ops, 0, scales, routing, want_frag=False, width=24, row_div=xs)
+    B_div = [pkg.kernels.div_rows_bf16(v, ws) for v in B_ops]
     bd = None if b is None else b.to(dev)
-    y = pkg.kernels.gemm_fwd_fp8(xq, xs, wq, ws, bd, h_rows, B_ops, routing)
+    y = pkg.kernels.gemm_fwd_fp8(xq, xs, wq, ws, bd, h_rows, B_div, routing)
     torch.cuda.synchronize()
     off, ids_ = routing.seg_offsets, routing.adapter_ids
     Af, Bf = [f64(a) for a in As], [f64(v) for v in Bs]
