@@ -10,29 +10,25 @@
 //
 // Quantisation of row m: amax = max_k |x[m,k]|; scale[m] = amax / 448 and
 // q = e4m3_rne(x * (448 / amax)) (both divisions IEEE fp32; an all-zero row
-// gets scale 1). The conversion is written out (round to nearest even on the
-// 3 mantissa bits, subnormals in steps of 2^-9, saturation at 448) so that
-// the bytes are reproducible from the definition of the format.
+// gets scale 1). Round to nearest even on the 3 mantissa bits, subnormals in
+// steps of 2^-9; |x·(448/amax)| <= 448 so nothing saturates.
 //
-// One wave per row: pass 1 reduces the absmax over 16-byte loads, pass 2
-// re-reads the row (an L2 hit) and writes 8 bytes per lane. Memory-bound:
-// 3 bytes of HBM traffic per element.
+// One wave per row. Rows of up to 9216 elements are loaded once into
+// registers (all 16-byte loads of the row in flight together), reduced to the
+// absmax and written back as 8 bytes per lane; longer rows take two passes
+// (the second re-reads the row, an L2 hit). Memory-bound: 3 bytes of HBM
+// traffic per element.
 #include "mlora_common.h"
 #include "mlora_host.h"
 
 namespace mlora {
 
-__device__ __forceinline__ uint32_t f32_to_e4m3(float f) {
-  const uint32_t sign = (__float_as_uint(f) >> 24) & 0x80u;
-  const float a = fabsf(f);
-  if (!(a < 464.f)) return sign | 0x7Eu;  // rounds past 448 (or NaN): saturate
-  if (a < 0.015625f) {                     // below 2^-6: subnormal grid 2^-9
-    return sign | (uint32_t)rintf(a * 512.f);  // 8 lands on 0x08 = 2^-6
-  }
-  uint32_t v = __float_as_uint(a);
-  v += 0x7FFFFu + ((v >> 20) & 1u);  // round the fp32 mantissa to 3 bits, ties to even
-  const uint32_t e = (v >> 23) - 120u;  // rebias 127 -> 7
-  return sign | (e << 3) | ((v >> 20) & 7u);
+// Four values (each |v| <= 448) to e4m3 bytes 0..3 of a dword with the gfx950
+// packed conversion (v_cvt_pk_fp8_f32: OCP e4m3, round to nearest even, the
+// subnormal grid included).
+__device__ __forceinline__ uint32_t pack4_e4m3(float a, float b, float c, float d) {
+  const int lo = __builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false);
+  return (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(c, d, lo, true);
 }
 
 __device__ __forceinline__ float e4m3_to_f32(uint32_t c) {
@@ -73,12 +69,45 @@ __global__ __launch_bounds__(256) void quantize_rows_kernel(const QuantArgs a) {
   uint8_t *qrow = a.q + (int64_t)m * a.ldq;
   for (int k = 8 * lane; k < a.K; k += 512) {
     const u32x4 v = buf_load16(rx, 2 * k);
-    uint32_t o[2] = {0u, 0u};
+    uint32_t o[2];
 #pragma unroll
-    for (int w = 0; w < 4; ++w) {
-      const uint32_t lo = f32_to_e4m3(bf16_to_f32(v[w] & 0xffff) * inv);
-      const uint32_t hi = f32_to_e4m3(bf16_to_f32(v[w] >> 16) * inv);
-      o[w >> 1] |= (lo | (hi << 8)) << (16 * (w & 1));
+    for (int h = 0; h < 2; ++h)
+      o[h] = pack4_e4m3(bf16_to_f32(v[2 * h] & 0xffff) * inv, bf16_to_f32(v[2 * h] >> 16) * inv,
+                        bf16_to_f32(v[2 * h + 1] & 0xffff) * inv, bf16_to_f32(v[2 * h + 1] >> 16) * inv);
+    *(MLORA_GLOBAL u32x2 *)(qrow + k) = u32x2{o[0], o[1]};
+  }
+}
+
+// Row held in registers: NI 16-byte chunks per lane (K <= 512 * NI).
+template <int NI>
+__global__ __launch_bounds__(256) void quantize_rows_reg_kernel(const QuantArgs a) {
+  const int lane = threadIdx.x & 63;
+  const int m = blockIdx.x * 4 + wave_id();
+  if (m >= a.M) return;
+  const __amdgpu_buffer_rsrc_t rx = make_rsrc(a.x + (int64_t)m * a.ldx, (int64_t)a.K * 2);
+  u32x4 v[NI];
+#pragma unroll
+  for (int it = 0; it < NI; ++it) v[it] = buf_load16(rx, 2 * (8 * lane + 512 * it));  // past K: reads zero
+  float amax = 0.f;
+#pragma unroll
+  for (int it = 0; it < NI; ++it)
+#pragma unroll
+    for (int w = 0; w < 4; ++w)
+      amax = fmaxf(amax, fmaxf(fabsf(bf16_to_f32(v[it][w] & 0xffff)), fabsf(bf16_to_f32(v[it][w] >> 16))));
+  amax = wave_max(amax);
+  const float inv = amax > 0.f ? 448.f / amax : 1.f;
+  if (lane == 0) a.scale[m] = amax > 0.f ? amax / 448.f : 1.f;
+  uint8_t *qrow = a.q + (int64_t)m * a.ldq;
+#pragma unroll
+  for (int it = 0; it < NI; ++it) {
+    const int k = 8 * lane + 512 * it;
+    if (k >= a.K) break;
+    uint32_t o[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const u32x4 &c = v[it];
+      o[h] = pack4_e4m3(bf16_to_f32(c[2 * h] & 0xffff) * inv, bf16_to_f32(c[2 * h] >> 16) * inv,
+                        bf16_to_f32(c[2 * h + 1] & 0xffff) * inv, bf16_to_f32(c[2 * h + 1] >> 16) * inv);
     }
     *(MLORA_GLOBAL u32x2 *)(qrow + k) = u32x2{o[0], o[1]};
   }
@@ -149,8 +178,14 @@ extern "C" int mlora_quantize_rows_fp8(const void *x, int64_t ldx, int64_t M, in
   if (M == 0 || K == 0) return MLORA_OK;
   if (scale == nullptr) return MLORA_ERR_INVALID;
   QuantArgs a{static_cast<const uint16_t *>(x), static_cast<uint8_t *>(xq), scale, ldx, ldq, (int32_t)M, (int32_t)K};
-  hipLaunchKernelGGL(quantize_rows_kernel, dim3((unsigned)((M + 3) / 4)), dim3(256), 0,
-                     static_cast<hipStream_t>(stream), a);
+  const dim3 grid((unsigned)((M + 3) / 4)), block(256);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int64_t ni = (K + 511) / 512;  // 16-byte chunks per lane
+  if (ni <= 2) hipLaunchKernelGGL(quantize_rows_reg_kernel<2>, grid, block, 0, s, a);
+  else if (ni <= 4) hipLaunchKernelGGL(quantize_rows_reg_kernel<4>, grid, block, 0, s, a);
+  else if (ni <= 8) hipLaunchKernelGGL(quantize_rows_reg_kernel<8>, grid, block, 0, s, a);
+  else if (ni <= 18) hipLaunchKernelGGL(quantize_rows_reg_kernel<18>, grid, block, 0, s, a);
+  else hipLaunchKernelGGL(quantize_rows_kernel, grid, block, 0, s, a);
   return launch_status();
 }
 
