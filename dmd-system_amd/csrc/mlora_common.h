@@ -135,6 +135,67 @@ __device__ __forceinline__ void transpose8x8_b16(const u32x4 (&in)[8], u32x4 (&o
 // Wave index within the workgroup, as a value the compiler knows is uniform
 // (threadIdx.x >> 6 alone is treated as divergent, which would force
 // waterfall loops around scalar buffer operands and M0 writes).
+// Four pairs of ds_read_b64_tr_b16 (gfx950 transposing LDS read) followed by a
+// wait for their data, as one inline-assembly block: pair t reads at a[t] and
+// a[t] + OFF2 bytes. Within each 16-lane group, lane j of a read receives
+// element (j & 3) of the 8 bytes addressed by lanes 4e + (j >> 2), e = 0..3.
+// The compiler's builtin for this instruction carries no memory-operand
+// information, so the compiler makes it wait for every direct-to-LDS load
+// still in flight (vmcnt(0)), which drains the load pipelines; in assembly the
+// reads see only the LDS stage they name (the caller's barriers order it), and
+// the trailing lgkmcnt(0) makes the outputs valid where the compiler uses them.
+template <int OFF2>
+__device__ __forceinline__ void lds_read_tr16_x4(const MLORA_LDS char *base, const int32_t (&a)[4], u32x4 (&out)[4]) {
+  u32x2 r0, r1, r2, r3, r4, r5, r6, r7;
+  const uint32_t b = (uint32_t)(uintptr_t)base;
+  asm volatile(
+      "ds_read_b64_tr_b16 %0, %8\n\t"
+      "ds_read_b64_tr_b16 %1, %8 offset:%12\n\t"
+      "ds_read_b64_tr_b16 %2, %9\n\t"
+      "ds_read_b64_tr_b16 %3, %9 offset:%12\n\t"
+      "ds_read_b64_tr_b16 %4, %10\n\t"
+      "ds_read_b64_tr_b16 %5, %10 offset:%12\n\t"
+      "ds_read_b64_tr_b16 %6, %11\n\t"
+      "ds_read_b64_tr_b16 %7, %11 offset:%12\n\t"
+      "s_waitcnt lgkmcnt(0)"
+      : "=&v"(r0), "=&v"(r1), "=&v"(r2), "=&v"(r3), "=&v"(r4), "=&v"(r5), "=&v"(r6), "=&v"(r7)
+      : "v"(b + a[0]), "v"(b + a[1]), "v"(b + a[2]), "v"(b + a[3]), "i"(OFF2)
+      : "memory");
+  out[0] = u32x4{r0[0], r0[1], r1[0], r1[1]};
+  out[1] = u32x4{r2[0], r2[1], r3[0], r3[1]};
+  out[2] = u32x4{r4[0], r4[1], r5[0], r5[1]};
+  out[3] = u32x4{r6[0], r6[1], r7[0], r7[1]};
+}
+
+// The same for two pairs.
+template <int OFF2>
+__device__ __forceinline__ void lds_read_tr16_x2(const MLORA_LDS char *base, const int32_t (&a)[2], u32x4 (&out)[2]) {
+  u32x2 r0, r1, r2, r3;
+  const uint32_t b = (uint32_t)(uintptr_t)base;
+  asm volatile(
+      "ds_read_b64_tr_b16 %0, %4\n\t"
+      "ds_read_b64_tr_b16 %1, %4 offset:%6\n\t"
+      "ds_read_b64_tr_b16 %2, %5\n\t"
+      "ds_read_b64_tr_b16 %3, %5 offset:%6\n\t"
+      "s_waitcnt lgkmcnt(0)"
+      : "=&v"(r0), "=&v"(r1), "=&v"(r2), "=&v"(r3)
+      : "v"(b + a[0]), "v"(b + a[1]), "i"(OFF2)
+      : "memory");
+  out[0] = u32x4{r0[0], r0[1], r1[0], r1[1]};
+  out[1] = u32x4{r2[0], r2[1], r3[0], r3[1]};
+}
+
+// Workgroup barrier for LDS pipelines fed by direct-to-LDS loads: waits for
+// this wave's LDS reads, then s_barrier, with compiler-level memory fences on
+// both sides. __syncthreads() would also wait for every direct-to-LDS load in
+// flight (its release fence covers LDS writes), so callers wait explicitly,
+// with vmcnt, for just the loads the next stage needs.
+__device__ __forceinline__ void lds_pipeline_barrier() {
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
 __device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane(threadIdx.x >> 6); }
 
 // ---------------------------------------------------------------- LDS layout

@@ -230,17 +230,24 @@ __device__ __forceinline__ void read_frag(int r, bf16x8 (&af)[C::TM], bf16x8 (&b
     af[r] = as_bf16x8(*(const lds_u4 *)(lds + fa.a[s] + (4096 * r + ST * C::A_BYTES)));
     return;
   }
-  const int j = r - C::TM;
-  if constexpr (!C::NN) {
+  if constexpr (!C::NN) {  // NN Q fragments are read per substep by read_q_nn
+    const int j = r - C::TM;
     bf[j] = as_bf16x8(*(const lds_u4 *)(lds + fa.b[s] + (4096 * j + ST * C::B_BYTES)));
-  } else {
-    typedef short v4i16 __attribute__((ext_vector_type(4)));
-    const MLORA_LDS char *p = lds + fa.b[j] + (ST * C::B_BYTES + 16 * C::QROW * s);
-    const v4i16 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((MLORA_LDS v4i16 *)p);
-    const v4i16 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((MLORA_LDS v4i16 *)(p + 4 * C::QROW));
-    const u32x2 l2 = __builtin_bit_cast(u32x2, lo), h2 = __builtin_bit_cast(u32x2, hi);
-    bf[j] = as_bf16x8(u32x4{l2[0], l2[1], h2[0], h2[1]});
   }
+}
+
+// All TN Q fragments of substep s of an NN stage: pairs of transposing reads
+// (rows 16s + 8h + (i>>2) and 4 rows further) in one block that also waits
+// for them (see lds_read_tr16_x4).
+template <class C, int ST>
+__device__ __forceinline__ void read_q_nn(bf16x8 (&bf)[C::TN], const MLORA_LDS char *lds, const FragAddr<C> &fa,
+                                          int s) {
+  u32x4 q[C::TN];
+  const MLORA_LDS char *base = lds + (ST * C::B_BYTES + 16 * C::QROW * s);
+  if constexpr (C::TN == 4) lds_read_tr16_x4<4 * C::QROW>(base, fa.b, q);
+  else lds_read_tr16_x2<4 * C::QROW>(base, fa.b, q);
+#pragma unroll
+  for (int j = 0; j < C::TN; ++j) bf[j] = as_bf16x8(q[j]);
 }
 
 // One 64-deep k-tile from LDS stage ST: 4 substeps of 16, entered with the
@@ -252,17 +259,20 @@ __device__ __forceinline__ void read_frag(int r, bf16x8 (&af)[C::TM], bf16x8 (&b
 template <class C, int ST>
 __device__ __forceinline__ void mma_stage(f32x16 (&acc)[C::TM][C::TN], MLORA_LDS char *lds, const FragAddr<C> &fa,
                                           const Pipe<C> &pipe, int k0, bool kmask, bool live, int wave, int lane) {
-  constexpr int NR = C::TM + C::TN;                      // fragment reads per substep
-  constexpr int DSR = C::TM + (C::NN ? 2 : 1) * C::TN;  // DS read instructions per substep
+  // NN: the TN Q fragments come from read_q_nn (transposing reads + wait, in assembly)
+  constexpr int NR = C::NN ? C::TM : C::TM + C::TN;  // compiler-visible fragment reads per substep
+  constexpr int DSR = NR;                            // DS read instructions per substep
   bf16x8 af[2][C::TM], bf[2][C::TN];
 #pragma unroll
   for (int r = 0; r < NR; ++r) read_frag<C, ST>(r, af[0], bf[0], lds, fa, 0);
+  if constexpr (C::NN) read_q_nn<C, ST>(bf[0], lds, fa, 0);
 #pragma unroll
   for (int s = 0; s < 4; ++s) {
     const int cur = s & 1;
     if (s < 3) {
 #pragma unroll
       for (int r = 0; r < NR; ++r) read_frag<C, ST>(r, af[cur ^ 1], bf[cur ^ 1], lds, fa, s + 1);
+      if constexpr (C::NN) read_q_nn<C, ST>(bf[cur ^ 1], lds, fa, s + 1);
     }
 #pragma unroll
     for (int g = 0; g < C::TMN; ++g) {

@@ -22,6 +22,8 @@
 #include "mlora_common.h"
 #include "mlora_host.h"
 
+#include <type_traits>
+
 namespace mlora {
 
 // Padded-row start of every segment (shared by shrink and seg_outer).
@@ -234,21 +236,28 @@ static void launch_shrink_rt(const ShrinkArgs &a, int nblocks, hipStream_t strea
 
 // ============================================================== seg_outer
 //
-// Work item = (row chunk of one segment, 64-wide j block, 64-wide c block).
-// The 4 waves of a workgroup take interleaved 32-row steps of the chunk and
-// are summed through LDS at the end (fixed order), so each item leaves one
-// fp32 partial [64 c x 64 j]. A second kernel adds an adapter's partials in
-// chunk order.
-// Per 32-row step a lane loads an 8x4 block of P (8 rows x 4 columns) and
-// transposes it in registers into 4 MFMA A-fragments (one per column); the
-// h fragments (hi and lo) are read ready-made. The next step's loads are in
-// flight while the current step's 32 MFMAs run; two waves share each SIMD.
-// v_mfma_f32_16x16x32_bf16: rows <- c (c = c0 + 4*i + t for fragment t),
-// columns <- j, contraction <- m.
+// Work item = (row chunk of one segment, 64-wide j block, 256-wide c block).
+// The 4 waves of a workgroup walk the chunk's 32-row steps together, each wave
+// owning 64 of the 256 columns, and each item leaves one fp32 partial
+// [256 c x 64 j]; a second kernel adds an adapter's partials in chunk order.
+// Per step the workgroup moves, with direct-to-LDS loads, the P block
+// [32 rows x 256 c] (512 contiguous bytes per row) and the step's h fragments
+// (hi and lo, 64 j) into one of OUTER_STAGES LDS stages, so several steps are
+// in flight while one is multiplied. P stays in its natural layout; the gfx950
+// transposing LDS read (ds_read_b64_tr_b16) turns 4 rows x 4 columns into
+// per-column runs of rows, i.e. the A operand of v_mfma_f32_16x16x32_bf16
+// (rows <- c, contraction <- the 32 rows of the step, columns <- j). The h
+// fragments are stored by the shrink in that MFMA's B-operand order and are
+// read as they are (16 bytes per lane).
 
-constexpr int OUT_C = 64;   // c per workgroup
+constexpr int OUT_C = 256;  // c per workgroup (4 waves x 64)
 constexpr int OUT_J = 64;   // j per workgroup
 constexpr int kMaxChunkRows = 32768;
+constexpr int OUTER_STAGES = 3;
+constexpr int OUTER_P_BYTES = 32 * OUT_C * 2;  // one step of P: 32 rows x 512 bytes
+constexpr int OUTER_H_BYTES = 8 * 1024;        // one step of h: 4 j-tiles x {hi, lo} x 1 KB
+constexpr int OUTER_STAGE_BYTES = OUTER_P_BYTES + OUTER_H_BYTES;
+constexpr int OUTER_DMA = (OUTER_P_BYTES + OUTER_H_BYTES) / 1024 / 4;  // 1 KB loads per wave and step
 
 struct OuterArgs {
   const uint16_t *P;
@@ -266,14 +275,16 @@ struct OuterArgs {
   SegTable seg;
 };
 
-struct OuterStep {
-  uint2 blk[8];
-  u32x4 hi[4], lo[4];
-};
+// vmcnt(n) with the other counters left alone (gfx9 s_waitcnt encoding).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | 0x0F70);
+}
 
 __global__ __launch_bounds__(256, 2) void seg_outer_kernel(const OuterArgs args) {
-  __shared__ f32x4 red_smem[3 * 16 * 64];  // waves 1..3: 16 f32x4 accumulators x 64 lanes
-  lds_f4 *red = (lds_f4 *)red_smem;
+  __shared__ u32x4 smem[OUTER_STAGES * OUTER_STAGE_BYTES / 16];
+  MLORA_LDS char *lds = (MLORA_LDS char *)smem;
   const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
   const int item = blockIdx.x;
   const int cb = item % args.cblocks;
@@ -291,37 +302,54 @@ __global__ __launch_bounds__(256, 2) void seg_outer_kernel(const OuterArgs args)
   const int nsteps = (rend - row0 + 31) / 32;
   const int64_t block0 = (args.pad.start[s] + rel0) / 32;
   const int c0 = cb * OUT_C;
-  const int li = lane & 15, lq = lane >> 4;
-  const int ccol = c0 + 4 * li;  // this lane's 4 columns
   const int32_t ldp_b = (int32_t)(args.ldp * 2);
-  // rows past the chunk end fall outside this resource and read as zero
-  const __amdgpu_buffer_rsrc_t rp = make_rsrc(args.P + (int64_t)row0 * args.ldp, (int64_t)(rend - row0) * ldp_b);
+  // P rows past the chunk end fall outside rp and read as zero
+  const __amdgpu_buffer_rsrc_t rp =
+      make_rsrc(args.P + (int64_t)row0 * args.ldp + c0, (int64_t)(rend - row0) * ldp_b);
   const __amdgpu_buffer_rsrc_t rh =
       make_rsrc(args.Hf + (block0 * args.jtiles) * 128, (int64_t)nsteps * args.jtiles * 2048);
-  // per-lane offsets at step 0; a step adds 32 rows of P and one fragment block
-  const int32_t p_off = ccol < args.C ? (8 * lq) * ldp_b + ccol * 2 : kOOB;
-  const int32_t p_step = 32 * ldp_b;
-  const int32_t h_step = args.jtiles * 2048;
-  int32_t h_off[4];
-#pragma unroll
-  for (int q = 0; q < 4; ++q) {
-    const int t = (j0 >> 4) + q;
-    h_off[q] = 16 * t < r ? (t * 2 * 64 + lane) * 16 : kOOB;
-  }
 
-  auto load = [&](OuterStep &st, int step) {
-    // a step past the end reads zeros (soffset beyond both resources)
-    const int32_t sp = step < nsteps ? step * p_step : kOOB;
-    const int32_t sh = step < nsteps ? step * h_step : kOOB;
+  // Loader. A 1 KB P load covers 2 rows (32 chunks of 16 bytes each); chunk
+  // cc of step row rr sits at LDS slot cc ^ (4 * (rr & 3)), so lane L fetches
+  // the chunk whose slot it fills: two lane patterns by the load's parity.
+  int32_t p_off[2];
 #pragma unroll
-    for (int e = 0; e < 8; ++e)
-      st.blk[e] = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(rp, p_off + e * ldp_b, sp, 0));
+  for (int par = 0; par < 2; ++par) {
+    const int cc = (lane & 31) ^ (4 * ((2 * par + (lane >> 5)) & 3));
+    p_off[par] = c0 + 8 * cc < args.C ? (lane >> 5) * ldp_b + 16 * cc : kOOB;
+  }
+  const int32_t h_step = args.jtiles * 2048;
+  // this wave's loads: P loads 4w..4w+3 of the 16 per step, h loads 2w, 2w+1 of the 8
+  auto issue = [&](auto st_c, int step) {
+    MLORA_LDS char *base = lds + decltype(st_c)::value * OUTER_STAGE_BYTES;
+    const bool live = step < nsteps;
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      st.hi[q] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rh, h_off[q], sh, 0));
-      st.lo[q] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rh, h_off[q] + 1024, sh, 0));
+    for (int i = 0; i < 4; ++i) {
+      const int q = 4 * wave + i;  // wave-uniform
+      const int32_t off = live ? p_off[q & 1] : kOOB;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rp, base + q * 1024, 16, off, (32 * step + 2 * q) * ldp_b, 0, 0);
+    }
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int q = 2 * wave + i;  // (j-tile, part) = (q / 2, q % 2) of this j block
+      const int t = (j0 >> 4) + (q >> 1);
+      const int32_t off = live && 16 * t < r ? ((t * 2 + (q & 1)) * 64 + lane) * 16 : kOOB;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rh, base + OUTER_P_BYTES + q * 1024, 16, off, step * h_step, 0, 0);
     }
   };
+
+  // Fragment addresses (stage-relative). A operand of c tile t (16 columns):
+  // lane i of a 16-lane group reads rows 8g + (i>>2) (+4) and the 4 columns at
+  // 16t + 4(i&3) of this wave's 64; the transposing read hands lane j column
+  // 16t + j, rows 8g..8g+3: 4 of the 8 rows the MFMA wants from lane 16g + j.
+  const int li = lane & 15, lg = lane >> 4;
+  int32_t a_addr[4];
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    const int row = 8 * lg + (li >> 2);
+    const int cc = 8 * wave + 2 * t + ((li & 3) >> 1);
+    a_addr[t] = row * (OUT_C * 2) + 16 * (cc ^ (4 * (row & 3))) + 8 * (li & 1);
+  }
 
   f32x4 acc[4][4];
 #pragma unroll
@@ -329,67 +357,61 @@ __global__ __launch_bounds__(256, 2) void seg_outer_kernel(const OuterArgs args)
 #pragma unroll
     for (int q = 0; q < 4; ++q) acc[t][q] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  auto compute = [&](const OuterStep &st) {
+  auto compute = [&](auto st_c) {
+    const MLORA_LDS char *base = lds + decltype(st_c)::value * OUTER_STAGE_BYTES;
+    bf16x8 hi[4], lo[4], af[4];
 #pragma unroll
-    for (int t = 0; t < 4; ++t) {
-      // column t of the 8x4 block: element t of rows 2q (low half) and 2q+1 (high half)
-      uint32_t o[4];
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const uint32_t x = (t >> 1) ? st.blk[2 * q].y : st.blk[2 * q].x;
-        const uint32_t y = (t >> 1) ? st.blk[2 * q + 1].y : st.blk[2 * q + 1].x;
-        o[q] = (t & 1) ? ((x >> 16) | (y & 0xffff0000u)) : ((x & 0xffffu) | (y << 16));
-      }
-      const bf16x8 frag = as_bf16x8(u32x4{o[0], o[1], o[2], o[3]});
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        acc[t][q] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(frag, as_bf16x8(st.hi[q]), acc[t][q], 0, 0, 0);
-        acc[t][q] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(frag, as_bf16x8(st.lo[q]), acc[t][q], 0, 0, 0);
-      }
+    for (int q = 0; q < 4; ++q) {
+      hi[q] = as_bf16x8(*(const lds_u4 *)(base + OUTER_P_BYTES + (2 * q) * 1024 + 16 * lane));
+      lo[q] = as_bf16x8(*(const lds_u4 *)(base + OUTER_P_BYTES + (2 * q + 1) * 1024 + 16 * lane));
     }
+    u32x4 at[4];
+    lds_read_tr16_x4<4 * OUT_C * 2>(base, a_addr, at);  // rows +4: the second half of each fragment
+#pragma unroll
+    for (int t = 0; t < 4; ++t) af[t] = as_bf16x8(at[t]);
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        acc[t][q] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[t], hi[q], acc[t][q], 0, 0, 0);
+        acc[t][q] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[t], lo[q], acc[t][q], 0, 0, 0);
+      }
   };
 
-  // two register stages, unrolled so no copies are needed between them
-  OuterStep s0, s1;
-  int step = wave;
-  load(s0, step);
-  while (step < nsteps) {
-    load(s1, step + 4);
-    __builtin_amdgcn_sched_barrier(0);
-    compute(s0);
-    __builtin_amdgcn_sched_barrier(0);
-    step += 4;
-    if (step >= nsteps) break;
-    load(s0, step + 4);
-    __builtin_amdgcn_sched_barrier(0);
-    compute(s1);
-    __builtin_amdgcn_sched_barrier(0);
-    step += 4;
+  // OUTER_STAGES-deep pipeline, one barrier per step: wait for step i, make it
+  // visible, refill the stage step i-1 used (every wave is past it), multiply.
+  // Loads past the last step carry no data but keep the wait counts uniform.
+  // The loop is unrolled by the stage count so that every stage offset is a
+  // constant: with run-time stage indices the compiler cannot tell the loads
+  // in flight from the stage being read and waits for all of them.
+  static_assert(OUTER_STAGES == 3, "pipeline unrolled for 3 stages");
+  using S0 = std::integral_constant<int, 0>;
+  using S1 = std::integral_constant<int, 1>;
+  using S2 = std::integral_constant<int, 2>;
+  issue(S0{}, 0);
+  issue(S1{}, 1);
+  auto step = [&](auto cur, auto refill, int i) {
+    wait_vmcnt<(OUTER_STAGES - 2) * OUTER_DMA>();  // this wave's loads of step i landed
+    lds_pipeline_barrier();                        // everyone's did; everyone is done with step i-1
+    issue(refill, i + OUTER_STAGES - 1);
+    compute(cur);
+  };
+  for (int i = 0; i < nsteps; i += 3) {
+    step(S0{}, S2{}, i);
+    if (i + 1 >= nsteps) break;
+    step(S1{}, S0{}, i + 1);
+    if (i + 2 >= nsteps) break;
+    step(S2{}, S1{}, i + 2);
   }
+  wait_vmcnt<0>();  // nothing may still write LDS when the workgroup ends
 
-  // fixed-order cross-wave sum: wave0 + wave1 + wave2 + wave3
-  if (wave > 0) {
-#pragma unroll
-    for (int t = 0; t < 4; ++t)
-#pragma unroll
-      for (int q = 0; q < 4; ++q) red[((wave - 1) * 16 + t * 4 + q) * 64 + lane] = acc[t][q];
-  }
-  __syncthreads();
-  if (wave != 0) return;
-#pragma unroll
-  for (int w = 0; w < 3; ++w)
-#pragma unroll
-    for (int t = 0; t < 4; ++t)
-#pragma unroll
-      for (int q = 0; q < 4; ++q) acc[t][q] += red[(w * 16 + t * 4 + q) * 64 + lane];
-
-  // partial layout: ws[chunk][c][rpad]; lane holds c = c0 + 4*(4*lq + v) + t, j = j0 + 16*q + li
+  // partial layout: ws[chunk][c][rpad]; lane holds c = c0 + 64w + 16t + 4(l/16) + v, j = j0 + 16q + l%16
   MLORA_GLOBAL float *dst = gp(args.ws) + (int64_t)chunk * args.C * args.rpad;
 #pragma unroll
   for (int t = 0; t < 4; ++t)
 #pragma unroll
     for (int v = 0; v < 4; ++v) {
-      const int c = c0 + 4 * (4 * lq + v) + t;
+      const int c = c0 + 64 * wave + 16 * t + 4 * lg + v;
       if (c >= args.C) continue;
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
