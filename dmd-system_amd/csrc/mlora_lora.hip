@@ -23,6 +23,7 @@
 #include "mlora_host.h"
 
 #include <type_traits>
+#include <utility>
 
 namespace mlora {
 
@@ -275,6 +276,16 @@ struct OuterArgs {
   SegTable seg;
 };
 
+// f(integral_constant<int, 0>), f(..1), ... f(..N-1), stopping at the first false.
+template <class F, int... K>
+__device__ __forceinline__ void static_for_impl(F &&f, std::integer_sequence<int, K...>) {
+  (void)(f(std::integral_constant<int, K>{}) && ...);
+}
+template <int N, class F>
+__device__ __forceinline__ void static_for(F &&f) {
+  static_for_impl(f, std::make_integer_sequence<int, N>{});
+}
+
 // vmcnt(n) with the other counters left alone (gfx9 s_waitcnt encoding).
 template <int N>
 __device__ __forceinline__ void wait_vmcnt() {
@@ -384,25 +395,21 @@ __global__ __launch_bounds__(256, 2) void seg_outer_kernel(const OuterArgs args)
   // The loop is unrolled by the stage count so that every stage offset is a
   // constant: with run-time stage indices the compiler cannot tell the loads
   // in flight from the stage being read and waits for all of them.
-  static_assert(OUTER_STAGES == 3, "pipeline unrolled for 3 stages");
-  using S0 = std::integral_constant<int, 0>;
-  using S1 = std::integral_constant<int, 1>;
-  using S2 = std::integral_constant<int, 2>;
-  issue(S0{}, 0);
-  issue(S1{}, 1);
-  auto step = [&](auto cur, auto refill, int i) {
+  auto step = [&](auto cur, int i) -> bool {
+    if (i >= nsteps) return false;
+    constexpr int refill = (decltype(cur)::value + OUTER_STAGES - 1) % OUTER_STAGES;
     wait_vmcnt<(OUTER_STAGES - 2) * OUTER_DMA>();  // this wave's loads of step i landed
     lds_pipeline_barrier();                        // everyone's did; everyone is done with step i-1
-    issue(refill, i + OUTER_STAGES - 1);
+    issue(std::integral_constant<int, refill>{}, i + OUTER_STAGES - 1);
     compute(cur);
+    return true;
   };
-  for (int i = 0; i < nsteps; i += 3) {
-    step(S0{}, S2{}, i);
-    if (i + 1 >= nsteps) break;
-    step(S1{}, S0{}, i + 1);
-    if (i + 2 >= nsteps) break;
-    step(S2{}, S1{}, i + 2);
-  }
+  static_for<OUTER_STAGES - 1>([&](auto p) {
+    issue(p, decltype(p)::value);
+    return true;
+  });
+  for (int i = 0; i < nsteps; i += OUTER_STAGES)
+    static_for<OUTER_STAGES>([&](auto k) { return step(k, i + decltype(k)::value); });
   wait_vmcnt<0>();  // nothing may still write LDS when the workgroup ends
 
   // partial layout: ws[chunk][c][rpad]; lane holds c = c0 + 64w + 16t + 4(l/16) + v, j = j0 + 16q + l%16
