@@ -229,6 +229,38 @@ def test_wan13b_full_shape(pkg, dev, name, K, N):
     assert torch.isfinite(y).all() and torch.isfinite(dx).all()
 
 
+@pytest.mark.parametrize("cfg_name,lin", [("wan22_5b", "ffn.0"), ("wan22_5b", "ffn.2"), ("flux", "q"), ("flux", "ffn.0")])
+def test_config_3_4_full_shape(pkg, dev, cfg_name, lin):
+    """BASELINE configs 3 (27280 tokens, 3 rank-128 adapters on seeded segments, scale 2) and
+    4 (16 samples x 4608 tokens, one adapter each, ranks from {16,32,64,128}) at full size:
+    Y and dX on 384 sampled rows vs the fp64 oracle, every adapter's gradients vs torch fp32
+    on the GPU."""
+    from dmd_system_amd import workloads as W
+    cfg = W.CONFIGS[cfg_name]
+    K, N = {name: (k, n) for name, k, n in cfg.linears()}[lin]
+    x, w, b, As, Bs, dy = W.make_linear(cfg, K, N, dev, seed=cfg.seed + 17)
+    routing = cfg.routing
+    n = len(cfg.ranks)
+    scales = [cfg.scale] * n
+    y, dx, dAs, dBs = run_hip(pkg, dev, x, w, b, As, Bs, dy, scales, routing)
+    rows = np.sort(np.random.default_rng(30).choice(cfg.tokens, 384, replace=False))
+    rows[0], rows[-1] = 0, cfg.tokens - 1
+    Af, Bf = [f64(a) for a in As], [f64(v) for v in Bs]
+    off, ids = routing.seg_offsets, routing.adapter_ids
+    loff, lids = _local_routing(rows, off, ids)
+    y_ref = O.forward_rows(np.arange(len(rows)), f64(x[rows]), f64(w), f64(b), Af, Bf, scales, loff, lids)
+    assert O.rel_l2(f64(y[rows]), y_ref) <= TOL
+    dx_ref = O.dx_rows(np.arange(len(rows)), f64(w), Af, Bf, scales, loff, lids, f64(dy[rows]))
+    assert O.rel_l2(f64(dx[rows]), dx_ref) <= TOL
+    for s_, a in enumerate(ids):
+        lo, hi = off[s_], off[s_ + 1]
+        xs, dys = x[lo:hi].float(), dy[lo:hi].float()
+        h = xs @ As[a].float().T
+        assert O.rel_l2(f64(dBs[a]), f64(scales[a] * dys.T @ h)) <= TOL
+        assert O.rel_l2(f64(dAs[a]), f64((scales[a] * dys @ Bs[a].float()).T @ xs)) <= TOL
+    assert torch.isfinite(y).all() and torch.isfinite(dx).all()
+
+
 def _local_routing(rows, off, ids):
     """Routing of the sampled rows (kept in order) as consecutive segments."""
     ad = O.row_adapters(off, ids)[rows]
