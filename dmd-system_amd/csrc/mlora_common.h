@@ -185,6 +185,44 @@ __device__ __forceinline__ void lds_read_tr16_x2(const MLORA_LDS char *base, con
   out[1] = u32x4{r2[0], r2[1], r3[0], r3[1]};
 }
 
+// One pair.
+template <int OFF2>
+__device__ __forceinline__ void lds_read_tr16_x1(const MLORA_LDS char *base, int32_t a, u32x4 &out) {
+  u32x2 r0, r1;
+  const uint32_t b = (uint32_t)(uintptr_t)base;
+  asm volatile(
+      "ds_read_b64_tr_b16 %0, %2\n\t"
+      "ds_read_b64_tr_b16 %1, %2 offset:%3\n\t"
+      "s_waitcnt lgkmcnt(0)"
+      : "=&v"(r0), "=&v"(r1)
+      : "v"(b + a), "i"(OFF2)
+      : "memory");
+  out = u32x4{r0[0], r0[1], r1[0], r1[1]};
+}
+
+// N pairs (N = 1, 2, 4 or 8), each pair at a[t] and a[t] + OFF2 bytes.
+template <int N, int OFF2>
+__device__ __forceinline__ void lds_read_tr16(const MLORA_LDS char *base, const int32_t (&a)[N], u32x4 (&out)[N]) {
+  if constexpr (N == 1) {
+    lds_read_tr16_x1<OFF2>(base, a[0], out[0]);
+  } else if constexpr (N == 2) {
+    lds_read_tr16_x2<OFF2>(base, a, out);
+  } else if constexpr (N == 4) {
+    lds_read_tr16_x4<OFF2>(base, a, out);
+  } else {
+    static_assert(N == 8, "1, 2, 4 or 8 pairs");
+    const int32_t lo[4] = {a[0], a[1], a[2], a[3]}, hi[4] = {a[4], a[5], a[6], a[7]};
+    u32x4 o0[4], o1[4];
+    lds_read_tr16_x4<OFF2>(base, lo, o0);
+    lds_read_tr16_x4<OFF2>(base, hi, o1);
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      out[t] = o0[t];
+      out[t + 4] = o1[t];
+    }
+  }
+}
+
 // Workgroup barrier for LDS pipelines fed by direct-to-LDS loads: waits for
 // this wave's LDS reads, then s_barrier, with compiler-level memory fences on
 // both sides. __syncthreads() would also wait for every direct-to-LDS load in
