@@ -13,6 +13,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <utility>
+
 #include "../../include/mlora.h"
 
 namespace mlora {
@@ -55,6 +57,10 @@ __device__ __forceinline__ float buf_load4f(__amdgpu_buffer_rsrc_t r, int32_t of
 
 __device__ __forceinline__ void buf_store8(__amdgpu_buffer_rsrc_t r, int32_t off, uint2 v) {
   __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(__attribute__((ext_vector_type(2))) unsigned, v), r, off, 0, 0);
+}
+
+__device__ __forceinline__ void buf_store16(__amdgpu_buffer_rsrc_t r, int32_t off, u32x4 v) {
+  __builtin_amdgcn_raw_buffer_store_b128(v, r, off, 0, 0);
 }
 
 constexpr int kMaxSeg = MLORA_MAX_SEGMENTS;
@@ -232,6 +238,23 @@ __device__ __forceinline__ void lds_pipeline_barrier() {
   asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
   __builtin_amdgcn_s_barrier();
   asm volatile("" ::: "memory");
+}
+
+// f(integral_constant<int, 0>), f(..1), ... f(..N-1), stopping at the first false.
+template <class F, int... K>
+__device__ __forceinline__ void static_for_impl(F &&f, std::integer_sequence<int, K...>) {
+  (void)(f(std::integral_constant<int, K>{}) && ...);
+}
+template <int N, class F>
+__device__ __forceinline__ void static_for(F &&f) {
+  static_for_impl(f, std::make_integer_sequence<int, N>{});
+}
+
+// vmcnt(n) with the other counters left alone (gfx9 s_waitcnt encoding).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | 0x0F70);
 }
 
 __device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane(threadIdx.x >> 6); }

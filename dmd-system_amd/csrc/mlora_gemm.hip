@@ -7,14 +7,15 @@
 // either "NT" ([Ncols, Kc], contraction contiguous: W in the forward, B_a) or
 // "NN" ([Kc, Ncols]: W and A_a in dX). The LoRA term is more contraction: after
 // the main loop over Kc, every segment that overlaps the tile's rows and has
-// an adapter runs ceil(r/64) extra k-tiles with P = Hs rows of that segment
+// an adapter runs ceil(r/32) extra k-tiles with P = Hs rows of that segment
 // (other rows read as zero) and Q = that adapter's B_a / A_a. Y is written once.
 //
 // gfx950 mapping: v_mfma_f32_32x32x16_bf16, wave64. A workgroup of WM x WN
 // waves owns a BM x BN tile; each wave a (BM/WM) x (BN/WN) sub-tile whose fp32
-// accumulators stay in registers. Operand tiles of 64 contraction elements are
-// double-buffered in LDS (one barrier per k-tile): the direct-to-LDS loads of
-// tile k+1 are issued one by one between the MFMAs of tile k. Global reads use raw buffer
+// accumulators stay in registers. Operand k-tiles of 32 contraction elements
+// stream through a ring of LDS stages filled by direct-to-LDS loads issued
+// one by one between the MFMAs, STAGES-1 k-tiles ahead (one barrier per
+// k-tile). Global reads use raw buffer
 // resources; out-of-range rows/columns are given an offset past the buffer and
 // read as zero, so tails need no branches. NN operands stay in their natural
 // layout in LDS and are read with the gfx950 transposing LDS read
@@ -45,7 +46,7 @@ struct GemmArgs {
   SegTable seg;
 };
 
-template <int BM_, int BN_, int WM_, int WN_, bool NN_, bool F8_ = false>
+template <int BM_, int BN_, int WM_, int WN_, bool NN_, bool F8_ = false, int KB_ = 128, int STAGES_ = 2>
 struct GemmCfg {
   static constexpr int BM = BM_, BN = BN_, WM = WM_, WN = WN_;
   static constexpr bool NN = NN_;
@@ -55,35 +56,54 @@ struct GemmCfg {
   static constexpr int THREADS = 64 * NW;
   static constexpr int TM = BM / WM / 32;  // 32x32 MFMA tiles per wave along m
   static constexpr int TN = BN / WN / 32;  // ... along n
-  static constexpr int A_DMA = BM / 8 / NW;  // 1 KB direct-to-LDS loads per wave for the P tile
-  static constexpr int B_DMA = BN / 8 / NW;  // the same for the Q tile (both layouts hold 64 x BN)
-  // NN Q tile: natural layout, one row of BN output columns per contraction index
-  static constexpr int QROW = BN * 2;       // bytes per NN row
-  static constexpr int QCPR = BN / 8;       // 16-byte chunks per NN row
-  static constexpr int QRPD = 1024 / QROW;  // NN rows per 1 KB load
-  static_assert(A_DMA * NW * 8 == BM, "P tile rows must split into 8-row loads over the waves");
-  static_assert(B_DMA * NW * 8 == BN, "Q tile must split into 1 KB loads over the waves");
-  static_assert(A_DMA % 2 == 0 && B_DMA % 2 == 0, "even 1 KB load counts per wave");
+  // A k-tile holds KB bytes of contraction per row (KB / 2 bf16 or KB e4m3) as
+  // CPR chunks of 16 bytes; an NN Q k-tile holds KB / 2 natural rows of BN
+  // columns. 128-byte rows make every direct-to-LDS load read whole 128-byte
+  // lines (64-byte rows move ~40% fewer bytes per CU, measured).
+  static constexpr int KB = KB_;
+  static_assert(KB == 64 || KB == 128, "64- or 128-byte k-tile rows");
+  static constexpr int CPR = KB / 16;    // chunks per row
+  static constexpr int RPD = 1024 / KB;  // rows per 1 KB load
+  static constexpr int NSUB = KB / 32;   // 16-deep bf16 substeps per k-tile (an e4m3 substep takes two)
+  static_assert(NSUB % 2 == 0, "the step's last substep reads the next tile's first into the first buffer");
+  static constexpr int STAGES = STAGES_;  // LDS ring depth
+  static constexpr int A_BYTES = BM * KB, B_BYTES = BN * KB;  // one stage of P / of Q
+  static constexpr int A_DMA = A_BYTES / 1024 / NW;           // 1 KB direct-to-LDS loads per wave for the P tile
+  static constexpr int B_DMA = B_BYTES / 1024 / NW;           // the same for the Q tile
+  static constexpr int QROW = BN * 2;                         // NN: bytes per contraction row
+  static constexpr int QCPR = BN / 8;                         // NN: 16-byte chunks per row
+  static constexpr int QRPD = 1024 / QROW;                    // NN: rows per 1 KB load
+  static_assert(A_DMA * NW * 1024 == A_BYTES && B_DMA * NW * 1024 == B_BYTES, "tiles split into 1 KB loads per wave");
   static_assert(!NN || (QCPR >= 16 && QRPD >= 1), "NN rows hold at least 16 chunks");
   static constexpr int NDMA = A_DMA + B_DMA;  // 1 KB loads per wave and k-tile
-  static constexpr int TMN = TM * TN;         // MFMAs per wave and 16-deep substep
-  // The next tile's loads are spread over the MFMAs of this tile's first two
-  // substeps, one after every DMA_EVERY-th MFMA (the stage barrier after the
-  // last substep waits for them).
-  static constexpr int DMA_EVERY = 2 * TMN / NDMA > 1 ? 2 * TMN / NDMA : 1;
-  static_assert(NDMA * DMA_EVERY <= (F8 ? 2 : 4) * TMN, "every load is issued within the k-tile");
-  // LDS (bytes): P stage 0 | P stage 1 | Q stage 0 | Q stage 1
-  static constexpr int A_BYTES = BM * 128, B_BYTES = BN * 128;
-  static constexpr int B_BASE = 2 * A_BYTES;
-  static constexpr int LDS_BYTES = 2 * (A_BYTES + B_BYTES);
-  static_assert(A_BYTES < 65536 && B_BYTES < 65536, "stage offsets must fit the ds_read offset field");
+  static constexpr int TMN = TM * TN;  // MFMAs per wave and 16-deep bf16 substep (or e4m3 substep)
+  // LDS (bytes): P stages 0..STAGES-1 | Q stages 0..STAGES-1
+  static constexpr int B_BASE = STAGES * A_BYTES;
+  static constexpr int LDS_BYTES = STAGES * (A_BYTES + B_BYTES);
+  static_assert(LDS_BYTES <= 163840, "the ring must fit the 160 KB of LDS");
   static constexpr int GROUP_M = 8;
+  // occupancy the register budget is sized for: a 256x256 tile fills the LDS
+  // (one workgroup per CU, NW / 4 waves per SIMD); 128x128 tiles run two
+  // workgroups per CU
+  static constexpr int WAVES_PER_SIMD = BM == 256 ? (NW >= 8 ? NW / 4 : 1) : 2;
 };
+
+// Chunk swizzle of a tile row with CPR chunks: chunk c of row r sits at slot
+// c ^ swzk<CPR>(r). The 16 lanes of one fragment read (16 consecutive
+// 16-aligned rows, one chunk) then hit 16 distinct 16-byte bank groups of the
+// 256-byte bank period: 8 chunks per row — the slot carries r % 8, the parity
+// of r / 8 picks the half period; 4 chunks — the row sits at r % 4 of the
+// period, the slot carries (r / 4) % 4. Both depend on r % 16 only.
+template <int CPR>
+__device__ __forceinline__ int swzk(int row) {
+  if constexpr (CPR == 8) return swz(row);
+  else return (row >> 2) & 3;
+}
 
 // One contraction source (wave-uniform): P rows valid in [row_lo, row_hi),
 // contraction valid below klim (elements) for both operands. esz is the
-// element size (2: bf16, 1: e4m3); an LDS k-tile always holds 128 bytes of
-// contraction per row, i.e. 128 / esz elements.
+// element size (2: bf16, 1: e4m3); an LDS k-tile always holds KB bytes of
+// contraction per row, i.e. KB / esz elements.
 struct KSource {
   const char *P;
   const char *Q;
@@ -94,18 +114,18 @@ struct KSource {
 };
 
 // Per-thread state of one contraction source. Global tiles go to LDS with the
-// gfx950 direct-to-LDS buffer load: one wave instruction fills 1 KB (8 rows of
-// 8 chunks); lane L lands at chunk slot L of that KB, so it fetches the
-// logical chunk (L%8) ^ swz(row) that the XOR-swizzled layout keeps there.
-// With swz depending on row%16 only, the 1 KB loads of one wave differ by a
-// whole number of rows plus one of two lane patterns (even / odd 8-row block),
-// so the per-load row step and the tile's k offset travel in soffset.
+// gfx950 direct-to-LDS buffer load: one wave instruction fills 1 KB (RPD rows
+// of CPR chunks); lane L lands at chunk slot L % CPR of row L / CPR of that KB,
+// so it fetches logical chunk (L % CPR) ^ swzk(row). The swizzle depends on
+// row % 16 only, so the 1 KB loads of a wave differ by a whole number of rows
+// plus (8-row loads) one of two lane patterns, even or odd load; the load's row
+// and the tile's k offset travel in soffset.
 template <class C>
 struct Pipe {
   __amdgpu_buffer_rsrc_t rp, rq;
-  int32_t a_off[2];     // even / odd 8-row block: this lane's P chunk offset at k = 0 (rows past the tile: kOOB)
-  int32_t a_kc[2];      // contraction index of that chunk
-  int32_t a_row0;       // first P row (tile-local) of this wave's loads
+  int32_t a_off[2];  // this lane's P chunk offset at k = 0 in an even / odd load (rows past the tile: kOOB)
+  int32_t a_kc[2];   // contraction index of that chunk
+  int32_t a_row0;    // first P row (tile-local) of this wave's loads
   int32_t b_off[2], b_kc[2];
   int32_t b_row0;
   int32_t klim, ldp_b, ldq_b, p_rows, esz;
@@ -121,21 +141,21 @@ struct Pipe {
     // P rows of the tile are read relative to m0; rows outside [row_lo, row_hi) read zero
     rp = make_rsrc(s.P + (int64_t)m0 * s.ldp_b, (int64_t)(s.row_hi - m0) * ldp_b);
     p_rows = base_row - m0;  // tile rows below this index belong to another segment
-    a_row0 = 8 * wave * C::A_DMA;
+    a_row0 = C::RPD * wave * C::A_DMA;
 #pragma unroll
     for (int par = 0; par < 2; ++par) {
-      const int c = (lane & 7) ^ (lane >> 3) ^ par;
+      const int c = (lane % C::CPR) ^ swzk<C::CPR>(C::RPD * par + lane / C::CPR);
       a_kc[par] = chunk_elems * c;
-      a_off[par] = (lane >> 3) * ldp_b + 16 * c;
+      a_off[par] = (lane / C::CPR) * ldp_b + 16 * c;
     }
     if constexpr (!C::NN) {
       rq = make_rsrc(s.Q + (int64_t)n0 * s.ldq_b, (int64_t)(Ncols - n0) * s.ldq_b);
-      b_row0 = 8 * wave * C::B_DMA;
+      b_row0 = C::RPD * wave * C::B_DMA;
 #pragma unroll
       for (int par = 0; par < 2; ++par) {
-        const int c = (lane & 7) ^ (lane >> 3) ^ par;
+        const int c = (lane % C::CPR) ^ swzk<C::CPR>(C::RPD * par + lane / C::CPR);
         b_kc[par] = chunk_elems * c;
-        b_off[par] = (lane >> 3) * ldq_b + 16 * c;  // rows past Ncols fall outside rq
+        b_off[par] = (lane / C::CPR) * ldq_b + 16 * c;  // rows past Ncols fall outside rq
       }
     } else {
       // NN (bf16 only): rows are contraction indices, chunk c of row k at slot c ^ (4 * (k & 3))
@@ -143,10 +163,10 @@ struct Pipe {
       const int p = lane % C::QCPR, rl = lane / C::QCPR;
 #pragma unroll
       for (int par = 0; par < 2; ++par) {
-        const int c = p ^ (4 * ((C::QRPD * par + rl) & 3));
-        b_off[par] = (n0 + 8 * c < Ncols) ? rl * ldq_b + 16 * c : kOOB;
+        const int cc = p ^ (4 * ((C::QRPD * par + rl) & 3));
+        b_off[par] = (n0 + 8 * cc < Ncols) ? rl * ldq_b + 16 * cc : kOOB;
       }
-      b_kc[0] = rl;  // row of this lane within its 1 KB load
+      b_kc[0] = b_kc[1] = rl;  // row of this lane within its 1 KB load
     }
   }
 
@@ -156,58 +176,57 @@ struct Pipe {
   __device__ __forceinline__ void issue_one(MLORA_LDS char *lds, int q, int st, int k0, int wave, int lane, bool KMASK,
                                             bool live) const {
     if (q < C::A_DMA) {
-      MLORA_LDS void *dst = lds + st * C::A_BYTES + (wave * C::A_DMA + q) * 1024;
-      const int row = a_row0 + 8 * q;  // wave-uniform
-      const int par = q & 1;
+      const int blk = wave * C::A_DMA + q;  // wave-uniform
+      MLORA_LDS void *dst = lds + st * C::A_BYTES + blk * 1024;
+      const int row = a_row0 + C::RPD * q;
+      const int par = blk & 1;
       int32_t off = a_off[par];
-      if (p_rows > 0 && row + (lane >> 3) < p_rows) off = kOOB;  // rows of an earlier segment
+      if (p_rows > 0 && row + lane / C::CPR < p_rows) off = kOOB;  // rows of an earlier segment
       if (KMASK && k0 + a_kc[par] >= klim) off = kOOB;
       if (!live) off = kOOB;
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rp, dst, 16, off, row * ldp_b + k0 * esz, 0, 0);
+      const int32_t soff = row * ldp_b + k0 * esz;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rp, dst, 16, off, soff, 0, 0);
     } else if constexpr (!C::NN) {
       const int qb = q - C::A_DMA;
-      MLORA_LDS void *dst = lds + C::B_BASE + st * C::B_BYTES + (wave * C::B_DMA + qb) * 1024;
-      const int row = b_row0 + 8 * qb;
-      const int par = qb & 1;
+      const int blk = wave * C::B_DMA + qb;
+      MLORA_LDS void *dst = lds + C::B_BASE + st * C::B_BYTES + blk * 1024;
+      const int row = b_row0 + C::RPD * qb;
+      const int par = blk & 1;
       int32_t off = (KMASK && k0 + b_kc[par] >= klim) ? kOOB : b_off[par];
       if (!live) off = kOOB;
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rq, dst, 16, off, row * ldq_b + k0 * esz, 0, 0);
+      const int32_t soff = row * ldq_b + k0 * esz;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rq, dst, 16, off, soff, 0, 0);
     } else {
       const int blk = wave * C::B_DMA + (q - C::A_DMA);  // wave-uniform
       MLORA_LDS void *dst = lds + C::B_BASE + st * C::B_BYTES + blk * 1024;
       const int row = C::QRPD * blk;
       int32_t off = (KMASK && k0 + row + b_kc[0] >= klim) ? kOOB : b_off[blk & 1];
       if (!live) off = kOOB;
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rq, dst, 16, off, (k0 + row) * ldq_b, 0, 0);
+      const int32_t soff = (k0 + row) * ldq_b;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rq, dst, 16, off, soff, 0, 0);
     }
-  }
-
-  // All loads of the k-tile starting at k0, back to back (pipeline prologue).
-  __device__ __forceinline__ void issue(MLORA_LDS char *lds, int st, int k0, int wave, int lane, bool KMASK) const {
-#pragma unroll
-    for (int q = 0; q < C::NDMA; ++q) issue_one(lds, q, st, k0, wave, lane, KMASK, true);
   }
 };
 
-// Byte addresses (stage 0, first 32-row tile) of this lane's fragments per
-// substep; further tiles are +4096 bytes and stage 1 is +A_BYTES / +B_BYTES,
-// all folded into the ds_read offset field.
+// Byte addresses (stage 0, first 32-row tile) of this lane's fragments for
+// each 16-deep substep of a k-tile; further tiles are +32 * KB bytes and stage
+// s is +s * A_BYTES / +s * B_BYTES, folded into the ds_read offset field.
 // NN: b[j] is the first of the two transposing reads of tile j at substep 0
-// (substep s adds 16 rows, the second read 4 rows). ds_read_b64_tr_b16 gives
+// (substep h adds 16 rows, the second read 4 rows). ds_read_b64_tr_b16 gives
 // lane j of a 16-lane group element e = element (j & 3) of the 8 bytes
 // addressed by lane 4e + (j >> 2); lane i pointing at row k0 + (i >> 2),
 // column c0 + 4(i & 3) therefore yields 4 consecutive contraction values of
 // column c0 + j: half of the B fragment of v_mfma_f32_32x32x16_bf16.
 template <class C>
 struct FragAddr {
-  int32_t a[4], b[C::NN ? C::TN : 4];
+  int32_t a[C::NSUB], b[C::NN ? C::TN : C::NSUB];
   __device__ __forceinline__ void init(int wm0, int wn0, int lane) {
-    const int z = swz(lane & 31);  // lane-constant: fragment rows are 32-aligned + lane
+    const int z = swzk<C::CPR>(lane & 31);  // lane-constant: fragment rows are 32-aligned + lane
 #pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      const int slot = (2 * s + (lane >> 5)) ^ z;
-      a[s] = (wm0 + (lane & 31)) * 128 + 16 * slot;
-      if constexpr (!C::NN) b[s] = C::B_BASE + (wn0 + (lane & 31)) * 128 + 16 * slot;
+    for (int h = 0; h < C::NSUB; ++h) {
+      const int slot = (2 * h + (lane >> 5)) ^ z;
+      a[h] = (wm0 + (lane & 31)) * C::KB + 16 * slot;
+      if constexpr (!C::NN) b[h] = C::B_BASE + (wn0 + (lane & 31)) * C::KB + 16 * slot;
     }
     if constexpr (C::NN) {
       const int i = lane & 15, h = lane >> 5, g1 = (lane >> 4) & 1;
@@ -221,138 +240,148 @@ struct FragAddr {
   }
 };
 
-// Fragment read r of substep s from LDS stage ST: r < TM reads P tile r
-// (af[r]), the others Q tile r - TM (bf[r - TM]).
+// A lane's operand fragments of one 16-deep substep of a k-tile: the chunk of
+// every 32-row tile of P (a) and of Q (b). A bf16 k-tile multiplies substep h
+// on its own; an e4m3 substep multiplies two of them at once as the 32-byte
+// fragments of v_mfma_scale_f32_32x32x64_f8f6f4, whose lane l holds 32
+// contraction bytes of row (A) / column (B) l % 32 at positions
+// 32 * (l / 32) + e; any assignment of contraction indices to (l / 32, e) gives
+// the same product as long as A and B agree, so the fp8 form reads exactly
+// the bytes of the bf16 form.
+template <class C>
+struct Half {
+  u32x4 a[C::TM];
+  u32x4 b[C::TN];
+};
+
+// LDS reads per substep visible to the compiler: the P chunks, then (NT) the
+// Q chunks; NN Q chunks come from read_q_nn (assembly).
+template <class C>
+constexpr int half_reads() {
+  return C::NN ? C::TM : C::TM + C::TN;
+}
+
+// Read number r of substep h of the k-tile in stage ST.
 template <class C, int ST>
-__device__ __forceinline__ void read_frag(int r, bf16x8 (&af)[C::TM], bf16x8 (&bf)[C::TN], const MLORA_LDS char *lds,
-                                          const FragAddr<C> &fa, int s) {
+__device__ __forceinline__ void read_frag(int r, int h, Half<C> &f, const MLORA_LDS char *lds, const FragAddr<C> &fa) {
   if (r < C::TM) {
-    af[r] = as_bf16x8(*(const lds_u4 *)(lds + fa.a[s] + (4096 * r + ST * C::A_BYTES)));
+    f.a[r] = *(const lds_u4 *)(lds + fa.a[h] + (32 * C::KB * r + ST * C::A_BYTES));
     return;
   }
-  if constexpr (!C::NN) {  // NN Q fragments are read per substep by read_q_nn
+  if constexpr (!C::NN) {
     const int j = r - C::TM;
-    bf[j] = as_bf16x8(*(const lds_u4 *)(lds + fa.b[s] + (4096 * j + ST * C::B_BYTES)));
+    f.b[j] = *(const lds_u4 *)(lds + fa.b[h] + (32 * C::KB * j + ST * C::B_BYTES));
   }
 }
 
-// All TN Q fragments of substep s of an NN stage: pairs of transposing reads
-// (rows 16s + 8h + (i>>2) and 4 rows further) in one block that also waits
-// for them (see lds_read_tr16_x4).
+// NN: all TN Q fragments of substep h of stage ST: pairs of transposing reads
+// (rows 16h + 8(l/32) + (l%16)/4 and 4 rows further) in one block that also
+// waits for them (see lds_read_tr16_x4).
 template <class C, int ST>
-__device__ __forceinline__ void read_q_nn(bf16x8 (&bf)[C::TN], const MLORA_LDS char *lds, const FragAddr<C> &fa,
-                                          int s) {
-  u32x4 q[C::TN];
-  const MLORA_LDS char *base = lds + (ST * C::B_BYTES + 16 * C::QROW * s);
-  if constexpr (C::TN == 4) lds_read_tr16_x4<4 * C::QROW>(base, fa.b, q);
-  else lds_read_tr16_x2<4 * C::QROW>(base, fa.b, q);
-#pragma unroll
-  for (int j = 0; j < C::TN; ++j) bf[j] = as_bf16x8(q[j]);
+__device__ __forceinline__ void read_q_nn(Half<C> &f, const MLORA_LDS char *lds, const FragAddr<C> &fa, int h) {
+  const MLORA_LDS char *base = lds + (ST * C::B_BYTES + 16 * C::QROW * h);
+  lds_read_tr16<C::TN, 4 * C::QROW>(base, fa.b, f.b);
 }
 
-// One 64-deep k-tile from LDS stage ST: 4 substeps of 16, entered with the
-// substep-0 fragments in af0/bf0 (and leaving the next stage's there). The
-// fragments of substep s+1 are read while the TM*TN MFMAs of substep s run,
-// and the loads of the next k-tile (into the other stage) are issued between
-// the MFMAs, one after every DMA_EVERY-th MFMA: issued back to back they fill
-// the texture unit's queue and stall the waves' MFMA issue behind them.
+// Substep h of the k-tile in stage ST, all reads back to back.
 template <class C, int ST>
-__device__ __forceinline__ void mma_stage(f32x16 (&acc)[C::TM][C::TN], MLORA_LDS char *lds, const FragAddr<C> &fa,
-                                          const Pipe<C> &pipe, int k0, bool kmask, bool live, int wave, int lane) {
-  // NN: the TN Q fragments come from read_q_nn (transposing reads + wait, in assembly)
-  constexpr int NR = C::NN ? C::TM : C::TM + C::TN;  // compiler-visible fragment reads per substep
-  constexpr int DSR = NR;                            // DS read instructions per substep
-  bf16x8 af[2][C::TM], bf[2][C::TN];
+__device__ __forceinline__ void read_half(Half<C> &f, int h, const MLORA_LDS char *lds, const FragAddr<C> &fa) {
 #pragma unroll
-  for (int r = 0; r < NR; ++r) read_frag<C, ST>(r, af[0], bf[0], lds, fa, 0);
-  if constexpr (C::NN) read_q_nn<C, ST>(bf[0], lds, fa, 0);
+  for (int r = 0; r < half_reads<C>(); ++r) read_frag<C, ST>(r, h, f, lds, fa);
+  if constexpr (C::NN) read_q_nn<C, ST>(f, lds, fa, h);
+}
+
+// One bf16 substep: TMN MFMAs on the fragments in `x` while substep rh of the
+// k-tile in stage RS is read into rd and loads Q0..Q1-1 of the k-tile at k0
+// go to stage LS. Reads and loads are spread evenly over the MFMAs
+// (scheduling hints keep that order): issued back to back, loads fill the
+// texture unit's queue and stall the wave's MFMA issue behind them. MFMA rows
+// <- Q (n), columns <- P (m), so each lane ends up with 4 consecutive n of
+// one row m, stored as one 8-byte write.
+template <class C, int RS, int LS, int Q0, int Q1>
+__device__ __forceinline__ void mma_half(f32x16 (&acc)[C::TM][C::TN], const Half<C> &x, Half<C> &rd, int rh,
+                                         MLORA_LDS char *lds, const FragAddr<C> &fa, const Pipe<C> &pipe, int k0,
+                                         bool kmask, bool live, int wave, int lane) {
+  constexpr int NM = C::TMN;
+  constexpr int NR = half_reads<C>();
+  constexpr int NQ = Q1 - Q0;  // loads q = Q0 + (g * NQ) / NM ... follow MFMA g
 #pragma unroll
-  for (int s = 0; s < 4; ++s) {
-    const int cur = s & 1;
-    if (s < 3) {
+  for (int g = 0; g < NM; ++g) {
 #pragma unroll
-      for (int r = 0; r < NR; ++r) read_frag<C, ST>(r, af[cur ^ 1], bf[cur ^ 1], lds, fa, s + 1);
-      if constexpr (C::NN) read_q_nn<C, ST>(bf[cur ^ 1], lds, fa, s + 1);
+    for (int r = (g * NR) / NM; r < ((g + 1) * NR) / NM; ++r) read_frag<C, RS>(r, rh, rd, lds, fa);
+    if constexpr (C::NN) {
+      if (g == NM / 2) read_q_nn<C, RS>(rd, lds, fa, rh);
     }
+    const int j = g / C::TM, i = g % C::TM;
+    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(x.b[j]), as_bf16x8(x.a[i]), acc[i][j], 0, 0, 0);
 #pragma unroll
-    for (int g = 0; g < C::TMN; ++g) {
-      const int i = g / C::TN, j = g % C::TN;
-      // MFMA rows <- Q (n), columns <- P (m): each lane ends up with 4
-      // consecutive n of one row m, stored as one 8-byte write.
-      acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bf[cur][j], af[cur][i], acc[i][j], 0, 0, 0);
-      const int idx = s * C::TMN + g;
-      if (idx % C::DMA_EVERY == 0 && idx / C::DMA_EVERY < C::NDMA)
-        pipe.issue_one(lds, idx / C::DMA_EVERY, ST ^ 1, k0, wave, lane, kmask, live);
-    }
-    // scheduling hints: DS reads spread evenly over the MFMAs, each load right after its MFMA
+    for (int q = (g * NQ) / NM; q < ((g + 1) * NQ) / NM; ++q)
+      pipe.issue_one(lds, Q0 + q, LS, k0, wave, lane, kmask, live);
+  }
 #pragma unroll
-    for (int g = 0; g < C::TMN; ++g) {
-      const int nr = s < 3 ? ((g + 1) * DSR) / C::TMN - (g * DSR) / C::TMN : 0;
+  for (int g = 0; g < NM; ++g) {
+    const int nr = ((g + 1) * NR) / NM - (g * NR) / NM;
+    const int nq = ((g + 1) * NQ) / NM - (g * NQ) / NM;
 #pragma unroll
-      for (int r = 0; r < nr; ++r) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // one DS read
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                                // one MFMA
-      const int idx = s * C::TMN + g;
-      if (idx % C::DMA_EVERY == 0 && idx / C::DMA_EVERY < C::NDMA)
-        __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // one load
-    }
+    for (int r = 0; r < nr; ++r) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // one DS read
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                                // one MFMA
+#pragma unroll
+    for (int q = 0; q < nq; ++q) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // one load
   }
 }
 
-// The fp8 form of mma_stage: one 128-element (128-byte) k-tile of e4m3 in 2
-// substeps of v_mfma_scale_f32_32x32x64_f8f6f4 (unit block scales). That MFMA
-// gives lane l the 32 contraction bytes of row (A) / column (B) l%32 at
-// positions 32*(l/32) + e; any assignment of k to (l/32, e) works as long as A
-// and B agree, so each operand fragment is simply the two 16-byte chunks that
-// the bf16 substeps 2s and 2s+1 read: the LDS layout and addresses are shared.
-template <class C, int ST>
-__device__ __forceinline__ void mma_stage_fp8(f32x16 (&acc)[C::TM][C::TN], MLORA_LDS char *lds, const FragAddr<C> &fa,
-                                              const Pipe<C> &pipe, int k0, bool kmask, bool live, int wave, int lane) {
-  typedef int i32x8 __attribute__((ext_vector_type(8)));
-  // one 32-byte fragment: P tile r (r < TM) or Q tile r - TM, fp8 substep s
-  auto frag = [&](int r, int s) -> i32x8 {
-    bf16x8 a[C::TM], b[C::TN];
-    read_frag<C, ST>(r, a, b, lds, fa, 2 * s);
-    const u32x4 lo = __builtin_bit_cast(u32x4, r < C::TM ? a[r] : b[r - C::TM]);
-    read_frag<C, ST>(r, a, b, lds, fa, 2 * s + 1);
-    const u32x4 hi = __builtin_bit_cast(u32x4, r < C::TM ? a[r] : b[r - C::TM]);
-    return i32x8{(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3], (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
-  };
-  i32x8 ac[C::TM], bc[C::TN], an[C::TM];
-#pragma unroll
-  for (int i = 0; i < C::TM; ++i) ac[i] = frag(i, 0);
-#pragma unroll
-  for (int j = 0; j < C::TN; ++j) bc[j] = frag(C::TM + j, 0);
-#pragma unroll
-  for (int s = 0; s < 2; ++s) {
-    if (s == 0) {
-#pragma unroll
-      for (int i = 0; i < C::TM; ++i) an[i] = frag(i, 1);
-    }
-    // j-major order: once tile j's MFMAs are issued its fragment is dead and
-    // the next substep's fragment of tile j can take its registers
-#pragma unroll
-    for (int j = 0; j < C::TN; ++j) {
-#pragma unroll
-      for (int i = 0; i < C::TM; ++i) {
-        // MFMA rows <- Q (n), columns <- P (m), as in the bf16 form
-        acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(bc[j], ac[i], acc[i][j], 0, 0, 0, 127, 0, 127);
-        const int idx = s * C::TMN + j * C::TM + i;
-        if (idx % C::DMA_EVERY == 0 && idx / C::DMA_EVERY < C::NDMA)
-          pipe.issue_one(lds, idx / C::DMA_EVERY, ST ^ 1, k0, wave, lane, kmask, live);
-      }
-      if (s == 0) bc[j] = frag(C::TM + j, 1);
-    }
-    if (s == 0) {
-#pragma unroll
-      for (int i = 0; i < C::TM; ++i) ac[i] = an[i];
-    }
-  }
+// The fragments of one e4m3 substep: two 16-byte chunks of each 32-row tile
+// as one 32-byte MFMA operand (bf16 substep 2u in elements 0-3, 2u+1 in 4-7).
+typedef int i32x8 __attribute__((ext_vector_type(8)));
+template <class C>
+struct Frag8 {
+  i32x8 a[C::TM];
+  i32x8 b[C::TN];
+};
+
+// Read number r (P tiles, then Q tiles) of e4m3 substep u of the k-tile in stage RS.
+template <class C, int RS>
+__device__ __forceinline__ i32x8 read_frag8(int r, int u, const MLORA_LDS char *lds, const FragAddr<C> &fa) {
+  Half<C> lo, hi;
+  read_frag<C, RS>(r, 2 * u, lo, lds, fa);
+  read_frag<C, RS>(r, 2 * u + 1, hi, lds, fa);
+  const u32x4 l = r < C::TM ? lo.a[r] : lo.b[r - C::TM];
+  const u32x4 h = r < C::TM ? hi.a[r] : hi.b[r - C::TM];
+  return i32x8{(int)l[0], (int)l[1], (int)l[2], (int)l[3], (int)h[0], (int)h[1], (int)h[2], (int)h[3]};
 }
 
-// Wait for this wave's direct-to-LDS loads, then publish the stage to all waves.
-__device__ __forceinline__ void stage_barrier() {
-  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
-  __syncthreads();
+// One e4m3 substep (NT only): TMN scaled MFMAs on the fragments in f, column
+// by column; once column j's MFMAs are issued its Q fragment is replaced by
+// that of e4m3 substep RU of the k-tile in stage RS, and the P fragments after
+// the last column, so the next substep's fragments reuse the registers. Loads
+// Q0..Q1-1 of the k-tile at k0 go to stage LS, spread over the MFMAs.
+template <class C, int RS, int RU, int LS, int Q0, int Q1>
+__device__ __forceinline__ void mma_fp8(f32x16 (&acc)[C::TM][C::TN], Frag8<C> &f, MLORA_LDS char *lds,
+                                        const FragAddr<C> &fa, const Pipe<C> &pipe, int k0, bool kmask, bool live,
+                                        int wave, int lane) {
+  static_assert(!C::NN, "e4m3 k-tiles are NT");
+  constexpr int NM = C::TMN;
+  constexpr int NQ = Q1 - Q0;  // loads q = Q0 + (g * NQ) / NM ... follow MFMA g
+#pragma unroll
+  for (int g = 0; g < NM; ++g) {
+    const int j = g / C::TM, i = g % C::TM;
+    acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(f.b[j], f.a[i], acc[i][j], 0, 0, 0, 127, 0, 127);
+#pragma unroll
+    for (int q = (g * NQ) / NM; q < ((g + 1) * NQ) / NM; ++q)
+      pipe.issue_one(lds, Q0 + q, LS, k0, wave, lane, kmask, live);
+    if (i == C::TM - 1) f.b[j] = read_frag8<C, RS>(C::TM + j, RU, lds, fa);
+  }
+#pragma unroll
+  for (int i = 0; i < C::TM; ++i) f.a[i] = read_frag8<C, RS>(i, RU, lds, fa);
+#pragma unroll
+  for (int g = 0; g < NM; ++g) {
+    const int nq = ((g + 1) * NQ) / NM - (g * NQ) / NM;
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+#pragma unroll
+    for (int q = 0; q < nq; ++q) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // one load
+    if (g % C::TM == C::TM - 1) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);  // two DS reads
+  }
+  __builtin_amdgcn_sched_group_barrier(0x100, 2 * C::TM, 0);
 }
 
 // Finds the next LoRA source of this tile: the next segment from `seg` on that
@@ -374,14 +403,26 @@ __device__ __forceinline__ bool next_lora_source(const GemmArgs &args, bool nn, 
 }
 
 // All contraction of one tile in a single pipelined loop over "virtual"
-// k-tiles: first the main X·Wᵀ (or dY·W) tiles, then ceil(r/64) tiles per LoRA
-// segment overlapping the tile. At a source boundary the loader is re-pointed
-// (a few scalars and two offsets); the LDS stages and the MFMA code are shared,
-// so the accumulators stay in place. Tiles past a source's contraction length
-// mask their chunks.
+// k-tiles: first the main X·Wᵀ (or dY·W) tiles, then ceil(r / (KB/2)) tiles
+// per LoRA segment overlapping the tile. At a source boundary the loader is
+// re-pointed (a few scalars and two offsets); the LDS stages and the MFMA code
+// are shared, so the accumulators stay in place. Tiles past a source's
+// contraction length mask their chunks.
+//
+// Pipeline: a ring of S = STAGES LDS stages; k-tile t lives in stage t % S.
+// Step t multiplies tile t substep by substep, each substep's fragments read
+// during the previous one. Before its last substep every wave waits for its
+// own loads of tile t+1 and the workgroup meets at a barrier: all of tile t+1
+// is then in LDS (the last substep reads its first fragments) and every wave
+// has read all of tile t, so the loads of tile t+S go to stage t % S, spread
+// over the MFMAs of the last substep. Loads past the last tile are issued
+// with every offset out of range (no data moves), so every step issues the
+// same number of loads and the vmcnt thresholds are constants; the stage loop
+// is unrolled so every LDS offset is a constant as well.
 template <class C>
 __device__ __forceinline__ void contract_tile(f32x16 (&acc)[C::TM][C::TN], const GemmArgs &args, MLORA_LDS char *lds,
                                               const FragAddr<C> &fa, int m0, int n0, int tid) {
+  constexpr int S = C::STAGES, NSUB = C::NSUB, NDMA = C::NDMA;
   const int wave = wave_id(), lane = tid & 63;
   const int row_end = min(m0 + C::BM, args.M);
   int seg = args.E != nullptr ? seg_of_row(args.seg, m0) : args.seg.n;
@@ -389,168 +430,288 @@ __device__ __forceinline__ void contract_tile(f32x16 (&acc)[C::TM][C::TN], const
   constexpr int esz0 = C::F8 ? 1 : 2;
   KSource src{static_cast<const char *>(args.P), static_cast<const char *>(args.Q), esz0 * args.ldp, esz0 * args.ldq,
               0, args.M, args.Kc, esz0};
-  int bk = 128 / src.esz;  // contraction elements per k-tile of the current source
+  int bk = C::KB / src.esz;  // contraction elements per k-tile of the current source
   int ntile = (src.klim + bk - 1) / bk;
+  // e4m3: the main contraction is padded to a multiple of S k-tiles (zero
+  // chunks) so the bf16 LoRA k-tiles start at stage 0
+  if constexpr (C::F8) ntile = (ntile + S - 1) / S * S;
+  const int n_main = ntile;  // e4m3 k-tiles (F8), before the first LoRA tile
   if (ntile == 0) {
     if (!next_lora_source(args, C::NN, m0, row_end, seg, src)) return;
-    bk = 128 / src.esz;
+    bk = C::KB / src.esz;
     ntile = (src.klim + bk - 1) / bk;
   }
-  bool kmask = src.klim % bk != 0;
+  bool kmask = ntile * bk != src.klim;
   pipe.init(src, m0, n0, args.Ncols, tid);
   int t_in_src = 0;  // index of the tile being loaded within its source
-  pipe.issue(lds, 0, 0, wave, lane, kmask);
-  stage_barrier();
-  // `more`: whether a tile after the current one exists (and was loaded)
+  bool exhausted = false;
+  int n_real = 1;  // k-tiles with data issued so far
+  // moves the loader to the next k-tile; false once every source is done
   auto advance = [&]() -> bool {
-    if (++t_in_src < ntile) return true;
-    if (!next_lora_source(args, C::NN, m0, row_end, seg, src)) return false;
-    bk = 128 / src.esz;
+    if (exhausted) return false;
+    if (t_in_src + 1 < ntile) {
+      ++t_in_src;
+      ++n_real;
+      return true;
+    }
+    if (!next_lora_source(args, C::NN, m0, row_end, seg, src)) {
+      exhausted = true;
+      return false;
+    }
+    bk = C::KB / src.esz;
     ntile = (src.klim + bk - 1) / bk;
     kmask = src.klim % bk != 0;
     pipe.init(src, m0, n0, args.Ncols, tid);
     t_in_src = 0;
+    ++n_real;
     return true;
   };
-  // One step: multiply the tile in LDS stage ST while the next tile (if any)
-  // loads into the other stage; returns whether there is a next tile.
-  auto step = [&](auto st_c, auto f8_c) -> bool {
-    constexpr int ST = decltype(st_c)::value;
-    const bool more = advance();
-    if constexpr (decltype(f8_c)::value) mma_stage_fp8<C, ST>(acc, lds, fa, pipe, t_in_src * bk, kmask, more, wave, lane);
-    else mma_stage<C, ST>(acc, lds, fa, pipe, t_in_src * bk, kmask, more, wave, lane);
-    stage_barrier();
-    return more;
+  static_for<S>([&](auto p) {  // the prologue loads k-tiles 0..S-1
+    constexpr int P = decltype(p)::value;
+    const bool live = P == 0 ? true : advance();
+#pragma unroll
+    for (int q = 0; q < NDMA; ++q) pipe.issue_one(lds, q, P, t_in_src * bk, wave, lane, kmask, live);
+    return true;
+  });
+  wait_vmcnt<(S - 1) * NDMA>();  // this wave's loads of tile 0
+  lds_pipeline_barrier();
+  int t = 0;
+  bool done = false;
+  // Runs steps from tile 0 until every tile is done or t reaches stop_at; the
+  // stage loop is unrolled so every LDS offset is a constant.
+  auto run = [&](int stop_at, auto &&step) {
+    while (!done && t < stop_at) static_for<S>([&](auto st) -> bool {
+        step(st);
+        ++t;
+        done = t >= n_real;
+        return !done && t < stop_at;
+      });
   };
-  using S0 = std::integral_constant<int, 0>;
-  using S1 = std::integral_constant<int, 1>;
-  using E4 = std::true_type;
-  using B16 = std::false_type;
+  // this wave's loads still allowed in flight at the barrier of a step: those
+  // of the tiles after t+1
+  constexpr int WAIT = (S - 2) * NDMA;
+  Half<C> h0, h1;  // fragments of the current and the next substep
   if constexpr (C::F8) {
-    // the e4m3 main contraction (at least one tile), then the bf16 LoRA tiles
-    // (operands pre-divided by the scales) from whichever stage holds the next one
-    bool more;
-    int st;
-    while (true) {
-      more = step(S0{}, E4{});
-      st = 1;
-      if (!more || src.esz != 1) break;
-      more = step(S1{}, E4{});
-      st = 0;
-      if (!more || src.esz != 1) break;
-    }
-    if (!more) return;
-    if (st == 1 && !step(S1{}, B16{})) return;
+    // e4m3 steps (NSUB / 2 substeps of TMN scaled MFMAs), the same barrier
+    // and load placement as the bf16 steps. n_main is a multiple of S, so the
+    // bf16 LoRA k-tiles start at stage 0.
+    constexpr int NS8 = NSUB / 2;
+    Frag8<C> f;
+#pragma unroll
+    for (int r = 0; r < C::TM; ++r) f.a[r] = read_frag8<C, 0>(r, 0, lds, fa);
+#pragma unroll
+    for (int r = 0; r < C::TN; ++r) f.b[r] = read_frag8<C, 0>(C::TM + r, 0, lds, fa);
+    run(n_main, [&](auto st) {
+      constexpr int ST = decltype(st)::value, NS = (ST + 1) % S;
+      const bool live = advance();
+      const int k0 = t_in_src * bk;
+      static_for<NS8>([&](auto u_c) {
+        constexpr int U = decltype(u_c)::value;
+        if constexpr (U == NS8 - 1) {
+          wait_vmcnt<WAIT>();  // this wave's loads of tile t + 1
+          lds_pipeline_barrier();
+          mma_fp8<C, NS, 0, ST, 0, NDMA>(acc, f, lds, fa, pipe, k0, kmask, live, wave, lane);
+        } else {
+          mma_fp8<C, ST, U + 1, ST, 0, 0>(acc, f, lds, fa, pipe, k0, kmask, live, wave, lane);
+        }
+        return true;
+      });
+    });
+#pragma unroll
+    for (int r = 0; r < C::TM; ++r)
+      h0.a[r] = u32x4{(uint32_t)f.a[r][0], (uint32_t)f.a[r][1], (uint32_t)f.a[r][2], (uint32_t)f.a[r][3]};
+#pragma unroll
+    for (int r = 0; r < C::TN; ++r)
+      h0.b[r] = u32x4{(uint32_t)f.b[r][0], (uint32_t)f.b[r][1], (uint32_t)f.b[r][2], (uint32_t)f.b[r][3]};
+  } else {
+    read_half<C, 0>(h0, 0, lds, fa);
   }
-  while (true) {
-    if (!step(S0{}, B16{})) break;
-    if (!step(S1{}, B16{})) break;
-  }
+  // bf16 steps: substep s from h[s % 2] while substep s+1 is read into the
+  // other; before the last substep the wait and barrier; the last substep
+  // reads substep 0 of tile t+1.
+  run(INT32_MAX, [&](auto st) {
+    constexpr int ST = decltype(st)::value, NS = (ST + 1) % S;
+    const bool live = advance();
+    const int k0 = t_in_src * bk;
+    static_for<NSUB>([&](auto s_c) {
+      constexpr int SS = decltype(s_c)::value;
+      Half<C> &x = SS % 2 == 0 ? h0 : h1;
+      Half<C> &y = SS % 2 == 0 ? h1 : h0;
+      if constexpr (SS < NSUB - 1) {
+        mma_half<C, ST, ST, 0, 0>(acc, x, y, SS + 1, lds, fa, pipe, k0, kmask, live, wave, lane);
+      } else {
+        wait_vmcnt<WAIT>();  // this wave's loads of tile t + 1
+        lds_pipeline_barrier();
+        mma_half<C, NS, ST, 0, NDMA>(acc, x, y, 0, lds, fa, pipe, k0, kmask, live, wave, lane);
+      }
+      return true;
+    });
+  });
+  wait_vmcnt<0>();
 }
 
+// Output tile of physical index p: XCD-contiguous logical ids (workgroups
+// are dealt round-robin over the 8 XCDs), then groups of GROUP_M row-tiles
+// walked column by column so concurrently running tiles share P rows and Q
+// columns in L2.
 template <class C>
-__global__ __launch_bounds__(C::THREADS) void gemm_kernel(const GemmArgs args) {
-  __shared__ u32x4 smem[C::LDS_BYTES / 16];
-  MLORA_LDS char *lds = (MLORA_LDS char *)smem;
-  const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
-  const int wm0 = (wave / C::WN) * (C::BM / C::WM);
-  const int wn0 = (wave % C::WN) * (C::BN / C::WN);
-
-  // Tile order: XCD-contiguous ids, then groups of GROUP_M row-tiles walked
-  // column by column so concurrently running tiles share P rows and Q columns in L2.
+__device__ __forceinline__ void tile_origin(const GemmArgs &args, int p, int &m0, int &n0) {
   const int nblocks = args.tiles_m * args.tiles_n;
-  const int id = xcd_remap(blockIdx.x, nblocks);
+  const int id = xcd_remap(p, nblocks);
   const int per_group = C::GROUP_M * args.tiles_n;
   const int group = id / per_group;
   const int first_m = group * C::GROUP_M;
   const int gsize = min(args.tiles_m - first_m, C::GROUP_M);
   const int tm = first_m + (id % per_group) % gsize;
   const int tn = (id % per_group) / gsize;
-  const int m0 = tm * C::BM, n0 = tn * C::BN;
+  m0 = tm * C::BM;
+  n0 = tn * C::BN;
+}
 
-  // Register 4g + e of tile (i, j) holds row m = m0 + wm0 + 32i + lane%32 and
-  // column n = n0 + wn0 + 32j + 8g + 4(lane/32) + e.
-  auto bias_of = [&](int n, float (&v)[4]) {
-    v[0] = v[1] = v[2] = v[3] = 0.f;
-    if (n < args.Ncols) {
-      if (args.bias_dtype == MLORA_F32) {
-        const f32x4 b = *(const MLORA_GLOBAL f32x4 *)(static_cast<const float *>(args.bias) + n);
-        v[0] = b[0]; v[1] = b[1]; v[2] = b[2]; v[3] = b[3];
-      } else if (args.bias_dtype == MLORA_BF16) {
-        const u32x2 b = *(const MLORA_GLOBAL u32x2 *)(static_cast<const uint16_t *>(args.bias) + n);
-        v[0] = bf16_to_f32(b.x & 0xffff); v[1] = bf16_to_f32(b.x >> 16);
-        v[2] = bf16_to_f32(b.y & 0xffff); v[3] = bf16_to_f32(b.y >> 16);
-      }
-    }
-  };
-  f32x16 acc[C::TM][C::TN];
-  if constexpr (!C::F8) {
-    // bf16: accumulators start at the bias of their column
-#pragma unroll
-    for (int j = 0; j < C::TN; ++j) {
-      f32x16 b0;
-#pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        float v[4];
-        bias_of(n0 + wn0 + 32 * j + 8 * g + 4 * (lane >> 5), v);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) b0[4 * g + e] = v[e];
-      }
-#pragma unroll
-      for (int i = 0; i < C::TM; ++i) acc[i][j] = b0;
-    }
+// Entries c + 4 * hi .. c + 4 * hi + 3 of a per-column vector (f32, or bf16
+// when BF16) as f32: the eight entries c..c+7 come through the scalar data
+// cache (c is wave-uniform; Ncols is a multiple of 8, so they are all in
+// range or all past Ncols: zeros) and each lane picks its half. Scalar loads
+// are waited for with lgkmcnt, so the epilogue does not wait for
+// direct-to-LDS loads still in flight.
+typedef const __attribute__((address_space(4))) float cf32;
+typedef const __attribute__((address_space(4))) uint32_t cu32;
+__device__ __forceinline__ f32x4 col4(const void *p, bool bf16, int c, int ncols, bool hi) {
+  c = __builtin_amdgcn_readfirstlane(c);  // uniform by construction; keeps the loads scalar
+  if (c >= ncols) return f32x4{0.f, 0.f, 0.f, 0.f};
+  f32x4 lo4, hi4;
+  if (bf16) {
+    const cu32 *q = (const cu32 *)((const uint16_t *)p + c);
+    const uint32_t w0 = q[0], w1 = q[1], w2 = q[2], w3 = q[3];
+    lo4 = f32x4{bf16_to_f32(w0 & 0xffff), bf16_to_f32(w0 >> 16), bf16_to_f32(w1 & 0xffff), bf16_to_f32(w1 >> 16)};
+    hi4 = f32x4{bf16_to_f32(w2 & 0xffff), bf16_to_f32(w2 >> 16), bf16_to_f32(w3 & 0xffff), bf16_to_f32(w3 >> 16)};
   } else {
-#pragma unroll
-    for (int i = 0; i < C::TM; ++i)
-#pragma unroll
-      for (int j = 0; j < C::TN; ++j)
-#pragma unroll
-        for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
+    const cf32 *q = (const cf32 *)((const float *)p + c);
+    lo4 = f32x4{q[0], q[1], q[2], q[3]};
+    hi4 = f32x4{q[4], q[5], q[6], q[7]};
   }
-  FragAddr<C> fa;
-  fa.init(wm0, wn0, lane);
+  return hi ? hi4 : lo4;
+}
 
-  contract_tile<C>(acc, args, lds, fa, m0, n0, tid);
-
-  // epilogue: (fp8: scale and bias), (+ Y), round to bf16, 8-byte stores of 4 consecutive n
+// Epilogue of one output tile, column tile by column tile: (fp8:
+// x_scale[m]·w_scale[n]), + bias, (+ Y), round to bf16. Register 4g + e of
+// tile (i, j) holds row m = m0 + wm0 + 32i + lane%32 and column
+// n = n0 + wn0 + 32j + 8g + 4(lane/32) + e.
+// STAGED: the rounded tile is staged in LDS (whose operand stages must be
+// free), row-major with 16-byte chunk q of row r at slot q ^ (r % CH), and
+// leaves in 16-byte stores that cover whole rows. Otherwise (and always when
+// accumulating into Y, which adds the old value in fp32 before the one
+// rounding) each lane stores its 4 consecutive columns directly.
+template <class C, bool STAGED, bool ACCUM = true>
+__device__ __forceinline__ void store_tile(const f32x16 (&acc)[C::TM][C::TN], const GemmArgs &args, MLORA_LDS char *lds,
+                                           int m0, int n0, int wm0, int wn0, int lane, int wave) {
   const int rows_here = min(C::BM, args.M - m0);
   const int64_t ldy_b = args.ldy * 2;
   const __amdgpu_buffer_rsrc_t ry = make_rsrc(args.Y + (int64_t)m0 * args.ldy, rows_here * ldy_b);
+  constexpr int ROWB = C::BN * 2;  // bytes per staged row
+  constexpr int CH = C::BN / 8;    // 16-byte chunks per staged row
+  static_assert(!STAGED || C::LDS_BYTES >= C::BM * ROWB, "the staged output tile fits the operand stages");
+  const bool staged = STAGED && !(ACCUM && args.accumulate);
+  if (staged) lds_pipeline_barrier();  // every wave's operand loads have landed and been read
+  float ps[C::TM];  // fp8: x_scale of each row tile's row
 #pragma unroll
   for (int i = 0; i < C::TM; ++i) {
-    const int ml = wm0 + 32 * i + (lane & 31);
-    float ps = 1.f;
-    if constexpr (C::F8) ps = m0 + ml < args.M ? args.psc[m0 + ml] : 0.f;
+    const int m = m0 + wm0 + 32 * i + (lane & 31);
+    ps[i] = 1.f;
+    if constexpr (C::F8) ps[i] = m < args.M ? args.psc[m] : 0.f;
+  }
 #pragma unroll
-    for (int j = 0; j < C::TN; ++j) {
+  for (int j = 0; j < C::TN; ++j) {
+    // bias and (fp8) w_scale of this lane's 16 columns of tile j, zero past Ncols
+    float bias[16], qs[16];
 #pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const int n = n0 + wn0 + 32 * j + 8 * g + 4 * (lane >> 5);
-        float v[4];
+    for (int v = 0; v < 16; ++v) bias[v] = 0.f, qs[v] = 1.f;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) v[e] = acc[i][j][4 * g + e];
-        if constexpr (C::F8) {
-          // acc = Σ xq·wq + Σ (h/x_scale)·(B/w_scale): one scaling restores both, then the bias
-          float b[4], qs[4] = {0.f, 0.f, 0.f, 0.f};
-          bias_of(n, b);
-          if (n < args.Ncols) {
-            const f32x4 q = *(const MLORA_GLOBAL f32x4 *)(args.qsc + n);
-            qs[0] = q[0]; qs[1] = q[1]; qs[2] = q[2]; qs[3] = q[3];
-          }
+    for (int g = 0; g < 4; ++g) {
+      const int c = n0 + wn0 + 32 * j + 8 * g;  // wave-uniform: this lane takes c + 4 * (lane / 32) + e
+      const bool hi = lane >= 32;
+      if (args.bias_dtype >= 0) {
+        const f32x4 b4 = col4(args.bias, args.bias_dtype == MLORA_BF16, c, args.Ncols, hi);
 #pragma unroll
-          for (int e = 0; e < 4; ++e) v[e] = v[e] * (ps * qs[e]) + b[e];
-        }
-        // rows past M / columns past Ncols fall outside ry or are dropped
-        const int32_t off = (ml < rows_here && n < args.Ncols) ? (int32_t)(ml * ldy_b + n * 2) : kOOB;
-        if (args.accumulate && off != kOOB) {
-          const u32x2 o = *(const MLORA_GLOBAL u32x2 *)(args.Y + (int64_t)(m0 + ml) * args.ldy + n);
-          v[0] += bf16_to_f32(o.x & 0xffff); v[1] += bf16_to_f32(o.x >> 16);
-          v[2] += bf16_to_f32(o.y & 0xffff); v[3] += bf16_to_f32(o.y >> 16);
-        }
-        buf_store8(ry, off, make_uint2(pack2_bf16(v[0], v[1]), pack2_bf16(v[2], v[3])));
+        for (int e = 0; e < 4; ++e) bias[4 * g + e] = b4[e];
+      }
+      if constexpr (C::F8) {
+        const f32x4 q4 = col4(args.qsc, false, c, args.Ncols, hi);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) qs[4 * g + e] = q4[e];
       }
     }
+#pragma unroll
+    for (int i = 0; i < C::TM; ++i) {
+      const int ml = wm0 + 32 * i + (lane & 31);
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int nl = wn0 + 32 * j + 8 * g + 4 * (lane >> 5);  // tile-local column
+        const int n = n0 + nl;
+        float v[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          v[e] = acc[i][j][4 * g + e];
+          // e4m3: acc = Σ xq·wq + Σ (h/x_scale)·(B/w_scale): one scaling restores both
+          if constexpr (C::F8) v[e] *= ps[i] * qs[4 * g + e];
+          v[e] += bias[4 * g + e];
+        }
+        if (staged) {
+          const int slot = (nl >> 3) ^ (ml % CH);
+          *(MLORA_LDS u32x2 *)(lds + ml * ROWB + 16 * slot + 8 * ((nl >> 2) & 1)) =
+              u32x2{pack2_bf16(v[0], v[1]), pack2_bf16(v[2], v[3])};
+        } else {
+          // rows past M / columns past Ncols fall outside ry or are dropped
+          const int32_t off = (ml < rows_here && n < args.Ncols) ? (int32_t)(ml * ldy_b + n * 2) : kOOB;
+          if (ACCUM && args.accumulate && off != kOOB) {
+            const u32x2 o = *(const MLORA_GLOBAL u32x2 *)(args.Y + (int64_t)(m0 + ml) * args.ldy + n);
+            v[0] += bf16_to_f32(o.x & 0xffff); v[1] += bf16_to_f32(o.x >> 16);
+            v[2] += bf16_to_f32(o.y & 0xffff); v[3] += bf16_to_f32(o.y >> 16);
+          }
+          buf_store8(ry, off, make_uint2(pack2_bf16(v[0], v[1]), pack2_bf16(v[2], v[3])));
+        }
+      }
+      __builtin_amdgcn_sched_barrier(0);  // one accumulator tile at a time
+    }
   }
+  if (!staged) return;
+  lds_pipeline_barrier();
+  // each wave stores BM / NW rows, 1 KB (1024 / ROWB rows) per instruction
+  constexpr int RPI = 1024 / ROWB;
+  constexpr int ROWS_W = C::BM / C::NW;
+  static_assert(ROWS_W % RPI == 0, "whole store instructions per wave");
+#pragma unroll
+  for (int it = 0; it < ROWS_W / RPI; ++it) {
+    const int r = wave * ROWS_W + it * RPI + lane / CH;
+    const int q = lane % CH;
+    const u32x4 d = *(const lds_u4 *)(lds + r * ROWB + 16 * (q ^ (r % CH)));
+    const int n = n0 + 8 * q;
+    const int32_t off = (r < rows_here && n < args.Ncols) ? (int32_t)(r * ldy_b + n * 2) : kOOB;
+    buf_store16(ry, off, d);
+  }
+}
+
+// One workgroup per output tile.
+template <class C>
+__global__ __launch_bounds__(C::THREADS, C::WAVES_PER_SIMD) void gemm_kernel(const GemmArgs args) {
+  __shared__ u32x4 smem[C::LDS_BYTES / 16];
+  MLORA_LDS char *lds = (MLORA_LDS char *)smem;
+  const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
+  const int wm0 = (wave / C::WN) * (C::BM / C::WM);
+  const int wn0 = (wave % C::WN) * (C::BN / C::WN);
+  int m0, n0;
+  tile_origin<C>(args, blockIdx.x, m0, n0);
+  f32x16 acc[C::TM][C::TN];
+#pragma unroll
+  for (int i = 0; i < C::TM; ++i)
+#pragma unroll
+    for (int j = 0; j < C::TN; ++j)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
+  FragAddr<C> fa;
+  fa.init(wm0, wn0, lane);
+  contract_tile<C>(acc, args, lds, fa, m0, n0, tid);
+  store_tile<C, true>(acc, args, lds, m0, n0, wm0, wn0, lane, wave);
 }
 
 using CfgNT256 = GemmCfg<256, 256, 4, 2, false>;
@@ -573,6 +734,8 @@ static int launch_gemm(GemmArgs &a, hipStream_t stream) {
 
 // Tile choice (measured on MI355X at the Wan shapes): the 8-wave 256x256 tile
 // whenever it still gives every CU a tile; the 4-wave 128x128 tile otherwise.
+// (A persistent form whose k-tile ring runs across output tiles, and
+// 256x128 tiles with a 3-stage ring, both measured slower.)
 template <class Big, class Small>
 static int dispatch_gemm(GemmArgs &a, hipStream_t stream) {
   const int64_t big_tiles = (int64_t)((a.M + 255) / 256) * ((a.Ncols + 255) / 256);

@@ -42,23 +42,6 @@ static int64_t build_pad(PadTable &pt, const SegTable &st) {
   return p;
 }
 
-// f(integral_constant<int, 0>), f(..1), ... f(..N-1), stopping at the first false.
-template <class F, int... K>
-__device__ __forceinline__ void static_for_impl(F &&f, std::integer_sequence<int, K...>) {
-  (void)(f(std::integral_constant<int, K>{}) && ...);
-}
-template <int N, class F>
-__device__ __forceinline__ void static_for(F &&f) {
-  static_for_impl(f, std::make_integer_sequence<int, N>{});
-}
-
-// vmcnt(n) with the other counters left alone (gfx9 s_waitcnt encoding).
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-  static_assert(N >= 0 && N < 64, "vmcnt range");
-  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | 0x0F70);
-}
-
 // ============================================================== shrink
 //
 // Workgroup: 4 waves x 32 rows of one segment, all r <= 32*RT columns of its
