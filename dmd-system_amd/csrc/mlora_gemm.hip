@@ -46,7 +46,8 @@ struct GemmArgs {
   SegTable seg;
 };
 
-template <int BM_, int BN_, int WM_, int WN_, bool NN_, bool F8_ = false, int KB_ = 128, int STAGES_ = 2>
+template <int BM_, int BN_, int WM_, int WN_, bool NN_, bool F8_ = false, int KB_ = 128, int STAGES_ = 2,
+          bool RING5_ = false>
 struct GemmCfg {
   static constexpr int BM = BM_, BN = BN_, WM = WM_, WN = WN_;
   static constexpr bool NN = NN_;
@@ -77,9 +78,24 @@ struct GemmCfg {
   static_assert(!NN || (QCPR >= 16 && QRPD >= 1), "NN rows hold at least 16 chunks");
   static constexpr int NDMA = A_DMA + B_DMA;  // 1 KB loads per wave and k-tile
   static constexpr int TMN = TM * TN;  // MFMAs per wave and 16-deep bf16 substep (or e4m3 substep)
-  // LDS (bytes): P stages 0..STAGES-1 | Q stages 0..STAGES-1
-  static constexpr int B_BASE = STAGES * A_BYTES;
-  static constexpr int LDS_BYTES = STAGES * (A_BYTES + B_BYTES);
+  // LDS layout. Stages: P stages 0..STAGES-1 | Q stages 0..STAGES-1; k-tile t
+  // in stage t % STAGES, and a step loads the k-tile STAGES ahead into the
+  // stage its barrier freed. RING5 (bf16 256x256, 128-byte rows): five 32 KB
+  // slots, k-tile t's P in slot 2t % 5 and Q in slot (2t + 1) % 5: a step
+  // loads the k-tile 2 ahead, its P into the slot the previous barrier freed
+  // (issued in the first substep) and its Q into the slot its own barrier
+  // frees — 1.5 k-tiles in flight instead of 1 in the same 160 KB.
+  static constexpr bool RING5 = RING5_;
+  static_assert(!RING5 || (!F8 && A_BYTES == 32768 && B_BYTES == 32768), "slots hold one 256-row operand tile");
+  static constexpr int PERIOD = RING5 ? 5 : STAGES;  // steps until the LDS offsets repeat
+  static constexpr int AHEAD = RING5 ? 2 : STAGES;   // a step loads the k-tile this far ahead
+  static constexpr int B_BASE = RING5 ? 0 : STAGES * A_BYTES;
+  static constexpr int LDS_BYTES = RING5 ? 5 * A_BYTES : STAGES * (A_BYTES + B_BYTES);
+  // LDS offsets of the P and Q tiles of a k-tile in phase ph (its index mod
+  // PERIOD). Stages: the Q fragment addresses carry B_BASE, so q_off is
+  // relative to it and stays within the 16-bit ds_read offset field.
+  static constexpr int p_off(int ph) { return RING5 ? ((2 * ph) % 5) * A_BYTES : ph * A_BYTES; }
+  static constexpr int q_off(int ph) { return RING5 ? ((2 * ph + 1) % 5) * A_BYTES : ph * B_BYTES; }
   static_assert(LDS_BYTES <= 163840, "the ring must fit the 160 KB of LDS");
   static constexpr int GROUP_M = 8;
   // occupancy the register budget is sized for: a 256x256 tile fills the LDS
@@ -171,13 +187,14 @@ struct Pipe {
   }
 
   // Issue 1 KB load number q (of NDMA per wave) of the k-tile starting at k0
-  // into LDS stage `st`: q < A_DMA are P rows, the rest Q. live == false turns
-  // every lane's offset out of range: the instruction then moves no data.
-  __device__ __forceinline__ void issue_one(MLORA_LDS char *lds, int q, int st, int k0, int wave, int lane, bool KMASK,
+  // into the LDS tiles of phase ph: q < A_DMA are P rows, the rest Q.
+  // live == false turns every lane's offset out of range: the instruction then
+  // moves no data.
+  __device__ __forceinline__ void issue_one(MLORA_LDS char *lds, int q, int ph, int k0, int wave, int lane, bool KMASK,
                                             bool live) const {
     if (q < C::A_DMA) {
       const int blk = wave * C::A_DMA + q;  // wave-uniform
-      MLORA_LDS void *dst = lds + st * C::A_BYTES + blk * 1024;
+      MLORA_LDS void *dst = lds + C::p_off(ph) + blk * 1024;
       const int row = a_row0 + C::RPD * q;
       const int par = blk & 1;
       int32_t off = a_off[par];
@@ -189,7 +206,7 @@ struct Pipe {
     } else if constexpr (!C::NN) {
       const int qb = q - C::A_DMA;
       const int blk = wave * C::B_DMA + qb;
-      MLORA_LDS void *dst = lds + C::B_BASE + st * C::B_BYTES + blk * 1024;
+      MLORA_LDS void *dst = lds + C::B_BASE + C::q_off(ph) + blk * 1024;
       const int row = b_row0 + C::RPD * qb;
       const int par = blk & 1;
       int32_t off = (KMASK && k0 + b_kc[par] >= klim) ? kOOB : b_off[par];
@@ -198,7 +215,7 @@ struct Pipe {
       __builtin_amdgcn_raw_ptr_buffer_load_lds(rq, dst, 16, off, soff, 0, 0);
     } else {
       const int blk = wave * C::B_DMA + (q - C::A_DMA);  // wave-uniform
-      MLORA_LDS void *dst = lds + C::B_BASE + st * C::B_BYTES + blk * 1024;
+      MLORA_LDS void *dst = lds + C::B_BASE + C::q_off(ph) + blk * 1024;
       const int row = C::QRPD * blk;
       int32_t off = (KMASK && k0 + row + b_kc[0] >= klim) ? kOOB : b_off[blk & 1];
       if (!live) off = kOOB;
@@ -208,9 +225,9 @@ struct Pipe {
   }
 };
 
-// Byte addresses (stage 0, first 32-row tile) of this lane's fragments for
-// each 16-deep substep of a k-tile; further tiles are +32 * KB bytes and stage
-// s is +s * A_BYTES / +s * B_BYTES, folded into the ds_read offset field.
+// Byte addresses (first 32-row tile, phase 0 layout: P at 0, Q at B_BASE) of
+// this lane's fragments for each 16-deep substep of a k-tile; further tiles
+// are +32 * KB bytes and the phase's p_off / q_off is added as a constant.
 // NN: b[j] is the first of the two transposing reads of tile j at substep 0
 // (substep h adds 16 rows, the second read 4 rows). ds_read_b64_tr_b16 gives
 // lane j of a 16-lane group element e = element (j & 3) of the 8 bytes
@@ -261,39 +278,39 @@ constexpr int half_reads() {
   return C::NN ? C::TM : C::TM + C::TN;
 }
 
-// Read number r of substep h of the k-tile in stage ST.
-template <class C, int ST>
+// Read number r of substep h of the k-tile in phase PH.
+template <class C, int PH>
 __device__ __forceinline__ void read_frag(int r, int h, Half<C> &f, const MLORA_LDS char *lds, const FragAddr<C> &fa) {
   if (r < C::TM) {
-    f.a[r] = *(const lds_u4 *)(lds + fa.a[h] + (32 * C::KB * r + ST * C::A_BYTES));
+    f.a[r] = *(const lds_u4 *)(lds + fa.a[h] + (32 * C::KB * r + C::p_off(PH)));
     return;
   }
   if constexpr (!C::NN) {
     const int j = r - C::TM;
-    f.b[j] = *(const lds_u4 *)(lds + fa.b[h] + (32 * C::KB * j + ST * C::B_BYTES));
+    f.b[j] = *(const lds_u4 *)(lds + fa.b[h] + (32 * C::KB * j + C::q_off(PH)));
   }
 }
 
-// NN: all TN Q fragments of substep h of stage ST: pairs of transposing reads
-// (rows 16h + 8(l/32) + (l%16)/4 and 4 rows further) in one block that also
-// waits for them (see lds_read_tr16_x4).
-template <class C, int ST>
+// NN: all TN Q fragments of substep h of the k-tile in phase PH: pairs of
+// transposing reads (rows 16h + 8(l/32) + (l%16)/4 and 4 rows further) in one
+// block that also waits for them (see lds_read_tr16_x4).
+template <class C, int PH>
 __device__ __forceinline__ void read_q_nn(Half<C> &f, const MLORA_LDS char *lds, const FragAddr<C> &fa, int h) {
-  const MLORA_LDS char *base = lds + (ST * C::B_BYTES + 16 * C::QROW * h);
+  const MLORA_LDS char *base = lds + (C::q_off(PH) + 16 * C::QROW * h);
   lds_read_tr16<C::TN, 4 * C::QROW>(base, fa.b, f.b);
 }
 
-// Substep h of the k-tile in stage ST, all reads back to back.
-template <class C, int ST>
+// Substep h of the k-tile in phase PH, all reads back to back.
+template <class C, int PH>
 __device__ __forceinline__ void read_half(Half<C> &f, int h, const MLORA_LDS char *lds, const FragAddr<C> &fa) {
 #pragma unroll
-  for (int r = 0; r < half_reads<C>(); ++r) read_frag<C, ST>(r, h, f, lds, fa);
-  if constexpr (C::NN) read_q_nn<C, ST>(f, lds, fa, h);
+  for (int r = 0; r < half_reads<C>(); ++r) read_frag<C, PH>(r, h, f, lds, fa);
+  if constexpr (C::NN) read_q_nn<C, PH>(f, lds, fa, h);
 }
 
 // One bf16 substep: TMN MFMAs on the fragments in `x` while substep rh of the
-// k-tile in stage RS is read into rd and loads Q0..Q1-1 of the k-tile at k0
-// go to stage LS. Reads and loads are spread evenly over the MFMAs
+// k-tile in phase RS is read into rd and loads Q0..Q1-1 of the k-tile at k0
+// go to the LDS tiles of phase LS. Reads and loads are spread evenly over the MFMAs
 // (scheduling hints keep that order): issued back to back, loads fill the
 // texture unit's queue and stall the wave's MFMA issue behind them. MFMA rows
 // <- Q (n), columns <- P (m), so each lane ends up with 4 consecutive n of
@@ -339,7 +356,7 @@ struct Frag8 {
   i32x8 b[C::TN];
 };
 
-// Read number r (P tiles, then Q tiles) of e4m3 substep u of the k-tile in stage RS.
+// Read number r (P tiles, then Q tiles) of e4m3 substep u of the k-tile in phase RS.
 template <class C, int RS>
 __device__ __forceinline__ i32x8 read_frag8(int r, int u, const MLORA_LDS char *lds, const FragAddr<C> &fa) {
   Half<C> lo, hi;
@@ -352,9 +369,9 @@ __device__ __forceinline__ i32x8 read_frag8(int r, int u, const MLORA_LDS char *
 
 // One e4m3 substep (NT only): TMN scaled MFMAs on the fragments in f, column
 // by column; once column j's MFMAs are issued its Q fragment is replaced by
-// that of e4m3 substep RU of the k-tile in stage RS, and the P fragments after
+// that of e4m3 substep RU of the k-tile in phase RS, and the P fragments after
 // the last column, so the next substep's fragments reuse the registers. Loads
-// Q0..Q1-1 of the k-tile at k0 go to stage LS, spread over the MFMAs.
+// Q0..Q1-1 of the k-tile at k0 go to the tiles of phase LS, spread over the MFMAs.
 template <class C, int RS, int RU, int LS, int Q0, int Q1>
 __device__ __forceinline__ void mma_fp8(f32x16 (&acc)[C::TM][C::TN], Frag8<C> &f, MLORA_LDS char *lds,
                                         const FragAddr<C> &fa, const Pipe<C> &pipe, int k0, bool kmask, bool live,
@@ -409,20 +426,22 @@ __device__ __forceinline__ bool next_lora_source(const GemmArgs &args, bool nn, 
 // are shared, so the accumulators stay in place. Tiles past a source's
 // contraction length mask their chunks.
 //
-// Pipeline: a ring of S = STAGES LDS stages; k-tile t lives in stage t % S.
-// Step t multiplies tile t substep by substep, each substep's fragments read
-// during the previous one. Before its last substep every wave waits for its
-// own loads of tile t+1 and the workgroup meets at a barrier: all of tile t+1
-// is then in LDS (the last substep reads its first fragments) and every wave
-// has read all of tile t, so the loads of tile t+S go to stage t % S, spread
-// over the MFMAs of the last substep. Loads past the last tile are issued
-// with every offset out of range (no data moves), so every step issues the
-// same number of loads and the vmcnt thresholds are constants; the stage loop
-// is unrolled so every LDS offset is a constant as well.
+// Pipeline: k-tile t lives in the LDS tiles of phase t % PERIOD (see
+// GemmCfg). Step t multiplies tile t substep by substep, each substep's
+// fragments read during the previous one. Before its last substep every wave
+// waits for its own loads of tile t+1 and the workgroup meets at a barrier:
+// all of tile t+1 is then in LDS (the last substep reads its first fragments)
+// and every wave has read all of tile t, whose tiles the loads of tile
+// t+AHEAD now fill, spread over the MFMAs of the last substep (RING5: the P
+// half of those loads goes, during the first substep, to the slot the
+// previous barrier freed). Loads past the last tile are issued with every
+// offset out of range (no data moves), so every step issues the same number
+// of loads and the vmcnt thresholds are constants; the phase loop is unrolled
+// so every LDS offset is a constant as well.
 template <class C>
 __device__ __forceinline__ void contract_tile(f32x16 (&acc)[C::TM][C::TN], const GemmArgs &args, MLORA_LDS char *lds,
                                               const FragAddr<C> &fa, int m0, int n0, int tid) {
-  constexpr int S = C::STAGES, NSUB = C::NSUB, NDMA = C::NDMA;
+  constexpr int S = C::PERIOD, NSUB = C::NSUB, NDMA = C::NDMA;
   const int wave = wave_id(), lane = tid & 63;
   const int row_end = min(m0 + C::BM, args.M);
   int seg = args.E != nullptr ? seg_of_row(args.seg, m0) : args.seg.n;
@@ -466,14 +485,14 @@ __device__ __forceinline__ void contract_tile(f32x16 (&acc)[C::TM][C::TN], const
     ++n_real;
     return true;
   };
-  static_for<S>([&](auto p) {  // the prologue loads k-tiles 0..S-1
+  static_for<C::AHEAD>([&](auto p) {  // the prologue loads k-tiles 0..AHEAD-1
     constexpr int P = decltype(p)::value;
     const bool live = P == 0 ? true : advance();
 #pragma unroll
     for (int q = 0; q < NDMA; ++q) pipe.issue_one(lds, q, P, t_in_src * bk, wave, lane, kmask, live);
     return true;
   });
-  wait_vmcnt<(S - 1) * NDMA>();  // this wave's loads of tile 0
+  wait_vmcnt<(C::AHEAD - 1) * NDMA>();  // this wave's loads of tile 0
   lds_pipeline_barrier();
   int t = 0;
   bool done = false;
@@ -488,8 +507,10 @@ __device__ __forceinline__ void contract_tile(f32x16 (&acc)[C::TM][C::TN], const
       });
   };
   // this wave's loads still allowed in flight at the barrier of a step: those
-  // of the tiles after t+1
-  constexpr int WAIT = (S - 2) * NDMA;
+  // of the tiles after t+1 (RING5: the P half of tile t+2, issued in the first
+  // substep)
+  constexpr int PQ = C::RING5 ? C::A_DMA : 0;  // loads of a step issued before its barrier
+  constexpr int WAIT = C::RING5 ? PQ : (C::AHEAD - 2) * NDMA;
   Half<C> h0, h1;  // fragments of the current and the next substep
   if constexpr (C::F8) {
     // e4m3 steps (NSUB / 2 substeps of TMN scaled MFMAs), the same barrier
@@ -530,19 +551,20 @@ __device__ __forceinline__ void contract_tile(f32x16 (&acc)[C::TM][C::TN], const
   // other; before the last substep the wait and barrier; the last substep
   // reads substep 0 of tile t+1.
   run(INT32_MAX, [&](auto st) {
-    constexpr int ST = decltype(st)::value, NS = (ST + 1) % S;
-    const bool live = advance();
+    constexpr int ST = decltype(st)::value, NS = (ST + 1) % S, LS = (ST + C::AHEAD) % S;
+    const bool live = advance();  // tile t + AHEAD
     const int k0 = t_in_src * bk;
     static_for<NSUB>([&](auto s_c) {
       constexpr int SS = decltype(s_c)::value;
       Half<C> &x = SS % 2 == 0 ? h0 : h1;
       Half<C> &y = SS % 2 == 0 ? h1 : h0;
       if constexpr (SS < NSUB - 1) {
-        mma_half<C, ST, ST, 0, 0>(acc, x, y, SS + 1, lds, fa, pipe, k0, kmask, live, wave, lane);
+        constexpr int Q1 = SS == 0 ? PQ : 0;
+        mma_half<C, ST, LS, 0, Q1>(acc, x, y, SS + 1, lds, fa, pipe, k0, kmask, live, wave, lane);
       } else {
         wait_vmcnt<WAIT>();  // this wave's loads of tile t + 1
         lds_pipeline_barrier();
-        mma_half<C, NS, ST, 0, NDMA>(acc, x, y, 0, lds, fa, pipe, k0, kmask, live, wave, lane);
+        mma_half<C, NS, LS, PQ, NDMA>(acc, x, y, 0, lds, fa, pipe, k0, kmask, live, wave, lane);
       }
       return true;
     });
@@ -714,10 +736,10 @@ __global__ __launch_bounds__(C::THREADS, C::WAVES_PER_SIMD) void gemm_kernel(con
   store_tile<C, true>(acc, args, lds, m0, n0, wm0, wn0, lane, wave);
 }
 
-using CfgNT256 = GemmCfg<256, 256, 4, 2, false>;
+using CfgNT256 = GemmCfg<256, 256, 4, 2, false, false, 128, 2, true>;
 using CfgF8256 = GemmCfg<256, 256, 4, 2, false, true>;
 using CfgF8128 = GemmCfg<128, 128, 2, 2, false, true>;
-using CfgNN256 = GemmCfg<256, 256, 4, 2, true>;
+using CfgNN256 = GemmCfg<256, 256, 4, 2, true, false, 128, 2, true>;
 using CfgNT128 = GemmCfg<128, 128, 2, 2, false>;
 using CfgNN128 = GemmCfg<128, 128, 2, 2, true>;
 
