@@ -113,12 +113,14 @@ def main():
         L = dict(name=name, K=K, N=N, x=x, w=w, b=b, As=As, Bs=Bs, dy=dy)
         if fp8:
             L["wq"], L["ws"] = kernels.quantize_rows_fp8(w)
+            L["wqt"] = L["wq"].t().contiguous()  # the frozen e4m3 base transposed, for the e4m3 dX
         lins.append(L)
     torch.cuda.synchronize()
 
     def forward(L):
         if fp8:
-            return pkg.multi_lora_linear_fp8(L["x"], L["wq"], L["ws"], L["b"], L["As"], L["Bs"], scales, routing)
+            return pkg.multi_lora_linear_fp8(L["x"], L["wq"], L["ws"], L["b"], L["As"], L["Bs"], scales, routing,
+                                             wq_t=L["wqt"])
         return pkg.multi_lora_linear(L["x"], L["w"], L["b"], L["As"], L["Bs"], scales, routing)
 
     def step():
@@ -170,7 +172,7 @@ def main():
     R = kernels.padded_rank(cfg.ranks)
     fams = ["gemm_fwd", "gemm_dx", "shrink_x", "shrink_dy", "seg_outer_dB", "seg_outer_dA"]
     if fp8:
-        fams += ["quantize_x", "dequant_w"]
+        fams += ["quantize_x", "quantize_dy"]
     fam = {k: {"time": 0.0, "flops": 0, "bytes": 0, "launches": 0} for k in fams}
     with torch.no_grad():
         for L in lins:
@@ -202,8 +204,14 @@ def main():
                 xq, xs = kernels.quantize_rows_fp8(x)
                 runs["gemm_fwd"] = (lambda: kernels.gemm_fwd_fp8(xq, xs, L["wq"], L["ws"], L["b"], h_rows, B_ops,
                                                                  routing), 2 * M * K * N + 2 * lora_mr * N, 0)
+                dyq, dys = kernels.quantize_rows_fp8(dy, col_scale=L["ws"])
+                g_div, _ = kernels.shrink(dy, B_ops, 1, scales, routing, False, R, row_div=dys)
+                a_t = [a.t().contiguous() for a in A_ops]
+                runs["gemm_dx"] = (lambda: kernels.gemm_fwd_fp8(dyq, dys, L["wqt"], None, None, g_div, a_t, routing),
+                                   2 * M * K * N + 2 * lora_mr * K, 0)
                 runs["quantize_x"] = (lambda: kernels.quantize_rows_fp8(x), 0, M * K * 3 + M * 4)
-                runs["dequant_w"] = (lambda: kernels.dequant_rows_fp8(L["wq"], L["ws"]), 0, N * K * 3 + N * 4)
+                runs["quantize_dy"] = (lambda: kernels.quantize_rows_fp8(dy, col_scale=L["ws"]), 0,
+                                       M * N * 3 + M * 4 + N * 4)
             for k, (fn, fl, by) in runs.items():
                 t = timed(fn)
                 fam[k]["time"] += t
@@ -229,7 +237,7 @@ def main():
                 "avg_launch_us": round(gem["time"] / gem["launches"] * 1e6, 2),
                 "flops_per_launch": gem["flops"] // gem["launches"]}
     lora = {}
-    for k in ("shrink_x", "shrink_dy", "seg_outer_dB", "seg_outer_dA") + (("quantize_x", "dequant_w") if fp8 else ()):
+    for k in ("shrink_x", "shrink_dy", "seg_outer_dB", "seg_outer_dA") + (("quantize_x", "quantize_dy") if fp8 else ()):
         v = fam[k]
         gbs = v["bytes"] / v["time"] / 1e9
         lora[k] = {"achieved_gbs": round(gbs, 1), "frac_hbm": round(gbs / HBM_PEAK_GBS, 4),

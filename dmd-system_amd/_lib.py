@@ -10,7 +10,7 @@ from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "libmlora.so"
 
-ABI_VERSION = 2
+ABI_VERSION = 3
 MAX_SEGMENTS = 128
 MAX_ADAPTERS = 32
 MAX_RANK = 256
@@ -40,7 +40,7 @@ SIGNATURES = {
     "mlora_seg_outer": (_int, [_vp, _i64, _i64, _i64, _vp, _i32, _pvp, _int, _int, _pi32, _i32,
                                _pi64, _pi32, _i32, _vp, _i64, _vp]),
     "mlora_seg_outer_workspace_bytes": (_i64, [_i64, _i64, _pi32, _i32, _pi64, _pi32, _i32]),
-    "mlora_quantize_rows_fp8": (_int, [_vp, _i64, _i64, _i64, _vp, _i64, _vp, _vp]),
+    "mlora_quantize_rows_fp8": (_int, [_vp, _i64, _i64, _i64, _vp, _vp, _i64, _vp, _vp]),
     "mlora_dequant_rows_fp8": (_int, [_vp, _i64, _vp, _i64, _i64, _vp, _i64, _vp]),
     "mlora_div_rows_bf16": (_int, [_vp, _i64, _vp, _i64, _i64, _vp, _i64, _vp]),
     "mlora_gemm_fwd_fp8": (_int, [_vp, _i64, _vp, _i64, _i64, _vp, _i64, _vp, _i64, _vp, _int, _vp, _i64,

@@ -1,15 +1,18 @@
 // e4m3 (OCP E4M3FN: bias 7, max 448, no infinities) conversions for the
 // quantised-base variant of the multi-LoRA linear:
 //
-//   mlora_quantize_rows_fp8 : per-row absmax scaling of a bf16 matrix to e4m3
-//                             (activations X before the fp8 base GEMM)
+//   mlora_quantize_rows_fp8 : per-row absmax scaling of a bf16 matrix, each
+//                             column optionally multiplied by an fp32 factor
+//                             first, to e4m3 (activations X before the fp8 base
+//                             GEMM; dY·w_scale before the fp8 dX GEMM)
 //   mlora_dequant_rows_fp8  : e4m3 rows times a per-row fp32 scale back to bf16
 //                             (the frozen base W for the bf16 dX GEMM)
 //   mlora_div_rows_bf16     : bf16 rows divided by a per-row fp32 value
 //                             (lora_b / w_scale for the e4m3 forward)
 //
-// Quantisation of row m: amax = max_k |x[m,k]|; scale[m] = amax / 448 and
-// q = e4m3_rne(x * (448 / amax)) (both divisions IEEE fp32; an all-zero row
+// Quantisation of row m: v[k] = x[m,k] (times col_scale[k] when given, one
+// fp32 product); amax = max_k |v[k]|; scale[m] = amax / 448 and
+// q = e4m3_rne(v * (448 / amax)) (both divisions IEEE fp32; an all-zero row
 // gets scale 1). Round to nearest even on the 3 mantissa bits, subnormals in
 // steps of 2^-9; |x·(448/amax)| <= 448 so nothing saturates.
 //
@@ -45,12 +48,34 @@ __device__ __forceinline__ float wave_max(float v) {
 
 struct QuantArgs {
   const uint16_t *x;
+  const float *cs;  // per-column factor or nullptr
   uint8_t *q;
   float *scale;
   int64_t ldx, ldq;
   int32_t M, K;
 };
 
+// The 8 values of bf16 chunk v (columns k..k+7), times the column factors when CS.
+template <bool CS>
+__device__ __forceinline__ void chunk_values(const u32x4 &v, const QuantArgs &a, int k, float (&o)[8]) {
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    o[2 * w] = bf16_to_f32(v[w] & 0xffff);
+    o[2 * w + 1] = bf16_to_f32(v[w] >> 16);
+  }
+  if constexpr (CS) {
+    if (k < a.K) {  // K is a multiple of 8: a chunk is all in range or all past K
+      const f32x4 c0 = *(const MLORA_GLOBAL f32x4 *)(a.cs + k), c1 = *(const MLORA_GLOBAL f32x4 *)(a.cs + k + 4);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        o[e] *= c0[e];
+        o[4 + e] *= c1[e];
+      }
+    }
+  }
+}
+
+template <bool CS>
 __global__ __launch_bounds__(256) void quantize_rows_kernel(const QuantArgs a) {
   const int lane = threadIdx.x & 63;
   const int m = blockIdx.x * 4 + wave_id();
@@ -58,28 +83,28 @@ __global__ __launch_bounds__(256) void quantize_rows_kernel(const QuantArgs a) {
   const __amdgpu_buffer_rsrc_t rx = make_rsrc(a.x + (int64_t)m * a.ldx, (int64_t)a.K * 2);
   float amax = 0.f;
   for (int k = 8 * lane; k < a.K; k += 512) {
-    const u32x4 v = buf_load16(rx, 2 * k);
+    float f[8];
+    chunk_values<CS>(buf_load16(rx, 2 * k), a, k, f);
 #pragma unroll
-    for (int w = 0; w < 4; ++w)
-      amax = fmaxf(amax, fmaxf(fabsf(bf16_to_f32(v[w] & 0xffff)), fabsf(bf16_to_f32(v[w] >> 16))));
+    for (int e = 0; e < 8; ++e) amax = fmaxf(amax, fabsf(f[e]));
   }
   amax = wave_max(amax);
   const float inv = amax > 0.f ? 448.f / amax : 1.f;
   if (lane == 0) a.scale[m] = amax > 0.f ? amax / 448.f : 1.f;
   uint8_t *qrow = a.q + (int64_t)m * a.ldq;
   for (int k = 8 * lane; k < a.K; k += 512) {
-    const u32x4 v = buf_load16(rx, 2 * k);
-    uint32_t o[2];
-#pragma unroll
-    for (int h = 0; h < 2; ++h)
-      o[h] = pack4_e4m3(bf16_to_f32(v[2 * h] & 0xffff) * inv, bf16_to_f32(v[2 * h] >> 16) * inv,
-                        bf16_to_f32(v[2 * h + 1] & 0xffff) * inv, bf16_to_f32(v[2 * h + 1] >> 16) * inv);
-    *(MLORA_GLOBAL u32x2 *)(qrow + k) = u32x2{o[0], o[1]};
+    float f[8];
+    chunk_values<CS>(buf_load16(rx, 2 * k), a, k, f);
+    const uint32_t o0 = pack4_e4m3(f[0] * inv, f[1] * inv, f[2] * inv, f[3] * inv);
+    const uint32_t o1 = pack4_e4m3(f[4] * inv, f[5] * inv, f[6] * inv, f[7] * inv);
+    *(MLORA_GLOBAL u32x2 *)(qrow + k) = u32x2{o0, o1};
   }
 }
 
-// Row held in registers: NI 16-byte chunks per lane (K <= 512 * NI).
-template <int NI>
+// Row held in registers: NI 16-byte chunks per lane (K <= 512 * NI). With
+// column factors (CS) the products are formed once, in the absmax pass, and
+// kept as fp32 for the conversion pass.
+template <int NI, bool CS>
 __global__ __launch_bounds__(256) void quantize_rows_reg_kernel(const QuantArgs a) {
   const int lane = threadIdx.x & 63;
   const int m = blockIdx.x * 4 + wave_id();
@@ -89,11 +114,17 @@ __global__ __launch_bounds__(256) void quantize_rows_reg_kernel(const QuantArgs 
 #pragma unroll
   for (int it = 0; it < NI; ++it) v[it] = buf_load16(rx, 2 * (8 * lane + 512 * it));  // past K: reads zero
   float amax = 0.f;
+  float f[CS ? NI : 1][8];
 #pragma unroll
-  for (int it = 0; it < NI; ++it)
+  for (int it = 0; it < NI; ++it) {
+    float t[8];
+    chunk_values<CS>(v[it], a, 8 * lane + 512 * it, t);
 #pragma unroll
-    for (int w = 0; w < 4; ++w)
-      amax = fmaxf(amax, fmaxf(fabsf(bf16_to_f32(v[it][w] & 0xffff)), fabsf(bf16_to_f32(v[it][w] >> 16))));
+    for (int e = 0; e < 8; ++e) {
+      amax = fmaxf(amax, fabsf(t[e]));
+      if constexpr (CS) f[it][e] = t[e];
+    }
+  }
   amax = wave_max(amax);
   const float inv = amax > 0.f ? 448.f / amax : 1.f;
   if (lane == 0) a.scale[m] = amax > 0.f ? amax / 448.f : 1.f;
@@ -102,14 +133,16 @@ __global__ __launch_bounds__(256) void quantize_rows_reg_kernel(const QuantArgs 
   for (int it = 0; it < NI; ++it) {
     const int k = 8 * lane + 512 * it;
     if (k >= a.K) break;
-    uint32_t o[2];
+    float t[8];
+    if constexpr (CS) {
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      const u32x4 &c = v[it];
-      o[h] = pack4_e4m3(bf16_to_f32(c[2 * h] & 0xffff) * inv, bf16_to_f32(c[2 * h] >> 16) * inv,
-                        bf16_to_f32(c[2 * h + 1] & 0xffff) * inv, bf16_to_f32(c[2 * h + 1] >> 16) * inv);
+      for (int e = 0; e < 8; ++e) t[e] = f[it][e];
+    } else {
+      chunk_values<false>(v[it], a, k, t);
     }
-    *(MLORA_GLOBAL u32x2 *)(qrow + k) = u32x2{o[0], o[1]};
+    const uint32_t o0 = pack4_e4m3(t[0] * inv, t[1] * inv, t[2] * inv, t[3] * inv);
+    const uint32_t o1 = pack4_e4m3(t[4] * inv, t[5] * inv, t[6] * inv, t[7] * inv);
+    *(MLORA_GLOBAL u32x2 *)(qrow + k) = u32x2{o0, o1};
   }
 }
 
@@ -168,8 +201,19 @@ __global__ __launch_bounds__(256) void div_rows_kernel(const DivArgs a) {
 
 using namespace mlora;
 
-extern "C" int mlora_quantize_rows_fp8(const void *x, int64_t ldx, int64_t M, int64_t K, void *xq, int64_t ldq,
-                                       float *scale, void *stream) {
+template <bool CS>
+static void launch_quantize(const QuantArgs &a, int64_t K, hipStream_t s) {
+  const dim3 grid((unsigned)((a.M + 3) / 4)), block(256);
+  const int64_t ni = (K + 511) / 512;  // 16-byte chunks per lane
+  if (ni <= 2) hipLaunchKernelGGL((quantize_rows_reg_kernel<2, CS>), grid, block, 0, s, a);
+  else if (ni <= 4) hipLaunchKernelGGL((quantize_rows_reg_kernel<4, CS>), grid, block, 0, s, a);
+  else if (ni <= 8) hipLaunchKernelGGL((quantize_rows_reg_kernel<8, CS>), grid, block, 0, s, a);
+  else if (ni <= 18) hipLaunchKernelGGL((quantize_rows_reg_kernel<18, CS>), grid, block, 0, s, a);
+  else hipLaunchKernelGGL(quantize_rows_kernel<CS>, grid, block, 0, s, a);
+}
+
+extern "C" int mlora_quantize_rows_fp8(const void *x, int64_t ldx, int64_t M, int64_t K, const float *col_scale,
+                                       void *xq, int64_t ldq, float *scale, void *stream) {
   if (M < 0 || K < 0) return MLORA_ERR_INVALID;
   if (M > INT32_MAX - 4 || K > INT32_MAX / 2) return MLORA_ERR_LIMIT;
   int st = check_bf16_matrix(x, ldx, M, K);
@@ -177,15 +221,12 @@ extern "C" int mlora_quantize_rows_fp8(const void *x, int64_t ldx, int64_t M, in
   if ((st = check_fp8_matrix(xq, ldq, M, K))) return st;
   if (M == 0 || K == 0) return MLORA_OK;
   if (scale == nullptr) return MLORA_ERR_INVALID;
-  QuantArgs a{static_cast<const uint16_t *>(x), static_cast<uint8_t *>(xq), scale, ldx, ldq, (int32_t)M, (int32_t)K};
-  const dim3 grid((unsigned)((M + 3) / 4)), block(256);
+  if (col_scale != nullptr && !aligned16(col_scale)) return MLORA_ERR_UNSUPPORTED;
+  QuantArgs a{static_cast<const uint16_t *>(x), col_scale, static_cast<uint8_t *>(xq), scale, ldx, ldq, (int32_t)M,
+              (int32_t)K};
   hipStream_t s = static_cast<hipStream_t>(stream);
-  const int64_t ni = (K + 511) / 512;  // 16-byte chunks per lane
-  if (ni <= 2) hipLaunchKernelGGL(quantize_rows_reg_kernel<2>, grid, block, 0, s, a);
-  else if (ni <= 4) hipLaunchKernelGGL(quantize_rows_reg_kernel<4>, grid, block, 0, s, a);
-  else if (ni <= 8) hipLaunchKernelGGL(quantize_rows_reg_kernel<8>, grid, block, 0, s, a);
-  else if (ni <= 18) hipLaunchKernelGGL(quantize_rows_reg_kernel<18>, grid, block, 0, s, a);
-  else hipLaunchKernelGGL(quantize_rows_kernel, grid, block, 0, s, a);
+  if (col_scale != nullptr) launch_quantize<true>(a, K, s);
+  else launch_quantize<false>(a, K, s);
   return launch_status();
 }
 

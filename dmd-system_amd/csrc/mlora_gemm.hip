@@ -34,7 +34,7 @@ struct GemmArgs {
   const void *Q;       // bf16, or e4m3 in the fp8 forward
   const uint16_t *E;   // extension rows (Hs / Gs), [M, lde]
   const float *psc;    // fp8 forward: per-row scale of P [M]
-  const float *qsc;    // fp8 forward: per-row scale of Q [Ncols]
+  const float *qsc;    // fp8 forward: per-row scale of Q [Ncols] (nullptr: 1)
   const void *bias;
   uint16_t *Y;
   int64_t ldp, ldq, lde, ldy;
@@ -657,7 +657,7 @@ __device__ __forceinline__ void store_tile(const f32x16 (&acc)[C::TM][C::TN], co
 #pragma unroll
         for (int e = 0; e < 4; ++e) bias[4 * g + e] = b4[e];
       }
-      if constexpr (C::F8) {
+      if (C::F8 && args.qsc != nullptr) {
         const f32x4 q4 = col4(args.qsc, false, c, args.Ncols, hi);
 #pragma unroll
         for (int e = 0; e < 4; ++e) qs[4 * g + e] = q4[e];
@@ -865,9 +865,9 @@ extern "C" int mlora_gemm_fwd_fp8(const void *xq, int64_t ldx, const float *x_sc
   if ((st = check_fp8_matrix(wq, ldw, N, K))) return st;
   if ((st = check_bf16_matrix(y, ldy, M, N))) return st;
   if (M == 0 || N == 0) return MLORA_OK;
-  if (y == nullptr || xq == nullptr || wq == nullptr || x_scale == nullptr || w_scale == nullptr) return MLORA_ERR_INVALID;
+  if (y == nullptr || xq == nullptr || wq == nullptr || x_scale == nullptr) return MLORA_ERR_INVALID;
   if (K == 0) return MLORA_ERR_UNSUPPORTED;  // the contraction loop starts with an e4m3 k-tile
-  if (!aligned16(w_scale)) return MLORA_ERR_UNSUPPORTED;
+  if (w_scale != nullptr && !aligned16(w_scale)) return MLORA_ERR_UNSUPPORTED;  // NULL: all 1
   if (bias != nullptr) {
     if (bias_dtype != MLORA_F32 && bias_dtype != MLORA_BF16) return MLORA_ERR_UNSUPPORTED;
     if (!aligned16(bias)) return MLORA_ERR_UNSUPPORTED;

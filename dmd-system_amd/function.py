@@ -70,19 +70,22 @@ def _prepare(ctx, x, N: int, ab, scales, routing: SegmentRouting, grad0: int, ro
     return A_ops, B_ops, h_rows
 
 
-def _backward(ctx, dy, x, weight, A_ops, B_ops):
-    """dX (bf16 base `weight`), dA_i, dB_i; returns (dx, dAs, dBs)."""
+def _backward(ctx, dy, x, dx_gemm, A_ops, B_ops, row_div=None):
+    """dX (dx_gemm(g_rows)), dA_i, dB_i; returns (dx, dAs, dBs).
+
+    dy is bf16 contiguous; g_rows (the LoRA term of dX) are divided by row_div
+    when given (the e4m3 dX folds dY's row scale into them)."""
     n, g0, routing = ctx.n, ctx.grad0, ctx.routing
     need_x = ctx.needs_input_grad[0]
     need_a = [ctx.needs_input_grad[g0 + i] for i in range(n)]
     need_b = [ctx.needs_input_grad[g0 + n + i] for i in range(n)]
-    dy = dy.to(torch.bfloat16).contiguous()
     dx = None
     g_rows = g_frag = None
     if ctx.width > 0 and (need_x or any(need_a)):
-        g_rows, g_frag = kernels.shrink(dy, B_ops, 1, ctx.scales, routing, want_frag=any(need_a), width=ctx.width)
+        g_rows, g_frag = kernels.shrink(dy, B_ops, 1, ctx.scales, routing, want_frag=any(need_a), width=ctx.width,
+                                        row_div=row_div)
     if need_x:
-        dx = kernels.gemm_dx(dy, weight(), g_rows, A_ops, routing)
+        dx = dx_gemm(g_rows)
     dAs: list = [None] * n
     dBs: list = [None] * n
     if any(need_b):
@@ -117,40 +120,54 @@ class MultiLoRAFunction(torch.autograd.Function):
     def backward(ctx, dy):
         n = ctx.n
         x, weight, *ops = ctx.saved_tensors
-        dx, dAs, dBs = _backward(ctx, dy, x, lambda: weight, ops[:n], ops[n:])
+        dy = dy.to(torch.bfloat16).contiguous()
+        dx_gemm = lambda g_rows: kernels.gemm_dx(dy, weight, g_rows, ops[:n], ctx.routing)
+        dx, dAs, dBs = _backward(ctx, dy, x, dx_gemm, ops[:n], ops[n:])
         return (dx, None, None, None, None, *dAs, *dBs)
 
 
 class MultiLoRAFP8Function(torch.autograd.Function):
-    """``apply(x, wq, w_scale, bias, routing, scales, *lora_as, *lora_bs)``: the
-    same linear with the frozen base stored as e4m3 ``wq`` [N, K] and one fp32
-    scale per output channel ``w_scale`` [N] (base weight = w_scale[n]·wq[n, k]).
+    """``apply(x, wq, w_scale, wq_t, bias, routing, scales, *lora_as, *lora_bs)``:
+    the same linear with the frozen base stored as e4m3 ``wq`` [N, K] and one
+    fp32 scale per output channel ``w_scale`` [N] (base weight =
+    w_scale[n]·wq[n, k]); ``wq_t`` is wq transposed ([K, N], for dX).
 
     Forward: X is quantised per token to e4m3 (mlora_quantize_rows_fp8) and the
     base product runs on the e4m3 MFMA with fp32 accumulation; the LoRA shrink
-    and expand stay bf16 on the unquantised X. Backward: dX runs the bf16 dX
-    GEMM over the dequantised W (dY is not quantised); dA, dB as in the bf16 path.
+    and expand stay bf16 on the unquantised X. Backward: dX = dY·W + g·A runs
+    on the e4m3 MFMA as well — dY·w_scale[n] quantised per row (scale
+    dy_scale), times wq_t, plus the bf16 LoRA term g/dy_scale times A_aᵀ, all
+    scaled by dy_scale[m] in the epilogue; dA, dB as in the bf16 path.
     """
 
     @staticmethod
-    def forward(ctx, x, wq, w_scale, bias, routing: SegmentRouting, scales: Sequence[float], *ab):
-        if any(ctx.needs_input_grad[1:4]):
+    def forward(ctx, x, wq, w_scale, wq_t, bias, routing: SegmentRouting, scales: Sequence[float], *ab):
+        if any(ctx.needs_input_grad[1:5]):
             raise RuntimeError("multi-LoRA: the base weight, its scale and the bias are frozen")
         xq, x_scale = kernels.quantize_rows_fp8(x)
         # the LoRA operands enter the e4m3 accumulators divided by the scales the
         # epilogue multiplies back: h / x_scale[m] (shrink) and lora_b / w_scale[n]
-        A_ops, B_ops, h_rows = _prepare(ctx, x, wq.shape[0], ab, scales, routing, grad0=6, row_div=x_scale)
+        A_ops, B_ops, h_rows = _prepare(ctx, x, wq.shape[0], ab, scales, routing, grad0=7, row_div=x_scale)
         B_div = [kernels.div_rows_bf16(b, w_scale) for b in B_ops]
         y = kernels.gemm_fwd_fp8(xq, x_scale, wq, w_scale, bias, h_rows, B_div, routing)
-        ctx.save_for_backward(x, wq, w_scale, *A_ops, *B_ops)
+        ctx.save_for_backward(x, wq_t, w_scale, *A_ops, *B_ops)
         return y
 
     @staticmethod
     def backward(ctx, dy):
         n = ctx.n
-        x, wq, w_scale, *ops = ctx.saved_tensors
-        dx, dAs, dBs = _backward(ctx, dy, x, lambda: kernels.dequant_rows_fp8(wq, w_scale), ops[:n], ops[n:])
-        return (dx, None, None, None, None, None, *dAs, *dBs)
+        x, wq_t, w_scale, *ops = ctx.saved_tensors
+        dy = dy.to(torch.bfloat16).contiguous()
+        dyq = dy_scale = None
+        if ctx.needs_input_grad[0]:
+            dyq, dy_scale = kernels.quantize_rows_fp8(dy, col_scale=w_scale)
+
+        def dx_gemm(g_rows):
+            a_t = [a.t().contiguous() for a in ops[:n]]  # A_aᵀ [K, r]: the NT form of the LoRA term
+            return kernels.gemm_fwd_fp8(dyq, dy_scale, wq_t, None, None, g_rows, a_t, ctx.routing)
+
+        dx, dAs, dBs = _backward(ctx, dy, x, dx_gemm, ops[:n], ops[n:], row_div=dy_scale)
+        return (dx, None, None, None, None, None, None, *dAs, *dBs)
 
 
 def multi_lora_linear(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None,
@@ -175,8 +192,12 @@ def multi_lora_linear(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor 
 
 def multi_lora_linear_fp8(x: torch.Tensor, wq: torch.Tensor, w_scale: torch.Tensor, bias: torch.Tensor | None,
                           lora_as: Sequence[torch.Tensor], lora_bs: Sequence[torch.Tensor],
-                          scales: Sequence[float], routing: SegmentRouting) -> torch.Tensor:
-    """Functional form with an e4m3 base (wq [N, K] float8_e4m3fn, w_scale [N] fp32); bf16 out."""
+                          scales: Sequence[float], routing: SegmentRouting,
+                          wq_t: torch.Tensor | None = None) -> torch.Tensor:
+    """Functional form with an e4m3 base (wq [N, K] float8_e4m3fn, w_scale [N] fp32); bf16 out.
+
+    wq_t: wq transposed ([K, N], contiguous) for the e4m3 dX; made here when not given (a frozen
+    base keeps it, see MultiLoRALinear.quantize_base_fp8)."""
     K = x.shape[-1]
     lead = x.shape[:-1]
     x2 = x.reshape(-1, K)
@@ -187,7 +208,9 @@ def multi_lora_linear_fp8(x: torch.Tensor, wq: torch.Tensor, w_scale: torch.Tens
                            "or call it under torch.autocast('cuda', dtype=torch.bfloat16)")
     if not x2.is_cuda:
         raise RuntimeError("multi-LoRA linear runs on the ROCm device only (HIP kernels, no CPU path)")
+    if wq_t is None:
+        wq_t = wq.t().contiguous()
     with torch.autocast("cuda", enabled=False):
-        y = MultiLoRAFP8Function.apply(x2.contiguous(), wq, w_scale, bias, routing, tuple(scales),
+        y = MultiLoRAFP8Function.apply(x2.contiguous(), wq, w_scale, wq_t, bias, routing, tuple(scales),
                                        *lora_as, *lora_bs)
     return y.reshape(*lead, wq.shape[0])

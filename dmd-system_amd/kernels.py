@@ -57,7 +57,8 @@ def shrink(p: torch.Tensor, ops: Sequence[torch.Tensor], op_layout: int, scales:
            row_div: torch.Tensor | None = None) -> tuple[torch.Tensor, list | None]:
     """h = s·P·Op_aᵀ per segment -> (h_rows bf16 [M, width], per-call-group hi/lo fragments or None).
 
-    row_div [M] fp32 (optional) divides the rows of h_rows only (the e4m3 forward's activation scales).
+    row_div [M] fp32 (optional) divides the rows of h_rows only (the row scales of the e4m3 forward's X
+    and of the e4m3 dX's dY).
     """
     M, K = p.shape
     _check_rows("P", p)
@@ -210,15 +211,18 @@ def _check_scale(name: str, s: torch.Tensor, n: int) -> None:
              f"{name} must be a contiguous float32 vector of length {n}")
 
 
-def quantize_rows_fp8(x: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
-    """Per-row absmax e4m3 quantisation: (q float8_e4m3fn [M, K], scale float32 [M]), x ≈ q·scale."""
+def quantize_rows_fp8(x: torch.Tensor, col_scale: torch.Tensor | None = None) -> tuple[torch.Tensor, torch.Tensor]:
+    """Per-row absmax e4m3 quantisation of x (times col_scale[k] per column when given):
+    (q float8_e4m3fn [M, K], scale float32 [M]), x·col_scale ≈ q·scale."""
     M, K = x.shape
     _check_rows("X", x, K)
+    if col_scale is not None:
+        _check_scale("col_scale", col_scale, K)
     q = torch.empty((M, K), dtype=torch.float8_e4m3fn, device=x.device)
     scale = torch.empty((M,), dtype=torch.float32, device=x.device)
     lib = _lib.load()
     _lib.check("mlora_quantize_rows_fp8", lib.mlora_quantize_rows_fp8(
-        x.data_ptr(), x.stride(0), M, K, q.data_ptr(), q.stride(0), scale.data_ptr(), _stream(x)))
+        x.data_ptr(), x.stride(0), M, K, _ptr(col_scale), q.data_ptr(), q.stride(0), scale.data_ptr(), _stream(x)))
     return q, scale
 
 
@@ -246,20 +250,22 @@ def div_rows_bf16(x: torch.Tensor, div: torch.Tensor) -> torch.Tensor:
     return y
 
 
-def gemm_fwd_fp8(xq: torch.Tensor, x_scale: torch.Tensor, wq: torch.Tensor, w_scale: torch.Tensor,
+def gemm_fwd_fp8(xq: torch.Tensor, x_scale: torch.Tensor, wq: torch.Tensor, w_scale: torch.Tensor | None,
                  bias: torch.Tensor | None, h_rows: torch.Tensor | None, bs: Sequence[torch.Tensor],
                  routing: SegmentRouting) -> torch.Tensor:
     """Y = (Xq·Wqᵀ + per-segment h_rows·B_aᵀ)·x_scale[m]·w_scale[n] + bias, bf16 out (e4m3 MFMA base).
 
     h_rows and bs are the LoRA operands divided by the scales: shrink(..., row_div=x_scale) and
-    div_rows_bf16(lora_b, w_scale).
+    div_rows_bf16(lora_b, w_scale); w_scale None means 1. The e4m3 dX is the same product:
+    xq = dY·w_scale quantised per row, wq = Wqᵀ [K, N], w_scale None, bs = A_aᵀ [K, r].
     """
     M, K = xq.shape
     N = wq.shape[0]
     _check_fp8_rows("Xq", xq, K)
     _check_fp8_rows("Wq", wq, K)
     _check_scale("x_scale", x_scale, M)
-    _check_scale("w_scale", w_scale, N)
+    if w_scale is not None:
+        _check_scale("w_scale", w_scale, N)
     if bias is not None:
         _require(bias.is_cuda and bias.dtype in _DT and bias.is_contiguous() and bias.shape == (N,), "bias")
     ranks = [int(b.shape[1]) for b in bs]
@@ -278,7 +284,7 @@ def gemm_fwd_fp8(xq: torch.Tensor, x_scale: torch.Tensor, wq: torch.Tensor, w_sc
         hr = None if h_rows is None else h_rows[r0:r1].data_ptr()
         _lib.check("mlora_gemm_fwd_fp8", lib.mlora_gemm_fwd_fp8(
             xq[r0:r1].data_ptr(), xq.stride(0), x_scale[r0:r1].data_ptr(), r1 - r0, K,
-            wq.data_ptr(), wq.stride(0), w_scale.data_ptr(), N,
+            wq.data_ptr(), wq.stride(0), _ptr(w_scale), N,
             _ptr(bias), _DT[bias.dtype] if bias is not None else 0, hr, ldh,
             ptrs, rk, len(bs), o, i, n, y[r0:r1].data_ptr(), y.stride(0), 0, stream))
     return y

@@ -133,18 +133,21 @@ class MultiLoRALinear(nn.Module):
 
     def quantize_base_fp8(self) -> "MultiLoRALinear":
         """Store the frozen base weight as e4m3 with one fp32 scale per output
-        channel (buffers ``base_wq`` [out, in], ``base_wscale`` [out]); forward
-        then runs the e4m3 base GEMM. The bf16/fp32 ``base.weight`` is left in
-        place for its other users (shared construction aliases it)."""
+        channel (buffers ``base_wq`` [out, in], ``base_wscale`` [out], and
+        ``base_wq_t`` = base_wq transposed for the e4m3 dX); forward and dX then
+        run on the e4m3 MFMA. The bf16/fp32 ``base.weight`` is left in place for
+        its other users (shared construction aliases it)."""
         w = self.base.weight.detach().to(torch.bfloat16).contiguous()
         wq, ws = quantize_rows_fp8(w)
         self.register_buffer("base_wq", wq, persistent=True)
         self.register_buffer("base_wscale", ws, persistent=True)
+        self.register_buffer("base_wq_t", wq.t().contiguous(), persistent=False)
         return self
 
     def forward(self, x: torch.Tensor, routing: SegmentRouting) -> torch.Tensor:
         if getattr(self, "base_wq", None) is not None:
             return multi_lora_linear_fp8(x, self.base_wq, self.base_wscale, self.base.bias, list(self.lora_a),
-                                         list(self.lora_b), self.scales, routing)
+                                         list(self.lora_b), self.scales, routing,
+                                         wq_t=getattr(self, "base_wq_t", None))
         return multi_lora_linear(x, self.base.weight, self.base.bias, list(self.lora_a), list(self.lora_b),
                                  self.scales, routing)

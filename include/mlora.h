@@ -43,7 +43,7 @@
 extern "C" {
 #endif
 
-#define MLORA_ABI_VERSION 2
+#define MLORA_ABI_VERSION 3
 
 /* Limits of one call (kernel-argument tables). Callers with more segments
  * split the rows into several calls; the Python host layer does this. */
@@ -170,11 +170,14 @@ int64_t mlora_seg_outer_workspace_bytes(int64_t M, int64_t C,
  * these three entry points serve the variant whose frozen W is stored as e4m3 with one fp32
  * scale per output channel, with the same LoRA semantics (low_rank.py:28) on top. */
 
-/* Per-row absmax quantisation of a bf16 matrix: scale[m] = max_k |x[m,k]| / 448 (1 for an
- * all-zero row), q[m,k] = e4m3_rne(x[m,k] · (448 / max_k |x[m,k]|)), saturating at 448.
- * q: [M, K] bytes (ldq and K multiples of 16, 16-byte aligned). Used for activations (per
- * token) and to produce the per-output-channel weight format. */
+/* Per-row absmax quantisation of a bf16 matrix, optionally after a per-column fp32 factor:
+ * v[m,k] = x[m,k] · col_scale[k] (col_scale may be NULL: factor 1; else 16-byte aligned, [K]),
+ * scale[m] = max_k |v[m,k]| / 448 (1 for an all-zero row), q[m,k] = e4m3_rne(v[m,k] · (448 /
+ * max_k |v[m,k]|)), saturating at 448. q: [M, K] bytes (ldq and K multiples of 16, 16-byte
+ * aligned). Used for activations (per token), for dY·w_scale before the e4m3 dX GEMM, and to
+ * produce the per-output-channel weight format. */
 int mlora_quantize_rows_fp8(const void *x, int64_t ldx, int64_t M, int64_t K,
+                            const float *col_scale,
                             void *q, int64_t ldq, float *scale,
                             void *stream);
 
@@ -191,11 +194,15 @@ int mlora_div_rows_bf16(const void *x, int64_t ldx, const float *div, int64_t M,
 /* mlora_gemm_fwd with an e4m3 base contraction (v_mfma_scale_f32_32x32x64_f8f6f4):
  *   Y[m, n] = bf16( x_scale[m]·w_scale[n]·( Σ_k xq[m,k]·wq[n,k] + Σ_j h_rows[m,j]·B_a[n,j] ) + bias[n] )
  * xq [M, K] and wq [N, K] e4m3 bytes (mlora_quantize_rows_fp8 layout, K >= 16); x_scale [M],
- * w_scale [N] fp32 (w_scale 16-byte aligned). The LoRA operands are bf16 and enter the same
+ * w_scale [N] fp32 (16-byte aligned; NULL: all 1). The LoRA operands are bf16 and enter the same
  * fp32 accumulators as the e4m3 products, so the caller passes them divided by the scales:
  * h_rows = h / x_scale[m] (mlora_shrink with row_div = x_scale) and B_a = lora_b / w_scale[n]
  * (mlora_div_rows_bf16); one scaling in the epilogue then restores both terms.
- * Reference semantics: low_rank.py:28 with base weight w_scale[n]·wq[n,k]. */
+ * Reference semantics: low_rank.py:28 with base weight w_scale[n]·wq[n,k].
+ * The same entry point computes the e4m3 dX of that linear (dX = dY·W + g·A, the transposed
+ * GEMM of the reference's autograd backward): xq = dY·w_scale quantised per row (scale
+ * dy_scale), wq = the frozen e4m3 W transposed ([K, N]), w_scale = NULL, no bias,
+ * h_rows = g / dy_scale[m] (mlora_shrink with row_div = dy_scale) and b_ptrs = A_aᵀ ([K, r]). */
 int mlora_gemm_fwd_fp8(const void *xq, int64_t ldx, const float *x_scale, int64_t M, int64_t K,
                        const void *wq, int64_t ldw, const float *w_scale, int64_t N,
                        const void *bias, int bias_dtype,

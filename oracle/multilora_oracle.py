@@ -97,13 +97,16 @@ def e4m3_encode(a) -> np.ndarray:
     return (code.astype(np.uint64) | sign).astype(np.uint8).reshape(f.shape)
 
 
-def quantize_rows_e4m3(x):
+def quantize_rows_e4m3(x, col_scale=None):
     """Per-row absmax quantisation -> (q uint8 [M, K], scale float32 [M]).
 
-    scale = amax / 448 and q = e4m3(x · (448 / amax)), both quotients in fp32;
-    an all-zero row gets scale 1 (and q = 0).
+    With col_scale, each column is first multiplied by its factor (one fp32
+    product). scale = amax / 448 and q = e4m3(x · (448 / amax)), both quotients
+    in fp32; an all-zero row gets scale 1 (and q = 0).
     """
     x = np.asarray(x, dtype=np.float32)
+    if col_scale is not None:
+        x = (x * np.asarray(col_scale, np.float32)[None, :]).astype(np.float32)
     amax = np.abs(x).max(axis=1) if x.shape[1] else np.zeros(x.shape[0], np.float32)
     pos = amax > 0
     safe = np.where(pos, amax, np.float32(1)).astype(np.float32)
@@ -136,6 +139,19 @@ def forward_fp8_quantized_x(x, wq, w_scale, b, As, Bs, scales, seg_offsets, adap
     if b is not None:
         base = base + np.asarray(b, np.float64)[None, :]
     lora = forward(x, np.zeros((base.shape[1], x.shape[1])), None, As, Bs, scales, seg_offsets, adapter_ids)
+    return base + lora
+
+
+def dx_fp8_quantized_dy(dy, wq, w_scale, As, Bs, scales, seg_offsets, adapter_ids) -> np.ndarray:
+    """The e4m3 dX arithmetic, exactly: dX = dY·W + Σ_seg s·(dY·B_a)·A_a with
+    W = w_scale[n]·e4m3(wq[n, k]), where the base product uses dY·w_scale
+    quantised per row (quantize_rows_e4m3 with col_scale = w_scale) times e4m3(wq)
+    and the row scale, and the LoRA term the unquantised dY; fp64 sums."""
+    dy = np.asarray(dy, np.float64)
+    dq, ds = quantize_rows_e4m3(dy.astype(np.float32), col_scale=w_scale)
+    base = (e4m3_decode(dq).astype(np.float64) @ e4m3_decode(wq).astype(np.float64)) * ds.astype(np.float64)[:, None]
+    lora = dx_rows(np.arange(dy.shape[0]), np.zeros((dy.shape[1], base.shape[1])), As, Bs, scales, seg_offsets,
+                   adapter_ids, dy)
     return base + lora
 
 

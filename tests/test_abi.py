@@ -35,7 +35,7 @@ def test_library_exports_every_declared_symbol(lib, pkg):
 
 
 def test_abi_version_and_status_strings(lib, pkg):
-    assert lib.mlora_abi_version() == pkg._lib.ABI_VERSION == 2
+    assert lib.mlora_abi_version() == pkg._lib.ABI_VERSION == 3
     for code in (0, -1, -2, -3, -4, -5):
         assert lib.mlora_status_string(code)
     assert b"unknown" in lib.mlora_status_string(-99)
@@ -122,11 +122,13 @@ def test_shrink_validation(lib, pkg):
 
 def test_fp8_entry_points_validate_before_launch(lib, pkg):
     L = pkg._lib
-    # quantize: K must be a multiple of 16 for the e4m3 rows, ld >= K, non-null scale
-    assert lib.mlora_quantize_rows_fp8(0x1000, 40, 4, 40, 0x2000, 48, 0x3000, None) == L.ERR_UNSUPPORTED
-    assert lib.mlora_quantize_rows_fp8(0x1000, 32, 4, 32, 0x2000, 16, 0x3000, None) == L.ERR_INVALID
-    assert lib.mlora_quantize_rows_fp8(0x1000, 32, 4, 32, 0x2000, 32, None, None) == L.ERR_INVALID
-    assert lib.mlora_quantize_rows_fp8(0x1000, 32, 0, 32, 0x2000, 32, None, None) == L.OK
+    # quantize: K must be a multiple of 16 for the e4m3 rows, ld >= K, non-null scale,
+    # a column-factor vector (optional) 16-byte aligned
+    assert lib.mlora_quantize_rows_fp8(0x1000, 40, 4, 40, None, 0x2000, 48, 0x3000, None) == L.ERR_UNSUPPORTED
+    assert lib.mlora_quantize_rows_fp8(0x1000, 32, 4, 32, None, 0x2000, 16, 0x3000, None) == L.ERR_INVALID
+    assert lib.mlora_quantize_rows_fp8(0x1000, 32, 4, 32, None, 0x2000, 32, None, None) == L.ERR_INVALID
+    assert lib.mlora_quantize_rows_fp8(0x1000, 32, 4, 32, 0x5004, 0x2000, 32, 0x3000, None) == L.ERR_UNSUPPORTED
+    assert lib.mlora_quantize_rows_fp8(0x1000, 32, 0, 32, None, 0x2000, 32, None, None) == L.OK
     assert lib.mlora_dequant_rows_fp8(0x1001, 32, 0x3000, 4, 32, 0x2000, 32, None) == L.ERR_UNSUPPORTED
     assert lib.mlora_dequant_rows_fp8(0x1000, 32, None, 4, 32, 0x2000, 32, None) == L.ERR_INVALID
     assert lib.mlora_div_rows_bf16(0x1000, 32, None, 4, 32, 0x2000, 32, None) == L.ERR_INVALID
@@ -141,8 +143,9 @@ def test_fp8_entry_points_validate_before_launch(lib, pkg):
     assert fwd8(K=40, ldx=48) == L.ERR_UNSUPPORTED       # K not a multiple of 16
     assert fwd8(ldx=72) == L.ERR_UNSUPPORTED             # ld not a multiple of 16
     assert fwd8(ldx=32) == L.ERR_INVALID                 # ld < K
-    assert fwd8(xs=None) == L.ERR_INVALID                # scales required
+    assert fwd8(xs=None) == L.ERR_INVALID                # the row scales are required
     assert fwd8(ws=0x7004) == L.ERR_UNSUPPORTED          # w_scale 16-byte aligned
     assert fwd8(K=0, ldx=0) == L.ERR_UNSUPPORTED         # an e4m3 contraction is required
     assert fwd8(off=[0, 60]) == L.ERR_INVALID            # routing must cover M rows
     assert fwd8(M=0, off=[0, 0]) == L.OK
+    assert fwd8(M=0, off=[0, 0], ws=None) == L.OK        # w_scale may be NULL (all 1: the e4m3 dX)

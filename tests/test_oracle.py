@@ -355,3 +355,59 @@ def test_fp8_forward_variants_match_brute_force():
     np.testing.assert_allclose(O.forward_fp8_base(x, wq, ws, b, As, Bs, scales, off, ids), want_base, rtol=1e-12, atol=1e-12)
     np.testing.assert_allclose(O.forward_fp8_quantized_x(x, wq, ws, b, As, Bs, scales, off, ids), want_q,
                                rtol=1e-12, atol=1e-12)
+
+
+def test_quantize_rows_e4m3_column_factor():
+    """A column factor is one fp32 product before the absmax: with power-of-two
+    factors that product is exact, so quantising x·cs equals quantising x with
+    the factors; all-ones factors change nothing; the absmax column maps to ±448."""
+    rng = np.random.default_rng(24)
+    x = O.bf16_round(rng.standard_normal((6, 48)))
+    cs = (2.0 ** rng.integers(-6, 7, 48)).astype(np.float32)
+    q1, s1 = O.quantize_rows_e4m3(x, col_scale=cs)
+    q2, s2 = O.quantize_rows_e4m3((x * cs[None, :]).astype(np.float32))
+    assert np.array_equal(q1, q2) and np.array_equal(s1, s2)
+    q3, s3 = O.quantize_rows_e4m3(x, col_scale=np.ones(48, np.float32))
+    q4, s4 = O.quantize_rows_e4m3(x)
+    assert np.array_equal(q3, q4) and np.array_equal(s3, s4)
+    cs2 = rng.uniform(0.1, 3.0, 48).astype(np.float32)
+    q5, s5 = O.quantize_rows_e4m3(x, col_scale=cs2)
+    v = (x * cs2[None, :]).astype(np.float32)
+    for m in range(6):
+        k = int(np.argmax(np.abs(v[m])))
+        assert s5[m] == np.abs(v[m]).max() / np.float32(448) and (q5[m, k] & 0x7F) == 0x7E
+
+
+def test_fp8_dx_matches_brute_force():
+    """dx_fp8_quantized_dy against loops: the base product from the quantised
+    dY·w_scale rows, the LoRA term from the exact dY; and, when every dY·w_scale
+    row is already on the e4m3 grid at scale 1, equal to the exact dX."""
+    rng = np.random.default_rng(25)
+    M, K, N = 7, 16, 32
+    x, w, b, As, Bs, off, ids = _case(rng, M=M, K=K, N=N, ranks=(2, 3), lengths=(2, 3, 2), ids=(1, -1, 0))
+    wq, ws = O.quantize_rows_e4m3(w)  # w [N, K]: W = ws[n]·e4m3(wq[n, k])
+    scales = [0.5, 2.0]
+    dy = O.bf16_round(rng.standard_normal((M, N)))
+    dq, ds = O.quantize_rows_e4m3(dy, col_scale=ws)
+    Wd = O.e4m3_decode(wq).astype(np.float64)
+    aid = O.row_adapters(off, ids)
+    want = np.zeros((M, K))
+    for m in range(M):
+        for k in range(K):
+            base = sum(float(O.e4m3_decode([dq[m, n]])[0]) * Wd[n, k] for n in range(N)) * float(ds[m])
+            lora = 0.0
+            if aid[m] >= 0:
+                A, B = As[aid[m]], Bs[aid[m]]
+                g = [sum(float(dy[m, n]) * float(B[n, j]) for n in range(N)) for j in range(A.shape[0])]
+                lora = scales[aid[m]] * sum(g[j] * float(A[j, k]) for j in range(A.shape[0]))
+            want[m, k] = base + lora
+    got = O.dx_fp8_quantized_dy(dy, wq, ws, As, Bs, scales, off, ids)
+    np.testing.assert_allclose(got, want, rtol=1e-12, atol=1e-12)
+    # dY·w_scale on the e4m3 grid with row absmax 448: quantisation is exact
+    grid = O.e4m3_decode(np.arange(0, 0x7F, dtype=np.uint8))
+    dy2 = rng.choice(np.concatenate([grid, -grid]), (M, N)).astype(np.float64)
+    dy2[:, 0] = 448.0
+    ws1 = np.ones(N, np.float32)
+    exact = O.backward(x, Wd, As, Bs, scales, off, ids, dy2)[0]
+    np.testing.assert_allclose(O.dx_fp8_quantized_dy(dy2, wq, ws1, As, Bs, scales, off, ids), exact,
+                               rtol=1e-12, atol=1e-9)
