@@ -73,6 +73,31 @@ def test_dequant_rows_bit_exact(pkg, dev):
     assert np.array_equal(y.float().cpu().numpy(), want)
 
 
+def test_bf16_rounding_is_rne_with_ties_and_subnormals(pkg, dev):
+    """The kernels' fp32 -> bf16 rounding (the gfx950 packed conversion) is
+    round-to-nearest-even bit for bit: dequantisation products that land exactly
+    halfway between two bf16 values (scales 1 + odd·2^-8 on the e4m3 grid),
+    arbitrary products, and products in the fp32/bf16 subnormal range."""
+    codes = np.arange(256, dtype=np.uint8)
+    codes = codes[(codes & 0x7F) != 0x7F]                                      # no NaN codes
+    row = np.concatenate([codes, codes[::-1], np.zeros(4, np.uint8)]).reshape(1, 512)  # 2 x 254 codes + pad
+    ties = [np.float32(2.0 ** e * (1 + k * 2.0 ** -8)) for e in (-3, 0, 5) for k in (1, 3, 5, 127, 129, 255)]
+    g = np.random.default_rng(8)
+    rand = list((np.exp(g.standard_normal(24)) * 0.37).astype(np.float32))
+    tiny = [np.float32(2.0 ** -120), np.float32(2.0 ** -126 * 1.5), np.float32(2.0 ** -117 * (1 + 2.0 ** -8))]
+    scale = np.array(ties + rand + tiny, dtype=np.float32)
+    q = np.repeat(row, len(scale), axis=0)
+    y = pkg.kernels.dequant_rows_fp8(torch.from_numpy(q).view(torch.float8_e4m3fn).to(dev),
+                                     torch.from_numpy(scale).to(dev))
+    torch.cuda.synchronize()
+    want = O.bf16_round(O.dequant_rows_e4m3(q, scale))
+    got = y.float().cpu().numpy()
+    assert np.array_equal(got.view(np.uint32), want.astype(np.float32).view(np.uint32))
+    exact = O.dequant_rows_e4m3(q, scale)
+    assert np.any((exact.view(np.uint32) & 0xFFFF) == 0x8000)                 # the case holds exact ties
+    assert np.any((np.abs(exact) < 2.0 ** -126) & (exact != 0))               # and subnormal products
+
+
 def _case(M, K, N, ranks, seed, bias=True):
     g = torch.Generator().manual_seed(seed)
     x = torch.randn(M, K, generator=g).to(torch.bfloat16)
