@@ -13,9 +13,12 @@ cores, timed on a bounded sample of the same workload).
 
 Other configurations (parity-test cases, measured on request): --config
 tiny | wan22_5b | flux | wan13b_fp8 (frozen base stored e4m3 with a per-output-
-channel scale: forward on the e4m3 MFMA), and --fwd-only for a forward-only step.
+channel scale: forward on the e4m3 MFMA) | wan13b_roles (the multi-role call site:
+teacher conditional + unconditional rows base-only and the fake critic's rows with its
+adapter, in one call), --fwd-only for a forward-only step, and --per-role to time the
+same step as one call per role (this library, and the reference's unfused torch path).
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--config wan13b] [--fwd-only]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--config wan13b] [--fwd-only] [--per-role]
 """
 from __future__ import annotations
 
@@ -44,6 +47,9 @@ def parse():
     p.add_argument("--kernel-reps", type=int, default=10)
     p.add_argument("--cpu-seconds", type=float, default=12.0, help="bounded CPU-baseline sample budget")
     p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--per-role", action="store_true",
+                   help="also time the same step as one call per segment (role), with this library and with "
+                        "the reference's unfused torch path on the GPU")
     p.add_argument("--copy-calibration", action="store_true",
                    help="only run a plain 1 GiB device copy 4 times (scale for rocprofv3 FETCH_SIZE/WRITE_SIZE)")
     return p.parse_args()
@@ -251,6 +257,8 @@ def main():
             t = timed(lambda: torch.matmul(x, L["w"].T))
             vendor[f"{L['name']} {L['K']}->{L['N']}"] = round(2 * cfg.tokens * L["K"] * L["N"] / t / 1e12, 1)
 
+    per_role = per_role_timing(pkg, cfg, lins, scales, args, flops_step) if args.per_role else None
+
     # ---------------- CPU baseline: reference per-adapter path, fp32 torch, bounded sample
     cpu = None
     if not args.no_cpu_baseline:
@@ -283,10 +291,65 @@ def main():
         "lora_hbm": lora,
         "kernels": kern,
         "vendor_gemm_tflops": vendor,
+        **({"per_role": per_role} if per_role is not None else {}),
         "device": {"name": props.name, "cus": props.multi_processor_count,
                    "gcn_arch": getattr(props, "gcnArchName", "")},
     }
     print(json.dumps(out), flush=True)
+
+
+def per_role_timing(pkg, cfg, lins, scales, args, flops_step):
+    """The step of the batched call, split into one call per segment (one role per call, as
+    the reference calls its roles, training/dmd.py:324-345): with this library's op, and
+    with the reference's unfused autocast path (low_rank.py:26-28: base GEMM, two skinny
+    GEMMs, bf16 scale and add; a base-only role is the plain linear) in torch on the GPU."""
+    import torch
+    import torch.nn.functional as F
+    segs = [(a, b, ad) for a, b, ad in zip(cfg.routing.seg_offsets, cfg.routing.seg_offsets[1:],
+                                           cfg.routing.adapter_ids) if b > a]
+    # each role owns its input (a leaf of its own, not a slice of the batched one)
+    xs = {(id(L), r0): L["x"].detach()[r0:r1].clone().requires_grad_(not args.fwd_only)
+          for L in lins for r0, r1, _ in segs}
+
+    def lib_call(L, r0, r1, ad):
+        return pkg.multi_lora_linear(xs[id(L), r0], L["w"], L["b"], L["As"], L["Bs"], scales,
+                                     pkg.SegmentRouting.single(r1 - r0, ad))
+
+    def torch_call(L, r0, r1, ad):
+        x = xs[id(L), r0]
+        y = F.linear(x, L["w"], L["b"])
+        if ad < 0:
+            return y
+        return y + scales[ad] * F.linear(F.linear(x, L["As"][ad]), L["Bs"][ad])
+
+    def step_of(call):
+        def step():
+            if args.fwd_only:
+                with torch.no_grad():
+                    for L in lins:
+                        for r0, r1, ad in segs:
+                            call(L, r0, r1, ad)
+                return
+            for L in lins:
+                for t in [*L["As"], *L["Bs"]] + [xs[id(L), r0] for r0, _, _ in segs]:
+                    t.grad = None
+                for r0, r1, ad in segs:
+                    call(L, r0, r1, ad).backward(L["dy"][r0:r1])
+        return step
+
+    out = {"segments": len(segs)}
+    for key, call in (("library", lib_call), ("torch_unfused", torch_call)):
+        step = step_of(call)
+        for _ in range(args.warmup):
+            step()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(args.steps):
+            step()
+        torch.cuda.synchronize()
+        ms = (time.perf_counter() - t0) * 1e3 / args.steps
+        out[key] = {"ms_per_step": round(ms, 4), "tflops": round(flops_step / (ms * 1e-3) / 1e12, 2)}
+    return out
 
 
 def cpu_baseline(cfg, budget_s: float, fwd_only: bool = False):

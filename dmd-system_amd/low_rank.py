@@ -87,7 +87,8 @@ class MultiLoRALinear(nn.Module):
     """One frozen base nn.Linear shared by several adapters, routed by segment.
 
     ``forward(x, routing)``: x [..., in]; routing a SegmentRouting over the
-    flattened rows (adapter id -1 = base only, the teacher role).
+    flattened rows (adapter id -1 = base only, the teacher role), or, with no
+    routing, the RoleBatch that ``roles.roles_active`` set on the module.
     """
 
     def __init__(self, base: nn.Linear, *, ranks: Sequence[int], alphas: Sequence[float], dtype=None):
@@ -103,28 +104,40 @@ class MultiLoRALinear(nn.Module):
         self.lora_a = nn.ParameterList([a for a, _ in pairs])
         self.lora_b = nn.ParameterList([b for _, b in pairs])
         self.scales = [float(al) / r for r, al in zip(ranks, alphas)]
+        self.role_ids: dict[str, int] = {}  # role name -> adapter id (multi-role call sites)
+        self.active_roles = None             # RoleBatch routing calls without an explicit routing
 
     @classmethod
-    def from_roles(cls, roles: Sequence[TrainableLowRankLinear]) -> "MultiLoRALinear":
+    def from_roles(cls, roles: Sequence[TrainableLowRankLinear], *, base: nn.Linear | None = None,
+                   role_names: Sequence[str] | None = None) -> "MultiLoRALinear":
         """Batch per-role TrainableLowRankLinear modules that alias one frozen base.
 
         The adapters are the roles' own Parameters (not copies), so each role's
         optimizer keeps owning exactly its trainables (open_workload/dmd.py:266-275);
         the base must be the same Parameter object in every role, as
         construction_sharing.place_frozen_role arranges (construction_sharing.py:105-118).
+        ``base`` (default: the first role's) may be a base-only role's own nn.Linear over
+        the same Parameters; ``role_names`` names the roles in order, adapter i being
+        role_names[i] (used by a RoleBatch routing).
         """
         _require(len(roles) > 0, 'at least one role module required')
-        base = roles[0].base
+        base = roles[0].base if base is None else base
+        _require(type(base) is nn.Linear, 'multi-LoRA base must be an actual native Linear')
         for m in roles:
             _require(isinstance(m, TrainableLowRankLinear), 'roles must be TrainableLowRankLinear modules')
             _require(m.base.weight is base.weight and m.base.bias is base.bias,
                      'roles must alias one frozen base (shared construction)')
+        names = list(role_names) if role_names is not None else []
+        _require(role_names is None or (len(names) == len(roles) and len(set(names)) == len(names)),
+                 'one distinct role name per adapter required')
         obj = cls.__new__(cls)
         nn.Module.__init__(obj)
         obj.base = base
         obj.lora_a = nn.ParameterList([m.lora_a for m in roles])
         obj.lora_b = nn.ParameterList([m.lora_b for m in roles])
         obj.scales = [m.scale for m in roles]
+        obj.role_ids = {n: i for i, n in enumerate(names)}
+        obj.active_roles = None
         return obj
 
     @property
@@ -144,7 +157,14 @@ class MultiLoRALinear(nn.Module):
         self.register_buffer("base_wq_t", wq.t().contiguous(), persistent=False)
         return self
 
-    def forward(self, x: torch.Tensor, routing: SegmentRouting) -> torch.Tensor:
+    def forward(self, x: torch.Tensor, routing: SegmentRouting | None = None) -> torch.Tensor:
+        """x [..., in] -> [..., out]. Without ``routing`` the active RoleBatch (set by
+        ``roles.roles_active``) routes x's sample-major rows."""
+        if routing is None:
+            if self.active_roles is None:
+                raise ValueError('multi-LoRA linear: no routing given and no role batch active')
+            rows = x.numel() // x.shape[-1] if x.dim() and x.shape[-1] else 0
+            routing = self.active_roles.routing(rows, self.role_ids)
         if getattr(self, "base_wq", None) is not None:
             return multi_lora_linear_fp8(x, self.base_wq, self.base_wscale, self.base.bias, list(self.lora_a),
                                          list(self.lora_b), self.scales, routing,

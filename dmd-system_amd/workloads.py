@@ -93,6 +93,11 @@ CONFIGS: dict[str, LoraConfig] = {
         name="wan13b_fp8", tokens=65520, hidden=1536, ffn=8960, ranks=(64, 64, 64, 64),
         seg_lengths=_partition(65520, 4, 5), seg_adapters=(0, 1, 2, 3), scale=1.0, seed=5, base_fp8=True,
         notes="config wan13b with the frozen base stored fp8 e4m3 + per-output-channel scale, 4 adapters"),
+    "wan13b_roles": LoraConfig(
+        name="wan13b_roles", tokens=98280, hidden=1536, ffn=8960, ranks=(64,), seg_lengths=(65520, 32760),
+        seg_adapters=(-1, 0), scale=1.0, seed=6,
+        notes="multi-role call site at the Wan-1.3B shape: teacher conditional + unconditional passes "
+              "(base only, 2 x 32760 tokens) and the fake critic (rank 64, 32760 tokens) in one call"),
 }
 
 
