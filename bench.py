@@ -15,10 +15,12 @@ Other configurations (parity-test cases, measured on request): --config
 tiny | wan22_5b | flux | wan13b_fp8 (frozen base stored e4m3 with a per-output-
 channel scale: forward on the e4m3 MFMA) | wan13b_roles (the multi-role call site:
 teacher conditional + unconditional rows base-only and the fake critic's rows with its
-adapter, in one call), --fwd-only for a forward-only step, and --per-role to time the
-same step as one call per role (this library, and the reference's unfused torch path).
+adapter, in one call), --fwd-only for a forward-only step, --per-role to time the
+same step as one call per role (this library, and the reference's unfused torch path),
+and --shared-qkv to feed q, k, v one input and run them as one stacked call (the step
+with three separate calls on that input is timed beside it).
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--config wan13b] [--fwd-only] [--per-role]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--config wan13b] [--fwd-only] [--per-role] [--shared-qkv]
 """
 from __future__ import annotations
 
@@ -47,6 +49,9 @@ def parse():
     p.add_argument("--kernel-reps", type=int, default=10)
     p.add_argument("--cpu-seconds", type=float, default=12.0, help="bounded CPU-baseline sample budget")
     p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--shared-qkv", action="store_true",
+                   help="q, k, v read one input (as in a DiT block) and run as one stacked call; the same "
+                        "step with three separate calls is timed beside it")
     p.add_argument("--per-role", action="store_true",
                    help="also time the same step as one call per segment (role), with this library and with "
                         "the reference's unfused torch path on the GPU")
@@ -123,21 +128,40 @@ def main():
         lins.append(L)
     torch.cuda.synchronize()
 
+    if args.shared_qkv:
+        if fp8:
+            raise SystemExit("--shared-qkv stacks bf16 bases only")
+        qkv = lins[:3]
+        for L in qkv[1:]:
+            L["x"] = qkv[0]["x"]  # one input, as the block's q / k / v read the normed hidden states
+
+    def stacked_step(fwd_only):
+        outs = pkg.shared_input_multi_lora(qkv[0]["x"], [L["w"] for L in qkv], [L["b"] for L in qkv],
+                                           [L["As"] for L in qkv], [L["Bs"] for L in qkv], scales, routing)
+        if not fwd_only:
+            torch.autograd.backward(list(outs), [L["dy"] for L in qkv])
+
     def forward(L):
         if fp8:
             return pkg.multi_lora_linear_fp8(L["x"], L["wq"], L["ws"], L["b"], L["As"], L["Bs"], scales, routing,
                                              wq_t=L["wqt"])
         return pkg.multi_lora_linear(L["x"], L["w"], L["b"], L["As"], L["Bs"], scales, routing)
 
-    def step():
+    def step(stack=args.shared_qkv):
+        rest = lins[3:] if stack else lins
         if args.fwd_only:
             with torch.no_grad():
-                for L in lins:
+                if stack:
+                    stacked_step(True)
+                for L in rest:
                     forward(L)
             return
         for L in lins:
             for t in [L["x"], *L["As"], *L["Bs"]]:
                 t.grad = None
+        if stack:
+            stacked_step(False)
+        for L in rest:
             forward(L).backward(L["dy"])
 
     for _ in range(args.warmup):
@@ -157,6 +181,17 @@ def main():
     flops_step = sum(flops_fn(L["K"], L["N"]) for L in lins)
     tflops = flops_step / (ms_per_step * 1e-3) / 1e12
     print(f"# step {ms_per_step:.3f} ms, {tflops:.1f} TFLOP/s", file=sys.stderr, flush=True)
+    unstacked = None
+    if args.shared_qkv:  # the same step, q / k / v as three calls on their one input
+        for _ in range(args.warmup):
+            step(False)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(args.steps):
+            step(False)
+        torch.cuda.synchronize()
+        ms = (time.perf_counter() - t0) * 1e3 / args.steps
+        unstacked = {"ms_per_step": round(ms, 4), "tflops": round(flops_step / (ms * 1e-3) / 1e12, 2)}
 
     # ---------------- per-kernel timing with HIP events on the launch stream
     reps = args.kernel_reps
@@ -283,7 +318,8 @@ def main():
         "config": {"workload": f"{cfg.name}: {pass_name} of the 6 DiT block linears "
                                f"(q,k,v,o {cfg.hidden}->{cfg.hidden}; ffn {cfg.hidden}->{cfg.ffn}->{cfg.hidden}), "
                                f"{cfg.tokens} tokens in segments {list(cfg.seg_lengths)}, ranks {list(cfg.ranks)}, "
-                               f"scale {cfg.scale}, bias on" + (", frozen base e4m3 + per-channel scale" if fp8 else ""),
+                               f"scale {cfg.scale}, bias on" + (", frozen base e4m3 + per-channel scale" if fp8 else "")
+                               + ("; q, k, v read one input and run as one stacked call" if args.shared_qkv else ""),
                    "tokens": cfg.tokens, "flops_per_step": flops_step, "pct_bf16_mfma_peak": round(
                        tflops / MFMA_BF16_PEAK_TFLOPS * 100, 2)},
         "roofline": roofline,
@@ -292,6 +328,7 @@ def main():
         "kernels": kern,
         "vendor_gemm_tflops": vendor,
         **({"per_role": per_role} if per_role is not None else {}),
+        **({"qkv_unstacked": unstacked} if unstacked is not None else {}),
         "device": {"name": props.name, "cus": props.multi_processor_count,
                    "gcn_arch": getattr(props, "gcnArchName", "")},
     }

@@ -6,6 +6,7 @@ Public API:
     MultiLoRAFP8Function, multi_lora_linear_fp8   the same with an e4m3 frozen base
     TrainableLowRankLinear, trainable_scope, MultiLoRALinear   drop-in modules
     RoleBatch, fuse_roles, roles_active  several roles' forwards in one pass over the shared base
+    fuse_shared_inputs, SharedInputGroup, SharedInputMultiLoRAFunction   linears reading one input, stacked
     kernels                              torch front end of each C-ABI entry point
     load_library()                       load libmlora.so (raises if missing)
 
@@ -14,10 +15,12 @@ The directory name is not a Python identifier; importers load it as
 ``__graft_entry__.py``).
 """
 from . import _lib, kernels
-from .function import MultiLoRAFP8Function, MultiLoRAFunction, multi_lora_linear, multi_lora_linear_fp8
+from .function import (MultiLoRAFP8Function, MultiLoRAFunction, SharedInputMultiLoRAFunction, multi_lora_linear,
+                       multi_lora_linear_fp8, shared_input_multi_lora)
 from .low_rank import MultiLoRALinear, TrainableLowRankLinear, trainable_scope
 from .roles import RoleBatch, fuse_roles, roles_active
 from .routing import BASE_ONLY, SegmentRouting
+from .shared_input import SharedInputGroup, fuse_shared_inputs, release_shared_inputs
 
 
 def load_library():
@@ -27,6 +30,7 @@ def load_library():
 __all__ = [
     "BASE_ONLY", "SegmentRouting", "MultiLoRAFunction", "multi_lora_linear", "MultiLoRAFP8Function",
     "multi_lora_linear_fp8", "MultiLoRALinear",
-    "TrainableLowRankLinear", "trainable_scope", "RoleBatch", "fuse_roles", "roles_active", "kernels",
-    "load_library",
+    "TrainableLowRankLinear", "trainable_scope", "RoleBatch", "fuse_roles", "roles_active",
+    "SharedInputMultiLoRAFunction", "shared_input_multi_lora", "SharedInputGroup", "fuse_shared_inputs",
+    "release_shared_inputs", "kernels", "load_library",
 ]

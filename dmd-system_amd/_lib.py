@@ -10,7 +10,7 @@ from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "libmlora.so"
 
-ABI_VERSION = 3
+ABI_VERSION = 4
 MAX_SEGMENTS = 128
 MAX_ADAPTERS = 32
 MAX_RANK = 256
@@ -36,7 +36,7 @@ SIGNATURES = {
     "mlora_gemm_fwd": (_int, [_vp, _i64, _i64, _i64, _vp, _i64, _i64, _vp, _int, _vp, _i64,
                               _pvp, _pi32, _i32, _pi64, _pi32, _i32, _vp, _i64, _int, _vp]),
     "mlora_gemm_dx": (_int, [_vp, _i64, _i64, _i64, _vp, _i64, _i64, _vp, _i64,
-                             _pvp, _pi32, _i32, _pi64, _pi32, _i32, _vp, _i64, _vp]),
+                             _pvp, _pi32, _i32, _pi64, _pi32, _i32, _vp, _i64, _int, _vp]),
     "mlora_seg_outer": (_int, [_vp, _i64, _i64, _i64, _vp, _i32, _pvp, _int, _int, _pi32, _i32,
                                _pi64, _pi32, _i32, _vp, _i64, _vp]),
     "mlora_seg_outer_workspace_bytes": (_i64, [_i64, _i64, _pi32, _i32, _pi64, _pi32, _i32]),

@@ -828,7 +828,7 @@ extern "C" int mlora_gemm_fwd(const void *x, int64_t ldx, int64_t M, int64_t K, 
 extern "C" int mlora_gemm_dx(const void *dy, int64_t lddy, int64_t M, int64_t N, const void *w, int64_t ldw, int64_t K,
                              const void *g_rows, int64_t ldg, const void *const *a_ptrs, const int32_t *ranks,
                              int32_t n_adapters, const int64_t *seg_offsets, const int32_t *adapter_ids,
-                             int32_t n_segments, void *dx, int64_t lddx, void *stream) {
+                             int32_t n_segments, void *dx, int64_t lddx, int accumulate, void *stream) {
   GemmArgs a{};
   // contraction over N, output columns K
   int st = fill_common(a, M, N, K, g_rows, ldg, a_ptrs, ranks, n_adapters, seg_offsets, adapter_ids, n_segments);
@@ -848,7 +848,7 @@ extern "C" int mlora_gemm_dx(const void *dy, int64_t lddy, int64_t M, int64_t N,
   a.bias_dtype = -1;
   a.Y = static_cast<uint16_t *>(dx);
   a.ldy = lddx;
-  a.accumulate = 0;
+  a.accumulate = accumulate ? 1 : 0;
   return dispatch_gemm<CfgNN256, CfgNN128>(a, static_cast<hipStream_t>(stream));
 }
 

@@ -599,6 +599,10 @@ extern "C" int mlora_shrink(const void *p, int64_t ldp, int64_t M, int64_t K, co
   if (rt <= 1) launch_shrink_rt<1>(a, (int)n, s);
   else if (rt == 2) launch_shrink_rt<2>(a, (int)n, s);
   else if (rt <= 4) launch_shrink_rt<4>(a, (int)n, s);
+  // ranks up to 192 in layout 0 (the stacked A of three linears that read one input):
+  // six 32-column tiles instead of eight (layout 1 needs 1 KB loads of whole k rows)
+  else if (rt <= 6 && a.op_layout == 0)
+    hipLaunchKernelGGL((shrink_kernel<6, 0>), dim3((int)n), dim3(256), 0, s, a);
   else launch_shrink_rt<8>(a, (int)n, s);
   return launch_status();
 }

@@ -22,7 +22,7 @@ from typing import Sequence
 import torch
 import torch.nn.functional as F
 
-from . import kernels
+from . import _lib, kernels
 from .routing import SegmentRouting
 
 
@@ -168,6 +168,132 @@ class MultiLoRAFP8Function(torch.autograd.Function):
 
         dx, dAs, dBs = _backward(ctx, dy, x, dx_gemm, ops[:n], ops[n:], row_div=dy_scale)
         return (dx, None, None, None, None, None, None, *dAs, *dBs)
+
+
+class SharedInputMultiLoRAFunction(torch.autograd.Function):
+    """``apply(x, routing, scales, groups, weights, biases, *lora_as, *lora_bs)``: G = ``groups``
+    multi-LoRA linears that read the same input x [M, K].
+
+    weights / biases: tuples of the G frozen bases ([N_g, K] bf16; bias [N_g] or None);
+    lora_as = [A_g,i for g < G for i < n] ([R, K] each), lora_bs likewise ([N_g, R]): one rank R
+    (a multiple of 16) for every linear and adapter, adapter i's scale scales[i] in every
+    linear. Returns the G outputs [M, N_g], each equal to its own multi-LoRA linear's.
+
+    Forward: one shrink of X by the stacked [A_0,i; …; A_{G-1},i] (X read once instead of G
+    times), then each linear's fused GEMM reading its R columns of the stacked h. Backward:
+    the G shrinks g_g = s·dY_g·B_g write side by side into one g [M, G·R] and its fragments;
+    dX accumulates the G linears' dY_g·W_g + g_g·A_g in the dX GEMM's epilogue (fp32 sum,
+    one bf16 rounding per call, instead of autograd's G-1 separate bf16 additions); dA of
+    every linear is one reduction over X (X read once); dB_g one reduction per dY_g.
+    """
+
+    @staticmethod
+    def forward(ctx, x, routing: SegmentRouting, scales: Sequence[float], groups: int, weights, biases, *ab):
+        G = int(groups)
+        n = len(ab) // (2 * G) if G > 0 else 0
+        if G < 2 or n == 0 or len(ab) != 2 * G * n or len(scales) != n or len(weights) != G or len(biases) != G:
+            raise ValueError("shared-input multi-LoRA: G >= 2 linears, G·n lora_a and G·n lora_b, one scale per adapter")
+        if any(w.requires_grad for w in weights) or any(b is not None and b.requires_grad for b in biases):
+            raise RuntimeError("multi-LoRA: the base weight and bias are frozen (requires_grad=False)")
+        M, K = x.shape
+        As = [list(ab[g * n:(g + 1) * n]) for g in range(G)]
+        Bs = [list(ab[G * n + g * n:G * n + (g + 1) * n]) for g in range(G)]
+        R = int(As[0][0].shape[0])
+        routing.validate_for(M, n)
+        for g in range(G):
+            N = weights[g].shape[0]
+            if weights[g].shape[1] != K:
+                raise ValueError(f"shared-input multi-LoRA: linear {g} has in_features {weights[g].shape[1]}, "
+                                 f"the input has {K}")
+            for a, b in zip(As[g], Bs[g]):
+                if a.shape != (R, K) or b.shape != (N, R):
+                    raise ValueError(f"shared-input multi-LoRA: lora_a {tuple(a.shape)} / lora_b {tuple(b.shape)} "
+                                     f"of linear {g} do not match rank {R}, in {K}, out {N}")
+        if R % 16:
+            raise ValueError("shared-input multi-LoRA: the rank must be a multiple of 16")
+        A_cat = [torch.cat([_as_operand(As[g][i]) for g in range(G)]) for i in range(n)]  # [G·R, K]
+        B_ops = [[_as_operand(b) for b in Bs[g]] for g in range(G)]
+        need_b_grad = any(ctx.needs_input_grad[6 + G * n:])
+        h_rows, h_frag = kernels.shrink(x, A_cat, 0, scales, routing, want_frag=need_b_grad, width=G * R)
+        ys = [kernels.gemm_fwd(x, weights[g], biases[g], h_rows[:, g * R:(g + 1) * R], B_ops[g], routing)
+              for g in range(G)]
+        ctx.save_for_backward(x, *A_cat, *[b for bg in B_ops for b in bg])
+        ctx.weights = tuple(weights)  # frozen bases: held, not saved for autograd
+        ctx.routing, ctx.scales, ctx.n, ctx.G, ctx.R = routing, tuple(float(v) for v in scales), n, G, R
+        ctx.h_frag = h_frag
+        ctx.a_dtypes = [[a.dtype for a in As[g]] for g in range(G)]
+        ctx.b_dtypes = [[b.dtype for b in Bs[g]] for g in range(G)]
+        return tuple(ys)
+
+    @staticmethod
+    def backward(ctx, *dys):
+        n, G, R, routing, ws = ctx.n, ctx.G, ctx.R, ctx.routing, ctx.weights
+        x, *ops = ctx.saved_tensors
+        A_cat = ops[:n]
+        B_ops = [ops[n + g * n:n + (g + 1) * n] for g in range(G)]
+        M = x.shape[0]
+        # an output nobody used has no gradient: it contributes zeros
+        dys = [torch.zeros((M, ws[g].shape[0]), dtype=torch.bfloat16, device=x.device) if d is None
+               else d.to(torch.bfloat16).contiguous() for g, d in enumerate(dys)]
+        need_x = ctx.needs_input_grad[0]
+        need_a = any(ctx.needs_input_grad[6:6 + G * n])
+        need_b = any(ctx.needs_input_grad[6 + G * n:])
+        jt = G * R // 16
+        g_rows = g_frag = None
+        if need_x or need_a:
+            g_rows = torch.empty((M, G * R), dtype=torch.bfloat16, device=x.device)
+            g_frag = kernels.alloc_frags(routing, jt, x.device) if need_a else None
+            for g in range(G):
+                kernels.shrink(dys[g], B_ops[g], 1, ctx.scales, routing, want_frag=need_a, width=G * R,
+                               h_out=g_rows[:, g * R:(g + 1) * R], frag_out=g_frag, frag_jt=jt, frag_t0=g * R // 16)
+        dx = None
+        if need_x:
+            for g in range(G):
+                dx = kernels.gemm_dx(dys[g], ws[g], g_rows[:, g * R:(g + 1) * R],
+                                     [a[g * R:(g + 1) * R] for a in A_cat], routing, out=dx, accumulate=g > 0)
+        dA = [[None] * n for _ in range(G)]
+        dB = [[None] * n for _ in range(G)]
+        if need_b:
+            for g in range(G):
+                outs = kernels.seg_outer(dys[g], ctx.h_frag, G * R, [R] * n, routing, 0, ctx.b_dtypes[g],
+                                         frag_jt=jt, frag_t0=g * R // 16)
+                dB[g] = [o if ctx.needs_input_grad[6 + G * n + g * n + i] else None for i, o in enumerate(outs)]
+        if need_a:
+            outs = kernels.seg_outer(x, g_frag, G * R, [G * R] * n, routing, 1, [torch.float32] * n)
+            dA = [[outs[i][g * R:(g + 1) * R].to(ctx.a_dtypes[g][i]) if ctx.needs_input_grad[6 + g * n + i] else None
+                   for i in range(n)] for g in range(G)]
+        return (dx, None, None, None, None, None, *[d for dg in dA for d in dg], *[d for dg in dB for d in dg])
+
+
+def _bf16_rows(x: torch.Tensor, weight_dtype: torch.dtype) -> torch.Tensor:
+    """x [..., K] as contiguous bf16 rows [M, K] (under bf16 autocast the cast is done here)."""
+    x2 = x.reshape(-1, x.shape[-1])
+    if torch.is_autocast_enabled("cuda") and torch.get_autocast_dtype("cuda") == torch.bfloat16:
+        x2 = x2.to(torch.bfloat16)
+        weight_dtype = torch.bfloat16
+    if x2.dtype != torch.bfloat16 or weight_dtype != torch.bfloat16:
+        raise RuntimeError("multi-LoRA linear computes in bfloat16: pass bf16 input and base weight, "
+                           "or call it under torch.autocast('cuda', dtype=torch.bfloat16)")
+    if not x2.is_cuda:
+        raise RuntimeError("multi-LoRA linear runs on the ROCm device only (HIP kernels, no CPU path)")
+    return x2.contiguous()
+
+
+def shared_input_multi_lora(x: torch.Tensor, weights: Sequence[torch.Tensor], biases: Sequence[torch.Tensor | None],
+                            lora_as: Sequence[Sequence[torch.Tensor]], lora_bs: Sequence[Sequence[torch.Tensor]],
+                            scales: Sequence[float], routing: SegmentRouting) -> tuple[torch.Tensor, ...]:
+    """Functional form of SharedInputMultiLoRAFunction over x [..., K]: the G linears' outputs
+    [..., N_g]; lora_as[g][i] / lora_bs[g][i] are linear g's adapter i."""
+    lead = x.shape[:-1]
+    G = len(weights)
+    x2 = _bf16_rows(x, weights[0].dtype)
+    ws = tuple(w.detach().to(torch.bfloat16) for w in weights)  # a no-op unless autocast runs fp32 bases
+    bs = tuple(None if b is None else b.detach() for b in biases)
+    flat_a = [a for g in range(G) for a in lora_as[g]]
+    flat_b = [b for g in range(G) for b in lora_bs[g]]
+    with torch.autocast("cuda", enabled=False):
+        ys = SharedInputMultiLoRAFunction.apply(x2, routing, tuple(scales), G, ws, bs, *flat_a, *flat_b)
+    return tuple(y.reshape(*lead, w.shape[0]) for y, w in zip(ys, ws))
 
 
 def multi_lora_linear(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None,

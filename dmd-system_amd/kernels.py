@@ -52,13 +52,35 @@ def frag_jtiles(width: int) -> int:
     return (width + 15) // 16
 
 
+_FRAG_TILE_BYTES = 2 * 64 * 16  # one j-tile (hi + lo) of one 32-row block in the fragment layout
+
+
+def alloc_frags(routing: SegmentRouting, jtiles: int, device) -> list:
+    """Empty hi/lo fragment buffers (one per call group of `routing`) of `jtiles` j-tiles."""
+    lib = _lib.load()
+    out = []
+    for r0, r1, off, ids in routing.groups(_lib.MAX_SEGMENTS):
+        o, i, n = _routing_arrays(off, ids)
+        nbytes = lib.mlora_frag_bytes(r1 - r0, jtiles, o, i, n)
+        _lib.check("mlora_frag_bytes", nbytes if nbytes < 0 else 0)
+        out.append(torch.empty(max(nbytes, 16) // 2, dtype=torch.bfloat16, device=device))
+    return out
+
+
 def shrink(p: torch.Tensor, ops: Sequence[torch.Tensor], op_layout: int, scales: Sequence[float],
            routing: SegmentRouting, want_frag: bool, width: int,
-           row_div: torch.Tensor | None = None) -> tuple[torch.Tensor, list | None]:
+           row_div: torch.Tensor | None = None, h_out: torch.Tensor | None = None,
+           frag_out: list | None = None, frag_jt: int | None = None,
+           frag_t0: int = 0) -> tuple[torch.Tensor, list | None]:
     """h = s·P·Op_aᵀ per segment -> (h_rows bf16 [M, width], per-call-group hi/lo fragments or None).
 
     row_div [M] fp32 (optional) divides the rows of h_rows only (the row scales of the e4m3 forward's X
     and of the e4m3 dX's dY).
+
+    Writing into a part of larger buffers (the stacked LoRA operands of linears that share
+    an input): h_out is a row-major view [M, >= r] whose row stride is the buffer's (rows
+    get their r_a values at its first columns), frag_out fragment buffers of `frag_jt`
+    j-tiles per block (alloc_frags) that receive h's j-tiles at j-tile `frag_t0` on.
     """
     M, K = p.shape
     _check_rows("P", p)
@@ -69,25 +91,27 @@ def shrink(p: torch.Tensor, ops: Sequence[torch.Tensor], op_layout: int, scales:
         _require(o.shape == ((r, K) if op_layout == 0 else (K, r)), "adapter operand shape")
     if row_div is not None:
         _check_scale("row_div", row_div, M)
-    h_rows = torch.empty((M, width), dtype=torch.bfloat16, device=p.device)
+    if h_out is not None:
+        _check_rows("h_out", h_out)
+        _require(h_out.shape[0] == M and h_out.shape[1] >= max([0, *ranks]), "h_out is [M, >= max rank]")
+    h_rows = h_out if h_out is not None else torch.empty((M, width), dtype=torch.bfloat16, device=p.device)
     lib = _lib.load()
     ptrs, rk, sc = _lib.ptr_array([_ptr(o) for o in ops]), _lib.i32_array(ranks), _lib.f32_array(scales)
-    jt = frag_jtiles(width)
+    jt = frag_jtiles(width) if frag_jt is None else frag_jt
+    _require(0 <= frag_t0 and frag_t0 * 16 + max([0, *ranks]) <= jt * 16, "fragment j-tiles out of range")
     stream = _stream(p)
-    frags = [] if want_frag else None
-    for r0, r1, off, ids in routing.groups(_lib.MAX_SEGMENTS):
+    frags = None
+    if want_frag:
+        frags = frag_out if frag_out is not None else alloc_frags(routing, jt, p.device)
+        _require(len(frags) == len(list(routing.groups(_lib.MAX_SEGMENTS))), "one fragment buffer per call group")
+    for g, (r0, r1, off, ids) in enumerate(routing.groups(_lib.MAX_SEGMENTS)):
         o, i, n = _routing_arrays(off, ids)
-        frag = None
-        if want_frag:
-            nbytes = lib.mlora_frag_bytes(r1 - r0, jt, o, i, n)
-            _lib.check("mlora_frag_bytes", nbytes if nbytes < 0 else 0)
-            frag = torch.empty(max(nbytes, 16) // 2, dtype=torch.bfloat16, device=p.device)
-            frags.append(frag)
+        fptr = None if frags is None else frags[g].data_ptr() + frag_t0 * _FRAG_TILE_BYTES
         if r1 == r0:
             continue
         _lib.check("mlora_shrink", lib.mlora_shrink(
             p[r0:r1].data_ptr(), p.stride(0), r1 - r0, K, ptrs, op_layout, rk, sc, len(ops),
-            o, i, n, h_rows[r0:r1].data_ptr(), width, _ptr(frag), jt,
+            o, i, n, h_rows[r0:r1].data_ptr(), h_rows.stride(0), fptr, jt,
             None if row_div is None else row_div[r0:r1].data_ptr(), stream))
     return h_rows, frags
 
@@ -95,7 +119,8 @@ def shrink(p: torch.Tensor, ops: Sequence[torch.Tensor], op_layout: int, scales:
 def gemm_fwd(x: torch.Tensor, w: torch.Tensor, bias: torch.Tensor | None, h_rows: torch.Tensor | None,
              bs: Sequence[torch.Tensor], routing: SegmentRouting, out: torch.Tensor | None = None,
              accumulate: bool = False) -> torch.Tensor:
-    """Y = X·Wᵀ + bias + per-segment h_rows·B_aᵀ, bf16 out."""
+    """Y = X·Wᵀ + bias + per-segment h_rows·B_aᵀ, bf16 out. h_rows may be a column slice of a
+    wider buffer (its row stride is passed)."""
     M, K = x.shape
     N = w.shape[0]
     _check_rows("X", x, K)
@@ -125,8 +150,9 @@ def gemm_fwd(x: torch.Tensor, w: torch.Tensor, bias: torch.Tensor | None, h_rows
 
 
 def gemm_dx(dy: torch.Tensor, w: torch.Tensor, g_rows: torch.Tensor | None, as_: Sequence[torch.Tensor],
-            routing: SegmentRouting) -> torch.Tensor:
-    """dX = dY·W + per-segment g_rows·A_a, bf16 out."""
+            routing: SegmentRouting, out: torch.Tensor | None = None, accumulate: bool = False) -> torch.Tensor:
+    """dX = dY·W + per-segment g_rows·A_a, bf16 out (accumulate: dX += ..., into `out`).
+    g_rows may be a column slice of a wider buffer (its row stride is passed)."""
     M, N = dy.shape
     K = w.shape[1]
     _check_rows("dY", dy, N)
@@ -135,7 +161,9 @@ def gemm_dx(dy: torch.Tensor, w: torch.Tensor, g_rows: torch.Tensor | None, as_:
     for a in as_:
         _check_rows("lora_a", a, K)
         _require(a.is_contiguous(), "lora_a must be contiguous [r, K]")
-    dx = torch.empty((M, K), dtype=torch.bfloat16, device=dy.device)
+    _require(not accumulate or out is not None, "accumulate needs the dX to add to")
+    dx = out if out is not None else torch.empty((M, K), dtype=torch.bfloat16, device=dy.device)
+    _check_rows("dX", dx, K)
     lib = _lib.load()
     ptrs, rk = _lib.ptr_array([_ptr(a) for a in as_]), _lib.i32_array(ranks)
     ldg = g_rows.stride(0) if g_rows is not None else 0
@@ -147,15 +175,17 @@ def gemm_dx(dy: torch.Tensor, w: torch.Tensor, g_rows: torch.Tensor | None, as_:
         gr = None if g_rows is None else g_rows[r0:r1].data_ptr()
         _lib.check("mlora_gemm_dx", lib.mlora_gemm_dx(
             dy[r0:r1].data_ptr(), dy.stride(0), r1 - r0, N, w.data_ptr(), w.stride(0), K, gr, ldg,
-            ptrs, rk, len(as_), o, i, n, dx[r0:r1].data_ptr(), dx.stride(0), stream))
+            ptrs, rk, len(as_), o, i, n, dx[r0:r1].data_ptr(), dx.stride(0), int(accumulate), stream))
     return dx
 
 
 def seg_outer(p: torch.Tensor, frags: list, width: int, ranks: Sequence[int], routing: SegmentRouting,
-              out_layout: int, out_dtypes: Sequence[torch.dtype]) -> list[torch.Tensor]:
+              out_layout: int, out_dtypes: Sequence[torch.dtype], frag_jt: int | None = None,
+              frag_t0: int = 0) -> list[torch.Tensor]:
     """Per-adapter Σ_m P[m,c]·h[m,j] -> [C, r_a] (layout 0) or [r_a, C] (layout 1).
 
-    `frags` are the hi/lo fragments written by `shrink` for the same routing and width.
+    `frags` are the hi/lo fragments written by `shrink` for the same routing and width; with
+    frag_jt / frag_t0, h is the part of fragments of frag_jt j-tiles that starts at j-tile frag_t0.
     """
     M, C = p.shape
     _check_rows("P", p, C)
@@ -164,7 +194,8 @@ def seg_outer(p: torch.Tensor, frags: list, width: int, ranks: Sequence[int], ro
     _require(frags is not None and len(frags) == len(groups), "h fragments from shrink() of the same routing")
     dtypes = list(out_dtypes)
     _require(all(d in _DT for d in dtypes), "adapter gradients are float32 or bfloat16")
-    jt = frag_jtiles(width)
+    jt = frag_jtiles(width) if frag_jt is None else frag_jt
+    _require(0 <= frag_t0 and frag_t0 * 16 + max([0, *ranks]) <= jt * 16, "fragment j-tiles out of range")
     outs: list[torch.Tensor | None] = [None] * len(ranks)
     stream = _stream(p)
     shape = (lambda r: (C, r)) if out_layout == 0 else (lambda r: (r, C))
@@ -182,7 +213,7 @@ def seg_outer(p: torch.Tensor, frags: list, width: int, ranks: Sequence[int], ro
             part = [torch.empty(shape(ranks[a]), dtype=dt if single else torch.float32, device=p.device)
                     if a in sel else None for a in range(len(ranks))]
             _lib.check("mlora_seg_outer", lib.mlora_seg_outer(
-                p[r0:r1].data_ptr(), p.stride(0), r1 - r0, C, _ptr(frag), jt,
+                p[r0:r1].data_ptr(), p.stride(0), r1 - r0, C, frag.data_ptr() + frag_t0 * _FRAG_TILE_BYTES, jt,
                 _lib.ptr_array([_ptr(t) for t in part]), out_layout, _DT[dt if single else torch.float32],
                 mask_ranks, len(ranks), o, i, n, ws.data_ptr(), ws.numel() * 4, stream))
             for a in sel:

@@ -56,6 +56,12 @@ class TrainableLowRankLinear(nn.Module):
         self.scale = float(alpha) / rank
 
     def forward(self, value):
+        group = self.__dict__.get('shared_input')
+        if group is not None:  # stacked with the other linears that read this input
+            return group(self, value)
+        return self._single(value)
+
+    def _single(self, value, routing=None):
         rows = value.numel() // value.shape[-1] if value.dim() else 0
         return multi_lora_linear(value, self.base.weight, self.base.bias, [self.lora_a], [self.lora_b],
                                  [self.scale], SegmentRouting.single(rows, 0))
@@ -160,6 +166,12 @@ class MultiLoRALinear(nn.Module):
     def forward(self, x: torch.Tensor, routing: SegmentRouting | None = None) -> torch.Tensor:
         """x [..., in] -> [..., out]. Without ``routing`` the active RoleBatch (set by
         ``roles.roles_active``) routes x's sample-major rows."""
+        group = self.__dict__.get('shared_input')
+        if group is not None:  # stacked with the other linears that read this input
+            return group(self, x, routing)
+        return self._single(x, routing)
+
+    def _single(self, x: torch.Tensor, routing: SegmentRouting | None = None) -> torch.Tensor:
         if routing is None:
             if self.active_roles is None:
                 raise ValueError('multi-LoRA linear: no routing given and no role batch active')

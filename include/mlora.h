@@ -43,7 +43,7 @@
 extern "C" {
 #endif
 
-#define MLORA_ABI_VERSION 3
+#define MLORA_ABI_VERSION 4
 
 /* Limits of one call (kernel-argument tables). Callers with more segments
  * split the rows into several calls; the Python host layer does this. */
@@ -134,13 +134,17 @@ int mlora_gemm_fwd(const void *x, int64_t ldx, int64_t M, int64_t K,
 /* Input gradient with the LoRA term fused into its epilogue:
  *   dX[m, k] = bf16( Σ_n dY[m,n]·W[n,k] + Σ_j g_rows[m,j]·A_a[j,k] )
  * g_rows = s_a·dY·B_a from mlora_shrink(op_layout=1). a_ptrs[i]: bf16 [r_i, K].
+ * If accumulate != 0, dX is read and the result added to it (dX += ...): the
+ * dX of linears that read one input, summed in fp32 before one rounding per
+ * call instead of autograd's separate bf16 additions (the q/k/v projections fed
+ * one tensor, runtime/wan13b_lora_cast.py:265-300).
  * Reference: autograd of low_rank.py:28 — dX = dY·W + (s·dY·B)·A. */
 int mlora_gemm_dx(const void *dy, int64_t lddy, int64_t M, int64_t N,
                   const void *w, int64_t ldw, int64_t K,
                   const void *g_rows, int64_t ldg,
                   const void *const *a_ptrs, const int32_t *ranks, int32_t n_adapters,
                   const int64_t *seg_offsets, const int32_t *adapter_ids, int32_t n_segments,
-                  void *dx, int64_t lddx,
+                  void *dx, int64_t lddx, int accumulate,
                   void *stream);
 
 /* Segmented outer-product reduction (adapter gradients):

@@ -35,7 +35,7 @@ def test_library_exports_every_declared_symbol(lib, pkg):
 
 
 def test_abi_version_and_status_strings(lib, pkg):
-    assert lib.mlora_abi_version() == pkg._lib.ABI_VERSION == 3
+    assert lib.mlora_abi_version() == pkg._lib.ABI_VERSION == 4
     for code in (0, -1, -2, -3, -4, -5):
         assert lib.mlora_status_string(code)
     assert b"unknown" in lib.mlora_status_string(-99)
@@ -149,3 +149,4 @@ def test_fp8_entry_points_validate_before_launch(lib, pkg):
     assert fwd8(off=[0, 60]) == L.ERR_INVALID            # routing must cover M rows
     assert fwd8(M=0, off=[0, 0]) == L.OK
     assert fwd8(M=0, off=[0, 0], ws=None) == L.OK        # w_scale may be NULL (all 1: the e4m3 dX)
+

@@ -94,6 +94,14 @@ def test_heterogeneous_ranks_many_adapters(pkg, dev):
     check_against_oracle(pkg, dev, case, [2.0] * 17, routing)
 
 
+def test_ranks_160_to_192(pkg, dev):
+    """Ranks 160..192: the forward shrink's six 32-column tiles (the backward's layout keeps eight)."""
+    lengths, ids = (300, 129, 211), (0, 1, 2)
+    case = make_case(sum(lengths), 320, 256, (192, 176, 160), lengths, ids, seed=21)
+    routing = pkg.SegmentRouting.from_lengths(lengths, ids)
+    check_against_oracle(pkg, dev, case, [0.25, 0.5, 1.0], routing)
+
+
 def test_more_segments_than_one_call(pkg, dev):
     """300 segments: the host splits the rows into calls of <= 128 segments."""
     rng = np.random.default_rng(14)

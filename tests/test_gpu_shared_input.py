@@ -1,0 +1,154 @@
+"""GPU parity of shared-input stacking: linears that read one tensor, run as one stacked
+call, give what each gives alone (forward), and the adapters and the input get the
+gradients of the separate calls (backward).
+
+Oracle: the exact fp64 product of the stacked linears, Σ_g over the members for dX
+(autograd's sum of the members' dX), per row segment (oracle/multilora_oracle.py
+restates it per linear). Tolerances: forward bit-exact against the same kernels called
+per member (each member's GEMM reads its own R columns of the stacked h, which the
+stacked shrink computes in the same order as the member's own); backward: dX, a sum over the G linears, within √G·2e-3 rel-L2 of the
+fp64 reference (one bf16 rounding per accumulating call) and no worse than the per-member
+path's (which rounds each member's dX and each bf16 addition), the adapters' gradients
+within 2e-3 of the per-member calls'.
+"""
+import pytest
+import torch
+from torch import nn
+
+from toy_dit import inputs, make_roles, rel_l2
+
+pytestmark = pytest.mark.gpu
+
+
+def _members(pkg, dev, G=3, K=512, N=256, ranks=(32, 32), seed=0):
+    g = torch.Generator().manual_seed(seed)
+    mods = []
+    for _ in range(G):
+        base = nn.Linear(K, N)
+        with torch.no_grad():
+            base.weight.copy_(torch.randn(N, K, generator=g) / K ** 0.5)
+            base.bias.copy_(torch.randn(N, generator=g) * 0.1)
+        m = pkg.MultiLoRALinear(base, ranks=list(ranks), alphas=[2.0 * r for r in ranks])
+        with torch.no_grad():
+            for b in m.lora_b:
+                b.copy_(torch.randn(b.shape, generator=g) * 0.05)
+        mods.append(m.to(dev, torch.bfloat16))
+    holder = nn.Module()
+    for i, m in enumerate(mods):
+        holder.add_module(f"m{i}", m)
+    return holder, mods
+
+
+def _reference(x, mods, routing, dys):
+    """fp64: per member Y_g, and dX = Σ_g dY_g·W_g + s·(dY_g·B_g)·A_g per segment."""
+    xd = x.double()
+    ys, dx = [], torch.zeros_like(xd)
+    for m, dy in zip(mods, dys):
+        W, b = m.base.weight.double(), m.base.bias.double()
+        y = xd @ W.T + b
+        dyd = dy.double()
+        dx += dyd @ W
+        for (r0, r1), a in zip(zip(routing.seg_offsets, routing.seg_offsets[1:]), routing.adapter_ids):
+            if a < 0 or r1 == r0:
+                continue
+            A, B, s = m.lora_a[a].double(), m.lora_b[a].double(), m.scales[a]
+            y[r0:r1] += s * (xd[r0:r1] @ A.T) @ B.T
+            dx[r0:r1] += s * (dyd[r0:r1] @ B) @ A
+        ys.append(y)
+    return ys, dx
+
+
+@pytest.mark.parametrize("lengths,ids,ranks", [((300, 212, 100), (0, 1, -1), (32, 32)), ((1000,), (1,), (32, 32)),
+                                               ((64, 64), (-1, 0), (32, 32)), ((400, 111), (1, 0), (64, 64))])
+def test_stacked_call_matches_members(pkg, dev, lengths, ids, ranks):
+    print(f"stacked q/k/v lengths {lengths} ids {ids} ranks {ranks}", flush=True)
+    holder, mods = _members(pkg, dev, ranks=ranks)
+    routing = pkg.SegmentRouting.from_lengths(lengths, ids)
+    M = sum(lengths)
+    x = torch.randn(M, 512, generator=torch.Generator().manual_seed(1)).to(dev, torch.bfloat16)
+    dys = [torch.randn(M, 256, generator=torch.Generator().manual_seed(2 + i)).to(dev, torch.bfloat16)
+           for i in range(3)]
+    params = [p for m in mods for p in (*m.lora_a, *m.lora_b)]
+
+    def run(fused):
+        for p in params:
+            p.grad = None
+        if fused:
+            pkg.fuse_shared_inputs(holder, [["m0", "m1", "m2"]])
+        xi = x.clone().requires_grad_(True)
+        ys = [m(xi, routing) for m in mods]
+        torch.autograd.backward(ys, dys)
+        if fused:
+            assert mods[0].shared_input.launches == 1
+            pkg.release_shared_inputs(holder)
+        return [y.detach() for y in ys], xi.grad, [None if p.grad is None else p.grad.clone() for p in params]
+
+    ys_f, dx_f, gr_f = run(True)
+    ys_s, dx_s, gr_s = run(False)
+    for a, b in zip(ys_f, ys_s):
+        assert torch.equal(a, b)
+    ref_y, ref_dx = _reference(x, mods, routing, dys)
+    for a, r in zip(ys_f, ref_y):
+        assert rel_l2(a, r) <= 2e-3
+    # dX sums G linears' products: the stacked path rounds once per accumulating call (G
+    # roundings), the separate path (autograd, as the reference runs it) rounds every member's
+    # dX and then each bf16 addition (2G-1 roundings, ~3e-3 here). The bound is the bf16 one
+    # per rounded partial sum, and the stacked dX must be no worse than the separate one.
+    G = len(mods)
+    assert rel_l2(dx_f, ref_dx) <= 2e-3 * G ** 0.5
+    assert rel_l2(dx_f, ref_dx) <= rel_l2(dx_s, ref_dx)
+    for a, b in zip(gr_f, gr_s):
+        assert (a is None) == (b is None)
+        if a is not None:
+            assert rel_l2(a, b) <= 2e-3
+
+
+def test_dit_block_with_roles_and_shared_inputs(pkg, dev):
+    """q/k/v and cross-attention k/v stacked inside the multi-role module tree: the block's
+    outputs and every adapter's gradients match the same tree without stacking."""
+    print("dit block roles + shared inputs", flush=True)
+    teacher, fake, gen = make_roles(pkg, hidden=256, ffn=512, heads=4, rank=16, device=dev, dtype=torch.bfloat16)
+    fused = pkg.fuse_roles({"teacher": teacher, "fake": fake, "gen": gen})
+    x, c = inputs(4, 48, 12, 256, dev, torch.bfloat16, seed=9)
+    w = torch.randn(4, 48, 256, generator=torch.Generator().manual_seed(10)).to(dev, torch.bfloat16)
+    rb = pkg.RoleBatch([("teacher", 1), ("fake", 2), ("gen", 1)])
+    params = [p for p in fused.parameters() if p.requires_grad]
+
+    def run(stacked):
+        for p in params:
+            p.grad = None
+        groups = pkg.fuse_shared_inputs(fused, [["q", "k", "v"], ["cross.k", "cross.v"]]) if stacked else []
+        with pkg.roles_active(fused, rb):
+            y = fused(x, c)
+        (y.float() * w.float()).sum().backward()
+        launches = [g.launches for g in groups]
+        pkg.release_shared_inputs(fused)
+        return y.detach(), [p.grad.clone() for p in params], launches
+
+    y_s, g_s, launches = run(True)
+    y_u, g_u, _ = run(False)
+    assert launches == [1, 1]
+    assert rel_l2(y_s, y_u) <= 1e-3
+    for a, b in zip(g_s, g_u):
+        assert rel_l2(a, b) <= 2e-3
+
+
+def test_reuse_only_for_the_same_unmodified_input(pkg, dev):
+    print("shared input reuse keys", flush=True)
+    holder, mods = _members(pkg, dev, G=2, ranks=(16,))
+    pkg.fuse_shared_inputs(holder, [["m0", "m1"]])
+    routing = pkg.SegmentRouting.single(256, 0)
+    x = torch.randn(256, 512, generator=torch.Generator().manual_seed(3)).to(dev, torch.bfloat16)
+    x0 = x.clone()
+    with torch.no_grad():
+        y0 = mods[0](x, routing)
+        x.add_(1.0)                      # in place: m1 must not reuse the stacked result
+        y1 = mods[1](x, routing)
+        assert mods[0].shared_input.launches == 2
+        y0b = mods[0](x0, routing)       # another tensor: a new stacked call, then m1 reuses it
+        y1b = mods[1](x0, routing)
+        assert mods[0].shared_input.launches == 3
+        pkg.release_shared_inputs(holder)
+        assert torch.equal(y0, mods[0](x0, routing)) and torch.equal(y0b, y0)
+        assert torch.equal(y1, mods[1](x, routing))
+        assert torch.equal(y1b, mods[1](x0, routing))

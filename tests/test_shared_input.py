@@ -1,0 +1,73 @@
+"""Host-side logic of shared-input stacking on CPU: which linears can be grouped, the
+fail-closed checks, and that grouping leaves parameters and state-dict keys alone.
+No kernel runs."""
+import pytest
+from torch import nn
+
+from toy_dit import make_roles
+
+GROUPS = [["q", "k", "v"], ["cross.k", "cross.v"]]
+
+
+def _fused(pkg, **kw):
+    teacher, fake, gen = make_roles(pkg, hidden=256, ffn=512, heads=4, rank=16, **kw)
+    return teacher, fake, gen, pkg.fuse_roles({"teacher": teacher, "fake": fake, "gen": gen})
+
+
+def test_groups_link_members_and_keep_state_dict(pkg):
+    _, fake, _, fused = _fused(pkg)
+    keys = list(fused.state_dict())
+    groups = pkg.fuse_shared_inputs(fused, GROUPS)
+    assert [g.names for g in groups] == [("q", "k", "v"), ("cross.k", "cross.v")]
+    assert all(fused.get_submodule(n).shared_input is groups[0] for n in GROUPS[0])
+    assert fused.cross.v.shared_input is groups[1] and fused.o.__dict__.get("shared_input") is None
+    assert (groups[0].K, groups[0].n, groups[0].rank) == (256, 2, 16)
+    assert list(fused.state_dict()) == keys
+    assert groups[0].members[1].lora_a[0] is fake.k.lora_a
+    pkg.release_shared_inputs(fused)
+    assert all(fused.get_submodule(n).shared_input is None for g in GROUPS for n in g)
+    # a single role's own modules group the same way
+    g = pkg.fuse_shared_inputs(fake, [["q", "k", "v"]])[0]
+    assert g.n == 1 and isinstance(g.members[0], pkg.TrainableLowRankLinear)
+
+
+def test_groups_fail_closed(pkg):
+    teacher, fake, gen, fused = _fused(pkg)
+    with pytest.raises(ValueError, match="shared input: missing linear nope"):
+        pkg.fuse_shared_inputs(fused, [["q", "nope"]])
+    with pytest.raises(ValueError, match="'norm1' is not a LoRA linear"):
+        pkg.fuse_shared_inputs(fused, [["q", "norm1"]])
+    with pytest.raises(ValueError, match="'k' is in two groups"):
+        pkg.fuse_shared_inputs(fused, [["q", "k"], ["k", "v"]])
+    pkg.release_shared_inputs(fused)
+    with pytest.raises(ValueError, match="one in_features"):
+        pkg.fuse_shared_inputs(fused, [["q", "ffn.2"]])
+    with pytest.raises(ValueError, match="at least two"):
+        pkg.fuse_shared_inputs(fused, [["q"]])
+    pkg.fuse_shared_inputs(fused, [["q", "k"]])
+    with pytest.raises(ValueError, match="already in a shared-input group"):
+        pkg.fuse_shared_inputs(fused, [["k", "v"]])
+    # rank 8 is not a whole 16-rank fragment tile
+    _, f8, _ = make_roles(pkg, hidden=256, ffn=512, heads=4, rank=8)
+    with pytest.raises(ValueError, match="multiple of 16"):
+        pkg.fuse_shared_inputs(f8, [["q", "k"]])
+    # linears of different out_features that read one input stack too (q with ffn.0)
+    _, small, _ = make_roles(pkg, hidden=32, ffn=64, heads=2, rank=16)
+    assert pkg.fuse_shared_inputs(small, [["q", "ffn.0"]])[0].K == 32
+    # members that route different roles cannot share one routing
+    _, _, _, partial = _fused(pkg, fake_targets=["q", "k", "v"], gen_targets=["q", "k"])
+    with pytest.raises(ValueError, match="members must have the same number of adapters|route different roles"):
+        pkg.fuse_shared_inputs(partial, [["q", "v"]])
+
+
+def test_scales_must_agree(pkg):
+    base = nn.Linear(256, 256)
+    a = pkg.MultiLoRALinear(base, ranks=[16], alphas=[16])
+    b = pkg.MultiLoRALinear(nn.Linear(256, 256), ranks=[16], alphas=[32])
+    holder = nn.Module()
+    holder.a, holder.b = a, b
+    with pytest.raises(ValueError, match="different scales"):
+        pkg.fuse_shared_inputs(holder, [["a", "b"]])
+    # biases may differ: one member with, one without
+    holder.b = pkg.MultiLoRALinear(nn.Linear(256, 512, bias=False), ranks=[16], alphas=[16])
+    assert len(pkg.fuse_shared_inputs(holder, [["a", "b"]])) == 1
