@@ -7,6 +7,7 @@ Public API:
     TrainableLowRankLinear, trainable_scope, MultiLoRALinear   drop-in modules
     RoleBatch, fuse_roles, roles_active  several roles' forwards in one pass over the shared base
     fuse_shared_inputs, SharedInputGroup, SharedInputMultiLoRAFunction   linears reading one input, stacked
+    export_adapters, import_adapters, save_adapters, load_adapters   PEFT / DiffSynth adapter state
     kernels                              torch front end of each C-ABI entry point
     load_library()                       load libmlora.so (raises if missing)
 
@@ -15,6 +16,7 @@ The directory name is not a Python identifier; importers load it as
 ``__graft_entry__.py``).
 """
 from . import _lib, kernels
+from .adapters import export_adapters, import_adapters, load_adapters, save_adapters
 from .function import (MultiLoRAFP8Function, MultiLoRAFunction, SharedInputMultiLoRAFunction, multi_lora_linear,
                        multi_lora_linear_fp8, shared_input_multi_lora)
 from .low_rank import MultiLoRALinear, TrainableLowRankLinear, trainable_scope
@@ -32,5 +34,6 @@ __all__ = [
     "multi_lora_linear_fp8", "MultiLoRALinear",
     "TrainableLowRankLinear", "trainable_scope", "RoleBatch", "fuse_roles", "roles_active",
     "SharedInputMultiLoRAFunction", "shared_input_multi_lora", "SharedInputGroup", "fuse_shared_inputs",
-    "release_shared_inputs", "kernels", "load_library",
+    "release_shared_inputs", "export_adapters", "import_adapters", "save_adapters", "load_adapters", "kernels",
+    "load_library",
 ]

@@ -108,3 +108,20 @@ def test_fused_block_backward_matches_roles(pkg, dev):
     assert all(a.abs().sum() > 0 for a in batched)
     assert rel_l2(dx_batched[1:], torch.cat(dxs[1:])) <= 2e-3
     assert rel_l2(dx_batched[:1], dxs[0]) <= 2e-3
+
+
+@pytest.mark.parametrize("fmt", ["peft", "diffsynth"])
+def test_exported_adapters_reload_bit_exact(pkg, dev, fmt):
+    """A role's adapters exported from the fused tree and imported into a fresh copy of the
+    role give the same outputs through the HIP path (power-of-two scale: exact in both formats)."""
+    print(f"adapter round trip {fmt}", flush=True)
+    teacher, fake, gen, fused = _roles(pkg, dev)
+    state, config = pkg.export_adapters(fused, role="fake", fmt=fmt)
+    teacher2, fake2, _ = make_roles(pkg, hidden=H, ffn=FFN, heads=HEADS, rank=RANK, device=dev,
+                                    dtype=torch.bfloat16, seed=7)
+    pkg.import_adapters(fake2, state, config, fmt=fmt)
+    x, c = inputs(2, 32, 8, H, dev, torch.bfloat16, seed=11)
+    with torch.no_grad():
+        for p, q in zip(teacher.parameters(), teacher2.parameters()):
+            q.copy_(p)  # the same frozen base (seed 7 drew another one)
+        assert torch.equal(fake(x, c), fake2(x, c))
