@@ -17,10 +17,12 @@ channel scale: forward on the e4m3 MFMA) | wan13b_roles (the multi-role call sit
 teacher conditional + unconditional rows base-only and the fake critic's rows with its
 adapter, in one call), --fwd-only for a forward-only step, --per-role to time the
 same step as one call per role (this library, and the reference's unfused torch path),
-and --shared-qkv to feed q, k, v one input and run them as one stacked call (the step
-with three separate calls on that input is timed beside it).
+--shared-qkv to feed q, k, v one input and run them as one stacked call (the step
+with three separate calls on that input is timed beside it), and --gated-residual to end o
+and ffn.2 in the block's gated residual x + y·gate fused into the GEMM epilogue (the step
+with the residual as torch ops after the linear is timed beside it).
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--config wan13b] [--fwd-only] [--per-role] [--shared-qkv]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--config wan13b] [--fwd-only] [--per-role] [--shared-qkv] [--gated-residual]
 """
 from __future__ import annotations
 
@@ -52,6 +54,10 @@ def parse():
     p.add_argument("--shared-qkv", action="store_true",
                    help="q, k, v read one input (as in a DiT block) and run as one stacked call; the same "
                         "step with three separate calls is timed beside it")
+    p.add_argument("--gated-residual", action="store_true",
+                   help="o and ffn.2 close their branch with the block's gated residual x + y*gate fused into "
+                        "the GEMM epilogue; the same step with the residual as torch ops after the linear is "
+                        "timed beside it")
     p.add_argument("--per-role", action="store_true",
                    help="also time the same step as one call per segment (role), with this library and with "
                         "the reference's unfused torch path on the GPU")
@@ -141,28 +147,52 @@ def main():
         if not fwd_only:
             torch.autograd.backward(list(outs), [L["dy"] for L in qkv])
 
-    def forward(L):
+    if args.gated_residual:
+        if fp8:
+            raise SystemExit("--gated-residual fuses into the bf16 GEMM only")
+        gen = torch.Generator(device=dev)
+        gen.manual_seed(99)
+        for L in lins:
+            if L["name"] in ("o", "ffn.2"):
+                L["res"] = torch.randn(cfg.tokens, L["N"], generator=gen, device=dev).to(torch.bfloat16)
+                L["res"].requires_grad_(not args.fwd_only)
+                # one gate row per role segment, as Wan's per-sample e[2] / e[5]
+                L["gate"] = torch.rand(len(cfg.seg_lengths), L["N"], generator=gen, device=dev) + 0.5
+        if len(set(cfg.seg_lengths)) != 1:
+            raise SystemExit("--gated-residual needs equal segment lengths (one gate row per segment)")
+
+    def unfused_gated(L):
+        y = pkg.multi_lora_linear(L["x"], L["w"], L["b"], L["As"], L["Bs"], scales, routing)
+        g = L["gate"].repeat_interleave(cfg.tokens // L["gate"].shape[0], dim=0)
+        return (L["res"].float() + y.float() * g).to(torch.bfloat16)
+
+    def forward(L, fuse=True):
+        if "gate" in L:
+            if fuse:
+                return pkg.multi_lora_linear_gated(L["x"], L["w"], L["b"], L["As"], L["Bs"], scales, routing,
+                                                   L["res"], L["gate"])
+            return unfused_gated(L)
         if fp8:
             return pkg.multi_lora_linear_fp8(L["x"], L["wq"], L["ws"], L["b"], L["As"], L["Bs"], scales, routing,
                                              wq_t=L["wqt"])
         return pkg.multi_lora_linear(L["x"], L["w"], L["b"], L["As"], L["Bs"], scales, routing)
 
-    def step(stack=args.shared_qkv):
+    def step(stack=args.shared_qkv, fuse=True):
         rest = lins[3:] if stack else lins
         if args.fwd_only:
             with torch.no_grad():
                 if stack:
                     stacked_step(True)
                 for L in rest:
-                    forward(L)
+                    forward(L, fuse)
             return
         for L in lins:
-            for t in [L["x"], *L["As"], *L["Bs"]]:
+            for t in [L["x"], *L["As"], *L["Bs"]] + ([L["res"]] if "res" in L else []):
                 t.grad = None
         if stack:
             stacked_step(False)
         for L in rest:
-            forward(L).backward(L["dy"])
+            forward(L, fuse).backward(L["dy"])
 
     for _ in range(args.warmup):
         step()
@@ -181,17 +211,21 @@ def main():
     flops_step = sum(flops_fn(L["K"], L["N"]) for L in lins)
     tflops = flops_step / (ms_per_step * 1e-3) / 1e12
     print(f"# step {ms_per_step:.3f} ms, {tflops:.1f} TFLOP/s", file=sys.stderr, flush=True)
-    unstacked = None
-    if args.shared_qkv:  # the same step, q / k / v as three calls on their one input
+    def timed_variant(**kw):
         for _ in range(args.warmup):
-            step(False)
+            step(**kw)
         torch.cuda.synchronize()
         t0 = time.perf_counter()
         for _ in range(args.steps):
-            step(False)
+            step(**kw)
         torch.cuda.synchronize()
         ms = (time.perf_counter() - t0) * 1e3 / args.steps
-        unstacked = {"ms_per_step": round(ms, 4), "tflops": round(flops_step / (ms * 1e-3) / 1e12, 2)}
+        return {"ms_per_step": round(ms, 4), "tflops": round(flops_step / (ms * 1e-3) / 1e12, 2)}
+
+    # the same step, q / k / v as three calls on their one input
+    unstacked = timed_variant(stack=False) if args.shared_qkv else None
+    # the same step, the gated residual as torch ops after the linear
+    unfused = timed_variant(fuse=False) if args.gated_residual else None
 
     # ---------------- per-kernel timing with HIP events on the launch stream
     reps = args.kernel_reps
@@ -319,7 +353,9 @@ def main():
                                f"(q,k,v,o {cfg.hidden}->{cfg.hidden}; ffn {cfg.hidden}->{cfg.ffn}->{cfg.hidden}), "
                                f"{cfg.tokens} tokens in segments {list(cfg.seg_lengths)}, ranks {list(cfg.ranks)}, "
                                f"scale {cfg.scale}, bias on" + (", frozen base e4m3 + per-channel scale" if fp8 else "")
-                               + ("; q, k, v read one input and run as one stacked call" if args.shared_qkv else ""),
+                               + ("; q, k, v read one input and run as one stacked call" if args.shared_qkv else "")
+                               + ("; o and ffn.2 end in the block's gated residual, fused" if args.gated_residual
+                                  else ""),
                    "tokens": cfg.tokens, "flops_per_step": flops_step, "pct_bf16_mfma_peak": round(
                        tflops / MFMA_BF16_PEAK_TFLOPS * 100, 2)},
         "roofline": roofline,
@@ -329,6 +365,7 @@ def main():
         "vendor_gemm_tflops": vendor,
         **({"per_role": per_role} if per_role is not None else {}),
         **({"qkv_unstacked": unstacked} if unstacked is not None else {}),
+        **({"gated_residual_unfused": unfused} if unfused is not None else {}),
         "device": {"name": props.name, "cus": props.multi_processor_count,
                    "gcn_arch": getattr(props, "gcnArchName", "")},
     }

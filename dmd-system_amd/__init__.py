@@ -4,6 +4,7 @@ Public API:
     SegmentRouting, BASE_ONLY            row-segment -> adapter routing
     MultiLoRAFunction, multi_lora_linear autograd op
     MultiLoRAFP8Function, multi_lora_linear_fp8   the same with an e4m3 frozen base
+    MultiLoRAGatedResidualFunction, multi_lora_linear_gated   with the block's gated residual fused
     TrainableLowRankLinear, trainable_scope, MultiLoRALinear   drop-in modules
     RoleBatch, fuse_roles, roles_active  several roles' forwards in one pass over the shared base
     fuse_shared_inputs, SharedInputGroup, SharedInputMultiLoRAFunction   linears reading one input, stacked
@@ -17,8 +18,9 @@ The directory name is not a Python identifier; importers load it as
 """
 from . import _lib, kernels
 from .adapters import export_adapters, import_adapters, load_adapters, save_adapters
-from .function import (MultiLoRAFP8Function, MultiLoRAFunction, SharedInputMultiLoRAFunction, multi_lora_linear,
-                       multi_lora_linear_fp8, shared_input_multi_lora)
+from .function import (MultiLoRAFP8Function, MultiLoRAFunction, MultiLoRAGatedResidualFunction,
+                       SharedInputMultiLoRAFunction, multi_lora_linear, multi_lora_linear_fp8,
+                       multi_lora_linear_gated, shared_input_multi_lora)
 from .low_rank import MultiLoRALinear, TrainableLowRankLinear, trainable_scope
 from .roles import RoleBatch, fuse_roles, roles_active
 from .routing import BASE_ONLY, SegmentRouting
@@ -31,7 +33,7 @@ def load_library():
 
 __all__ = [
     "BASE_ONLY", "SegmentRouting", "MultiLoRAFunction", "multi_lora_linear", "MultiLoRAFP8Function",
-    "multi_lora_linear_fp8", "MultiLoRALinear",
+    "multi_lora_linear_fp8", "MultiLoRAGatedResidualFunction", "multi_lora_linear_gated", "MultiLoRALinear",
     "TrainableLowRankLinear", "trainable_scope", "RoleBatch", "fuse_roles", "roles_active",
     "SharedInputMultiLoRAFunction", "shared_input_multi_lora", "SharedInputGroup", "fuse_shared_inputs",
     "release_shared_inputs", "export_adapters", "import_adapters", "save_adapters", "load_adapters", "kernels",

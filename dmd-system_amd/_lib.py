@@ -10,7 +10,7 @@ from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "libmlora.so"
 
-ABI_VERSION = 4
+ABI_VERSION = 5
 MAX_SEGMENTS = 128
 MAX_ADAPTERS = 32
 MAX_RANK = 256
@@ -35,6 +35,10 @@ SIGNATURES = {
     "mlora_frag_bytes": (_i64, [_i64, _i32, _pi64, _pi32, _i32]),
     "mlora_gemm_fwd": (_int, [_vp, _i64, _i64, _i64, _vp, _i64, _i64, _vp, _int, _vp, _i64,
                               _pvp, _pi32, _i32, _pi64, _pi32, _i32, _vp, _i64, _int, _vp]),
+    "mlora_gemm_fwd_gated": (_int, [_vp, _i64, _i64, _i64, _vp, _i64, _i64, _vp, _int, _vp, _i64,
+                                    _pvp, _pi32, _i32, _pi64, _pi32, _i32, _vp, _i64, _vp, _i64, _i64,
+                                    _vp, _i64, _vp]),
+    "mlora_gate_scale_rows": (_int, [_vp, _i64, _i64, _i64, _vp, _i64, _i64, _vp, _i64, _vp]),
     "mlora_gemm_dx": (_int, [_vp, _i64, _i64, _i64, _vp, _i64, _i64, _vp, _i64,
                              _pvp, _pi32, _i32, _pi64, _pi32, _i32, _vp, _i64, _int, _vp]),
     "mlora_seg_outer": (_int, [_vp, _i64, _i64, _i64, _vp, _i32, _pvp, _int, _int, _pi32, _i32,

@@ -44,6 +44,12 @@ struct GemmArgs {
   int32_t tiles_m, tiles_n;
   AdapterTable ext;  // NT: B_a [Ncols, r]; NN: A_a [r, Ncols]
   SegTable seg;
+  // Gated residual epilogue (gemm_kernel<C, true>): the stored value is
+  // bf16(res[m, n] + bf16(Y[m, n])·gate[m / gate_rows, n]) instead of Y.
+  const uint16_t *res;
+  const float *gate;
+  int64_t ldres, ldgate;
+  int32_t gate_rows;
 };
 
 template <int BM_, int BN_, int WM_, int WN_, bool NN_, bool F8_ = false, int KB_ = 128, int STAGES_ = 2,
@@ -624,7 +630,16 @@ __device__ __forceinline__ f32x4 col4(const void *p, bool bf16, int c, int ncols
 // leaves in 16-byte stores that cover whole rows. Otherwise (and always when
 // accumulating into Y, which adds the old value in fp32 before the one
 // rounding) each lane stores its 4 consecutive columns directly.
-template <class C, bool STAGED, bool ACCUM = true>
+// x + y·g of the reference's gated residual: fp32 multiply, then fp32 add, each
+// rounded to nearest (no fused multiply-add), as runtime/helios_residual_kernel.py:66-86
+// states it.
+__device__ __forceinline__ float gated_add(float x, float y, float g) {
+#pragma clang fp contract(off)
+  const float p = y * g;
+  return x + p;
+}
+
+template <class C, bool STAGED, bool ACCUM = true, bool RESID = false>
 __device__ __forceinline__ void store_tile(const f32x16 (&acc)[C::TM][C::TN], const GemmArgs &args, MLORA_LDS char *lds,
                                            int m0, int n0, int wm0, int wn0, int lane, int wave) {
   const int rows_here = min(C::BM, args.M - m0);
@@ -706,15 +721,35 @@ __device__ __forceinline__ void store_tile(const f32x16 (&acc)[C::TM][C::TN], co
   for (int it = 0; it < ROWS_W / RPI; ++it) {
     const int r = wave * ROWS_W + it * RPI + lane / CH;
     const int q = lane % CH;
-    const u32x4 d = *(const lds_u4 *)(lds + r * ROWB + 16 * (q ^ (r % CH)));
+    u32x4 d = *(const lds_u4 *)(lds + r * ROWB + 16 * (q ^ (r % CH)));
     const int n = n0 + 8 * q;
     const int32_t off = (r < rows_here && n < args.Ncols) ? (int32_t)(r * ldy_b + n * 2) : kOOB;
+    if constexpr (RESID) {
+      // the 8 bf16 values of d are bf16(Y); x and gate of the same 8 columns
+      if (off != kOOB) {
+        const int64_t m = m0 + r;
+        const u32x4 xv = *(const MLORA_GLOBAL u32x4 *)(args.res + m * args.ldres + n);
+        const MLORA_GLOBAL f32x4 *gp = (const MLORA_GLOBAL f32x4 *)(args.gate + (m / args.gate_rows) * args.ldgate + n);
+        const f32x4 g0 = gp[0], g1 = gp[1];
+        float o[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const uint32_t yw = d[e / 2], xw = xv[e / 2];
+          const float y = bf16_to_f32((uint16_t)(e % 2 ? yw >> 16 : yw & 0xffff));
+          const float x = bf16_to_f32((uint16_t)(e % 2 ? xw >> 16 : xw & 0xffff));
+          o[e] = gated_add(x, y, e < 4 ? g0[e] : g1[e - 4]);
+        }
+#pragma unroll
+        for (int e = 0; e < 4; ++e) d[e] = pack2_bf16(o[2 * e], o[2 * e + 1]);
+      }
+    }
     buf_store16(ry, off, d);
   }
 }
 
-// One workgroup per output tile.
-template <class C>
+// One workgroup per output tile. RESID: the stored value is the block's gated
+// residual of the result (see store_tile).
+template <class C, bool RESID = false>
 __global__ __launch_bounds__(C::THREADS, C::WAVES_PER_SIMD) void gemm_kernel(const GemmArgs args) {
   __shared__ u32x4 smem[C::LDS_BYTES / 16];
   MLORA_LDS char *lds = (MLORA_LDS char *)smem;
@@ -733,7 +768,7 @@ __global__ __launch_bounds__(C::THREADS, C::WAVES_PER_SIMD) void gemm_kernel(con
   FragAddr<C> fa;
   fa.init(wm0, wn0, lane);
   contract_tile<C>(acc, args, lds, fa, m0, n0, tid);
-  store_tile<C, true>(acc, args, lds, m0, n0, wm0, wn0, lane, wave);
+  store_tile<C, true, true, RESID>(acc, args, lds, m0, n0, wm0, wn0, lane, wave);
 }
 
 using CfgNT256 = GemmCfg<256, 256, 4, 2, false, false, 128, 2, true>;
@@ -743,14 +778,14 @@ using CfgNN256 = GemmCfg<256, 256, 4, 2, true, false, 128, 2, true>;
 using CfgNT128 = GemmCfg<128, 128, 2, 2, false>;
 using CfgNN128 = GemmCfg<128, 128, 2, 2, true>;
 
-template <class C>
+template <class C, bool RESID = false>
 static int launch_gemm(GemmArgs &a, hipStream_t stream) {
   a.tiles_m = (a.M + C::BM - 1) / C::BM;
   a.tiles_n = (a.Ncols + C::BN - 1) / C::BN;
   const int64_t nblocks = (int64_t)a.tiles_m * a.tiles_n;
   if (nblocks == 0) return MLORA_OK;
   if (nblocks > INT32_MAX) return MLORA_ERR_LIMIT;
-  hipLaunchKernelGGL(gemm_kernel<C>, dim3((unsigned)nblocks), dim3(C::THREADS), 0, stream, a);
+  hipLaunchKernelGGL((gemm_kernel<C, RESID>), dim3((unsigned)nblocks), dim3(C::THREADS), 0, stream, a);
   return launch_status();
 }
 
@@ -758,11 +793,11 @@ static int launch_gemm(GemmArgs &a, hipStream_t stream) {
 // whenever it still gives every CU a tile; the 4-wave 128x128 tile otherwise.
 // (A persistent form whose k-tile ring runs across output tiles, and
 // 256x128 tiles with a 3-stage ring, both measured slower.)
-template <class Big, class Small>
+template <class Big, class Small, bool RESID = false>
 static int dispatch_gemm(GemmArgs &a, hipStream_t stream) {
   const int64_t big_tiles = (int64_t)((a.M + 255) / 256) * ((a.Ncols + 255) / 256);
-  if (big_tiles >= 256) return launch_gemm<Big>(a, stream);
-  return launch_gemm<Small>(a, stream);
+  if (big_tiles >= 256) return launch_gemm<Big, RESID>(a, stream);
+  return launch_gemm<Small, RESID>(a, stream);
 }
 
 static int fill_common(GemmArgs &a, int64_t M, int64_t Kc, int64_t Ncols, const void *e, int64_t lde,
@@ -823,6 +858,44 @@ extern "C" int mlora_gemm_fwd(const void *x, int64_t ldx, int64_t M, int64_t K, 
   a.ldy = ldy;
   a.accumulate = accumulate ? 1 : 0;
   return dispatch_gemm<CfgNT256, CfgNT128>(a, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int mlora_gemm_fwd_gated(const void *x, int64_t ldx, int64_t M, int64_t K, const void *w, int64_t ldw,
+                                    int64_t N, const void *bias, int bias_dtype, const void *h_rows, int64_t ldh,
+                                    const void *const *b_ptrs, const int32_t *ranks, int32_t n_adapters,
+                                    const int64_t *seg_offsets, const int32_t *adapter_ids, int32_t n_segments,
+                                    const void *res, int64_t ldres, const float *gate, int64_t ldgate,
+                                    int64_t gate_rows, void *out, int64_t ldout, void *stream) {
+  GemmArgs a{};
+  int st = fill_common(a, M, K, N, h_rows, ldh, b_ptrs, ranks, n_adapters, seg_offsets, adapter_ids, n_segments);
+  if (st) return st;
+  if ((st = check_bf16_matrix(x, ldx, M, K))) return st;
+  if ((st = check_bf16_matrix(w, ldw, N, K))) return st;
+  if ((st = check_bf16_matrix(res, ldres, M, N))) return st;
+  if ((st = check_bf16_matrix(out, ldout, M, N))) return st;
+  if (M == 0 || N == 0) return MLORA_OK;
+  if (out == nullptr || res == nullptr || gate == nullptr || gate_rows < 1 || gate_rows > INT32_MAX)
+    return MLORA_ERR_INVALID;
+  if (ldgate < N || ldgate % 4 != 0 || !aligned16(gate)) return MLORA_ERR_UNSUPPORTED;  // 16-byte gate rows
+  if (bias != nullptr) {
+    if (bias_dtype != MLORA_F32 && bias_dtype != MLORA_BF16) return MLORA_ERR_UNSUPPORTED;
+    if (!aligned16(bias)) return MLORA_ERR_UNSUPPORTED;
+  }
+  if (!offsets_fit(ldx, 256) || !offsets_fit(ldout, 256) || !offsets_fit(ldw, 256)) return MLORA_ERR_LIMIT;
+  a.P = static_cast<const uint16_t *>(x);
+  a.Q = static_cast<const uint16_t *>(w);
+  a.ldp = ldx;
+  a.ldq = ldw;
+  a.bias = bias;
+  a.bias_dtype = bias ? bias_dtype : -1;
+  a.Y = static_cast<uint16_t *>(out);
+  a.ldy = ldout;
+  a.res = static_cast<const uint16_t *>(res);
+  a.ldres = ldres;
+  a.gate = gate;
+  a.ldgate = ldgate;
+  a.gate_rows = (int32_t)gate_rows;
+  return dispatch_gemm<CfgNT256, CfgNT128, true>(a, static_cast<hipStream_t>(stream));
 }
 
 extern "C" int mlora_gemm_dx(const void *dy, int64_t lddy, int64_t M, int64_t N, const void *w, int64_t ldw, int64_t K,

@@ -126,6 +126,42 @@ class MultiLoRAFunction(torch.autograd.Function):
         return (dx, None, None, None, None, *dAs, *dBs)
 
 
+class MultiLoRAGatedResidualFunction(torch.autograd.Function):
+    """``apply(x, weight, bias, routing, scales, residual, gate, *lora_as, *lora_bs)``: the linear
+    that closes a DiT block branch, with the block's gated residual fused into its epilogue:
+
+        out = bf16(residual + bf16(Y)·gate[row group]),   Y = the multi-LoRA linear of x
+
+    (reference/livewan_wan21/wan/modules/model.py:305-313, rounding as
+    runtime/helios_residual_kernel.py:66-86). residual [M, N] bf16, gate [G, N] fp32 frozen
+    (M / G consecutive rows per gate row: the tokens of one sample). Backward (frozen gate,
+    helios_residual_kernel.py:90-133): d residual = dOut; dY = bf16(dOut·gate), then the
+    linear's own backward.
+    """
+
+    @staticmethod
+    def forward(ctx, x, weight, bias, routing: SegmentRouting, scales: Sequence[float], residual, gate, *ab):
+        if ctx.needs_input_grad[1] or ctx.needs_input_grad[2]:
+            raise RuntimeError("multi-LoRA: the base weight and bias are frozen (requires_grad=False)")
+        if ctx.needs_input_grad[6]:
+            raise RuntimeError("gated residual: the gate is frozen (a trainable modulation is not fused)")
+        A_ops, B_ops, h_rows = _prepare(ctx, x, weight.shape[0], ab, scales, routing, grad0=7)
+        out = kernels.gemm_fwd_gated(x, weight, bias, h_rows, B_ops, routing, residual, gate)
+        ctx.save_for_backward(x, weight, gate, *A_ops, *B_ops)
+        return out
+
+    @staticmethod
+    def backward(ctx, dout):
+        n = ctx.n
+        x, weight, gate, *ops = ctx.saved_tensors
+        dout = dout.to(torch.bfloat16).contiguous()
+        dy = kernels.gate_scale_rows(dout, gate)
+        dx_gemm = lambda g_rows: kernels.gemm_dx(dy, weight, g_rows, ops[:n], ctx.routing)
+        dx, dAs, dBs = _backward(ctx, dy, x, dx_gemm, ops[:n], ops[n:])
+        d_res = dout if ctx.needs_input_grad[5] else None
+        return (dx, None, None, None, None, d_res, None, *dAs, *dBs)
+
+
 class MultiLoRAFP8Function(torch.autograd.Function):
     """``apply(x, wq, w_scale, wq_t, bias, routing, scales, *lora_as, *lora_bs)``:
     the same linear with the frozen base stored as e4m3 ``wq`` [N, K] and one
@@ -314,6 +350,30 @@ def multi_lora_linear(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor 
     with torch.autocast("cuda", enabled=False):
         y = MultiLoRAFunction.apply(x2.contiguous(), weight, bias, routing, tuple(scales), *lora_as, *lora_bs)
     return y.reshape(*lead, weight.shape[0])
+
+
+def multi_lora_linear_gated(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None,
+                            lora_as: Sequence[torch.Tensor], lora_bs: Sequence[torch.Tensor],
+                            scales: Sequence[float], routing: SegmentRouting, residual: torch.Tensor,
+                            gate: torch.Tensor) -> torch.Tensor:
+    """residual + linear(x)·gate, fused (MultiLoRAGatedResidualFunction). x [..., K]; residual
+    [..., N] bf16 with x's leading shape; gate fp32 [B, 1, N] (one row per sample of a [B, L, ...]
+    batch), [B, L, N] (per token) or [G, N]. Returns [..., N] bf16."""
+    K, N = x.shape[-1], weight.shape[0]
+    lead = x.shape[:-1]
+    x2 = _bf16_rows(x, weight.dtype)
+    weight = weight.to(torch.bfloat16)
+    if residual.dtype != torch.bfloat16 or residual.shape != (*lead, N):
+        raise RuntimeError("gated residual: the residual stream must be bf16 with the output's shape")
+    if gate.dtype != torch.float32 or gate.shape[-1] != N:
+        raise RuntimeError("gated residual: the gate must be float32 with out_features columns")
+    g2 = gate.reshape(-1, N)
+    if g2.stride(1) != 1 or g2.stride(0) % 4 or g2.data_ptr() % 16:
+        g2 = g2.contiguous()
+    with torch.autocast("cuda", enabled=False):
+        out = MultiLoRAGatedResidualFunction.apply(x2, weight, bias, routing, tuple(scales),
+                                                   residual.reshape(-1, N).contiguous(), g2, *lora_as, *lora_bs)
+    return out.reshape(*lead, N)
 
 
 def multi_lora_linear_fp8(x: torch.Tensor, wq: torch.Tensor, w_scale: torch.Tensor, bias: torch.Tensor | None,

@@ -149,6 +149,67 @@ def gemm_fwd(x: torch.Tensor, w: torch.Tensor, bias: torch.Tensor | None, h_rows
     return y
 
 
+def _gate_rows(gate: torch.Tensor, M: int, N: int) -> int:
+    """Rows of Y per gate row for a gate [G, N] (fp32, row pitch a multiple of 4) over M rows."""
+    _require(gate.is_cuda and gate.dtype == torch.float32 and gate.dim() == 2 and gate.shape[1] == N
+             and gate.stride(1) == 1 and gate.stride(0) % 4 == 0 and gate.data_ptr() % 16 == 0,
+             "gate must be a float32 [G, N] matrix with 16-byte rows")
+    G = gate.shape[0]
+    _require(G >= 1 and M % G == 0, f"{M} rows do not split evenly over {G} gate rows")
+    return M // G
+
+
+def gemm_fwd_gated(x: torch.Tensor, w: torch.Tensor, bias: torch.Tensor | None, h_rows: torch.Tensor | None,
+                   bs: Sequence[torch.Tensor], routing: SegmentRouting, res: torch.Tensor, gate: torch.Tensor,
+                   out: torch.Tensor | None = None) -> torch.Tensor:
+    """out = bf16(res + bf16(X·Wᵀ + bias + h_rows·B_aᵀ)·gate[row group]) (the block's gated residual;
+    gate [G, N] fp32, M / G consecutive rows per gate row). out may be res (in place)."""
+    M, K = x.shape
+    N = w.shape[0]
+    _check_rows("X", x, K)
+    _check_rows("W", w, K)
+    _check_rows("residual", res, N)
+    _require(res.shape[0] == M, "residual has the rows of X")
+    per = _gate_rows(gate, M, N)
+    if bias is not None:
+        _require(bias.is_cuda and bias.dtype in _DT and bias.is_contiguous() and bias.shape == (N,), "bias")
+    ranks = [int(b.shape[1]) for b in bs]
+    for b in bs:
+        _check_rows("lora_b", b)
+        _require(b.is_contiguous() and b.shape[0] == N, "lora_b must be contiguous [N, r]")
+    y = out if out is not None else torch.empty((M, N), dtype=torch.bfloat16, device=x.device)
+    _check_rows("out", y, N)
+    lib = _lib.load()
+    ptrs, rk = _lib.ptr_array([_ptr(b) for b in bs]), _lib.i32_array(ranks)
+    ldh = h_rows.stride(0) if h_rows is not None else 0
+    stream = _stream(x)
+    for r0, r1, off, ids in routing.groups(_lib.MAX_SEGMENTS):
+        if r1 == r0:
+            continue
+        _require(r0 % per == 0, "a call group must start at a gate-row boundary")
+        o, i, n = _routing_arrays(off, ids)
+        hr = None if h_rows is None else h_rows[r0:r1].data_ptr()
+        _lib.check("mlora_gemm_fwd_gated", lib.mlora_gemm_fwd_gated(
+            x[r0:r1].data_ptr(), x.stride(0), r1 - r0, K, w.data_ptr(), w.stride(0), N,
+            _ptr(bias), _DT[bias.dtype] if bias is not None else 0, hr, ldh,
+            ptrs, rk, len(bs), o, i, n, res[r0:r1].data_ptr(), res.stride(0),
+            gate[r0 // per:].data_ptr(), gate.stride(0), per, y[r0:r1].data_ptr(), y.stride(0), stream))
+    return y
+
+
+def gate_scale_rows(dout: torch.Tensor, gate: torch.Tensor) -> torch.Tensor:
+    """dY = bf16(dOut · gate[row group]): the frozen-gate derivative of the gated residual."""
+    M, N = dout.shape
+    _check_rows("dOut", dout, N)
+    per = _gate_rows(gate, M, N)
+    dy = torch.empty((M, N), dtype=torch.bfloat16, device=dout.device)
+    lib = _lib.load()
+    _lib.check("mlora_gate_scale_rows", lib.mlora_gate_scale_rows(
+        dout.data_ptr(), dout.stride(0), M, N, gate.data_ptr(), gate.stride(0), per, dy.data_ptr(), dy.stride(0),
+        _stream(dout)))
+    return dy
+
+
 def gemm_dx(dy: torch.Tensor, w: torch.Tensor, g_rows: torch.Tensor | None, as_: Sequence[torch.Tensor],
             routing: SegmentRouting, out: torch.Tensor | None = None, accumulate: bool = False) -> torch.Tensor:
     """dX = dY·W + per-segment g_rows·A_a, bf16 out (accumulate: dX += ..., into `out`).

@@ -20,7 +20,7 @@ from typing import Sequence
 import torch
 from torch import nn
 
-from .function import multi_lora_linear, multi_lora_linear_fp8
+from .function import multi_lora_linear, multi_lora_linear_fp8, multi_lora_linear_gated
 from .kernels import quantize_rows_fp8
 from .routing import SegmentRouting
 
@@ -65,6 +65,13 @@ class TrainableLowRankLinear(nn.Module):
         rows = value.numel() // value.shape[-1] if value.dim() else 0
         return multi_lora_linear(value, self.base.weight, self.base.bias, [self.lora_a], [self.lora_b],
                                  [self.scale], SegmentRouting.single(rows, 0))
+
+    def gated_residual(self, value, residual, gate):
+        """``residual + self(value) * gate`` of a DiT block (model.py:305-313), fused into the
+        GEMM epilogue (bf16 residual stream, frozen fp32 gate)."""
+        rows = value.numel() // value.shape[-1] if value.dim() else 0
+        return multi_lora_linear_gated(value, self.base.weight, self.base.bias, [self.lora_a], [self.lora_b],
+                                       [self.scale], SegmentRouting.single(rows, 0), residual, gate)
 
 
 def trainable_scope(native, config):
@@ -171,12 +178,25 @@ class MultiLoRALinear(nn.Module):
             return group(self, x, routing)
         return self._single(x, routing)
 
-    def _single(self, x: torch.Tensor, routing: SegmentRouting | None = None) -> torch.Tensor:
+    def _routing(self, x: torch.Tensor, routing: SegmentRouting | None) -> SegmentRouting:
         if routing is None:
             if self.active_roles is None:
                 raise ValueError('multi-LoRA linear: no routing given and no role batch active')
             rows = x.numel() // x.shape[-1] if x.dim() and x.shape[-1] else 0
             routing = self.active_roles.routing(rows, self.role_ids)
+        return routing
+
+    def gated_residual(self, x: torch.Tensor, residual: torch.Tensor, gate: torch.Tensor,
+                       routing: SegmentRouting | None = None) -> torch.Tensor:
+        """``residual + self(x, routing) * gate`` of a DiT block (model.py:305-313), fused into
+        the GEMM epilogue (bf16 residual stream, frozen fp32 gate)."""
+        if getattr(self, "base_wq", None) is not None:
+            raise RuntimeError("gated residual: the e4m3 base is not fused; call the linear and add")
+        return multi_lora_linear_gated(x, self.base.weight, self.base.bias, list(self.lora_a), list(self.lora_b),
+                                       self.scales, self._routing(x, routing), residual, gate)
+
+    def _single(self, x: torch.Tensor, routing: SegmentRouting | None = None) -> torch.Tensor:
+        routing = self._routing(x, routing)
         if getattr(self, "base_wq", None) is not None:
             return multi_lora_linear_fp8(x, self.base_wq, self.base_wscale, self.base.bias, list(self.lora_a),
                                          list(self.lora_b), self.scales, routing,

@@ -43,7 +43,7 @@
 extern "C" {
 #endif
 
-#define MLORA_ABI_VERSION 4
+#define MLORA_ABI_VERSION 5
 
 /* Limits of one call (kernel-argument tables). Callers with more segments
  * split the rows into several calls; the Python host layer does this. */
@@ -130,6 +130,33 @@ int mlora_gemm_fwd(const void *x, int64_t ldx, int64_t M, int64_t K,
                    const int64_t *seg_offsets, const int32_t *adapter_ids, int32_t n_segments,
                    void *y, int64_t ldy, int accumulate,
                    void *stream);
+
+/* mlora_gemm_fwd with the DiT block's gated residual fused into the epilogue: the linear
+ * closes a branch (attention out-projection, FFN down-projection) whose output y enters
+ * the residual stream as x' = x + y·gate (reference/livewan_wan21/wan/modules/model.py:305-313;
+ * the exact contract of runtime/helios_residual_kernel.py:66-86):
+ *   out[m, n] = bf16( RN( res[m, n] + RN( bf16(Y[m, n]) · gate[m / gate_rows, n] ) ) )
+ * with Y the value mlora_gemm_fwd would store, fp32 multiply then fp32 add, each rounded to
+ * nearest (no fused multiply-add). res (x) and out are bf16 [M, N] and may be the same
+ * matrix (in-place update of x); gate is fp32 with ⌈M / gate_rows⌉ rows of pitch ldgate
+ * (ldgate a multiple of 4, 16-byte aligned): gate_rows = tokens per sample for a per-sample
+ * gate [B, 1, N], 1 for a per-token gate. Y itself is not written. */
+int mlora_gemm_fwd_gated(const void *x, int64_t ldx, int64_t M, int64_t K,
+                         const void *w, int64_t ldw, int64_t N,
+                         const void *bias, int bias_dtype,
+                         const void *h_rows, int64_t ldh,
+                         const void *const *b_ptrs, const int32_t *ranks, int32_t n_adapters,
+                         const int64_t *seg_offsets, const int32_t *adapter_ids, int32_t n_segments,
+                         const void *res, int64_t ldres, const float *gate, int64_t ldgate, int64_t gate_rows,
+                         void *out, int64_t ldout,
+                         void *stream);
+/* Backward of that gated residual for a frozen gate: dY[m, n] = bf16(dOut[m, n] · gate[m / gate_rows, n])
+ * (one fp32 multiply rounded to nearest: runtime/helios_residual_kernel.py:90-133); the
+ * gradient of x is dOut. gate as in mlora_gemm_fwd_gated. */
+int mlora_gate_scale_rows(const void *dout, int64_t ldout, int64_t M, int64_t N,
+                          const float *gate, int64_t ldgate, int64_t gate_rows,
+                          void *dy, int64_t lddy,
+                          void *stream);
 
 /* Input gradient with the LoRA term fused into its epilogue:
  *   dX[m, k] = bf16( Σ_n dY[m,n]·W[n,k] + Σ_j g_rows[m,j]·A_a[j,k] )

@@ -307,6 +307,27 @@ def forward_livewan(x, w, b, As, Bs, scales, seg_offsets, adapter_ids) -> np.nda
 
 # ------------------------------------------------------------------ metrics
 
+def gated_residual(x, y, gate, gate_rows: int) -> np.ndarray:
+    """The DiT block's residual update x' = x + y·gate with the rounding contract of
+    runtime/helios_residual_kernel.py:66-86 (the Wan block: model.py:305-313):
+    bf16( RN_f32( f32(x) + RN_f32( f32(y) · gate[m // gate_rows] ) ) ) — a float32
+    multiply, then a float32 add (numpy rounds each operation; no fused multiply-add),
+    then bf16 round-to-nearest-even. x, y: bf16 values [M, N]; gate: float32 [G, N]."""
+    x = np.asarray(x, dtype=np.float32)
+    y = np.asarray(y, dtype=np.float32)
+    g = np.repeat(np.asarray(gate, dtype=np.float32), gate_rows, axis=0)[: x.shape[0]]
+    p = np.multiply(y, g, dtype=np.float32)
+    return bf16_round(np.add(x, p, dtype=np.float32))
+
+
+def gate_scale(dout, gate, gate_rows: int) -> np.ndarray:
+    """Frozen-gate backward of gated_residual (helios_residual_kernel.py:90-133):
+    dY = bf16(RN_f32(f32(dOut) · gate[m // gate_rows])); dX = dOut."""
+    d = np.asarray(dout, dtype=np.float32)
+    g = np.repeat(np.asarray(gate, dtype=np.float32), gate_rows, axis=0)[: d.shape[0]]
+    return bf16_round(np.multiply(d, g, dtype=np.float32))
+
+
 def rel_l2(got, want) -> float:
     got = np.asarray(got, np.float64)
     want = np.asarray(want, np.float64)

@@ -35,7 +35,7 @@ def test_library_exports_every_declared_symbol(lib, pkg):
 
 
 def test_abi_version_and_status_strings(lib, pkg):
-    assert lib.mlora_abi_version() == pkg._lib.ABI_VERSION == 4
+    assert lib.mlora_abi_version() == pkg._lib.ABI_VERSION == 5
     for code in (0, -1, -2, -3, -4, -5):
         assert lib.mlora_status_string(code)
     assert b"unknown" in lib.mlora_status_string(-99)
@@ -150,3 +150,33 @@ def test_fp8_entry_points_validate_before_launch(lib, pkg):
     assert fwd8(M=0, off=[0, 0]) == L.OK
     assert fwd8(M=0, off=[0, 0], ws=None) == L.OK        # w_scale may be NULL (all 1: the e4m3 dX)
 
+
+
+def test_gated_residual_entry_points_validate(lib, pkg):
+    L = pkg._lib
+    off, ids = L.i64_array([0, 64]), L.i32_array([-1])
+    b, rk = L.ptr_array([0x4000]), L.i32_array([8])
+
+    def fwd(res=0x7000, gate=0x8000, ldgate=64, gate_rows=16, out=0x9000, M=64):
+        o = L.i64_array([0, M])
+        return lib.mlora_gemm_fwd_gated(0x1000, 64, M, 64, 0x2000, 64, 64, None, 1, None, 0, b, rk, 1, o, ids, 1,
+                                        res, 64, gate, ldgate, gate_rows, out, 64, None)
+
+    assert fwd(res=None) == L.ERR_INVALID
+    assert fwd(gate=None) == L.ERR_INVALID
+    assert fwd(gate_rows=0) == L.ERR_INVALID
+    assert fwd(ldgate=60) == L.ERR_UNSUPPORTED                 # gate rows shorter than N
+    assert fwd(ldgate=66) == L.ERR_UNSUPPORTED                 # gate rows are 16-byte chunks
+    assert fwd(gate=0x8004) == L.ERR_UNSUPPORTED
+    assert fwd(res=0x7008) == L.ERR_UNSUPPORTED
+    assert fwd(M=0) == L.OK
+
+    def gs(dout=0x1000, gate=0x8000, ldgate=64, gate_rows=4, dy=0x3000, M=8, N=64):
+        return lib.mlora_gate_scale_rows(dout, 64, M, N, gate, ldgate, gate_rows, dy, 64, None)
+
+    assert gs(gate=None) == L.ERR_INVALID
+    assert gs(gate_rows=0) == L.ERR_INVALID
+    assert gs(ldgate=62) == L.ERR_UNSUPPORTED
+    assert gs(dy=0x3002) == L.ERR_UNSUPPORTED
+    assert gs(M=0) == L.OK
+    assert gs(M=-1) == L.ERR_INVALID

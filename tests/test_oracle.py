@@ -411,3 +411,40 @@ def test_fp8_dx_matches_brute_force():
     exact = O.backward(x, Wd, As, Bs, scales, off, ids, dy2)[0]
     np.testing.assert_allclose(O.dx_fp8_quantized_dy(dy2, wq, ws1, As, Bs, scales, off, ids), exact,
                                rtol=1e-12, atol=1e-9)
+
+
+# ------------------------------------------------------------------ gated residual
+
+def test_gated_residual_rounds_multiply_and_add_separately():
+    """bf16(RN(x + RN(y·g))) — helios_residual_kernel.py:66-86. Against torch's float32 ops
+    (an independent library doing one rounding per operation), and against a single-rounding
+    (fused multiply-add) evaluation, which must differ on some inputs: that pins the order."""
+    import torch
+    rng = np.random.default_rng(31)
+    M, N = 4096, 256
+    x = O.bf16_round(rng.standard_normal((M, N)).astype(np.float32))
+    y = O.bf16_round(rng.standard_normal((M, N)).astype(np.float32))
+    g = rng.standard_normal((4, N)).astype(np.float32)
+    got = O.gated_residual(x, y, g, M // 4)
+    tx, ty = torch.from_numpy(x), torch.from_numpy(y)
+    tg = torch.from_numpy(g).repeat_interleave(M // 4, dim=0)
+    want = (tx + ty * tg).to(torch.bfloat16).float().numpy()
+    assert np.array_equal(got, want)
+    gg = np.repeat(g, M // 4, axis=0).astype(np.float64)
+    fused = O.bf16_round((x.astype(np.float64) + y.astype(np.float64) * gg).astype(np.float32))
+    assert (fused != got).sum() > 0  # the contraction is observable after bf16 rounding
+    # gate rows: row m takes gate row m // gate_rows
+    one = O.gated_residual(np.zeros((6, 8), np.float32), np.ones((6, 8), np.float32),
+                           np.arange(16, dtype=np.float32).reshape(2, 8), 3)
+    assert np.array_equal(one[:3], np.tile(np.arange(8, dtype=np.float32), (3, 1)))
+    assert np.array_equal(one[3:], np.tile(np.arange(8, 16, dtype=np.float32), (3, 1)))
+
+
+def test_gate_scale_is_one_rounded_product():
+    import torch
+    rng = np.random.default_rng(32)
+    d = O.bf16_round(rng.standard_normal((64, 32)).astype(np.float32))
+    g = rng.standard_normal((64, 32)).astype(np.float32)
+    got = O.gate_scale(d, g, 1)
+    want = (torch.from_numpy(d) * torch.from_numpy(g)).to(torch.bfloat16).float().numpy()
+    assert np.array_equal(got, want)
