@@ -128,6 +128,7 @@ def main():
         for t in As + Bs:
             t.requires_grad_(not args.fwd_only)
         L = dict(name=name, K=K, N=N, x=x, w=w, b=b, As=As, Bs=Bs, dy=dy)
+        L["wt"] = w.t().contiguous()  # the frozen base transposed once, for the NT form of dX
         if fp8:
             L["wq"], L["ws"] = kernels.quantize_rows_fp8(w)
             L["wqt"] = L["wq"].t().contiguous()  # the frozen e4m3 base transposed, for the e4m3 dX
@@ -162,7 +163,7 @@ def main():
             raise SystemExit("--gated-residual needs equal segment lengths (one gate row per segment)")
 
     def unfused_gated(L):
-        y = pkg.multi_lora_linear(L["x"], L["w"], L["b"], L["As"], L["Bs"], scales, routing)
+        y = pkg.multi_lora_linear(L["x"], L["w"], L["b"], L["As"], L["Bs"], scales, routing, weight_t=L["wt"])
         g = L["gate"].repeat_interleave(cfg.tokens // L["gate"].shape[0], dim=0)
         return (L["res"].float() + y.float() * g).to(torch.bfloat16)
 
@@ -170,12 +171,12 @@ def main():
         if "gate" in L:
             if fuse:
                 return pkg.multi_lora_linear_gated(L["x"], L["w"], L["b"], L["As"], L["Bs"], scales, routing,
-                                                   L["res"], L["gate"])
+                                                   L["res"], L["gate"], weight_t=L["wt"])
             return unfused_gated(L)
         if fp8:
             return pkg.multi_lora_linear_fp8(L["x"], L["wq"], L["ws"], L["b"], L["As"], L["Bs"], scales, routing,
                                              wq_t=L["wqt"])
-        return pkg.multi_lora_linear(L["x"], L["w"], L["b"], L["As"], L["Bs"], scales, routing)
+        return pkg.multi_lora_linear(L["x"], L["w"], L["b"], L["As"], L["Bs"], scales, routing, weight_t=L["wt"])
 
     def step(stack=args.shared_qkv, fuse=True):
         rest = lins[3:] if stack else lins
@@ -257,12 +258,13 @@ def main():
             x, dy = L["x"].detach(), L["dy"]
             h_rows, h_frag = kernels.shrink(x, A_ops, 0, scales, routing, True, R)
             g_rows, g_frag = kernels.shrink(dy, B_ops, 1, scales, routing, True, R)
+            A_t = [a.t().contiguous() for a in A_ops]  # the NT form of dX contracts g with A_aᵀ
             lora_mr = sum(m * cfg.ranks[a] for m, a in seg if a >= 0)
             r_sum = sum(cfg.ranks)
             runs = {
                 "gemm_fwd": (lambda: kernels.gemm_fwd(x, L["w"], L["b"], h_rows, B_ops, routing),
                              2 * M * K * N + 2 * lora_mr * N, 0),
-                "gemm_dx": (lambda: kernels.gemm_dx(dy, L["w"], g_rows, A_ops, routing),
+                "gemm_dx": (lambda: kernels.gemm_fwd(dy, L["wt"], None, g_rows, A_t, routing),
                             2 * M * K * N + 2 * lora_mr * K, 0),
                 "shrink_x": (lambda: kernels.shrink(x, A_ops, 0, scales, routing, True, R),
                              2 * lora_mr * K, M * K * 2 + r_sum * K * 2 + lora_mr * (2 + 4)),
@@ -387,7 +389,7 @@ def per_role_timing(pkg, cfg, lins, scales, args, flops_step):
 
     def lib_call(L, r0, r1, ad):
         return pkg.multi_lora_linear(xs[id(L), r0], L["w"], L["b"], L["As"], L["Bs"], scales,
-                                     pkg.SegmentRouting.single(r1 - r0, ad))
+                                     pkg.SegmentRouting.single(r1 - r0, ad), weight_t=L["wt"])
 
     def torch_call(L, r0, r1, ad):
         x = xs[id(L), r0]

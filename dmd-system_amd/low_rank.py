@@ -30,6 +30,24 @@ def _require(value, message):
         raise ValueError('native trainable scope: ' + message)
 
 
+def _base_t(module: nn.Module, x: torch.Tensor) -> torch.Tensor | None:
+    """The frozen base weight transposed ([in, out] bf16, contiguous), for the NT form of the
+    dX GEMM; made on the first forward that will need dX and remade when the weight changes
+    (storage, in-place version, dtype or device). A plain attribute, not a buffer: no
+    state-dict entry. None when no dX will be computed or ``module.transposed_base_for_dx``
+    is False (then dX runs on the NN kernel and no copy is kept)."""
+    if not (torch.is_grad_enabled() and x.requires_grad) or not getattr(module, 'transposed_base_for_dx', True):
+        return None
+    w = module.base.weight
+    key = (w.data_ptr(), w._version, w.dtype, w.device)
+    cache = module.__dict__.get('_base_t_cache')
+    if cache is None or cache[0] != key:
+        with torch.no_grad():
+            cache = (key, w.detach().to(torch.bfloat16).t().contiguous())
+        module.__dict__['_base_t_cache'] = cache
+    return cache[1]
+
+
 def _init_pair(rank: int, base: nn.Linear, dtype=None) -> tuple[nn.Parameter, nn.Parameter]:
     # low_rank.py:21-23: A Kaiming-uniform(a=sqrt(5)) i.e. U(±1/sqrt(in)), B zeros
     dt = dtype or base.weight.dtype
@@ -64,14 +82,15 @@ class TrainableLowRankLinear(nn.Module):
     def _single(self, value, routing=None):
         rows = value.numel() // value.shape[-1] if value.dim() else 0
         return multi_lora_linear(value, self.base.weight, self.base.bias, [self.lora_a], [self.lora_b],
-                                 [self.scale], SegmentRouting.single(rows, 0))
+                                 [self.scale], SegmentRouting.single(rows, 0), weight_t=_base_t(self, value))
 
     def gated_residual(self, value, residual, gate):
         """``residual + self(value) * gate`` of a DiT block (model.py:305-313), fused into the
         GEMM epilogue (bf16 residual stream, frozen fp32 gate)."""
         rows = value.numel() // value.shape[-1] if value.dim() else 0
         return multi_lora_linear_gated(value, self.base.weight, self.base.bias, [self.lora_a], [self.lora_b],
-                                       [self.scale], SegmentRouting.single(rows, 0), residual, gate)
+                                       [self.scale], SegmentRouting.single(rows, 0), residual, gate,
+                                       weight_t=_base_t(self, value))
 
 
 def trainable_scope(native, config):
@@ -193,7 +212,8 @@ class MultiLoRALinear(nn.Module):
         if getattr(self, "base_wq", None) is not None:
             raise RuntimeError("gated residual: the e4m3 base is not fused; call the linear and add")
         return multi_lora_linear_gated(x, self.base.weight, self.base.bias, list(self.lora_a), list(self.lora_b),
-                                       self.scales, self._routing(x, routing), residual, gate)
+                                       self.scales, self._routing(x, routing), residual, gate,
+                                       weight_t=_base_t(self, x))
 
     def _single(self, x: torch.Tensor, routing: SegmentRouting | None = None) -> torch.Tensor:
         routing = self._routing(x, routing)
@@ -202,4 +222,4 @@ class MultiLoRALinear(nn.Module):
                                          list(self.lora_b), self.scales, routing,
                                          wq_t=getattr(self, "base_wq_t", None))
         return multi_lora_linear(x, self.base.weight, self.base.bias, list(self.lora_a), list(self.lora_b),
-                                 self.scales, routing)
+                                 self.scales, routing, weight_t=_base_t(self, x))

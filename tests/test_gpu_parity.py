@@ -33,19 +33,20 @@ def make_case(M, K, N, ranks, lengths, ids, seed, bias=True, dtype=torch.bfloat1
     return x, w, b, As, Bs, dy
 
 
-def run_hip(pkg, dev, x, w, b, As, Bs, dy, scales, routing, need_x=True):
+def run_hip(pkg, dev, x, w, b, As, Bs, dy, scales, routing, need_x=True, transposed=False):
     xg = x.to(dev).requires_grad_(need_x)
     Ag = [a.to(dev).requires_grad_(True) for a in As]
     Bg = [v.to(dev).requires_grad_(True) for v in Bs]
-    y = pkg.multi_lora_linear(xg, w.to(dev), None if b is None else b.to(dev), Ag, Bg, scales, routing)
+    wt = w.to(dev).t().contiguous() if transposed else None
+    y = pkg.multi_lora_linear(xg, w.to(dev), None if b is None else b.to(dev), Ag, Bg, scales, routing, weight_t=wt)
     y.backward(dy.to(dev))
     torch.cuda.synchronize()
     return y, (xg.grad if need_x else None), [a.grad for a in Ag], [v.grad for v in Bg]
 
 
-def check_against_oracle(pkg, dev, case, scales, routing, tol=TOL):
+def check_against_oracle(pkg, dev, case, scales, routing, tol=TOL, transposed=False):
     x, w, b, As, Bs, dy = case
-    y, dx, dAs, dBs = run_hip(pkg, dev, *case, scales, routing)
+    y, dx, dAs, dBs = run_hip(pkg, dev, *case, scales, routing, transposed=transposed)
     off, ids = routing.seg_offsets, routing.adapter_ids
     Af, Bf = [f64(a) for a in As], [f64(v) for v in Bs]
     y_ref = O.forward(f64(x), f64(w), None if b is None else f64(b), Af, Bf, scales, off, ids)
@@ -92,6 +93,15 @@ def test_heterogeneous_ranks_many_adapters(pkg, dev):
     case = make_case(sum(lengths), 512, 384, ranks, lengths, ids, seed=13)
     routing = pkg.SegmentRouting.from_lengths(lengths, ids)
     check_against_oracle(pkg, dev, case, [2.0] * 17, routing)
+
+
+@pytest.mark.parametrize("lengths,ids", [((77, 301, 1, 250, 371), (2, 0, 3, -1, 1)), ((512, 512), (0, 1))])
+def test_dx_on_the_transposed_base(pkg, dev, lengths, ids):
+    """dX through the NT GEMM against the frozen base held transposed (the modules' path)."""
+    M = sum(lengths)
+    case = make_case(M, 136, 200, (24, 8, 40, 16), lengths, ids, seed=33)
+    routing = pkg.SegmentRouting.from_lengths(lengths, ids)
+    check_against_oracle(pkg, dev, case, [0.5, 2.0, 1.0, 3.0], routing, transposed=True)
 
 
 def test_ranks_160_to_192(pkg, dev):
