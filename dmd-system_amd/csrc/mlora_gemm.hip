@@ -53,7 +53,7 @@ struct GemmArgs {
 };
 
 template <int BM_, int BN_, int WM_, int WN_, bool NN_, bool F8_ = false, int KB_ = 128, int STAGES_ = 2,
-          bool RING5_ = false>
+          bool RING5_ = false, bool SPREAD_ = false>
 struct GemmCfg {
   static constexpr int BM = BM_, BN = BN_, WM = WM_, WN = WN_;
   static constexpr bool NN = NN_;
@@ -100,6 +100,10 @@ struct GemmCfg {
   // LDS offsets of the P and Q tiles of a k-tile in phase ph (its index mod
   // PERIOD). Stages: the Q fragment addresses carry B_BASE, so q_off is
   // relative to it and stays within the 16-bit ds_read offset field.
+  // SPREAD (RING5): the P-half loads a step issues before its barrier are
+  // spread over all the substeps before the barrier instead of the first one
+  // (fewer loads queued at the texture unit at once: 1-3% per launch).
+  static constexpr bool SPREAD = SPREAD_;
   static constexpr int p_off(int ph) { return RING5 ? ((2 * ph) % 5) * A_BYTES : ph * A_BYTES; }
   static constexpr int q_off(int ph) { return RING5 ? ((2 * ph + 1) % 5) * A_BYTES : ph * B_BYTES; }
   static_assert(LDS_BYTES <= 163840, "the ring must fit the 160 KB of LDS");
@@ -240,9 +244,20 @@ struct Pipe {
 // addressed by lane 4e + (j >> 2); lane i pointing at row k0 + (i >> 2),
 // column c0 + 4(i & 3) therefore yields 4 consecutive contraction values of
 // column c0 + j: half of the B fragment of v_mfma_f32_32x32x16_bf16.
+// LDS offsets past 64 KB do not fit the 16-bit offset field of a ds_read, so
+// each fragment address also has copies 64 KB and 128 KB higher (a1/a2,
+// b1/b2) that the compiler cannot see through: reads of the upper slots use
+// them with an in-range immediate instead of one hoisted address register per
+// (substep, tile, slot).
+__device__ __forceinline__ int32_t opaque_vgpr(int32_t x) {
+  asm volatile("" : "+v"(x));
+  return x;
+}
+
 template <class C>
 struct FragAddr {
   int32_t a[C::NSUB], b[C::NN ? C::TN : C::NSUB];
+  int32_t a1[C::NSUB], a2[C::NSUB], b1[C::NSUB], b2[C::NSUB];
   __device__ __forceinline__ void init(int wm0, int wn0, int lane) {
     const int z = swzk<C::CPR>(lane & 31);  // lane-constant: fragment rows are 32-aligned + lane
 #pragma unroll
@@ -258,6 +273,15 @@ struct FragAddr {
       for (int j = 0; j < C::TN; ++j) {
         const int c = (wn0 + 32 * j + 16 * g1) / 8 + ((i & 3) >> 1);
         b[j] = C::B_BASE + (8 * h + (i >> 2)) * C::QROW + 16 * (c ^ (4 * m)) + 8 * (i & 1);
+      }
+    }
+#pragma unroll
+    for (int h = 0; h < C::NSUB; ++h) {
+      a1[h] = opaque_vgpr(a[h] + 65536);
+      a2[h] = opaque_vgpr(a[h] + 131072);
+      if constexpr (!C::NN) {
+        b1[h] = opaque_vgpr(b[h] + 65536);
+        b2[h] = opaque_vgpr(b[h] + 131072);
       }
     }
   }
@@ -288,12 +312,16 @@ constexpr int half_reads() {
 template <class C, int PH>
 __device__ __forceinline__ void read_frag(int r, int h, Half<C> &f, const MLORA_LDS char *lds, const FragAddr<C> &fa) {
   if (r < C::TM) {
-    f.a[r] = *(const lds_u4 *)(lds + fa.a[h] + (32 * C::KB * r + C::p_off(PH)));
+    const int off = 32 * C::KB * r + C::p_off(PH);
+    const int32_t base = off >= 131072 ? fa.a2[h] : off >= 65536 ? fa.a1[h] : fa.a[h];
+    f.a[r] = *(const lds_u4 *)(lds + base + (off & 65535));
     return;
   }
   if constexpr (!C::NN) {
     const int j = r - C::TM;
-    f.b[j] = *(const lds_u4 *)(lds + fa.b[h] + (32 * C::KB * j + C::q_off(PH)));
+    const int off = 32 * C::KB * j + C::q_off(PH);
+    const int32_t base = off >= 131072 ? fa.b2[h] : off >= 65536 ? fa.b1[h] : fa.b[h];
+    f.b[j] = *(const lds_u4 *)(lds + base + (off & 65535));
   }
 }
 
@@ -565,8 +593,9 @@ __device__ __forceinline__ void contract_tile(f32x16 (&acc)[C::TM][C::TN], const
       Half<C> &x = SS % 2 == 0 ? h0 : h1;
       Half<C> &y = SS % 2 == 0 ? h1 : h0;
       if constexpr (SS < NSUB - 1) {
-        constexpr int Q1 = SS == 0 ? PQ : 0;
-        mma_half<C, ST, LS, 0, Q1>(acc, x, y, SS + 1, lds, fa, pipe, k0, kmask, live, wave, lane);
+        constexpr int Q0 = C::SPREAD ? SS * PQ / (NSUB - 1) : 0;
+        constexpr int Q1 = C::SPREAD ? (SS + 1) * PQ / (NSUB - 1) : (SS == 0 ? PQ : 0);
+        mma_half<C, ST, LS, Q0, Q1>(acc, x, y, SS + 1, lds, fa, pipe, k0, kmask, live, wave, lane);
       } else {
         wait_vmcnt<WAIT>();  // this wave's loads of tile t + 1
         lds_pipeline_barrier();
@@ -771,10 +800,10 @@ __global__ __launch_bounds__(C::THREADS, C::WAVES_PER_SIMD) void gemm_kernel(con
   store_tile<C, true, true, RESID>(acc, args, lds, m0, n0, wm0, wn0, lane, wave);
 }
 
-using CfgNT256 = GemmCfg<256, 256, 4, 2, false, false, 128, 2, true>;
+using CfgNT256 = GemmCfg<256, 256, 4, 2, false, false, 128, 2, true, true>;
 using CfgF8256 = GemmCfg<256, 256, 4, 2, false, true>;
 using CfgF8128 = GemmCfg<128, 128, 2, 2, false, true>;
-using CfgNN256 = GemmCfg<256, 256, 4, 2, true, false, 128, 2, true>;
+using CfgNN256 = GemmCfg<256, 256, 4, 2, true, false, 128, 2, true, true>;
 using CfgNT128 = GemmCfg<128, 128, 2, 2, false>;
 using CfgNN128 = GemmCfg<128, 128, 2, 2, true>;
 
