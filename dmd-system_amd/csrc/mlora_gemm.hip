@@ -89,8 +89,9 @@ struct GemmCfg {
   // stage its barrier freed. RING5 (bf16 256x256, 128-byte rows): five 32 KB
   // slots, k-tile t's P in slot 2t % 5 and Q in slot (2t + 1) % 5: a step
   // loads the k-tile 2 ahead, its P into the slot the previous barrier freed
-  // (issued in the first substep) and its Q into the slot its own barrier
-  // frees — 1.5 k-tiles in flight instead of 1 in the same 160 KB.
+  // (issued before the barrier: in the first substep, or over all of them with
+  // SPREAD) and its Q into the slot its own barrier frees — 1.5 k-tiles in
+  // flight instead of 1 in the same 160 KB.
   static constexpr bool RING5 = RING5_;
   static_assert(!RING5 || (!F8 && A_BYTES == 32768 && B_BYTES == 32768), "slots hold one 256-row operand tile");
   static constexpr int PERIOD = RING5 ? 5 : STAGES;  // steps until the LDS offsets repeat
@@ -541,8 +542,8 @@ __device__ __forceinline__ void contract_tile(f32x16 (&acc)[C::TM][C::TN], const
       });
   };
   // this wave's loads still allowed in flight at the barrier of a step: those
-  // of the tiles after t+1 (RING5: the P half of tile t+2, issued in the first
-  // substep)
+  // of the tiles after t+1 (RING5: the P half of tile t+2, issued before the
+  // barrier)
   constexpr int PQ = C::RING5 ? C::A_DMA : 0;  // loads of a step issued before its barrier
   constexpr int WAIT = C::RING5 ? PQ : (C::AHEAD - 2) * NDMA;
   Half<C> h0, h1;  // fragments of the current and the next substep
