@@ -44,10 +44,10 @@ static int64_t build_pad(PadTable &pt, const SegTable &st) {
 
 // ============================================================== shrink
 //
-// Workgroup: 4 waves x 32 rows of one segment, all r <= 32*RT columns of its
+// Workgroup: NW waves x 32 rows of one segment, all r <= 32*RT columns of its
 // adapter, k in tiles of 64. Both operands go to LDS with direct-to-LDS loads
 // into a ring of ShrinkCfg::STAGES stages (up to STAGES-1 tiles in flight):
-//   P tile    [128 rows x 128 B], chunk c of row m at slot c ^ swz(m) (the
+//   P tile    [32*NW rows x 128 B], chunk c of row m at slot c ^ swz(m) (the
 //             GEMM layout: fragment reads conflict-free);
 //   Op tile   layout 0 ([r, K]): [32*RT rows j x 128 B], same swizzle;
 //             layout 1 ([K, r]): [64 rows k x 64*RT B] natural, read with the
@@ -56,19 +56,24 @@ static int64_t build_pad(PadTable &pt, const SegTable &st) {
 // P fragment holds row l%32 and k = 32*(l/32) + 8q + e in substep q; the Op
 // fragments use the same k set, so the products pair correctly.
 
-template <int RT>
+template <int RT, int NW = 4>
 struct ShrinkCfg {
+  static constexpr int BMS = 32 * NW;                 // rows per workgroup
   static constexpr int OPROWS = 32 * RT;              // j rows (layout 0) / j columns (layout 1)
-  static constexpr int P_BYTES = 128 * 128;           // 128 rows x 64 k
+  static constexpr int P_BYTES = BMS * 128;           // BMS rows x 64 k
   static constexpr int OP_BYTES = OPROWS * 128;       // 32*RT x 64 k
   static constexpr int STAGE_BYTES = P_BYTES + OP_BYTES;
-  // ranks <= 64: 3 stages (<= 72 KB) so that two workgroups share a CU (more
-  // bytes in flight per CU: measured 20% faster than 4 stages and one workgroup);
-  // larger ranks: as many stages as 160 KB allows
-  static constexpr int STAGES = RT <= 2 ? 3 : RT <= 4 ? 4 : 3;
-  static constexpr int WG_PER_CU = RT <= 2 ? 2 : 1;
-  static constexpr int P_DMA = P_BYTES / 1024 / 4;    // per wave per tile
-  static constexpr int OP_DMA = OP_BYTES / 1024 / 4;  // per wave per tile (layout 0 and 1 alike)
+  // 4 waves: ranks <= 64 take 3 stages (<= 72 KB) so that two workgroups share
+  // a CU (more bytes in flight per CU: measured 20% faster than 4 stages and one
+  // workgroup); larger ranks as many stages as 160 KB allows. 8 waves (256 rows,
+  // ranks 33-64): 4 stages of 40 KB, one workgroup per CU, 96 KB of P in flight.
+  static constexpr int STAGES = NW == 8 ? 4 : RT <= 2 ? 3 : RT <= 4 ? 4 : 3;
+  static constexpr int WG_PER_CU = NW == 8 ? 1 : RT <= 2 ? 2 : 1;
+  static constexpr int THREADS = 64 * NW;
+  static constexpr int P_DMA = P_BYTES / 1024 / NW;    // per wave per tile
+  static constexpr int OP_DMA = OP_BYTES / 1024 / NW;  // per wave per tile (layout 0 and 1 alike)
+  static_assert(P_DMA * NW * 1024 == P_BYTES && OP_DMA * NW * 1024 == OP_BYTES, "whole 1 KB loads per wave");
+  static_assert(STAGES * (P_BYTES + OP_BYTES) <= 163840, "the ring fits the LDS");
   static constexpr int DMA = P_DMA + OP_DMA;
   static constexpr int OPROW_B = OPROWS * 2;          // layout 1: bytes per k row
   static_assert(OP_DMA >= 1 && (STAGES - 2) * DMA < 64, "vmcnt field");
@@ -89,10 +94,11 @@ struct ShrinkArgs {
   SegTable seg;
 };
 
-template <int RT, int OPL>
-__global__ __launch_bounds__(256, ShrinkCfg<RT>::WG_PER_CU) void shrink_kernel(const ShrinkArgs args) {
-  using C = ShrinkCfg<RT>;
-  constexpr int BMS = 128;
+template <int RT, int OPL, int NW = 4>
+__global__ __launch_bounds__((ShrinkCfg<RT, NW>::THREADS), (ShrinkCfg<RT, NW>::WG_PER_CU)) void shrink_kernel(
+    const ShrinkArgs args) {
+  using C = ShrinkCfg<RT, NW>;
+  constexpr int BMS = C::BMS;
   constexpr int ST = C::STAGES;
   __shared__ u32x4 smem[ST * C::STAGE_BYTES / 16];  // the epilogue reuses it
   MLORA_LDS char *lds = (MLORA_LDS char *)smem;
@@ -281,12 +287,13 @@ __global__ __launch_bounds__(256, ShrinkCfg<RT>::WG_PER_CU) void shrink_kernel(c
   }
 }
 
-template <int RT>
+template <int RT, int NW = 4>
 static void launch_shrink_rt(const ShrinkArgs &a, int nblocks, hipStream_t stream) {
+  constexpr int T = ShrinkCfg<RT, NW>::THREADS;
   if (a.op_layout == 0)
-    hipLaunchKernelGGL((shrink_kernel<RT, 0>), dim3(nblocks), dim3(256), 0, stream, a);
+    hipLaunchKernelGGL((shrink_kernel<RT, 0, NW>), dim3(nblocks), dim3(T), 0, stream, a);
   else
-    hipLaunchKernelGGL((shrink_kernel<RT, 1>), dim3(nblocks), dim3(256), 0, stream, a);
+    hipLaunchKernelGGL((shrink_kernel<RT, 1, NW>), dim3(nblocks), dim3(T), 0, stream, a);
 }
 
 // ============================================================== seg_outer
@@ -588,7 +595,7 @@ extern "C" int mlora_shrink(const void *p, int64_t ldp, int64_t M, int64_t K, co
   if ((st = check_bf16_matrix(p, ldp, M, K))) return st;
   if ((st = check_bf16_matrix(h_rows, ldh, M, rmax))) return st;
   // 31-bit byte offsets inside the buffer resources of one tile / one operand
-  if (ldp * 2 * 128 >= kOOB || K * 2 * (int64_t)kMaxRank >= kOOB) return MLORA_ERR_LIMIT;
+  if (ldp * 2 * 256 >= kOOB || K * 2 * (int64_t)kMaxRank >= kOOB) return MLORA_ERR_LIMIT;
   if (h_frag != nullptr) {
     if (frag_jtiles * 16 < rmax || frag_jtiles > kMaxRank / 16) return MLORA_ERR_INVALID;
     if (!aligned16(h_frag)) return MLORA_ERR_UNSUPPORTED;
@@ -604,7 +611,9 @@ extern "C" int mlora_shrink(const void *p, int64_t ldp, int64_t M, int64_t K, co
   a.op_layout = op_layout;
   a.jtiles = frag_jtiles;
   build_pad(a.pad, a.seg);
-  constexpr int kTileRows = 128;
+  const int rt = (rmax + 31) / 32;
+  // ranks 33-64: 256-row workgroups of 8 waves (more of P in flight per CU)
+  const int kTileRows = rt == 2 ? ShrinkCfg<2, 8>::BMS : 128;
   int64_t n = 0;
   for (int s = 0; s < a.seg.n; ++s) {
     a.tile_start[s] = (int32_t)n;
@@ -615,9 +624,8 @@ extern "C" int mlora_shrink(const void *p, int64_t ldp, int64_t M, int64_t K, co
   a.tile_start[a.seg.n] = (int32_t)n;
   if (n == 0) return MLORA_OK;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  const int rt = (rmax + 31) / 32;
   if (rt <= 1) launch_shrink_rt<1>(a, (int)n, s);
-  else if (rt == 2) launch_shrink_rt<2>(a, (int)n, s);
+  else if (rt == 2) launch_shrink_rt<2, 8>(a, (int)n, s);
   else if (rt <= 4) launch_shrink_rt<4>(a, (int)n, s);
   // ranks up to 192 in layout 0 (the stacked A of three linears that read one input):
   // six 32-column tiles instead of eight (layout 1 needs 1 KB loads of whole k rows)
