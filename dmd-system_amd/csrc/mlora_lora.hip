@@ -63,10 +63,12 @@ struct ShrinkCfg {
   static constexpr int P_BYTES = BMS * 128;           // BMS rows x 64 k
   static constexpr int OP_BYTES = OPROWS * 128;       // 32*RT x 64 k
   static constexpr int STAGE_BYTES = P_BYTES + OP_BYTES;
-  // 4 waves: ranks <= 64 take 3 stages (<= 72 KB) so that two workgroups share
-  // a CU (more bytes in flight per CU: measured 20% faster than 4 stages and one
-  // workgroup); larger ranks as many stages as 160 KB allows. 8 waves (256 rows,
-  // ranks 33-64): 4 stages of 40 KB, one workgroup per CU, 96 KB of P in flight.
+  // The shrink streams P, so the rate follows the bytes of P in flight per CU.
+  // 4 waves (128 rows): ranks <= 64 take 3 stages (<= 72 KB) so that two
+  // workgroups share a CU (measured 20% faster than 4 stages and one workgroup;
+  // used for ranks <= 32); larger ranks as many stages as 160 KB allows. 8 waves
+  // (256 rows, used for ranks 33-64): 4 stages of 40 KB, one workgroup per CU,
+  // 96 KB of P in flight instead of 64 KB (3-7% faster at rank 64; slower at 128).
   static constexpr int STAGES = NW == 8 ? 4 : RT <= 2 ? 3 : RT <= 4 ? 4 : 3;
   static constexpr int WG_PER_CU = NW == 8 ? 1 : RT <= 2 ? 2 : 1;
   static constexpr int THREADS = 64 * NW;
