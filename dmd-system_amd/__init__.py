@@ -6,6 +6,8 @@ Public API:
     MultiLoRAFP8Function, multi_lora_linear_fp8   the same with an e4m3 frozen base
     MultiLoRAGatedResidualFunction, multi_lora_linear_gated   with the block's gated residual fused
     TrainableLowRankLinear, trainable_scope, MultiLoRALinear   drop-in modules
+    LoRALinear, install_lora             the native models' fp32-master LoRA (native/models.py)
+    MultiLoRAF32Function                 the float32 path (precision='fp32')
     RoleBatch, fuse_roles, roles_active  several roles' forwards in one pass over the shared base
     fuse_shared_inputs, SharedInputGroup, SharedInputMultiLoRAFunction   linears reading one input, stacked
     export_adapters, import_adapters, save_adapters, load_adapters   PEFT / DiffSynth adapter state
@@ -18,10 +20,10 @@ The directory name is not a Python identifier; importers load it as
 """
 from . import _lib, kernels
 from .adapters import export_adapters, import_adapters, load_adapters, save_adapters
-from .function import (MultiLoRAFP8Function, MultiLoRAFunction, MultiLoRAGatedResidualFunction,
-                       SharedInputMultiLoRAFunction, multi_lora_linear, multi_lora_linear_fp8,
-                       multi_lora_linear_gated, shared_input_multi_lora)
-from .low_rank import MultiLoRALinear, TrainableLowRankLinear, trainable_scope
+from .function import (MultiLoRAF32Function, MultiLoRAFP8Function, MultiLoRAFunction,
+                       MultiLoRAGatedResidualFunction, SharedInputMultiLoRAFunction, multi_lora_linear,
+                       multi_lora_linear_fp8, multi_lora_linear_gated, shared_input_multi_lora)
+from .low_rank import LoRALinear, MultiLoRALinear, TrainableLowRankLinear, install_lora, trainable_scope
 from .roles import RoleBatch, fuse_roles, roles_active
 from .routing import BASE_ONLY, SegmentRouting
 from .shared_input import SharedInputGroup, fuse_shared_inputs, release_shared_inputs
@@ -33,6 +35,7 @@ def load_library():
 
 __all__ = [
     "BASE_ONLY", "SegmentRouting", "MultiLoRAFunction", "multi_lora_linear", "MultiLoRAFP8Function",
+    "MultiLoRAF32Function", "LoRALinear", "install_lora",
     "multi_lora_linear_fp8", "MultiLoRAGatedResidualFunction", "multi_lora_linear_gated", "MultiLoRALinear",
     "TrainableLowRankLinear", "trainable_scope", "RoleBatch", "fuse_roles", "roles_active",
     "SharedInputMultiLoRAFunction", "shared_input_multi_lora", "SharedInputGroup", "fuse_shared_inputs",

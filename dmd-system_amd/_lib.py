@@ -1,7 +1,9 @@
 """ctypes binding of the C ABI in ``include/mlora.h`` (``libmlora.so``).
 
 The library is built in-tree by ``build.py``. Loading it never falls back to
-anything else: a missing or stale library is an error for every caller.
+anything else: a missing or stale library is an error for every caller. A library
+is stale when its ABI version differs, or when the sources next to it (csrc/ and
+include/) hash to another value than the one it was built with.
 """
 from __future__ import annotations
 
@@ -10,7 +12,7 @@ from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "libmlora.so"
 
-ABI_VERSION = 5
+ABI_VERSION = 6
 MAX_SEGMENTS = 128
 MAX_ADAPTERS = 32
 MAX_RANK = 256
@@ -30,7 +32,8 @@ _pf32 = ctypes.POINTER(ctypes.c_float)
 SIGNATURES = {
     "mlora_abi_version": (_int, []),
     "mlora_status_string": (ctypes.c_char_p, [_int]),
-    "mlora_shrink": (_int, [_vp, _i64, _i64, _i64, _pvp, _int, _pi32, _pf32, _i32,
+    "mlora_source_hash": (ctypes.c_char_p, []),
+    "mlora_shrink": (_int, [_vp, _i64, _i64, _i64, _pvp, _pvp, _int, _pi32, _pf32, _i32,
                             _pi64, _pi32, _i32, _vp, _i64, _vp, _i32, _vp, _vp]),
     "mlora_frag_bytes": (_i64, [_i64, _i32, _pi64, _pi32, _i32]),
     "mlora_gemm_fwd": (_int, [_vp, _i64, _i64, _i64, _vp, _i64, _i64, _vp, _int, _vp, _i64,
@@ -49,6 +52,14 @@ SIGNATURES = {
     "mlora_div_rows_bf16": (_int, [_vp, _i64, _vp, _i64, _i64, _vp, _i64, _vp]),
     "mlora_gemm_fwd_fp8": (_int, [_vp, _i64, _vp, _i64, _i64, _vp, _i64, _vp, _i64, _vp, _int, _vp, _i64,
                                   _pvp, _pi32, _i32, _pi64, _pi32, _i32, _vp, _i64, _int, _vp]),
+    "mlora_f32_shrink": (_int, [_vp, _i64, _i64, _i64, _pvp, _int, _pi32, _pf32, _i32,
+                                _pi64, _pi32, _i32, _vp, _i64, _i64, _vp]),
+    "mlora_f32_gemm_fwd": (_int, [_vp, _i64, _i64, _i64, _vp, _i64, _i64, _vp, _vp, _i64,
+                                  _pvp, _pi32, _i32, _pi64, _pi32, _i32, _vp, _i64, _vp]),
+    "mlora_f32_gemm_dx": (_int, [_vp, _i64, _i64, _i64, _vp, _i64, _i64, _vp, _i64,
+                                 _pvp, _pi32, _i32, _pi64, _pi32, _i32, _vp, _i64, _vp]),
+    "mlora_f32_seg_outer": (_int, [_vp, _i64, _i64, _i64, _vp, _i64, _pvp, _int, _pi32, _i32,
+                                   _pi64, _pi32, _i32, _vp]),
 }
 
 _LIB = None
@@ -78,8 +89,21 @@ def load():
     version = lib.mlora_abi_version()
     if version != ABI_VERSION:
         raise RuntimeError(f"libmlora ABI version {version} != expected {ABI_VERSION}; rebuild the library")
+    built = lib.mlora_source_hash().decode()
+    expected = expected_source_hash()
+    if expected is not None and built != expected:
+        raise RuntimeError(f"{LIB_PATH} was built from other sources (hash {built[:16]}…, the sources here hash "
+                           f"to {expected[:16]}…): rebuild it with `python dmd-system_amd/build.py`")
     _LIB = lib
     return lib
+
+
+def expected_source_hash() -> str | None:
+    """Hash of the HIP sources beside the library (None when they are not shipped with it)."""
+    from . import build
+    if not any(build.CSRC.glob("*.hip")):
+        return None
+    return build.source_hash()
 
 
 def check(name: str, status: int) -> None:

@@ -7,6 +7,7 @@ library next to this file. hipcc cross-compiles, so no GPU is needed.
 from __future__ import annotations
 
 import concurrent.futures
+import hashlib
 import os
 import shutil
 import subprocess
@@ -30,6 +31,24 @@ HIPCC_FLAGS = [
 ]
 
 
+def source_files() -> list[Path]:
+    """Every file the library is compiled from: the HIP sources, their headers and the C ABI."""
+    return sorted([*CSRC.glob("*.hip"), *CSRC.glob("*.h"), *INCLUDE.glob("*.h")])
+
+
+def source_hash() -> str:
+    """SHA-256 over the sources (name and bytes of each, in name order); the library
+    returns the value it was built with from mlora_source_hash()."""
+    h = hashlib.sha256()
+    root = PKG_DIR.parent
+    for f in source_files():
+        h.update(str(f.relative_to(root)).encode())
+        h.update(b"\0")
+        h.update(f.read_bytes())
+        h.update(b"\0")
+    return h.hexdigest()
+
+
 def _hipcc() -> str:
     exe = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
     if not Path(exe).exists():
@@ -50,9 +69,11 @@ def build(verbose: bool = False) -> Path:
     if not srcs:
         raise RuntimeError(f"no HIP sources under {CSRC}")
 
+    digest = source_hash()
+
     def compile_one(src: Path) -> Path:
         obj = obj_dir / (src.stem + ".o")
-        cmd = [hipcc, *HIPCC_FLAGS, f"-I{INCLUDE}", "-c", str(src), "-o", str(obj)]
+        cmd = [hipcc, *HIPCC_FLAGS, f"-I{INCLUDE}", f'-DMLORA_SOURCE_HASH="{digest}"', "-c", str(src), "-o", str(obj)]
         proc = subprocess.run(cmd, capture_output=True, text=True)
         out = "\n".join(line for line in (proc.stdout + proc.stderr).splitlines()
                         if "packed-fp32-ops" not in line)

@@ -56,12 +56,16 @@ static int64_t build_pad(PadTable &pt, const SegTable &st) {
 // P fragment holds row l%32 and k = 32*(l/32) + 8q + e in substep q; the Op
 // fragments use the same k set, so the products pair correctly.
 
-template <int RT, int NW = 4>
+template <int RT, int NW = 4, bool SPLIT = false>
 struct ShrinkCfg {
   static constexpr int BMS = 32 * NW;                 // rows per workgroup
   static constexpr int OPROWS = 32 * RT;              // j rows (layout 0) / j columns (layout 1)
   static constexpr int P_BYTES = BMS * 128;           // BMS rows x 64 k
-  static constexpr int OP_BYTES = OPROWS * 128;       // 32*RT x 64 k
+  static constexpr int OP_HALF = OPROWS * 128;        // 32*RT x 64 k of one operand
+  // SPLIT: the adapter operand arrives as two bf16 matrices hi + lo (hi = bf16(v),
+  // lo = bf16(v - hi): ~16 significant bits of an fp32 master); both tiles sit in
+  // the stage and every P fragment is multiplied by each, into one accumulator.
+  static constexpr int OP_BYTES = OP_HALF * (SPLIT ? 2 : 1);
   static constexpr int STAGE_BYTES = P_BYTES + OP_BYTES;
   // The shrink streams P, so the rate follows the bytes of P in flight per CU.
   // 4 waves (128 rows): ranks <= 64 take 3 stages (<= 72 KB) so that two
@@ -69,13 +73,17 @@ struct ShrinkCfg {
   // used for ranks <= 32); larger ranks as many stages as 160 KB allows. 8 waves
   // (256 rows, used for ranks 33-64): 4 stages of 40 KB, one workgroup per CU,
   // 96 KB of P in flight instead of 64 KB (3-7% faster at rank 64; slower at 128).
-  static constexpr int STAGES = NW == 8 ? 4 : RT <= 2 ? 3 : RT <= 4 ? 4 : 3;
-  static constexpr int WG_PER_CU = NW == 8 ? 1 : RT <= 2 ? 2 : 1;
+  // SPLIT: as many stages (at most 3) as fit.
+  static constexpr int STAGES_PLAIN = NW == 8 ? 4 : RT <= 2 ? 3 : RT <= 4 ? 4 : 3;
+  static constexpr int STAGES_FIT = 163840 / STAGE_BYTES;
+  static constexpr int STAGES = SPLIT ? (STAGES_FIT < 3 ? STAGES_FIT : 3) : STAGES_PLAIN;
+  static constexpr int WG_PER_CU = NW == 8 ? 1 : (RT <= 2 && 2 * STAGES * STAGE_BYTES <= 163840) ? 2 : 1;
   static constexpr int THREADS = 64 * NW;
   static constexpr int P_DMA = P_BYTES / 1024 / NW;    // per wave per tile
   static constexpr int OP_DMA = OP_BYTES / 1024 / NW;  // per wave per tile (layout 0 and 1 alike)
+  static constexpr int OP_HALF_DMA = OP_HALF / 1024;   // 1 KB loads of one operand tile (whole workgroup)
   static_assert(P_DMA * NW * 1024 == P_BYTES && OP_DMA * NW * 1024 == OP_BYTES, "whole 1 KB loads per wave");
-  static_assert(STAGES * (P_BYTES + OP_BYTES) <= 163840, "the ring fits the LDS");
+  static_assert(STAGES >= 2 && STAGES * (P_BYTES + OP_BYTES) <= 163840, "the ring fits the LDS");
   static constexpr int DMA = P_DMA + OP_DMA;
   static constexpr int OPROW_B = OPROWS * 2;          // layout 1: bytes per k row
   static_assert(OP_DMA >= 1 && (STAGES - 2) * DMA < 64, "vmcnt field");
@@ -93,13 +101,14 @@ struct ShrinkArgs {
   int32_t tile_start[kMaxSeg + 1];
   PadTable pad;
   AdapterTable op;
+  const uint16_t *op_lo[kMaxAdapters];  // SPLIT: the lo parts of the adapter operands
   SegTable seg;
 };
 
-template <int RT, int OPL, int NW = 4>
-__global__ __launch_bounds__((ShrinkCfg<RT, NW>::THREADS), (ShrinkCfg<RT, NW>::WG_PER_CU)) void shrink_kernel(
-    const ShrinkArgs args) {
-  using C = ShrinkCfg<RT, NW>;
+template <int RT, int OPL, int NW = 4, bool SPLIT = false>
+__global__ __launch_bounds__((ShrinkCfg<RT, NW, SPLIT>::THREADS), (ShrinkCfg<RT, NW, SPLIT>::WG_PER_CU)) void
+shrink_kernel(const ShrinkArgs args) {
+  using C = ShrinkCfg<RT, NW, SPLIT>;
   constexpr int BMS = C::BMS;
   constexpr int ST = C::STAGES;
   __shared__ u32x4 smem[ST * C::STAGE_BYTES / 16];  // the epilogue reuses it
@@ -120,6 +129,7 @@ __global__ __launch_bounds__((ShrinkCfg<RT, NW>::THREADS), (ShrinkCfg<RT, NW>::W
   const int nk = (K + 63) / 64;
   const int32_t ldp_b = (int32_t)(args.ldp * 2);
   const __amdgpu_buffer_rsrc_t rop = make_rsrc(args.op.ptr[a], (int64_t)r * K * 2);
+  const __amdgpu_buffer_rsrc_t rop_lo = SPLIT ? make_rsrc(args.op_lo[a], (int64_t)r * K * 2) : rop;
   // rows past the segment end fall outside this resource and read as zero
   const __amdgpu_buffer_rsrc_t rp = make_rsrc(args.P + (int64_t)m0 * args.ldp, (int64_t)(mend - m0) * ldp_b);
 
@@ -154,13 +164,17 @@ __global__ __launch_bounds__((ShrinkCfg<RT, NW>::THREADS), (ShrinkCfg<RT, NW>::W
     }
 #pragma unroll
     for (int i = 0; i < C::OP_DMA; ++i) {
-      const int q = wave * C::OP_DMA + i;
-      MLORA_LDS char *dst = base + C::P_BYTES + q * 1024;
+      const int qa = wave * C::OP_DMA + i;  // 1 KB block of the stage's operand tiles (wave-uniform)
+      MLORA_LDS char *dst = base + C::P_BYTES + qa * 1024;
+      // SPLIT: blocks past the first operand tile fill the lo tile from the lo matrix
+      const bool lo_half = SPLIT && qa >= C::OP_HALF_DMA;
+      const int q = lo_half ? qa - C::OP_HALF_DMA : qa;  // block within its operand tile
+      const __amdgpu_buffer_rsrc_t rsrc = lo_half ? rop_lo : rop;
       if constexpr (OPL == 0) {
         const int j = 8 * q + (lane >> 3);
         int32_t off = j < r ? p_off[q & 1] - (lane >> 3) * ldp_b + j * K * 2 : kOOB;
         if (!live || (kmask && k0 + p_kc[q & 1] >= K)) off = kOOB;
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(rop, dst, 16, off, 2 * k0, 0, 0);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, dst, 16, off, 2 * k0, 0, 0);
       } else {
         const int krow = q * (1024 / C::OPROW_B) + o1_row;  // k row within the tile
         int32_t off = o1_off;
@@ -168,7 +182,7 @@ __global__ __launch_bounds__((ShrinkCfg<RT, NW>::THREADS), (ShrinkCfg<RT, NW>::W
         // (the scalar offset goes through a variable: written inline in the builtin call,
         // this expression made the host compilation pass drop the kernel instantiation)
         const int32_t soff = (k0 + q * (1024 / C::OPROW_B)) * r * 2;
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(rop, dst, 16, off, soff, 0, 0);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, dst, 16, off, soff, 0, 0);
       }
     }
   };
@@ -203,21 +217,25 @@ __global__ __launch_bounds__((ShrinkCfg<RT, NW>::THREADS), (ShrinkCfg<RT, NW>::W
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
       const bf16x8 pf = as_bf16x8(*(const lds_u4 *)(base + pa[q]));
-      bf16x8 of[RT];
-      if constexpr (OPL == 0) {
 #pragma unroll
-        for (int j = 0; j < RT; ++j) of[j] = as_bf16x8(*(const lds_u4 *)(base + oa0[q] + 4096 * j));
-      } else {
-        int32_t ad[RT];
+      for (int part = 0; part < (SPLIT ? 2 : 1); ++part) {  // SPLIT: hi tile, then lo tile
+        const MLORA_LDS char *ob = base + part * C::OP_HALF;
+        bf16x8 of[RT];
+        if constexpr (OPL == 0) {
 #pragma unroll
-        for (int j = 0; j < RT; ++j) ad[j] = oa1[j] + 8 * q * C::OPROW_B;
-        u32x4 o[RT];
-        lds_read_tr16<RT, 4 * C::OPROW_B>(base, ad, o);
+          for (int j = 0; j < RT; ++j) of[j] = as_bf16x8(*(const lds_u4 *)(ob + oa0[q] + 4096 * j));
+        } else {
+          int32_t ad[RT];
 #pragma unroll
-        for (int j = 0; j < RT; ++j) of[j] = as_bf16x8(o[j]);
+          for (int j = 0; j < RT; ++j) ad[j] = oa1[j] + 8 * q * C::OPROW_B;
+          u32x4 o[RT];
+          lds_read_tr16<RT, 4 * C::OPROW_B>(ob, ad, o);
+#pragma unroll
+          for (int j = 0; j < RT; ++j) of[j] = as_bf16x8(o[j]);
+        }
+#pragma unroll
+        for (int j = 0; j < RT; ++j) acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(pf, of[j], acc[j], 0, 0, 0);
       }
-#pragma unroll
-      for (int j = 0; j < RT; ++j) acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(pf, of[j], acc[j], 0, 0, 0);
     }
   };
 
@@ -289,13 +307,13 @@ __global__ __launch_bounds__((ShrinkCfg<RT, NW>::THREADS), (ShrinkCfg<RT, NW>::W
   }
 }
 
-template <int RT, int NW = 4>
+template <int RT, int NW = 4, bool SPLIT = false>
 static void launch_shrink_rt(const ShrinkArgs &a, int nblocks, hipStream_t stream) {
-  constexpr int T = ShrinkCfg<RT, NW>::THREADS;
+  constexpr int T = ShrinkCfg<RT, NW, SPLIT>::THREADS;
   if (a.op_layout == 0)
-    hipLaunchKernelGGL((shrink_kernel<RT, 0, NW>), dim3(nblocks), dim3(T), 0, stream, a);
+    hipLaunchKernelGGL((shrink_kernel<RT, 0, NW, SPLIT>), dim3(nblocks), dim3(T), 0, stream, a);
   else
-    hipLaunchKernelGGL((shrink_kernel<RT, 1, NW>), dim3(nblocks), dim3(T), 0, stream, a);
+    hipLaunchKernelGGL((shrink_kernel<RT, 1, NW, SPLIT>), dim3(nblocks), dim3(T), 0, stream, a);
 }
 
 // ============================================================== seg_outer
@@ -582,16 +600,27 @@ extern "C" int64_t mlora_frag_bytes(int64_t M, int32_t frag_jtiles, const int64_
   return frag_bytes(st, frag_jtiles);
 }
 
-extern "C" int mlora_shrink(const void *p, int64_t ldp, int64_t M, int64_t K, const void *const *op_ptrs, int op_layout,
-                            const int32_t *ranks, const float *scales, int32_t n_adapters, const int64_t *seg_offsets,
-                            const int32_t *adapter_ids, int32_t n_segments, void *h_rows, int64_t ldh, void *h_frag,
-                            int32_t frag_jtiles, const float *row_div, void *stream) {
+extern "C" int mlora_shrink(const void *p, int64_t ldp, int64_t M, int64_t K, const void *const *op_ptrs,
+                            const void *const *op_lo_ptrs, int op_layout, const int32_t *ranks, const float *scales,
+                            int32_t n_adapters, const int64_t *seg_offsets, const int32_t *adapter_ids,
+                            int32_t n_segments, void *h_rows, int64_t ldh, void *h_frag, int32_t frag_jtiles,
+                            const float *row_div, void *stream) {
   ShrinkArgs a{};
   int st = build_segtable(a.seg, M, seg_offsets, adapter_ids, n_segments, n_adapters);
   if (st) return st;
   if ((st = build_adapters(a.op, a.seg, op_ptrs, ranks, scales, n_adapters))) return st;
   if (op_layout != 0 && op_layout != 1) return MLORA_ERR_INVALID;
   if (K < 0 || K > INT32_MAX - 1024) return MLORA_ERR_INVALID;
+  const bool split = op_lo_ptrs != nullptr;
+  for (int i = 0; i < kMaxAdapters; ++i) a.op_lo[i] = nullptr;
+  if (split) {  // every used operand needs its lo part, aligned like the hi part
+    for (int i = 0; i < n_adapters; ++i) {
+      if (a.op.ptr[i] == nullptr) continue;
+      if (op_lo_ptrs[i] == nullptr) return MLORA_ERR_INVALID;
+      if (!aligned16(op_lo_ptrs[i])) return MLORA_ERR_UNSUPPORTED;
+      a.op_lo[i] = static_cast<const uint16_t *>(op_lo_ptrs[i]);
+    }
+  }
   const int rmax = max_used_rank(a.seg, a.op);
   if (rmax == 0 || M == 0) return MLORA_OK;
   if ((st = check_bf16_matrix(p, ldp, M, K))) return st;
@@ -626,6 +655,14 @@ extern "C" int mlora_shrink(const void *p, int64_t ldp, int64_t M, int64_t K, co
   a.tile_start[a.seg.n] = (int32_t)n;
   if (n == 0) return MLORA_OK;
   hipStream_t s = static_cast<hipStream_t>(stream);
+  if (split) {
+    // fp32 masters: the same tile shapes with both operand parts in each stage
+    if (rt <= 1) launch_shrink_rt<1, 4, true>(a, (int)n, s);
+    else if (rt == 2) launch_shrink_rt<2, 8, true>(a, (int)n, s);
+    else if (rt <= 4) launch_shrink_rt<4, 4, true>(a, (int)n, s);
+    else launch_shrink_rt<8, 4, true>(a, (int)n, s);
+    return launch_status();
+  }
   if (rt <= 1) launch_shrink_rt<1>(a, (int)n, s);
   else if (rt == 2) launch_shrink_rt<2, 8>(a, (int)n, s);
   else if (rt <= 4) launch_shrink_rt<4>(a, (int)n, s);
@@ -733,6 +770,11 @@ extern "C" int mlora_seg_outer(const void *p, int64_t ldp, int64_t M, int64_t C,
 }
 
 extern "C" int mlora_abi_version(void) { return MLORA_ABI_VERSION; }
+
+#ifndef MLORA_SOURCE_HASH
+#define MLORA_SOURCE_HASH "unknown"
+#endif
+extern "C" const char *mlora_source_hash(void) { return MLORA_SOURCE_HASH; }
 
 extern "C" const char *mlora_status_string(int status) {
   switch (status) {

@@ -12,8 +12,18 @@ which is the autograd of the reference's per-adapter forward
 (training/low_rank.py:26-28) applied to each segment.
 
 Kernels: shrink -> fused GEMM forward; shrink(dY) -> fused dX GEMM and two
-segmented reductions. Compute is bf16 with fp32 accumulation; the adapter
-gradients come back in the parameters' dtype (fp32 masters stay fp32).
+segmented reductions. Arithmetic by input type:
+  * bf16 activations and base (or bf16 autocast, training/single_device.py:88): bf16
+    MFMA with fp32 accumulation; under autocast the adapters are rounded to bf16 as
+    autocast rounds F.linear's operands (low_rank.py:28 under autocast);
+  * bf16 activations and base with fp32 adapter masters outside autocast (the
+    fp32 LoRA compute of native/models.py:44-51,150-156): the shrinks multiply by the
+    masters split into two bf16 parts (hi + lo, ~16 significant bits), so h, g and
+    the adapter gradients are fp32-class; Y and dX stay bf16;
+  * fp32 activations, base and adapters outside autocast (precision='fp32',
+    training/single_device.py:77-80): MultiLoRAF32Function, every operation in
+    float32 on the fp32 MFMA.
+The adapter gradients come back in the parameters' dtype (fp32 masters stay fp32).
 """
 from __future__ import annotations
 
@@ -36,11 +46,13 @@ def _as_operand(t: torch.Tensor, rows_pad: int | None = None, cols_pad: int | No
     return t
 
 
-def _prepare(ctx, x, N: int, ab, scales, routing: SegmentRouting, grad0: int, row_div=None):
+def _prepare(ctx, x, N: int, ab, scales, routing: SegmentRouting, grad0: int, row_div=None, split: bool = False):
     """Validate adapters, build padded bf16 operands and run the forward shrink.
 
-    grad0 is the index of the first lora_a among the autograd inputs.
-    Returns (A_ops, B_ops, h_rows); records what backward needs on ctx.
+    grad0 is the index of the first lora_a among the autograd inputs. split: the adapters
+    are fp32 masters used at fp32-class precision (hi + lo bf16 parts in the shrinks).
+    Returns (A_ops, B_ops, A_lo, B_lo, h_rows, h_frag); A_lo / B_lo are empty lists unless
+    split. Records the routing and shapes on ctx.
     """
     n = len(ab) // 2
     if len(ab) != 2 * n or len(scales) != n:
@@ -54,27 +66,56 @@ def _prepare(ctx, x, N: int, ab, scales, routing: SegmentRouting, grad0: int, ro
             raise ValueError(f"multi-LoRA: lora_a {tuple(a.shape)} / lora_b {tuple(b.shape)} do not match "
                              f"rank {r}, in {K}, out {N}")
     pranks = [(r + 7) // 8 * 8 for r in ranks]
-    A_ops = [_as_operand(a, rows_pad=p) for a, p in zip(As, pranks)]
-    B_ops = [_as_operand(b, cols_pad=p) for b, p in zip(Bs, pranks)]
+    if split:
+        A_ops, A_lo = zip(*[kernels.split_hi_lo(_as_operand_f32(a, rows_pad=p)) for a, p in zip(As, pranks)])
+        B_ops, B_lo = zip(*[kernels.split_hi_lo(_as_operand_f32(b, cols_pad=p)) for b, p in zip(Bs, pranks)])
+        A_ops, A_lo, B_ops, B_lo = list(A_ops), list(A_lo), list(B_ops), list(B_lo)
+    else:
+        A_ops = [_as_operand(a, rows_pad=p) for a, p in zip(As, pranks)]
+        B_ops = [_as_operand(b, cols_pad=p) for b, p in zip(Bs, pranks)]
+        A_lo, B_lo = [], []
     width = kernels.padded_rank(pranks)
     need_b_grad = any(ctx.needs_input_grad[grad0 + n + i] for i in range(n))
-    h_rows, h_frag = (None, None)
+    h_rows, h_frag = (None, [])
     if width > 0:
         h_rows, h_frag = kernels.shrink(x, A_ops, 0, scales, routing, want_frag=need_b_grad, width=width,
-                                        row_div=row_div)
+                                        row_div=row_div, ops_lo=A_lo if split else None)
     ctx.routing, ctx.scales, ctx.n, ctx.grad0 = routing, tuple(float(s) for s in scales), n, grad0
-    ctx.ranks, ctx.pranks, ctx.width = ranks, pranks, width
+    ctx.ranks, ctx.pranks, ctx.width, ctx.split = ranks, pranks, width, split
     ctx.a_dtypes = [a.dtype for a in As]
     ctx.b_dtypes = [b.dtype for b in Bs]
-    ctx.h_frag = h_frag  # per call group; plain tensors produced and consumed here
-    return A_ops, B_ops, h_rows
+    return A_ops, B_ops, A_lo, B_lo, h_rows, list(h_frag or [])
 
 
-def _backward(ctx, dy, x, dx_gemm, A_ops, B_ops, row_div=None):
+def _as_operand_f32(t: torch.Tensor, rows_pad: int | None = None, cols_pad: int | None = None) -> torch.Tensor:
+    """float32 copy/view of an adapter matrix, zero-padded to a multiple of 8 ranks."""
+    t = t.detach().to(torch.float32)
+    if rows_pad is not None and rows_pad != t.shape[0]:
+        t = F.pad(t, (0, 0, 0, rows_pad - t.shape[0]))
+    if cols_pad is not None and cols_pad != t.shape[1]:
+        t = F.pad(t, (0, cols_pad - t.shape[1]))
+    return t
+
+
+def _save(ctx, *tensors, frag=()):
+    """save_for_backward of the call's tensors followed by the h fragments (one per call group)."""
+    ctx.n_frag = len(frag)
+    ctx.save_for_backward(*tensors, *frag)
+
+
+def _saved(ctx):
+    """(tensors, h fragments) as _save stored them."""
+    saved = list(ctx.saved_tensors)
+    k = len(saved) - ctx.n_frag
+    return saved[:k], saved[k:]
+
+
+def _backward(ctx, dy, x, dx_gemm, A_ops, B_ops, h_frag, B_lo=None, row_div=None):
     """dX (dx_gemm(g_rows)), dA_i, dB_i; returns (dx, dAs, dBs).
 
     dy is bf16 contiguous; g_rows (the LoRA term of dX) are divided by row_div
-    when given (the e4m3 dX folds dY's row scale into them)."""
+    when given (the e4m3 dX folds dY's row scale into them). B_lo: the lo parts of
+    split fp32 masters (g then uses hi + lo)."""
     n, g0, routing = ctx.n, ctx.grad0, ctx.routing
     need_x = ctx.needs_input_grad[0]
     need_a = [ctx.needs_input_grad[g0 + i] for i in range(n)]
@@ -83,13 +124,13 @@ def _backward(ctx, dy, x, dx_gemm, A_ops, B_ops, row_div=None):
     g_rows = g_frag = None
     if ctx.width > 0 and (need_x or any(need_a)):
         g_rows, g_frag = kernels.shrink(dy, B_ops, 1, ctx.scales, routing, want_frag=any(need_a), width=ctx.width,
-                                        row_div=row_div)
+                                        row_div=row_div, ops_lo=B_lo or None)
     if need_x:
         dx = dx_gemm(g_rows)
     dAs: list = [None] * n
     dBs: list = [None] * n
     if any(need_b):
-        outs = kernels.seg_outer(dy, ctx.h_frag, ctx.width, ctx.pranks, routing, 0,
+        outs = kernels.seg_outer(dy, h_frag, ctx.width, ctx.pranks, routing, 0,
                                  [ctx.b_dtypes[i] for i in range(n)])
         dBs = [o[:, :r] if nb else None for o, r, nb in zip(outs, ctx.ranks, need_b)]
     if any(need_a):
@@ -110,32 +151,84 @@ def _dx_gemm(dy, weight, weight_t, A_ops, routing):
 
 
 class MultiLoRAFunction(torch.autograd.Function):
-    """``apply(x, weight, weight_t, bias, routing, scales, *lora_as, *lora_bs)``.
+    """``apply(x, weight, weight_t, bias, routing, scales, split, *lora_as, *lora_bs)``.
 
     x [M, K] bf16 contiguous, weight [N, K] bf16 (frozen), weight_t None or weight
     transposed ([K, N] contiguous, frozen: dX then runs on the NT GEMM), bias [N] or None
     (frozen), routing a SegmentRouting over the M rows, scales one float per adapter;
-    lora_as[i] [r_i, K], lora_bs[i] [N, r_i] of any float dtype.
+    lora_as[i] [r_i, K], lora_bs[i] [N, r_i] of any float dtype. split: fp32 adapters are
+    used at fp32-class precision (hi + lo bf16 parts) instead of rounded to bf16.
     """
 
     @staticmethod
-    def forward(ctx, x, weight, weight_t, bias, routing: SegmentRouting, scales: Sequence[float], *ab):
+    def forward(ctx, x, weight, weight_t, bias, routing: SegmentRouting, scales: Sequence[float], split: bool, *ab):
         if any(ctx.needs_input_grad[1:4]):
             raise RuntimeError("multi-LoRA: the base weight and bias are frozen (requires_grad=False)")
-        A_ops, B_ops, h_rows = _prepare(ctx, x, weight.shape[0], ab, scales, routing, grad0=6)
+        A_ops, B_ops, A_lo, B_lo, h_rows, h_frag = _prepare(ctx, x, weight.shape[0], ab, scales, routing, grad0=7,
+                                                            split=bool(split))
         y = kernels.gemm_fwd(x, weight, bias, h_rows, B_ops, routing)
         ctx.has_wt = weight_t is not None
-        ctx.save_for_backward(x, weight, weight_t, *A_ops, *B_ops)
+        _save(ctx, x, weight, weight_t, *A_ops, *B_ops, *B_lo, frag=h_frag)
         return y
 
     @staticmethod
     def backward(ctx, dy):
         n = ctx.n
-        x, weight, weight_t, *ops = ctx.saved_tensors
+        (x, weight, weight_t, *ops), h_frag = _saved(ctx)
         dy = dy.to(torch.bfloat16).contiguous()
         dx_gemm = _dx_gemm(dy, weight, weight_t if ctx.has_wt else None, ops[:n], ctx.routing)
-        dx, dAs, dBs = _backward(ctx, dy, x, dx_gemm, ops[:n], ops[n:])
-        return (dx, None, None, None, None, None, *dAs, *dBs)
+        dx, dAs, dBs = _backward(ctx, dy, x, dx_gemm, ops[:n], ops[n:2 * n], h_frag, B_lo=ops[2 * n:])
+        return (dx, None, None, None, None, None, None, *dAs, *dBs)
+
+
+class MultiLoRAF32Function(torch.autograd.Function):
+    """``apply(x, weight, bias, routing, scales, *lora_as, *lora_bs)`` with every tensor float32: the
+    reference's precision='fp32' mode (training/single_device.py:77-80), where
+    TrainableLowRankLinear runs base(x) + s·F.linear(F.linear(x, A), B) (low_rank.py:26-28) and
+    its autograd backward in float32. Every product and sum is float32 on the fp32 MFMA, in a
+    fixed order: h = s·X·A_aᵀ, Y = X·Wᵀ + b + h·B_aᵀ; g = s·dY·B_a, dX = dY·W + g·A_a,
+    dA_a = gᵀ·X, dB_a = dYᵀ·h over each adapter's rows.
+    """
+
+    @staticmethod
+    def forward(ctx, x, weight, bias, routing: SegmentRouting, scales: Sequence[float], *ab):
+        if any(ctx.needs_input_grad[1:3]):
+            raise RuntimeError("multi-LoRA: the base weight and bias are frozen (requires_grad=False)")
+        n = len(ab) // 2
+        if len(ab) != 2 * n or len(scales) != n:
+            raise ValueError("multi-LoRA: one lora_a, one lora_b and one scale per adapter")
+        As, Bs = [a.detach().contiguous() for a in ab[:n]], [b.detach().contiguous() for b in ab[n:]]
+        M, K = x.shape
+        N = weight.shape[0]
+        routing.validate_for(M, n)
+        ranks = [int(a.shape[0]) for a in As]
+        for a, b, r in zip(As, Bs, ranks):
+            if a.shape != (r, K) or b.shape != (N, r):
+                raise ValueError(f"multi-LoRA: lora_a {tuple(a.shape)} / lora_b {tuple(b.shape)} do not match "
+                                 f"rank {r}, in {K}, out {N}")
+        width = max([0, *ranks])
+        h = kernels.f32_shrink(x, As, 0, scales, routing, width) if width else None
+        y = kernels.f32_gemm_fwd(x, weight, bias, h, Bs, routing)
+        ctx.routing, ctx.scales, ctx.n, ctx.ranks, ctx.width = routing, tuple(float(v) for v in scales), n, ranks, width
+        ctx.save_for_backward(x, weight, h, *As, *Bs)
+        return y
+
+    @staticmethod
+    def backward(ctx, dy):
+        n, routing = ctx.n, ctx.routing
+        x, weight, h, *ops = ctx.saved_tensors
+        As, Bs = ops[:n], ops[n:]
+        dy = dy.to(torch.float32).contiguous()
+        need_x = ctx.needs_input_grad[0]
+        need_a = any(ctx.needs_input_grad[5:5 + n])
+        need_b = any(ctx.needs_input_grad[5 + n:])
+        g = kernels.f32_shrink(dy, Bs, 1, ctx.scales, routing, ctx.width) if ctx.width and (need_x or need_a) else None
+        dx = kernels.f32_gemm_dx(dy, weight, g, As, routing) if need_x else None
+        dAs = kernels.f32_seg_outer(x, g, ctx.ranks, routing, 1) if need_a else [None] * n
+        dBs = kernels.f32_seg_outer(dy, h, ctx.ranks, routing, 0) if need_b else [None] * n
+        dAs = [d if ctx.needs_input_grad[5 + i] else None for i, d in enumerate(dAs)]
+        dBs = [d if ctx.needs_input_grad[5 + n + i] else None for i, d in enumerate(dBs)]
+        return (dx, None, None, None, None, *dAs, *dBs)
 
 
 class MultiLoRAGatedResidualFunction(torch.autograd.Function):
@@ -158,20 +251,20 @@ class MultiLoRAGatedResidualFunction(torch.autograd.Function):
             raise RuntimeError("multi-LoRA: the base weight and bias are frozen (requires_grad=False)")
         if ctx.needs_input_grad[7]:
             raise RuntimeError("gated residual: the gate is frozen (a trainable modulation is not fused)")
-        A_ops, B_ops, h_rows = _prepare(ctx, x, weight.shape[0], ab, scales, routing, grad0=8)
+        A_ops, B_ops, _, _, h_rows, h_frag = _prepare(ctx, x, weight.shape[0], ab, scales, routing, grad0=8)
         out = kernels.gemm_fwd_gated(x, weight, bias, h_rows, B_ops, routing, residual, gate)
         ctx.has_wt = weight_t is not None
-        ctx.save_for_backward(x, weight, weight_t, gate, *A_ops, *B_ops)
+        _save(ctx, x, weight, weight_t, gate, *A_ops, *B_ops, frag=h_frag)
         return out
 
     @staticmethod
     def backward(ctx, dout):
         n = ctx.n
-        x, weight, weight_t, gate, *ops = ctx.saved_tensors
+        (x, weight, weight_t, gate, *ops), h_frag = _saved(ctx)
         dout = dout.to(torch.bfloat16).contiguous()
         dy = kernels.gate_scale_rows(dout, gate)
         dx_gemm = _dx_gemm(dy, weight, weight_t if ctx.has_wt else None, ops[:n], ctx.routing)
-        dx, dAs, dBs = _backward(ctx, dy, x, dx_gemm, ops[:n], ops[n:])
+        dx, dAs, dBs = _backward(ctx, dy, x, dx_gemm, ops[:n], ops[n:], h_frag)
         d_res = dout if ctx.needs_input_grad[6] else None
         return (dx, None, None, None, None, None, d_res, None, *dAs, *dBs)
 
@@ -197,16 +290,17 @@ class MultiLoRAFP8Function(torch.autograd.Function):
         xq, x_scale = kernels.quantize_rows_fp8(x)
         # the LoRA operands enter the e4m3 accumulators divided by the scales the
         # epilogue multiplies back: h / x_scale[m] (shrink) and lora_b / w_scale[n]
-        A_ops, B_ops, h_rows = _prepare(ctx, x, wq.shape[0], ab, scales, routing, grad0=7, row_div=x_scale)
+        A_ops, B_ops, _, _, h_rows, h_frag = _prepare(ctx, x, wq.shape[0], ab, scales, routing, grad0=7,
+                                                      row_div=x_scale)
         B_div = [kernels.div_rows_bf16(b, w_scale) for b in B_ops]
         y = kernels.gemm_fwd_fp8(xq, x_scale, wq, w_scale, bias, h_rows, B_div, routing)
-        ctx.save_for_backward(x, wq_t, w_scale, *A_ops, *B_ops)
+        _save(ctx, x, wq_t, w_scale, *A_ops, *B_ops, frag=h_frag)
         return y
 
     @staticmethod
     def backward(ctx, dy):
         n = ctx.n
-        x, wq_t, w_scale, *ops = ctx.saved_tensors
+        (x, wq_t, w_scale, *ops), h_frag = _saved(ctx)
         dy = dy.to(torch.bfloat16).contiguous()
         dyq = dy_scale = None
         if ctx.needs_input_grad[0]:
@@ -216,7 +310,7 @@ class MultiLoRAFP8Function(torch.autograd.Function):
             a_t = [a.t().contiguous() for a in ops[:n]]  # A_aᵀ [K, r]: the NT form of the LoRA term
             return kernels.gemm_fwd_fp8(dyq, dy_scale, wq_t, None, None, g_rows, a_t, ctx.routing)
 
-        dx, dAs, dBs = _backward(ctx, dy, x, dx_gemm, ops[:n], ops[n:], row_div=dy_scale)
+        dx, dAs, dBs = _backward(ctx, dy, x, dx_gemm, ops[:n], ops[n:], h_frag, row_div=dy_scale)
         return (dx, None, None, None, None, None, None, *dAs, *dBs)
 
 
@@ -267,18 +361,17 @@ class SharedInputMultiLoRAFunction(torch.autograd.Function):
         h_rows, h_frag = kernels.shrink(x, A_cat, 0, scales, routing, want_frag=need_b_grad, width=G * R)
         ys = [kernels.gemm_fwd(x, weights[g], biases[g], h_rows[:, g * R:(g + 1) * R], B_ops[g], routing)
               for g in range(G)]
-        ctx.save_for_backward(x, *A_cat, *[b for bg in B_ops for b in bg])
-        ctx.weights = tuple(weights)  # frozen bases: held, not saved for autograd
+        _save(ctx, x, *weights, *A_cat, *[b for bg in B_ops for b in bg], frag=list(h_frag or []))
         ctx.routing, ctx.scales, ctx.n, ctx.G, ctx.R = routing, tuple(float(v) for v in scales), n, G, R
-        ctx.h_frag = h_frag
         ctx.a_dtypes = [[a.dtype for a in As[g]] for g in range(G)]
         ctx.b_dtypes = [[b.dtype for b in Bs[g]] for g in range(G)]
         return tuple(ys)
 
     @staticmethod
     def backward(ctx, *dys):
-        n, G, R, routing, ws = ctx.n, ctx.G, ctx.R, ctx.routing, ctx.weights
-        x, *ops = ctx.saved_tensors
+        n, G, R, routing = ctx.n, ctx.G, ctx.R, ctx.routing
+        (x, *ops), h_frag = _saved(ctx)
+        ws, ops = ops[:G], ops[G:]
         A_cat = ops[:n]
         B_ops = [ops[n + g * n:n + (g + 1) * n] for g in range(G)]
         M = x.shape[0]
@@ -305,7 +398,7 @@ class SharedInputMultiLoRAFunction(torch.autograd.Function):
         dB = [[None] * n for _ in range(G)]
         if need_b:
             for g in range(G):
-                outs = kernels.seg_outer(dys[g], ctx.h_frag, G * R, [R] * n, routing, 0, ctx.b_dtypes[g],
+                outs = kernels.seg_outer(dys[g], h_frag, G * R, [R] * n, routing, 0, ctx.b_dtypes[g],
                                          frag_jt=jt, frag_t0=g * R // 16)
                 dB[g] = [o if ctx.needs_input_grad[6 + G * n + g * n + i] else None for i, o in enumerate(outs)]
         if need_a:
@@ -346,26 +439,48 @@ def shared_input_multi_lora(x: torch.Tensor, weights: Sequence[torch.Tensor], bi
     return tuple(y.reshape(*lead, w.shape[0]) for y, w in zip(ys, ws))
 
 
+def _autocast_bf16() -> bool:
+    return torch.is_autocast_enabled("cuda") and torch.get_autocast_dtype("cuda") == torch.bfloat16
+
+
 def multi_lora_linear(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None,
                       lora_as: Sequence[torch.Tensor], lora_bs: Sequence[torch.Tensor],
                       scales: Sequence[float], routing: SegmentRouting,
                       weight_t: torch.Tensor | None = None) -> torch.Tensor:
-    """Functional form over x of shape [..., K]; returns [..., N] bf16. weight_t: the frozen
-    weight transposed ([K, N] bf16 contiguous, made once by the caller) for the faster dX."""
+    """Functional form over x of shape [..., K]; returns [..., N]. weight_t: the frozen
+    weight transposed ([K, N] bf16 contiguous, made once by the caller) for the faster dX.
+
+    Arithmetic follows the inputs, as the reference's F.linear calls would (see the module doc):
+    under bf16 autocast, or with bf16 x and weight, bf16 out (fp32 adapters outside autocast are
+    used at fp32-class precision); with float32 x, weight and adapters outside autocast, float32
+    out computed in float32 (MultiLoRAF32Function). Other combinations raise."""
     K = x.shape[-1]
     lead = x.shape[:-1]
     x2 = x.reshape(-1, K)
-    if torch.is_autocast_enabled("cuda") and torch.get_autocast_dtype("cuda") == torch.bfloat16:
+    split = f32 = False
+    if _autocast_bf16():
         x2 = x2.to(torch.bfloat16)
         weight = weight.to(torch.bfloat16)
-    if x2.dtype != torch.bfloat16 or weight.dtype != torch.bfloat16:
-        raise RuntimeError("multi-LoRA linear computes in bfloat16: pass bf16 input and base weight, "
-                           "or call it under torch.autocast('cuda', dtype=torch.bfloat16)")
+    elif x2.dtype == torch.float32 and weight.dtype == torch.float32:
+        tensors = [*lora_as, *lora_bs] + ([bias] if bias is not None else [])
+        if any(t.dtype != torch.float32 for t in tensors):
+            raise RuntimeError("multi-LoRA linear in float32: the bias and the adapters must be float32 too "
+                               "(as F.linear requires one dtype outside autocast)")
+        f32 = True
+    elif x2.dtype == torch.bfloat16 and weight.dtype == torch.bfloat16:
+        split = any(t.dtype == torch.float32 for t in [*lora_as, *lora_bs])
+    else:
+        raise RuntimeError("multi-LoRA linear computes in bfloat16 or float32: pass bf16 (or float32) input and "
+                           "base weight, or call it under torch.autocast('cuda', dtype=torch.bfloat16)")
     if not x2.is_cuda:
         raise RuntimeError("multi-LoRA linear runs on the ROCm device only (HIP kernels, no CPU path)")
     with torch.autocast("cuda", enabled=False):
-        y = MultiLoRAFunction.apply(x2.contiguous(), weight, weight_t, bias, routing, tuple(scales), *lora_as,
-                                    *lora_bs)
+        if f32:
+            y = MultiLoRAF32Function.apply(x2.contiguous(), weight.detach().contiguous(), bias, routing,
+                                           tuple(scales), *lora_as, *lora_bs)
+        else:
+            y = MultiLoRAFunction.apply(x2.contiguous(), weight, weight_t, bias, routing, tuple(scales), split,
+                                        *lora_as, *lora_bs)
     return y.reshape(*lead, weight.shape[0])
 
 

@@ -71,11 +71,14 @@ def shrink(p: torch.Tensor, ops: Sequence[torch.Tensor], op_layout: int, scales:
            routing: SegmentRouting, want_frag: bool, width: int,
            row_div: torch.Tensor | None = None, h_out: torch.Tensor | None = None,
            frag_out: list | None = None, frag_jt: int | None = None,
-           frag_t0: int = 0) -> tuple[torch.Tensor, list | None]:
+           frag_t0: int = 0, ops_lo: Sequence[torch.Tensor] | None = None) -> tuple[torch.Tensor, list | None]:
     """h = s·P·Op_aᵀ per segment -> (h_rows bf16 [M, width], per-call-group hi/lo fragments or None).
 
     row_div [M] fp32 (optional) divides the rows of h_rows only (the row scales of the e4m3 forward's X
     and of the e4m3 dX's dY).
+
+    ops_lo (optional): the lo parts of fp32 adapter operands split as ops = bf16(v), ops_lo =
+    bf16(v - ops) (split_hi_lo); h then uses both (~16 significant bits of v).
 
     Writing into a part of larger buffers (the stacked LoRA operands of linears that share
     an input): h_out is a row-major view [M, >= r] whose row stride is the buffer's (rows
@@ -89,6 +92,11 @@ def shrink(p: torch.Tensor, ops: Sequence[torch.Tensor], op_layout: int, scales:
         _check_rows("adapter operand", o)
         _require(o.is_contiguous(), "adapter operands must be contiguous")
         _require(o.shape == ((r, K) if op_layout == 0 else (K, r)), "adapter operand shape")
+    if ops_lo is not None:
+        _require(len(ops_lo) == len(ops), "one lo part per adapter operand")
+        for o, lo in zip(ops, ops_lo):
+            _check_rows("adapter operand lo part", lo)
+            _require(lo.is_contiguous() and lo.shape == o.shape, "lo part has its hi part's shape")
     if row_div is not None:
         _check_scale("row_div", row_div, M)
     if h_out is not None:
@@ -97,6 +105,7 @@ def shrink(p: torch.Tensor, ops: Sequence[torch.Tensor], op_layout: int, scales:
     h_rows = h_out if h_out is not None else torch.empty((M, width), dtype=torch.bfloat16, device=p.device)
     lib = _lib.load()
     ptrs, rk, sc = _lib.ptr_array([_ptr(o) for o in ops]), _lib.i32_array(ranks), _lib.f32_array(scales)
+    lo_ptrs = None if ops_lo is None else _lib.ptr_array([_ptr(o) for o in ops_lo])
     jt = frag_jtiles(width) if frag_jt is None else frag_jt
     _require(0 <= frag_t0 and frag_t0 * 16 + max([0, *ranks]) <= jt * 16, "fragment j-tiles out of range")
     stream = _stream(p)
@@ -110,7 +119,7 @@ def shrink(p: torch.Tensor, ops: Sequence[torch.Tensor], op_layout: int, scales:
         if r1 == r0:
             continue
         _lib.check("mlora_shrink", lib.mlora_shrink(
-            p[r0:r1].data_ptr(), p.stride(0), r1 - r0, K, ptrs, op_layout, rk, sc, len(ops),
+            p[r0:r1].data_ptr(), p.stride(0), r1 - r0, K, ptrs, lo_ptrs, op_layout, rk, sc, len(ops),
             o, i, n, h_rows[r0:r1].data_ptr(), h_rows.stride(0), fptr, jt,
             None if row_div is None else row_div[r0:r1].data_ptr(), stream))
     return h_rows, frags
@@ -380,3 +389,123 @@ def gemm_fwd_fp8(xq: torch.Tensor, x_scale: torch.Tensor, wq: torch.Tensor, w_sc
             _ptr(bias), _DT[bias.dtype] if bias is not None else 0, hr, ldh,
             ptrs, rk, len(bs), o, i, n, y[r0:r1].data_ptr(), y.stride(0), 0, stream))
     return y
+
+
+# ------------------------------------------------------------ fp32 arithmetic
+
+def split_hi_lo(t: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """(hi, lo) bf16 parts of a float matrix: hi = bf16(t), lo = bf16(t - hi), both contiguous.
+    hi + lo carries ~16 significant bits of t (relative error <= 2^-16)."""
+    t32 = t.detach().to(torch.float32)
+    hi = t32.to(torch.bfloat16)
+    lo = (t32 - hi.to(torch.float32)).to(torch.bfloat16)
+    return hi.contiguous(), lo.contiguous()
+
+
+def _check_f32(name: str, t: torch.Tensor, cols: int | None = None) -> None:
+    _require(t.is_cuda, f"{name} must be a ROCm device tensor")
+    _require(t.dtype == torch.float32, f"{name} must be float32, got {t.dtype}")
+    _require(t.dim() == 2 and t.stride(1) == 1, f"{name} must be a 2-D row-major matrix")
+    if cols is not None:
+        _require(t.shape[1] == cols, f"{name} has {t.shape[1]} columns, expected {cols}")
+
+
+def f32_shrink(p: torch.Tensor, ops: Sequence[torch.Tensor], op_layout: int, scales: Sequence[float],
+               routing: SegmentRouting, width: int) -> torch.Tensor:
+    """fp32 h = s_a·P·Op_aᵀ per segment -> h [M, width] float32 (zeros outside adapter rows / ranks)."""
+    M, K = p.shape
+    _check_f32("P", p)
+    ranks = [int(o.shape[0] if op_layout == 0 else o.shape[1]) for o in ops]
+    for o, r in zip(ops, ranks):
+        _check_f32("adapter operand", o)
+        _require(o.is_contiguous() and o.shape == ((r, K) if op_layout == 0 else (K, r)), "adapter operand shape")
+    h = torch.empty((M, width), dtype=torch.float32, device=p.device)
+    lib = _lib.load()
+    ptrs, rk, sc = _lib.ptr_array([_ptr(o) for o in ops]), _lib.i32_array(ranks), _lib.f32_array(scales)
+    stream = _stream(p)
+    for r0, r1, off, ids in routing.groups(_lib.MAX_SEGMENTS):
+        if r1 == r0:
+            continue
+        o, i, n = _routing_arrays(off, ids)
+        _lib.check("mlora_f32_shrink", lib.mlora_f32_shrink(
+            p[r0:r1].data_ptr(), p.stride(0), r1 - r0, K, ptrs, op_layout, rk, sc, len(ops), o, i, n,
+            h[r0:r1].data_ptr(), h.stride(0), width, stream))
+    return h
+
+
+def f32_gemm_fwd(x: torch.Tensor, w: torch.Tensor, bias: torch.Tensor | None, h: torch.Tensor | None,
+                 bs: Sequence[torch.Tensor], routing: SegmentRouting) -> torch.Tensor:
+    """fp32 Y = X·Wᵀ + bias + per-segment h·B_aᵀ."""
+    M, K = x.shape
+    N = w.shape[0]
+    _check_f32("X", x, K)
+    _check_f32("W", w, K)
+    if bias is not None:
+        _require(bias.is_cuda and bias.dtype == torch.float32 and bias.is_contiguous() and bias.shape == (N,), "bias")
+    ranks = [int(b.shape[1]) for b in bs]
+    for b in bs:
+        _check_f32("lora_b", b)
+        _require(b.is_contiguous() and b.shape[0] == N, "lora_b must be contiguous [N, r]")
+    y = torch.empty((M, N), dtype=torch.float32, device=x.device)
+    lib = _lib.load()
+    ptrs, rk = _lib.ptr_array([_ptr(b) for b in bs]), _lib.i32_array(ranks)
+    ldh = h.stride(0) if h is not None else 0
+    stream = _stream(x)
+    for r0, r1, off, ids in routing.groups(_lib.MAX_SEGMENTS):
+        if r1 == r0:
+            continue
+        o, i, n = _routing_arrays(off, ids)
+        _lib.check("mlora_f32_gemm_fwd", lib.mlora_f32_gemm_fwd(
+            x[r0:r1].data_ptr(), x.stride(0), r1 - r0, K, w.data_ptr(), w.stride(0), N, _ptr(bias),
+            None if h is None else h[r0:r1].data_ptr(), ldh, ptrs, rk, len(bs), o, i, n,
+            y[r0:r1].data_ptr(), y.stride(0), stream))
+    return y
+
+
+def f32_gemm_dx(dy: torch.Tensor, w: torch.Tensor, g: torch.Tensor | None, as_: Sequence[torch.Tensor],
+                routing: SegmentRouting) -> torch.Tensor:
+    """fp32 dX = dY·W + per-segment g·A_a."""
+    M, N = dy.shape
+    K = w.shape[1]
+    _check_f32("dY", dy, N)
+    _check_f32("W", w, K)
+    ranks = [int(a.shape[0]) for a in as_]
+    for a in as_:
+        _check_f32("lora_a", a, K)
+        _require(a.is_contiguous(), "lora_a must be contiguous [r, K]")
+    dx = torch.empty((M, K), dtype=torch.float32, device=dy.device)
+    lib = _lib.load()
+    ptrs, rk = _lib.ptr_array([_ptr(a) for a in as_]), _lib.i32_array(ranks)
+    ldg = g.stride(0) if g is not None else 0
+    stream = _stream(dy)
+    for r0, r1, off, ids in routing.groups(_lib.MAX_SEGMENTS):
+        if r1 == r0:
+            continue
+        o, i, n = _routing_arrays(off, ids)
+        _lib.check("mlora_f32_gemm_dx", lib.mlora_f32_gemm_dx(
+            dy[r0:r1].data_ptr(), dy.stride(0), r1 - r0, N, w.data_ptr(), w.stride(0), K,
+            None if g is None else g[r0:r1].data_ptr(), ldg, ptrs, rk, len(as_), o, i, n,
+            dx[r0:r1].data_ptr(), dx.stride(0), stream))
+    return dx
+
+
+def f32_seg_outer(p: torch.Tensor, h: torch.Tensor, ranks: Sequence[int], routing: SegmentRouting,
+                  out_layout: int) -> list[torch.Tensor]:
+    """fp32 per-adapter Σ_m P[m,c]·h[m,j] -> [C, r_a] (layout 0) or [r_a, C] (layout 1); row groups of
+    more than one call are added in group order."""
+    M, C = p.shape
+    _check_f32("P", p)
+    _check_f32("h", h)
+    lib = _lib.load()
+    shape = (lambda r: (C, r)) if out_layout == 0 else (lambda r: (r, C))
+    outs: list[torch.Tensor | None] = [None] * len(ranks)
+    stream = _stream(p)
+    for r0, r1, off, ids in routing.groups(_lib.MAX_SEGMENTS):
+        o, i, n = _routing_arrays(off, ids)
+        part = [torch.zeros(shape(r), dtype=torch.float32, device=p.device) for r in ranks]
+        _lib.check("mlora_f32_seg_outer", lib.mlora_f32_seg_outer(
+            p[r0:r1].data_ptr(), p.stride(0), r1 - r0, C, h[r0:r1].data_ptr(), h.stride(0),
+            _lib.ptr_array([t.data_ptr() for t in part]), out_layout, _lib.i32_array(list(ranks)), len(ranks),
+            o, i, n, stream))
+        outs = [t if acc is None else acc + t for acc, t in zip(outs, part)]
+    return outs  # type: ignore[return-value]

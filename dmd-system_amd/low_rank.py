@@ -15,6 +15,7 @@ launch of the base GEMM.
 from __future__ import annotations
 
 import math
+import weakref
 from typing import Sequence
 
 import torch
@@ -30,22 +31,41 @@ def _require(value, message):
         raise ValueError('native trainable scope: ' + message)
 
 
+# Transposed copies of frozen base weights, one per weight tensor: every module that aliases
+# one base (shared construction, fused roles, TrainableLowRankLinear and MultiLoRALinear
+# over the same Parameter) uses the same copy. Keyed by the weight's identity (tensors do
+# not hash by value); an entry is dropped when its weight tensor is freed.
+_BASE_T: dict[int, tuple] = {}
+
+
+def _drop_base_t(key: int) -> None:
+    _BASE_T.pop(key, None)
+
+
 def _base_t(module: nn.Module, x: torch.Tensor) -> torch.Tensor | None:
     """The frozen base weight transposed ([in, out] bf16, contiguous), for the NT form of the
-    dX GEMM; made on the first forward that will need dX and remade when the weight changes
-    (storage, in-place version, dtype or device). A plain attribute, not a buffer: no
-    state-dict entry. None when no dX will be computed or ``module.transposed_base_for_dx``
-    is False (then dX runs on the NN kernel and no copy is kept)."""
+    dX GEMM (3-5% faster than the NN form at the Wan shapes); made on the first forward that
+    will need dX and remade when the weight changes (storage, in-place version, device). It
+    costs in·out·2 bytes per distinct base weight, shared by every module over that weight;
+    not a buffer, so no state-dict entry. None when no dX will be computed, on the float32
+    path (no bf16 GEMM), or when ``module.transposed_base_for_dx`` is False (then dX runs on
+    the NN kernel and no copy is kept)."""
     if not (torch.is_grad_enabled() and x.requires_grad) or not getattr(module, 'transposed_base_for_dx', True):
         return None
     w = module.base.weight
-    key = (w.data_ptr(), w._version, w.dtype, w.device)
-    cache = module.__dict__.get('_base_t_cache')
-    if cache is None or cache[0] != key:
+    autocast = torch.is_autocast_enabled("cuda") and torch.get_autocast_dtype("cuda") == torch.bfloat16
+    if not autocast and w.dtype != torch.bfloat16:
+        return None
+    key = (w.data_ptr(), w._version, w.device)
+    entry = _BASE_T.get(id(w))
+    if entry is None or entry[0]() is not w:
+        entry = (weakref.ref(w), None, None)
+        weakref.finalize(w, _drop_base_t, id(w))
+    if entry[1] != key:
         with torch.no_grad():
-            cache = (key, w.detach().to(torch.bfloat16).t().contiguous())
-        module.__dict__['_base_t_cache'] = cache
-    return cache[1]
+            entry = (entry[0], key, w.detach().to(torch.bfloat16).t().contiguous())
+    _BASE_T[id(w)] = entry
+    return entry[2]
 
 
 def _init_pair(rank: int, base: nn.Linear, dtype=None) -> tuple[nn.Parameter, nn.Parameter]:
@@ -115,6 +135,56 @@ def trainable_scope(native, config):
         native.set_submodule(name, TrainableLowRankLinear(module, rank=config['rank'], alpha=config['alpha']))
 
 
+class LoRALinear(nn.Module):
+    """The reference's parameterised native LoRA (native/models.py:33-51), on the HIP path.
+
+    Frozen ``base`` (bf16 in the native models, models.py:150-156) and fp32 masters ``a``
+    [r, in] (Kaiming-uniform, a=sqrt(5)) and ``b`` [out, r] (zeros), ``scale = alpha /
+    rank``. The reference computes update = F.linear(F.linear(x.float(), a), b) in fp32 and
+    returns (base(x).float() + update·scale).to(base dtype); here the shrinks use the masters
+    at fp32-class precision (hi + lo bf16 parts) and the base GEMM adds the update in its fp32
+    accumulators before one rounding to the base dtype. A float32 base runs the float32 path.
+    ``use_fused`` / ``fused_calls`` keep the reference's switch and counter for its no-grad
+    fused epilogue (wan13b_lora_epilogue.py:55-92); the epilogue is always fused here.
+    """
+
+    def __init__(self, base: nn.Linear, task) -> None:
+        super().__init__()
+        self.base = base.requires_grad_(False)
+        self.scale = float(task.lora_alpha / task.lora_rank)
+        dev = base.weight.device
+        self.a = nn.Parameter(torch.empty(task.lora_rank, base.in_features, dtype=torch.float32, device=dev))
+        self.b = nn.Parameter(torch.zeros(base.out_features, task.lora_rank, dtype=torch.float32, device=dev))
+        nn.init.kaiming_uniform_(self.a, a=5 ** 0.5)
+        self.use_fused = False
+        self.fused_calls = 0
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        if self.use_fused and not torch.is_grad_enabled():
+            self.fused_calls += 1
+        rows = x.numel() // x.shape[-1] if x.dim() else 0
+        return multi_lora_linear(x, self.base.weight, self.base.bias, [self.a], [self.b], [self.scale],
+                                 SegmentRouting.single(rows, 0), weight_t=_base_t(self, x))
+
+
+def install_lora(model: nn.Module, task) -> list[str]:
+    """Replace the nn.Linear modules named (or suffixed ``.<key>``) by ``task.target_modules``
+    with LoRALinear (native/models.py:54-64): same matching, the same ValueError messages for
+    no match or an unmatched key; returns the replaced names."""
+    model.requires_grad_(False)
+    found = [(name, mod) for name, mod in model.named_modules() if isinstance(mod, nn.Linear)
+             and any(name == key or name.endswith("." + key) for key in task.target_modules)]
+    if not found:
+        raise ValueError("no matching LoRA targets in native model; cannot silently train zero parameters")
+    for key in task.target_modules:
+        if not any(n == key or n.endswith("." + key) for n, _ in found):
+            raise ValueError(f"unmatched LoRA target: {key}")
+    for name, mod in found:
+        parent, _, leaf = name.rpartition(".")
+        setattr(model.get_submodule(parent) if parent else model, leaf, LoRALinear(mod, task))
+    return [n for n, _ in found]
+
+
 class MultiLoRALinear(nn.Module):
     """One frozen base nn.Linear shared by several adapters, routed by segment.
 
@@ -178,16 +248,40 @@ class MultiLoRALinear(nn.Module):
 
     def quantize_base_fp8(self) -> "MultiLoRALinear":
         """Store the frozen base weight as e4m3 with one fp32 scale per output
-        channel (buffers ``base_wq`` [out, in], ``base_wscale`` [out], and
-        ``base_wq_t`` = base_wq transposed for the e4m3 dX); forward and dX then
-        run on the e4m3 MFMA. The bf16/fp32 ``base.weight`` is left in place for
-        its other users (shared construction aliases it)."""
+        channel (buffers ``base_wq`` [out, in], ``base_wscale`` [out]); forward and dX
+        then run on the e4m3 MFMA. The bf16/fp32 ``base.weight`` is left in place for
+        its other users (shared construction aliases it). The e4m3 copy follows the
+        weight: if ``base.weight`` changes (in place, or by a state-dict load) it is
+        quantised again on the next call; ``base_wq`` transposed (for the e4m3 dX) is
+        remade whenever ``base_wq`` changes."""
         w = self.base.weight.detach().to(torch.bfloat16).contiguous()
         wq, ws = quantize_rows_fp8(w)
-        self.register_buffer("base_wq", wq, persistent=True)
-        self.register_buffer("base_wscale", ws, persistent=True)
-        self.register_buffer("base_wq_t", wq.t().contiguous(), persistent=False)
+        if getattr(self, "base_wq", None) is None:
+            self.register_buffer("base_wq", wq, persistent=True)
+            self.register_buffer("base_wscale", ws, persistent=True)
+        else:
+            with torch.no_grad():
+                self.base_wq.copy_(wq)
+                self.base_wscale.copy_(ws)
+        self.__dict__['_wq_source'] = self._weight_key()
         return self
+
+    def _weight_key(self):
+        w = self.base.weight
+        return (w.data_ptr(), w._version, w.device)
+
+    def _fp8_base(self):
+        """(base_wq, base_wscale, base_wq transposed), requantised / re-transposed when stale."""
+        if self.__dict__.get('_wq_source') != self._weight_key():
+            self.quantize_base_fp8()
+        wq = self.base_wq
+        key = (wq.data_ptr(), wq._version, wq.device)
+        cache = self.__dict__.get('_wq_t_cache')
+        if cache is None or cache[0] != key:
+            with torch.no_grad():
+                cache = (key, wq.t().contiguous())
+            self.__dict__['_wq_t_cache'] = cache
+        return wq, self.base_wscale, cache[1]
 
     def forward(self, x: torch.Tensor, routing: SegmentRouting | None = None) -> torch.Tensor:
         """x [..., in] -> [..., out]. Without ``routing`` the active RoleBatch (set by
@@ -218,8 +312,8 @@ class MultiLoRALinear(nn.Module):
     def _single(self, x: torch.Tensor, routing: SegmentRouting | None = None) -> torch.Tensor:
         routing = self._routing(x, routing)
         if getattr(self, "base_wq", None) is not None:
-            return multi_lora_linear_fp8(x, self.base_wq, self.base_wscale, self.base.bias, list(self.lora_a),
-                                         list(self.lora_b), self.scales, routing,
-                                         wq_t=getattr(self, "base_wq_t", None))
+            wq, ws, wq_t = self._fp8_base()
+            return multi_lora_linear_fp8(x, wq, ws, self.base.bias, list(self.lora_a), list(self.lora_b),
+                                         self.scales, routing, wq_t=wq_t)
         return multi_lora_linear(x, self.base.weight, self.base.bias, list(self.lora_a), list(self.lora_b),
                                  self.scales, routing, weight_t=_base_t(self, x))

@@ -27,6 +27,7 @@ from typing import Sequence
 import torch
 from torch import nn
 
+from . import _lib
 from .function import shared_input_multi_lora
 from .low_rank import MultiLoRALinear, TrainableLowRankLinear
 from .routing import SegmentRouting
@@ -62,6 +63,8 @@ class SharedInputGroup:
         ranks = {int(a.shape[0]) for ad in ads for a in ad[0]}
         _require(len(ranks) == 1 and next(iter(ranks)) % 16 == 0,
                  f'one LoRA rank, a multiple of 16, for every member and adapter (got {sorted(ranks)})')
+        _require(len(members) * next(iter(ranks)) <= _lib.MAX_RANK,
+                 f'{len(members)} members of rank {next(iter(ranks))} exceed the stacked rank limit {_lib.MAX_RANK}')
         for i in range(n):
             _require(len({ad[2][i] for ad in ads}) == 1, f'adapter {i} has different scales across members')
         if kinds == {MultiLoRALinear}:
@@ -82,8 +85,18 @@ class SharedInputGroup:
             raise ValueError('multi-LoRA linear: no routing given and no role batch active')
         return member.active_roles.routing(rows, member.role_ids)
 
+    def _stackable(self, x: torch.Tensor) -> bool:
+        """The stacked call is the bf16 path with bf16-rounded adapters: under bf16 autocast, or
+        bf16 input with bf16 adapters. float32 inputs, and fp32 adapter masters outside autocast
+        (fp32-class LoRA), run per member."""
+        if torch.is_autocast_enabled("cuda") and torch.get_autocast_dtype("cuda") == torch.bfloat16:
+            return True
+        if x.dtype != torch.bfloat16:
+            return False
+        return all(t.dtype == torch.bfloat16 for m in self.members for ad in _adapters(m)[:2] for t in ad)
+
     def __call__(self, member: nn.Module, x: torch.Tensor, routing: SegmentRouting | None = None) -> torch.Tensor:
-        if x.is_inference():  # no in-place version counter to key the reuse on: one call per linear
+        if x.is_inference() or not self._stackable(x):  # one call per linear
             return member._single(x, routing)
         idx = next(i for i, m in enumerate(self.members) if m is member)
         routing = self._routing(member, x, routing)

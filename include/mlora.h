@@ -43,7 +43,7 @@
 extern "C" {
 #endif
 
-#define MLORA_ABI_VERSION 5
+#define MLORA_ABI_VERSION 6
 
 /* Limits of one call (kernel-argument tables). Callers with more segments
  * split the rows into several calls; the Python host layer does this. */
@@ -78,6 +78,9 @@ typedef enum mlora_status {
 
 int mlora_abi_version(void);
 const char *mlora_status_string(int status);
+/* SHA-256 (hex) of the sources this library was built from (csrc/ and include/), so a
+ * loader can refuse a library built from other sources with the same ABI version. */
+const char *mlora_source_hash(void);
 
 /* Shrink: for each row m of a segment with adapter a (rank r_a),
  *   h[m, j] = s_a · Σ_k P[m, k] · Op_a(j, k),   j < r_a
@@ -94,6 +97,12 @@ const char *mlora_status_string(int status);
  * op_layout 0: Op_a stored [r_a, K] (K contiguous, e.g. lora_a, low_rank.py:21)
  * op_layout 1: Op_a stored [K, r_a] (r contiguous, e.g. lora_b [N, r] for the
  *              backward g = s·dY·B, low_rank.py:22)
+ * op_lo_ptrs (may be NULL): the adapter operands as two bf16 parts, op_ptrs[i] =
+ *           hi = bf16(v) and op_lo_ptrs[i] = lo = bf16(v - hi) of an fp32 master v
+ *           (same shape and layout); h then uses hi + lo (~16 significant bits of v)
+ *           instead of bf16(v). This is the fp32 LoRA compute of
+ *           native/models.py:44-51 (update = F.linear(F.linear(x.float(), a), b) with
+ *           fp32 masters, models.py:150-156) over bf16 activations.
  * row_div (may be NULL): per-row divisors [M]; h_rows (not h_frag) then holds
  *           h[m, j] / row_div[m]. The e4m3 forward passes its activation scales
  *           here (see mlora_gemm_fwd_fp8).
@@ -102,7 +111,7 @@ const char *mlora_status_string(int status);
  * autograd LinearBackward of F.linear(h, lora_b) (dH = g·B, as written out in
  * runtime/helios_lora_b_gemm_kernel.py:105). */
 int mlora_shrink(const void *p, int64_t ldp, int64_t M, int64_t K,
-                 const void *const *op_ptrs, int op_layout,
+                 const void *const *op_ptrs, const void *const *op_lo_ptrs, int op_layout,
                  const int32_t *ranks, const float *scales, int32_t n_adapters,
                  const int64_t *seg_offsets, const int32_t *adapter_ids, int32_t n_segments,
                  void *h_rows, int64_t ldh, void *h_frag, int32_t frag_jtiles,
@@ -242,6 +251,57 @@ int mlora_gemm_fwd_fp8(const void *xq, int64_t ldx, const float *x_scale, int64_
                        const int64_t *seg_offsets, const int32_t *adapter_ids, int32_t n_segments,
                        void *y, int64_t ldy, int accumulate,
                        void *stream);
+
+/* ---- fp32 arithmetic (the reference's precision='fp32' mode: no autocast,
+ * training/single_device.py:77-80, so TrainableLowRankLinear computes
+ * base(x) + s·F.linear(F.linear(x, A), B) and its autograd backward in fp32,
+ * training/low_rank.py:26-28). Every operand, product and sum is IEEE float32 on the
+ * gfx950 fp32 matrix core (v_mfma_f32_32x32x2_f32); sums run in a fixed order
+ * (deterministic). Matrices are float32 row-major, 4-byte aligned, any shape; ranks are
+ * any value in [0, MLORA_MAX_RANK] (no padding). Routing as above. */
+
+/* h[m, j] = s_a · Σ_k P[m, k]·Op_a(j, k) for the rows of adapter segments (op_layout as
+ * mlora_shrink), j < width; other entries of h [M, width] are written as 0.
+ * Reference: F.linear(value, lora_a) (low_rank.py:28) and dH = s·dY·B of its backward. */
+int mlora_f32_shrink(const void *p, int64_t ldp, int64_t M, int64_t K,
+                     const void *const *op_ptrs, int op_layout,
+                     const int32_t *ranks, const float *scales, int32_t n_adapters,
+                     const int64_t *seg_offsets, const int32_t *adapter_ids, int32_t n_segments,
+                     void *h, int64_t ldh, int64_t width,
+                     void *stream);
+
+/* Y[m, n] = Σ_k X[m,k]·W[n,k] + bias[n] + Σ_j h[m,j]·B_a[n,j] (h from mlora_f32_shrink, it
+ * carries s_a); W [N, K], B_a [N, r_a] contiguous, bias NULL or [N].
+ * Reference: low_rank.py:28, base(value) + scale·F.linear(F.linear(value, A), B). */
+int mlora_f32_gemm_fwd(const void *x, int64_t ldx, int64_t M, int64_t K,
+                       const void *w, int64_t ldw, int64_t N, const void *bias,
+                       const void *h_rows, int64_t ldh,
+                       const void *const *b_ptrs, const int32_t *ranks, int32_t n_adapters,
+                       const int64_t *seg_offsets, const int32_t *adapter_ids, int32_t n_segments,
+                       void *y, int64_t ldy,
+                       void *stream);
+
+/* dX[m, k] = Σ_n dY[m,n]·W[n,k] + Σ_j g[m,j]·A_a[j,k] (g = s_a·dY·B_a from
+ * mlora_f32_shrink with op_layout 1); A_a [r_a, K] contiguous.
+ * Reference: autograd of low_rank.py:28, dX = dY·W + (s·dY·B)·A. */
+int mlora_f32_gemm_dx(const void *dy, int64_t lddy, int64_t M, int64_t N,
+                      const void *w, int64_t ldw, int64_t K,
+                      const void *g_rows, int64_t ldg,
+                      const void *const *a_ptrs, const int32_t *ranks, int32_t n_adapters,
+                      const int64_t *seg_offsets, const int32_t *adapter_ids, int32_t n_segments,
+                      void *dx, int64_t lddx,
+                      void *stream);
+
+/* D_a[c, j] = Σ_{m in segments of a} P[m, c]·H[m, j] (segments summed in routing order),
+ * written to out_ptrs[a] as [C, r_a] (out_layout 0: dB_a = dYᵀ·h with P = dY, H = h) or
+ * [r_a, C] (out_layout 1: dA_a = gᵀ·X with P = X, H = g). Adapters without rows get zeros.
+ * Reference: autograd of low_rank.py:28 (dB = s·dYᵀ·(x·Aᵀ), dA = (s·dY·B)ᵀ·x). */
+int mlora_f32_seg_outer(const void *p, int64_t ldp, int64_t M, int64_t C,
+                        const void *h, int64_t ldh,
+                        void *const *out_ptrs, int out_layout,
+                        const int32_t *ranks, int32_t n_adapters,
+                        const int64_t *seg_offsets, const int32_t *adapter_ids, int32_t n_segments,
+                        void *stream);
 
 #ifdef __cplusplus
 }

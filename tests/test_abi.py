@@ -35,7 +35,7 @@ def test_library_exports_every_declared_symbol(lib, pkg):
 
 
 def test_abi_version_and_status_strings(lib, pkg):
-    assert lib.mlora_abi_version() == pkg._lib.ABI_VERSION == 5
+    assert lib.mlora_abi_version() == pkg._lib.ABI_VERSION == 6
     for code in (0, -1, -2, -3, -4, -5):
         assert lib.mlora_status_string(code)
     assert b"unknown" in lib.mlora_status_string(-99)
@@ -112,12 +112,59 @@ def test_frag_bytes(lib, pkg):
 def test_shrink_validation(lib, pkg):
     L = pkg._lib
     off, ids = L.i64_array([0, 64]), L.i32_array([0])
-    args = lambda layout, ranks, h: lib.mlora_shrink(  # noqa: E731
-        0x1000, 64, 64, 64, L.ptr_array([0x2000]), layout, L.i32_array(ranks), L.f32_array([1.0]), 1,
+    args = lambda layout, ranks, h, lo=None: lib.mlora_shrink(  # noqa: E731
+        0x1000, 64, 64, 64, L.ptr_array([0x2000]), lo, layout, L.i32_array(ranks), L.f32_array([1.0]), 1,
         off, ids, 1, h, 64, None, 0, None, None)
     assert args(3, [8], 0x3000) == L.ERR_INVALID
     assert args(0, [12], 0x3000) == L.ERR_INVALID
     assert args(0, [8], 0) == L.ERR_INVALID
+    # split (fp32-master) operands: every used operand needs an aligned lo part
+    assert args(0, [8], 0x3000, lo=L.ptr_array([0])) == L.ERR_INVALID
+    assert args(0, [8], 0x3000, lo=L.ptr_array([0x4008])) == L.ERR_UNSUPPORTED
+
+
+def test_library_matches_its_sources(lib, pkg):
+    """The library reports the hash of the sources it was built from; the loader refuses a
+    library whose hash differs from the sources beside it (a stale prebuilt library)."""
+    built = lib.mlora_source_hash().decode()
+    assert len(built) == 64 and built == pkg._lib.expected_source_hash()
+    saved = pkg._lib._LIB
+    orig = pkg._lib.expected_source_hash
+    try:
+        pkg._lib._LIB = None
+        pkg._lib.expected_source_hash = lambda: "0" * 64
+        with pytest.raises(RuntimeError, match="other sources"):
+            pkg._lib.load()
+    finally:
+        pkg._lib.expected_source_hash = orig
+        pkg._lib._LIB = saved
+
+
+def test_f32_entry_points_validate_before_launch(lib, pkg):
+    L = pkg._lib
+    off, ids = L.i64_array([0, 64]), L.i32_array([0])
+    ptr, rk, sc = L.ptr_array([0x2000]), L.i32_array([5]), L.f32_array([1.0])
+    sh = lambda layout=0, h=0x3000, width=5, p=0x1000, o=off: lib.mlora_f32_shrink(  # noqa: E731
+        p, 64, 64, 64, ptr, layout, rk, sc, 1, o, ids, 1, h, width, width, None)
+    assert sh(layout=2) == L.ERR_INVALID
+    assert sh(width=4) == L.ERR_INVALID                 # narrower than the rank
+    assert sh(p=0x1002) == L.ERR_UNSUPPORTED            # float rows are 4-byte aligned
+    assert sh(h=0) == L.ERR_INVALID
+    assert sh(o=L.i64_array([0, 60])) == L.ERR_INVALID  # routing covers M rows
+    fwd = lambda ldw=64, h=0x5000, bias=None: lib.mlora_f32_gemm_fwd(  # noqa: E731
+        0x1000, 64, 64, 64, 0x2000, ldw, 48, bias, h, 8, ptr, rk, 1, off, ids, 1, 0x3000, 48, None)
+    assert fwd(ldw=32) == L.ERR_INVALID                 # ld < K
+    assert fwd(h=0) == L.ERR_INVALID                    # adapter rows need h
+    assert fwd(bias=0x6002) == L.ERR_UNSUPPORTED
+    dx = lambda g=0x5000: lib.mlora_f32_gemm_dx(  # noqa: E731
+        0x1000, 48, 64, 48, 0x2000, 64, 64, g, 8, ptr, rk, 1, off, ids, 1, 0x3000, 64, None)
+    assert dx(g=0) == L.ERR_INVALID
+    so = lambda layout=0, outs=(0x7000,): lib.mlora_f32_seg_outer(  # noqa: E731
+        0x1000, 64, 64, 64, 0x2000, 8, L.ptr_array(list(outs)), layout, rk, 1, off, ids, 1, None)
+    assert so(layout=3) == L.ERR_INVALID
+    assert so(outs=(0,)) == L.ERR_INVALID
+    assert lib.mlora_f32_shrink(0x1000, 64, 0, 64, ptr, 0, rk, sc, 1, L.i64_array([0, 0]), ids, 1, 0x3000, 5,
+                                5, None) == L.OK
 
 
 def test_fp8_entry_points_validate_before_launch(lib, pkg):

@@ -1,0 +1,214 @@
+"""float32 arithmetic and fp32 LoRA masters, vs the fp64 oracle.
+
+* precision='fp32' (training/single_device.py:77-80: no autocast): float32 x, W, b, A, B;
+  TrainableLowRankLinear computes base(x) + s·F.linear(F.linear(x, A), B) (low_rank.py:26-28)
+  and its backward in float32. Here every output (Y, dX, dA, dB) is float32 and must be within
+  rel-L2 <= 1e-5 of the exact (fp64) result on the same float32 inputs.
+* fp32 masters over a bf16 base (native/models.py:33-51,150-156): bf16 x and W, float32 A and
+  B used as float32 (not rounded to bf16). Y and dX are bf16 (<= 2e-3, one rounding); dA and
+  dB must be within 5e-5 of the exact gradients of the UNROUNDED masters — rounding the
+  masters to bf16 alone moves them ~1.6e-3, which this bound rejects (checked in the test).
+"""
+import math
+
+import numpy as np
+import pytest
+import torch
+from torch import nn
+
+from oracle import multilora_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+TOL_F32 = 1e-5
+TOL_BF16_OUT = 2e-3
+TOL_MASTER_GRAD = 5e-5
+
+
+def f64(t):
+    return t.detach().double().cpu().numpy()
+
+
+def case(M, K, N, ranks, seed, bias=True, dtype=torch.float32):
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn(M, K, generator=g).to(dtype)
+    w = (torch.randn(N, K, generator=g) / math.sqrt(K)).to(dtype)
+    b = (torch.randn(N, generator=g) / math.sqrt(K)).to(dtype) if bias else None
+    As = [(torch.rand(r, K, generator=g) * 2 - 1) / math.sqrt(K) for r in ranks]
+    Bs = [torch.randn(N, r, generator=g) * 0.02 for r in ranks]
+    dy = torch.randn(M, N, generator=g).to(dtype)
+    return x, w, b, As, Bs, dy
+
+
+def run(pkg, dev, x, w, b, As, Bs, dy, scales, routing):
+    xg = x.to(dev).requires_grad_(True)
+    Ag = [a.to(dev).requires_grad_(True) for a in As]
+    Bg = [v.to(dev).requires_grad_(True) for v in Bs]
+    y = pkg.multi_lora_linear(xg, w.to(dev), None if b is None else b.to(dev), Ag, Bg, scales, routing)
+    y.backward(dy.to(dev))
+    torch.cuda.synchronize()
+    return y, xg.grad, [a.grad for a in Ag], [v.grad for v in Bg]
+
+
+def errors(pkg, got, case_, scales, routing):
+    x, w, b, As, Bs, dy = case_
+    y, dx, dAs, dBs = got
+    off, ids = routing.seg_offsets, routing.adapter_ids
+    Af, Bf = [f64(a) for a in As], [f64(v) for v in Bs]
+    y_ref = O.forward(f64(x), f64(w), None if b is None else f64(b), Af, Bf, scales, off, ids)
+    dx_ref, dA_ref, dB_ref = O.backward(f64(x), f64(w), Af, Bf, scales, off, ids, f64(dy))
+    errs = {"y": O.rel_l2(f64(y), y_ref), "dx": O.rel_l2(f64(dx), dx_ref)}
+    for i in range(len(As)):
+        if np.abs(dA_ref[i]).max() == 0:
+            assert not dAs[i].any() and not dBs[i].any(), "adapter without rows must get zero gradient"
+            continue
+        errs[f"dA{i}"] = O.rel_l2(f64(dAs[i]), dA_ref[i])
+        errs[f"dB{i}"] = O.rel_l2(f64(dBs[i]), dB_ref[i])
+    print("rel-L2", {k: f"{v:.2e}" for k, v in errs.items()}, flush=True)
+    return errs
+
+
+@pytest.mark.parametrize("bias", [True, False])
+@pytest.mark.parametrize("lengths,ids", [((256, 256), (0, 1)), ((200, 56, 256), (0, -1, 1)),
+                                         ((0, 300, 212), (1, 0, -1))])
+def test_tiny_config_fp32(pkg, dev, bias, lengths, ids):
+    """BASELINE config 1 as specified: fp32, X [2x256 tokens, 256], W [256, 256] ~ N(0, 1/256), two
+    rank-8 adapters (Kaiming-uniform A, B ~ N(0, 0.02)), scale 1; plus null and empty segments."""
+    from dmd_system_amd import workloads as W
+    cfg = W.CONFIGS["tiny"]
+    x, w, b, As, Bs, dy = W.make_linear(cfg, 256, 256, torch.device("cpu"), seed=cfg.seed, dtype=torch.float32,
+                                        bias=bias)
+    routing = pkg.SegmentRouting.from_lengths(lengths, ids)
+    got = run(pkg, dev, x, w, b, As, Bs, dy, [cfg.scale] * 2, routing)
+    assert got[0].dtype == torch.float32 and got[1].dtype == torch.float32
+    assert all(g.dtype == torch.float32 for g in got[2] + got[3])
+    errs = errors(pkg, got, (x, w, b, As, Bs, dy), [cfg.scale] * 2, routing)
+    assert all(v <= TOL_F32 for v in errs.values()), errs
+
+
+def test_fp32_ragged_shapes_and_unpadded_ranks(pkg, dev):
+    """M, K, N off every tile size; ranks 24 / 8 / 40 / 5 (no padding in the float32 path)."""
+    lengths, ids = (77, 301, 1, 250, 371), (2, 0, 3, -1, 1)
+    c = case(1000, 136, 200, (24, 8, 40, 5), seed=41)
+    routing = pkg.SegmentRouting.from_lengths(lengths, ids)
+    scales = [0.5, 2.0, 1.0, 3.0]
+    errs = errors(pkg, run(pkg, dev, *c, scales, routing), c, scales, routing)
+    assert all(v <= TOL_F32 for v in errs.values()), errs
+
+
+def test_fp32_more_segments_than_one_call(pkg, dev):
+    """300 segments: the host splits the rows into calls of <= 128 segments (gradients summed in
+    group order)."""
+    rng = np.random.default_rng(42)
+    lengths = [int(v) for v in rng.integers(0, 12, size=300)]
+    ids = [int(v) for v in rng.integers(-1, 3, size=300)]
+    c = case(sum(lengths), 64, 72, (8, 16, 8), seed=42)
+    routing = pkg.SegmentRouting.from_lengths(lengths, ids)
+    scales = [1.0, 0.5, 2.0]
+    errs = errors(pkg, run(pkg, dev, *c, scales, routing), c, scales, routing)
+    assert all(v <= TOL_F32 for v in errs.values()), errs
+
+
+def test_fp32_rank_256_and_long_contraction(pkg, dev):
+    """A rank-256 adapter and K = 1536 (several 128-wide output tiles in every direction)."""
+    lengths, ids = (700, 324), (0, 1)
+    c = case(1024, 1536, 384, (256, 64), seed=43)
+    routing = pkg.SegmentRouting.from_lengths(lengths, ids)
+    scales = [0.25, 1.0]
+    errs = errors(pkg, run(pkg, dev, *c, scales, routing), c, scales, routing)
+    assert all(v <= TOL_F32 for v in errs.values()), errs
+
+
+def test_trainable_scope_in_fp32_precision(pkg, dev):
+    """The reference's precision='fp32' mode end to end: an fp32 model with trainable_scope, called
+    with no autocast, returns float32 and float32 gradients equal (1e-5) to the fp64 oracle."""
+    torch.manual_seed(44)
+    model = nn.Sequential(nn.Linear(64, 96), nn.GELU(), nn.Linear(96, 64))
+    pkg.trainable_scope(model, {'mode': 'lora', 'rank': 8, 'alpha': 16., 'targets': ['0', '2']})
+    with torch.no_grad():
+        for m in (model[0], model[2]):
+            m.lora_b.normal_(0, 0.05)
+    model = model.to(dev)
+    x = torch.randn(3, 40, 64, device=dev)
+    y = model(x)
+    assert y.dtype == torch.float32
+    m0 = model[0]
+    xr = x.reshape(-1, 64)
+    y0 = m0(xr)
+    dy = torch.randn_like(y0)
+    y0.backward(dy)
+    off, ids = [0, 120], [0]
+    want = O.forward(f64(xr), f64(m0.base.weight), f64(m0.base.bias), [f64(m0.lora_a)], [f64(m0.lora_b)], [2.0],
+                     off, ids)
+    _, dA, dB = O.backward(f64(xr), f64(m0.base.weight), [f64(m0.lora_a)], [f64(m0.lora_b)], [2.0], off, ids,
+                           f64(dy))
+    assert O.rel_l2(f64(y0), want) <= TOL_F32
+    assert m0.lora_a.grad.dtype == torch.float32
+    assert O.rel_l2(f64(m0.lora_a.grad), dA[0]) <= TOL_F32
+    assert O.rel_l2(f64(m0.lora_b.grad), dB[0]) <= TOL_F32
+    assert m0.base.weight.grad is None
+
+
+@pytest.mark.parametrize("K,N,rank", [(1536, 1536, 64), (512, 1024, 256), (136, 200, 24)])
+def test_fp32_masters_over_bf16_base(pkg, dev, K, N, rank):
+    """native/models.py:44-51 with fp32 masters (models.py:150-156): bf16 x and base, fp32 A / B.
+    dA / dB against the exact gradients of the unrounded masters (5e-5), Y / dX (bf16) within
+    one rounding; the same oracle on bf16-rounded masters is far outside 5e-5 (so the check
+    tells fp32 masters from rounded ones)."""
+    lengths, ids = (1500, 548), (0, 1)
+    x, w, b, As, Bs, dy = case(sum(lengths), K, N, (rank, rank), seed=45, dtype=torch.bfloat16)
+    routing = pkg.SegmentRouting.from_lengths(lengths, ids)
+    scales = [1.0, 0.5]
+    y, dx, dAs, dBs = run(pkg, dev, x, w, b, As, Bs, dy, scales, routing)
+    assert y.dtype == torch.bfloat16 and dx.dtype == torch.bfloat16
+    assert all(g.dtype == torch.float32 for g in dAs + dBs)
+    off, ids_ = routing.seg_offsets, routing.adapter_ids
+    Af, Bf = [f64(a) for a in As], [f64(v) for v in Bs]
+    y_ref = O.forward(f64(x), f64(w), f64(b), Af, Bf, scales, off, ids_)
+    dx_ref, dA_ref, dB_ref = O.backward(f64(x), f64(w), Af, Bf, scales, off, ids_, f64(dy))
+    errs = {"y": O.rel_l2(f64(y), y_ref), "dx": O.rel_l2(f64(dx), dx_ref)}
+    for i in range(2):
+        errs[f"dA{i}"] = O.rel_l2(f64(dAs[i]), dA_ref[i])
+        errs[f"dB{i}"] = O.rel_l2(f64(dBs[i]), dB_ref[i])
+    print("rel-L2", {k: f"{v:.2e}" for k, v in errs.items()}, flush=True)
+    assert errs["y"] <= TOL_BF16_OUT and errs["dx"] <= TOL_BF16_OUT, errs
+    assert all(errs[k] <= TOL_MASTER_GRAD for k in errs if k[0] == "d" and k[1] in "AB"), errs
+    rb = lambda t: O.bf16_round(t.numpy()).astype(np.float64)  # noqa: E731
+    _, dA_rounded, dB_rounded = O.backward(f64(x), f64(w), [rb(a) for a in As], [rb(v) for v in Bs], scales,
+                                           off, ids_, f64(dy))
+    assert O.rel_l2(dA_rounded[0], dA_ref[0]) > 10 * TOL_MASTER_GRAD
+    assert O.rel_l2(dB_rounded[0], dB_ref[0]) > 10 * TOL_MASTER_GRAD
+
+
+def test_native_lora_linear_drop_in(pkg, dev):
+    """install_lora on a bf16 model (the native models' layout): LoRALinear's fp32 masters get
+    fp32 gradients equal to the exact ones (5e-5); output dtype is the base's."""
+    from types import SimpleNamespace
+    torch.manual_seed(46)
+    model = nn.Sequential(nn.Linear(128, 256), nn.GELU(), nn.Linear(256, 128)).to(torch.bfloat16)
+    pkg.install_lora(model, SimpleNamespace(lora_rank=16, lora_alpha=32.0, target_modules=["0", "2"]))
+    with torch.no_grad():
+        for m in (model[0], model[2]):
+            m.b.normal_(0, 0.05)
+    model = model.to(dev)
+    x = torch.randn(500, 128, device=dev).to(torch.bfloat16)
+    m0 = model[0]
+    y = m0(x)
+    assert y.dtype == torch.bfloat16
+    dy = torch.randn_like(y)
+    y.backward(dy)
+    assert m0.a.grad.dtype == torch.float32 and m0.b.grad.dtype == torch.float32
+    off, ids = [0, 500], [0]
+    _, dA, dB = O.backward(f64(x), f64(m0.base.weight), [f64(m0.a)], [f64(m0.b)], [2.0], off, ids, f64(dy))
+    assert O.rel_l2(f64(m0.a.grad), dA[0]) <= TOL_MASTER_GRAD
+    assert O.rel_l2(f64(m0.b.grad), dB[0]) <= TOL_MASTER_GRAD
+    exact = O.forward(f64(x), f64(m0.base.weight), f64(m0.base.bias), [f64(m0.a)], [f64(m0.b)], [2.0], off, ids)
+    assert O.rel_l2(f64(y), exact) <= TOL_BF16_OUT  # one bf16 rounding of the exact output
+    # the reference's own arithmetic rounds twice (base to bf16, then the sum): within two roundings
+    ref = O.forward_fp32_update(f64(x), f64(m0.base.weight), f64(m0.base.bias), [f64(m0.a)], [f64(m0.b)], [2.0],
+                                off, ids)
+    assert O.rel_l2(f64(y), ref) <= 2 * TOL_BF16_OUT
+    m0.use_fused = True
+    with torch.no_grad():
+        m0(x)
+    assert m0.fused_calls == 1

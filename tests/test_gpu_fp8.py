@@ -201,12 +201,13 @@ def test_module_quantize_base_fp8(pkg, dev):
     assert all(p.grad is not None for p in lin.lora_a) and base.weight.grad is None
 
 
-def test_wan13b_fp8_full_shape(pkg, dev):
-    """Config 5 at full size (65520 tokens, 4 rank-64 adapters on seeded segments, q/k/v/o shape):
-    Y and dX on 512 sampled rows vs the oracle, adapter gradients vs torch fp32 on the GPU."""
+@pytest.mark.parametrize("K,N", [(1536, 1536), (1536, 8960), (8960, 1536)])
+def test_wan13b_fp8_full_shape(pkg, dev, K, N):
+    """Config 5 at full size (65520 tokens, 4 rank-64 adapters on seeded segments) at each of its
+    linear shapes (q/k/v/o, ffn.0, ffn.2): Y and dX on 512 sampled rows vs the oracle, adapter
+    gradients vs torch fp32 on the GPU."""
     from dmd_system_amd import workloads as W
     cfg = W.CONFIGS["wan13b_fp8"]
-    K = N = cfg.hidden
     x, w, b, As, Bs, dy = W.make_linear(cfg, K, N, dev, seed=cfg.seed)
     wq, ws = pkg.kernels.quantize_rows_fp8(w)
     routing = cfg.routing

@@ -154,19 +154,19 @@ def test_deterministic(pkg, dev):
 
 
 def test_fp32_masters_get_fp32_grads(pkg, dev):
-    """fp32 LoRA masters (native/models.py:38-39) are cast to bf16 for the kernels
-    (autocast semantics); gradients come back fp32. Oracle on the bf16-rounded values."""
+    """fp32 LoRA masters with bf16 activations outside autocast (native/models.py:38-39,150-156):
+    the gradients come back fp32 and are fp32-class against the oracle on the unrounded masters
+    (the fp32-master path is covered in depth by tests/test_gpu_fp32.py)."""
     lengths, ids = (256, 256), (0, 1)
     x, w, b, As, Bs, dy = make_case(512, 256, 256, (8, 8), lengths, ids, seed=17, dtype=torch.float32)
     routing = pkg.SegmentRouting.from_lengths(lengths, ids)
     y, dx, dAs, dBs = run_hip(pkg, dev, x, w, b, As, Bs, dy, [1.0, 1.0], routing)
     assert all(g.dtype == torch.float32 for g in dAs + dBs)
-    q = lambda t: f64(t.to(torch.bfloat16))  # noqa: E731
-    dx_ref, dA_ref, dB_ref = O.backward(f64(x), f64(w), [q(a) for a in As], [q(v) for v in Bs], [1.0, 1.0],
+    dx_ref, dA_ref, dB_ref = O.backward(f64(x), f64(w), [f64(a) for a in As], [f64(v) for v in Bs], [1.0, 1.0],
                                         routing.seg_offsets, routing.adapter_ids, f64(dy))
     for i in range(2):
-        assert O.rel_l2(f64(dAs[i]), dA_ref[i]) <= TOL
-        assert O.rel_l2(f64(dBs[i]), dB_ref[i]) <= TOL
+        assert O.rel_l2(f64(dAs[i]), dA_ref[i]) <= 5e-5
+        assert O.rel_l2(f64(dBs[i]), dB_ref[i]) <= 5e-5
 
 
 def test_drop_in_trainable_scope_under_autocast(pkg, dev):
@@ -213,17 +213,19 @@ def test_expand_standalone_accumulates(pkg, dev):
     assert O.rel_l2(f64(y), want) <= TOL
 
 
+@pytest.mark.parametrize("transposed", [False, True], ids=["dx_nn", "dx_nt"])
 @pytest.mark.parametrize("name,K,N", [("q", 1536, 1536), ("ffn.0", 1536, 8960), ("ffn.2", 8960, 1536)])
-def test_wan13b_full_shape(pkg, dev, name, K, N):
+def test_wan13b_full_shape(pkg, dev, name, K, N, transposed):
     """BASELINE config 2 (65520 tokens, 2 adapters rank 64) at full size:
     Y and dX on 512 sampled rows vs the fp64 oracle, adapter gradients vs torch
-    fp32 on the GPU, frozen W untouched."""
+    fp32 on the GPU, frozen W untouched. dX both on the NN kernel and on the NT kernel
+    against the frozen base held transposed (the modules' default and the benchmarked path)."""
     from dmd_system_amd import workloads as W
     cfg = W.CONFIGS["wan13b"]
     x, w, b, As, Bs, dy = W.make_linear(cfg, K, N, dev, seed=cfg.seed)
     w_sum = w.float().sum().item()
     routing = cfg.routing
-    y, dx, dAs, dBs = run_hip(pkg, dev, x, w, b, As, Bs, dy, [cfg.scale] * 2, routing)
+    y, dx, dAs, dBs = run_hip(pkg, dev, x, w, b, As, Bs, dy, [cfg.scale] * 2, routing, transposed=transposed)
     rows = np.sort(np.random.default_rng(20).choice(cfg.tokens, 512, replace=False))
     rows[0], rows[-1] = 0, cfg.tokens - 1
     Af, Bf = [f64(a) for a in As], [f64(v) for v in Bs]
@@ -247,12 +249,14 @@ def test_wan13b_full_shape(pkg, dev, name, K, N):
     assert torch.isfinite(y).all() and torch.isfinite(dx).all()
 
 
-@pytest.mark.parametrize("cfg_name,lin", [("wan22_5b", "ffn.0"), ("wan22_5b", "ffn.2"), ("flux", "q"), ("flux", "ffn.0")])
-def test_config_3_4_full_shape(pkg, dev, cfg_name, lin):
+@pytest.mark.parametrize("transposed", [False, True], ids=["dx_nn", "dx_nt"])
+@pytest.mark.parametrize("cfg_name,lin", [("wan22_5b", "ffn.0"), ("wan22_5b", "ffn.2"), ("flux", "q"),
+                                          ("flux", "ffn.0"), ("flux", "ffn.2")])
+def test_config_3_4_full_shape(pkg, dev, cfg_name, lin, transposed):
     """BASELINE configs 3 (27280 tokens, 3 rank-128 adapters on seeded segments, scale 2) and
     4 (16 samples x 4608 tokens, one adapter each, ranks from {16,32,64,128}) at full size:
     Y and dX on 384 sampled rows vs the fp64 oracle, every adapter's gradients vs torch fp32
-    on the GPU."""
+    on the GPU; dX on the NN kernel and on the NT kernel against the transposed base."""
     from dmd_system_amd import workloads as W
     cfg = W.CONFIGS[cfg_name]
     K, N = {name: (k, n) for name, k, n in cfg.linears()}[lin]
@@ -260,7 +264,7 @@ def test_config_3_4_full_shape(pkg, dev, cfg_name, lin):
     routing = cfg.routing
     n = len(cfg.ranks)
     scales = [cfg.scale] * n
-    y, dx, dAs, dBs = run_hip(pkg, dev, x, w, b, As, Bs, dy, scales, routing)
+    y, dx, dAs, dBs = run_hip(pkg, dev, x, w, b, As, Bs, dy, scales, routing, transposed=transposed)
     rows = np.sort(np.random.default_rng(30).choice(cfg.tokens, 384, replace=False))
     rows[0], rows[-1] = 0, cfg.tokens - 1
     Af, Bf = [f64(a) for a in As], [f64(v) for v in Bs]

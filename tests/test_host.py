@@ -110,8 +110,37 @@ def test_no_cpu_path(pkg):
     x = torch.randn(4, 16, dtype=torch.bfloat16)
     with pytest.raises(RuntimeError, match="ROCm device only"):
         m(x, pkg.SegmentRouting.single(4))
-    with pytest.raises(RuntimeError, match="bfloat16"):
-        m.float()(x.float(), pkg.SegmentRouting.single(4))
+    with pytest.raises(RuntimeError, match="ROCm device only"):
+        m.float()(x.float(), pkg.SegmentRouting.single(4))  # the float32 path is a device path too
+    with pytest.raises(RuntimeError, match="bfloat16 or float32"):
+        m(x.half(), pkg.SegmentRouting.single(4))
+    mixed = pkg.MultiLoRALinear(nn.Linear(16, 8), ranks=[8], alphas=[8], dtype=torch.bfloat16)
+    with pytest.raises(RuntimeError, match="adapters must be float32"):
+        mixed(x.float(), pkg.SegmentRouting.single(4))
+
+
+def test_native_lora_install_contract(pkg):
+    """install_lora / LoRALinear keep native/models.py:33-64: fp32 masters `a` (Kaiming-uniform) and
+    `b` (zeros) over a frozen base, scale alpha / rank, suffix matching, fail-closed messages."""
+    from types import SimpleNamespace
+    torch.manual_seed(0)
+    model = nn.Sequential(nn.Linear(8, 16), nn.GELU(), nn.Sequential(nn.Linear(16, 8)))
+    model.to(torch.bfloat16)
+    task = SimpleNamespace(lora_rank=4, lora_alpha=8.0, target_modules=["0", "2.0"])
+    names = pkg.install_lora(model, task)
+    assert names == ["0", "2.0"]
+    for m in (model[0], model[2][0]):
+        assert isinstance(m, pkg.LoRALinear) and m.scale == 2.0
+        assert m.a.dtype == torch.float32 and m.b.dtype == torch.float32 and not m.b.any()
+        assert m.a.shape == (4, m.base.in_features) and m.b.shape == (m.base.out_features, 4)
+        assert m.a.abs().max() <= 1 / m.base.in_features ** 0.5 + 1e-6
+        assert not m.base.weight.requires_grad and m.base.weight.dtype == torch.bfloat16
+    assert {n for n, p in model.named_parameters() if p.requires_grad} == {"0.a", "0.b", "2.0.a", "2.0.b"}
+    with pytest.raises(ValueError, match="no matching LoRA targets"):
+        pkg.install_lora(nn.Sequential(nn.Linear(2, 2)), SimpleNamespace(lora_rank=1, lora_alpha=1., target_modules=["q"]))
+    with pytest.raises(ValueError, match="unmatched LoRA target: q"):
+        pkg.install_lora(nn.Sequential(nn.Linear(2, 2)), SimpleNamespace(lora_rank=1, lora_alpha=1.,
+                                                                         target_modules=["0", "q"]))
 
 
 # ---------------------------------------------------------------- workloads
