@@ -20,7 +20,8 @@ MAX_RANK = 256
 F32, BF16, FP8_E4M3 = 0, 1, 2
 
 OK = 0
-ERR_INVALID, ERR_UNSUPPORTED, ERR_WORKSPACE, ERR_LAUNCH, ERR_LIMIT = -1, -2, -3, -4, -5
+ERR_INVALID, ERR_UNSUPPORTED, ERR_WORKSPACE, ERR_LAUNCH, ERR_LIMIT, ERR_DEVICE = -1, -2, -3, -4, -5, -6
+NOALLOC_SCRATCH_BYTES = 64 << 20
 
 # Every entry point declared in include/mlora.h with its ctypes signature.
 _vp, _i64, _i32, _int = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int32, ctypes.c_int
@@ -47,6 +48,8 @@ SIGNATURES = {
     "mlora_seg_outer": (_int, [_vp, _i64, _i64, _i64, _vp, _i32, _pvp, _int, _int, _pi32, _i32,
                                _pi64, _pi32, _i32, _vp, _i64, _vp]),
     "mlora_seg_outer_workspace_bytes": (_i64, [_i64, _i64, _pi32, _i32, _pi64, _pi32, _i32]),
+    "mlora_seg_outer_noalloc": (_int, [_vp, _i64, _i64, _i64, _vp, _i32, _pvp, _int, _int, _pi32, _i32,
+                                       _pi64, _pi32, _i32, _vp]),
     "mlora_quantize_rows_fp8": (_int, [_vp, _i64, _i64, _i64, _vp, _vp, _i64, _vp, _vp]),
     "mlora_dequant_rows_fp8": (_int, [_vp, _i64, _vp, _i64, _i64, _vp, _i64, _vp]),
     "mlora_div_rows_bf16": (_int, [_vp, _i64, _vp, _i64, _i64, _vp, _i64, _vp]),

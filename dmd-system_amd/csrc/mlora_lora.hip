@@ -22,6 +22,7 @@
 #include "mlora_common.h"
 #include "mlora_host.h"
 
+#include <mutex>
 #include <type_traits>
 #include <utility>
 
@@ -551,7 +552,8 @@ struct OuterPlan {
   int32_t chunk_start[kMaxSeg + 1];
 };
 
-static void plan_outer(OuterPlan &pl, const SegTable &st, const int32_t *rank, int64_t C) {
+// chunk_floor: the smallest chunk (rows) to use; 0 for the default plan.
+static void plan_outer(OuterPlan &pl, const SegTable &st, const int32_t *rank, int64_t C, int64_t chunk_floor = 0) {
   int rmax = 0;
   int64_t rows = 0;
   for (int s = 0; s < st.n; ++s) {
@@ -569,6 +571,7 @@ static void plan_outer(OuterPlan &pl, const SegTable &st, const int32_t *rank, i
   const int64_t target_items = 512;
   int64_t cr = rows * pl.cblocks * (pl.jblocks > 0 ? pl.jblocks : 1) / target_items;
   cr = cr < 512 ? 512 : cr;
+  cr = cr < chunk_floor ? chunk_floor : cr;
   cr = (cr + 127) / 128 * 128;
   pl.chunk_rows = (int32_t)(cr > kMaxChunkRows ? kMaxChunkRows : cr);
   int32_t n = 0;
@@ -702,15 +705,12 @@ extern "C" int64_t mlora_seg_outer_workspace_bytes(int64_t M, int64_t C, const i
   return (int64_t)pl.n_chunks * C * pl.rpad * (int64_t)sizeof(float);
 }
 
-extern "C" int mlora_seg_outer(const void *p, int64_t ldp, int64_t M, int64_t C, const void *h_frag,
-                               int32_t frag_jtiles, void *const *out_ptrs, int out_layout, int out_dtype,
-                               const int32_t *ranks, int32_t n_adapters, const int64_t *seg_offsets,
-                               const int32_t *adapter_ids, int32_t n_segments, void *workspace,
-                               int64_t workspace_bytes, void *stream) {
-  OuterArgs a{};
-  OuterPlan pl;
-  int st = outer_setup(a, pl, M, C, ranks, n_adapters, seg_offsets, adapter_ids, n_segments);
-  if (st) return st;
+// Validation and launches shared by mlora_seg_outer and mlora_seg_outer_noalloc; a and pl
+// come from outer_setup.
+static int seg_outer_run(OuterArgs &a, const OuterPlan &pl, const void *p, int64_t ldp, int64_t M, int64_t C,
+                         const void *h_frag, int32_t frag_jtiles, void *const *out_ptrs, int out_layout, int out_dtype,
+                         int32_t n_adapters, void *workspace, int64_t workspace_bytes, hipStream_t s) {
+  int st;
   if (out_layout != 0 && out_layout != 1) return MLORA_ERR_INVALID;
   if (out_dtype != MLORA_F32 && out_dtype != MLORA_BF16) return MLORA_ERR_UNSUPPORTED;
   if (n_adapters > 0 && out_ptrs == nullptr) return MLORA_ERR_INVALID;
@@ -718,7 +718,6 @@ extern "C" int mlora_seg_outer(const void *p, int64_t ldp, int64_t M, int64_t C,
     if (a.rank[i] > 0 && C > 0 && out_ptrs[i] == nullptr) return MLORA_ERR_INVALID;
   if (C == 0 || n_adapters == 0) return MLORA_OK;
   const int64_t need = (int64_t)pl.n_chunks * C * pl.rpad * (int64_t)sizeof(float);
-  hipStream_t s = static_cast<hipStream_t>(stream);
   if (pl.n_chunks > 0) {
     if ((st = check_bf16_matrix(p, ldp, M, C))) return st;
     if (h_frag == nullptr || !aligned16(h_frag)) return MLORA_ERR_INVALID;
@@ -769,6 +768,73 @@ extern "C" int mlora_seg_outer(const void *p, int64_t ldp, int64_t M, int64_t C,
   return launch_status();
 }
 
+extern "C" int mlora_seg_outer(const void *p, int64_t ldp, int64_t M, int64_t C, const void *h_frag,
+                               int32_t frag_jtiles, void *const *out_ptrs, int out_layout, int out_dtype,
+                               const int32_t *ranks, int32_t n_adapters, const int64_t *seg_offsets,
+                               const int32_t *adapter_ids, int32_t n_segments, void *workspace,
+                               int64_t workspace_bytes, void *stream) {
+  OuterArgs a{};
+  OuterPlan pl;
+  int st = outer_setup(a, pl, M, C, ranks, n_adapters, seg_offsets, adapter_ids, n_segments);
+  if (st) return st;
+  return seg_outer_run(a, pl, p, ldp, M, C, h_frag, frag_jtiles, out_ptrs, out_layout, out_dtype, n_adapters,
+                       workspace, workspace_bytes, static_cast<hipStream_t>(stream));
+}
+
+// ---------------------------------------------------------------- seg_outer without allocation
+//
+// The partial sums of mlora_seg_outer_noalloc live in this file-scope device array
+// (one instance per GPU, created when the library's code object is loaded on that
+// GPU and held until the process ends). Host code never passes `scratch` itself to a
+// kernel (on the host it is a stand-in symbol, not a device address): its device
+// address is looked up once per device with hipGetSymbolAddress and kept in
+// scratch_address.
+namespace mlora {
+
+static __device__ __align__(256) float scratch[MLORA_NOALLOC_SCRATCH_BYTES / sizeof(float)];
+
+constexpr int kMaxDevices = 64;
+
+// Device address of this GPU's scratch array (the current device), looked up on the
+// first call per device; MLORA_ERR_DEVICE if there is no current device or the lookup fails.
+static int scratch_address(void **out) {
+  static std::mutex mu;
+  static void *table[kMaxDevices] = {};
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return MLORA_ERR_DEVICE;
+  std::lock_guard<std::mutex> lock(mu);
+  if (table[dev] == nullptr) {
+    void *p = nullptr;
+    if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || p == nullptr) return MLORA_ERR_DEVICE;
+    table[dev] = p;
+  }
+  *out = table[dev];
+  return MLORA_OK;
+}
+
+}  // namespace mlora
+
+extern "C" int mlora_seg_outer_noalloc(const void *p, int64_t ldp, int64_t M, int64_t C, const void *h_frag,
+                                       int32_t frag_jtiles, void *const *out_ptrs, int out_layout, int out_dtype,
+                                       const int32_t *ranks, int32_t n_adapters, const int64_t *seg_offsets,
+                                       const int32_t *adapter_ids, int32_t n_segments, void *stream) {
+  OuterArgs a{};
+  OuterPlan pl;
+  int st = outer_setup(a, pl, M, C, ranks, n_adapters, seg_offsets, adapter_ids, n_segments);
+  if (st) return st;
+  if (out_layout != 0 && out_layout != 1) return MLORA_ERR_INVALID;
+  if (out_dtype != MLORA_F32 && out_dtype != MLORA_BF16) return MLORA_ERR_UNSUPPORTED;
+  if (n_adapters > 0 && out_ptrs == nullptr) return MLORA_ERR_INVALID;
+  if (C == 0 || n_adapters == 0) return MLORA_OK;
+  // mlora_seg_outer's plan (so the result is the same bit for bit) if its partial sums fit
+  const int64_t need = (int64_t)pl.n_chunks * C * pl.rpad * (int64_t)sizeof(float);
+  if (need > (int64_t)MLORA_NOALLOC_SCRATCH_BYTES) return MLORA_ERR_LIMIT;
+  void *ws = nullptr;
+  if ((st = scratch_address(&ws))) return st;
+  return seg_outer_run(a, pl, p, ldp, M, C, h_frag, frag_jtiles, out_ptrs, out_layout, out_dtype, n_adapters, ws,
+                       MLORA_NOALLOC_SCRATCH_BYTES, static_cast<hipStream_t>(stream));
+}
+
 extern "C" int mlora_abi_version(void) { return MLORA_ABI_VERSION; }
 
 #ifndef MLORA_SOURCE_HASH
@@ -784,6 +850,7 @@ extern "C" const char *mlora_status_string(int status) {
     case MLORA_ERR_WORKSPACE: return "workspace missing or too small";
     case MLORA_ERR_LAUNCH: return "kernel launch failed";
     case MLORA_ERR_LIMIT: return "segment/adapter/rank limit of one call exceeded";
+    case MLORA_ERR_DEVICE: return "no current device, or the device set-up of the library failed";
     default: return "unknown status";
   }
 }

@@ -63,7 +63,8 @@ typedef enum mlora_status {
   MLORA_ERR_UNSUPPORTED = -2, /* dtype/alignment combination not implemented */
   MLORA_ERR_WORKSPACE = -3,   /* workspace missing or too small */
   MLORA_ERR_LAUNCH = -4,      /* hipLaunchKernel reported an error */
-  MLORA_ERR_LIMIT = -5        /* more segments/adapters/rank than one call takes */
+  MLORA_ERR_LIMIT = -5,       /* more segments/adapters/rank than one call takes */
+  MLORA_ERR_DEVICE = -6       /* no current device, or the library's device set-up failed */
 } mlora_status;
 
 /* Segment routing shared by all entry points (host arrays).
@@ -204,6 +205,28 @@ int64_t mlora_seg_outer_workspace_bytes(int64_t M, int64_t C,
                                         const int32_t *ranks, int32_t n_adapters,
                                         const int64_t *seg_offsets, const int32_t *adapter_ids,
                                         int32_t n_segments);
+
+/* Bytes of the device array that holds mlora_seg_outer_noalloc's partial sums (per GPU). */
+#define MLORA_NOALLOC_SCRATCH_BYTES (64 << 20)
+
+/* mlora_seg_outer with no workspace argument and no allocation of any kind. It has no
+ * counterpart in the reference: it is for callers that cannot allocate device memory (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc). The
+ * partial sums live in a device array of MLORA_NOALLOC_SCRATCH_BYTES inside this library,
+ * one per GPU, held from the library's first use on that GPU until the process ends; its
+ * address is looked up on the first call on each device (the current device, which must be
+ * the stream's device). It runs mlora_seg_outer's kernels with mlora_seg_outer's plan, so the
+ * results are the same bit for bit; a call whose workspace (mlora_seg_outer_workspace_bytes)
+ * exceeds the array returns MLORA_ERR_LIMIT before any device work (the Wan-1.3B shapes need
+ * ~34 MB). Every call on one GPU uses that GPU's one array and
+ * nothing carries over between calls (each call writes every partial it reads), but calls
+ * that overlap in time on one GPU (different streams, or host threads) race on the array. */
+int mlora_seg_outer_noalloc(const void *p, int64_t ldp, int64_t M, int64_t C,
+                            const void *h_frag, int32_t frag_jtiles,
+                            void *const *out_ptrs, int out_layout, int out_dtype,
+                            const int32_t *ranks, int32_t n_adapters,
+                            const int64_t *seg_offsets, const int32_t *adapter_ids, int32_t n_segments,
+                            void *stream);
 
 /* ---- Quantised frozen base (OCP e4m3 / float8_e4m3fn, per-row fp32 scale).
  * The reference keeps its frozen base in bf16/fp32 (low_rank.py:20, native/models.py:150-156);
