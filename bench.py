@@ -9,7 +9,7 @@ through the drop-in autograd op with inputs resident in HBM.
 Prints one JSON line: metric/value (TFLOP/s of the whole step), the roofline
 of the dominant kernel measured with HIP events, the LoRA kernels' HBM GB/s,
 and a CPU baseline (the reference per-adapter path in fp32 torch on host
-cores, timed on a bounded sample of the same workload).
+cores, at the same shapes and token count).
 
 Other configurations (parity-test cases, measured on request): --config
 tiny | wan22_5b | flux | wan13b_fp8 (frozen base stored e4m3 with a per-output-
@@ -21,6 +21,12 @@ same step as one call per role (this library, and the reference's unfused torch 
 with three separate calls on that input is timed beside it), and --gated-residual to end o
 and ffn.2 in the block's gated residual x + y·gate fused into the GEMM epilogue (the step
 with the residual as torch ops after the linear is timed beside it).
+
+Measurement: `value` is the whole-job throughput of exactly K steps after W warmups (one HIP
+event pair and wall clock around them, the slower of the two); `step_distribution` times
+max(50, K) further steps one by one. Per-kernel rates (roofline, lora_hbm) are the median of
+--kernel-reps launches, each reading one of --rotate input sets after a 512 MB read that evicts
+L2 and the MALL.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--config wan13b] [--fwd-only] [--per-role] [--shared-qkv] [--gated-residual]
 """
@@ -44,12 +50,21 @@ MFMA_FP8_PEAK_TFLOPS = 5000.0   # dense fp8
 def parse():
     p = argparse.ArgumentParser()
     p.add_argument("--gpus", type=int, default=1)
-    p.add_argument("--steps", type=int, default=10)
-    p.add_argument("--warmup", type=int, default=3)
+    p.add_argument("--steps", type=int, default=50)
+    p.add_argument("--warmup", type=int, default=10)
     p.add_argument("--config", default="wan13b")
     p.add_argument("--fwd-only", action="store_true", help="time forward passes only (no autograd)")
-    p.add_argument("--kernel-reps", type=int, default=10)
-    p.add_argument("--cpu-seconds", type=float, default=12.0, help="bounded CPU-baseline sample budget")
+    p.add_argument("--kernel-reps", type=int, default=50,
+                   help="timed launches per kernel and linear (median reported); each launch reads one of "
+                        "--rotate input sets and follows a cache scrub")
+    p.add_argument("--rotate", type=int, default=3, help="input sets cycled by the per-kernel timing")
+    p.add_argument("--scrub-mb", type=int, default=512,
+                   help="MB read between timed kernel launches (evicts L2 and the 256 MB MALL)")
+    p.add_argument("--median-steps", type=int, default=50,
+                   help="extra steps timed one by one (per-step HIP events) for the step median")
+    p.add_argument("--cpu-reps", type=int, default=3, help="timed reps (median) per linear of the CPU baseline")
+    p.add_argument("--cpu-tokens", type=int, default=0,
+                   help="tokens of the CPU baseline (0: the configuration's full token count)")
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--shared-qkv", action="store_true",
                    help="q, k, v read one input (as in a DiT block) and run as one stacked call; the same "
@@ -211,7 +226,25 @@ def main():
     flops_fn = cfg.flops_fwd if args.fwd_only else cfg.flops_fwd_bwd
     flops_step = sum(flops_fn(L["K"], L["N"]) for L in lins)
     tflops = flops_step / (ms_per_step * 1e-3) / 1e12
+    peak_mem = torch.cuda.max_memory_allocated(dev)
     print(f"# step {ms_per_step:.3f} ms, {tflops:.1f} TFLOP/s", file=sys.stderr, flush=True)
+
+    # ---------------- per-step distribution: steps timed one by one with HIP events on the
+    # launch stream. One step cycles through the six linears' own tensors (~2.5 GB of distinct
+    # inputs and outputs), so no step finds the previous use of its operands in the 256 MB MALL.
+    n_med = max(args.median_steps, args.steps)
+    launch_stream = torch.cuda.current_stream(dev)
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(n_med)]
+    for e0, e1 in evs:
+        e0.record(launch_stream)
+        step()
+        e1.record(launch_stream)
+    torch.cuda.synchronize()
+    step_ms = sorted(e0.elapsed_time(e1) for e0, e1 in evs)
+    q = lambda f: step_ms[min(len(step_ms) - 1, int(f * len(step_ms)))]  # noqa: E731
+    step_stats = {"steps": n_med, "median_ms": round(q(0.5), 4), "p10_ms": round(q(0.1), 4),
+                  "p90_ms": round(q(0.9), 4), "median_tflops": round(flops_step / (q(0.5) * 1e-3) / 1e12, 2)}
+    print(f"# step median {q(0.5):.3f} ms over {n_med}", file=sys.stderr, flush=True)
     def timed_variant(**kw):
         for _ in range(args.warmup):
             step(**kw)
@@ -228,20 +261,31 @@ def main():
     # the same step, the gated residual as torch ops after the linear
     unfused = timed_variant(fuse=False) if args.gated_residual else None
 
-    # ---------------- per-kernel timing with HIP events on the launch stream
+    # ---------------- per-kernel timing: HIP events on the launch stream around each launch,
+    # every launch reading one of `rotate` input sets (distinct tensors of the linear's shape)
+    # and preceded by a read of `scrub_mb` MB (untimed) that evicts L2 and the 256 MB MALL, so
+    # a kernel's operands come from HBM as in a real step; the median launch is reported.
     reps = args.kernel_reps
     stream = torch.cuda.current_stream(dev)
+    scrub_buf = torch.ones(args.scrub_mb << 18, dtype=torch.float32, device=dev)
 
-    def timed(fn):
-        fn()
+    def timed(fns):
+        """Median seconds per launch of fns[i % len(fns)]() over `reps` launches. The scrub
+        reads (does not write) its buffer, so no dirty lines are left for the timed kernel
+        to write back."""
+        fns[0]()
         torch.cuda.synchronize()
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record(stream)
-        for _ in range(reps):
-            fn()
-        e1.record(stream)
+        pairs = []
+        for i in range(reps):
+            scrub_buf.amax()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(stream)
+            fns[i % len(fns)]()
+            e1.record(stream)
+            pairs.append((e0, e1))
         torch.cuda.synchronize()
-        return e0.elapsed_time(e1) / reps * 1e-3  # seconds per launch
+        ms = sorted(a.elapsed_time(b) for a, b in pairs)
+        return ms[len(ms) // 2] * 1e-3
 
     from dmd_system_amd.function import _as_operand
     seg = list(zip(cfg.seg_lengths, cfg.seg_adapters))
@@ -250,52 +294,65 @@ def main():
     if fp8:
         fams += ["quantize_x", "quantize_dy"]
     fam = {k: {"time": 0.0, "flops": 0, "bytes": 0, "launches": 0} for k in fams}
+    gen = torch.Generator(device=dev)
     with torch.no_grad():
-        for L in lins:
+        for li, L in enumerate(lins):
             M, K, N = cfg.tokens, L["K"], L["N"]
             A_ops = [_as_operand(a) for a in L["As"]]
             B_ops = [_as_operand(v) for v in L["Bs"]]
-            x, dy = L["x"].detach(), L["dy"]
-            h_rows, h_frag = kernels.shrink(x, A_ops, 0, scales, routing, True, R)
-            g_rows, g_frag = kernels.shrink(dy, B_ops, 1, scales, routing, True, R)
             A_t = [a.t().contiguous() for a in A_ops]  # the NT form of dX contracts g with A_aᵀ
+            sets = []
+            for r in range(max(1, args.rotate)):
+                if r == 0:
+                    x, dy = L["x"].detach(), L["dy"]
+                else:
+                    gen.manual_seed(1000 * li + r)
+                    x = torch.randn(M, K, generator=gen, device=dev).to(torch.bfloat16)
+                    dy = torch.randn(M, N, generator=gen, device=dev).to(torch.bfloat16)
+                h_rows, h_frag = kernels.shrink(x, A_ops, 0, scales, routing, True, R)
+                g_rows, g_frag = kernels.shrink(dy, B_ops, 1, scales, routing, True, R)
+                S = dict(x=x, dy=dy, h_rows=h_rows, h_frag=h_frag, g_rows=g_rows, g_frag=g_frag)
+                if fp8:
+                    S["xq"], S["xs"] = kernels.quantize_rows_fp8(x)
+                    S["dyq"], S["dys"] = kernels.quantize_rows_fp8(dy, col_scale=L["ws"])
+                    S["g_div"], _ = kernels.shrink(dy, B_ops, 1, scales, routing, False, R, row_div=S["dys"])
+                sets.append(S)
             lora_mr = sum(m * cfg.ranks[a] for m, a in seg if a >= 0)
             r_sum = sum(cfg.ranks)
+            bf = [torch.bfloat16] * len(cfg.ranks)
             runs = {
-                "gemm_fwd": (lambda: kernels.gemm_fwd(x, L["w"], L["b"], h_rows, B_ops, routing),
-                             2 * M * K * N + 2 * lora_mr * N, 0),
-                "gemm_dx": (lambda: kernels.gemm_fwd(dy, L["wt"], None, g_rows, A_t, routing),
-                            2 * M * K * N + 2 * lora_mr * K, 0),
-                "shrink_x": (lambda: kernels.shrink(x, A_ops, 0, scales, routing, True, R),
+                "gemm_fwd": ([lambda S=S: kernels.gemm_fwd(S["x"], L["w"], L["b"], S["h_rows"], B_ops, routing)
+                              for S in sets], 2 * M * K * N + 2 * lora_mr * N, 0),
+                "gemm_dx": ([lambda S=S: kernels.gemm_fwd(S["dy"], L["wt"], None, S["g_rows"], A_t, routing)
+                             for S in sets], 2 * M * K * N + 2 * lora_mr * K, 0),
+                "shrink_x": ([lambda S=S: kernels.shrink(S["x"], A_ops, 0, scales, routing, True, R) for S in sets],
                              2 * lora_mr * K, M * K * 2 + r_sum * K * 2 + lora_mr * (2 + 4)),
-                "shrink_dy": (lambda: kernels.shrink(dy, B_ops, 1, scales, routing, True, R),
+                "shrink_dy": ([lambda S=S: kernels.shrink(S["dy"], B_ops, 1, scales, routing, True, R) for S in sets],
                               2 * lora_mr * N, M * N * 2 + r_sum * N * 2 + lora_mr * (2 + 4)),
-                "seg_outer_dB": (lambda: kernels.seg_outer(dy, h_frag, R, cfg.ranks, routing, 0,
-                                                           [torch.bfloat16] * len(cfg.ranks)),
-                                 2 * lora_mr * N, M * N * 2 + lora_mr * 4 + r_sum * N * 2),
-                "seg_outer_dA": (lambda: kernels.seg_outer(x, g_frag, R, cfg.ranks, routing, 1,
-                                                           [torch.bfloat16] * len(cfg.ranks)),
-                                 2 * lora_mr * K, M * K * 2 + lora_mr * 4 + r_sum * K * 2),
+                "seg_outer_dB": ([lambda S=S: kernels.seg_outer(S["dy"], S["h_frag"], R, cfg.ranks, routing, 0, bf)
+                                  for S in sets], 2 * lora_mr * N, M * N * 2 + lora_mr * 4 + r_sum * N * 2),
+                "seg_outer_dA": ([lambda S=S: kernels.seg_outer(S["x"], S["g_frag"], R, cfg.ranks, routing, 1, bf)
+                                  for S in sets], 2 * lora_mr * K, M * K * 2 + lora_mr * 4 + r_sum * K * 2),
             }
             if fp8:
-                xq, xs = kernels.quantize_rows_fp8(x)
-                runs["gemm_fwd"] = (lambda: kernels.gemm_fwd_fp8(xq, xs, L["wq"], L["ws"], L["b"], h_rows, B_ops,
-                                                                 routing), 2 * M * K * N + 2 * lora_mr * N, 0)
-                dyq, dys = kernels.quantize_rows_fp8(dy, col_scale=L["ws"])
-                g_div, _ = kernels.shrink(dy, B_ops, 1, scales, routing, False, R, row_div=dys)
-                a_t = [a.t().contiguous() for a in A_ops]
-                runs["gemm_dx"] = (lambda: kernels.gemm_fwd_fp8(dyq, dys, L["wqt"], None, None, g_div, a_t, routing),
+                runs["gemm_fwd"] = ([lambda S=S: kernels.gemm_fwd_fp8(S["xq"], S["xs"], L["wq"], L["ws"], L["b"],
+                                                                      S["h_rows"], B_ops, routing) for S in sets],
+                                    2 * M * K * N + 2 * lora_mr * N, 0)
+                runs["gemm_dx"] = ([lambda S=S: kernels.gemm_fwd_fp8(S["dyq"], S["dys"], L["wqt"], None, None,
+                                                                     S["g_div"], A_t, routing) for S in sets],
                                    2 * M * K * N + 2 * lora_mr * K, 0)
-                runs["quantize_x"] = (lambda: kernels.quantize_rows_fp8(x), 0, M * K * 3 + M * 4)
-                runs["quantize_dy"] = (lambda: kernels.quantize_rows_fp8(dy, col_scale=L["ws"]), 0,
-                                       M * N * 3 + M * 4 + N * 4)
-            for k, (fn, fl, by) in runs.items():
-                t = timed(fn)
+                runs["quantize_x"] = ([lambda S=S: kernels.quantize_rows_fp8(S["x"]) for S in sets], 0,
+                                      M * K * 3 + M * 4)
+                runs["quantize_dy"] = ([lambda S=S: kernels.quantize_rows_fp8(S["dy"], col_scale=L["ws"])
+                                        for S in sets], 0, M * N * 3 + M * 4 + N * 4)
+            for k, (fns, fl, by) in runs.items():
+                t = timed(fns)
                 fam[k]["time"] += t
                 fam[k]["flops"] += fl
                 fam[k]["bytes"] += by
                 fam[k]["launches"] += 1
-            del h_rows, h_frag, g_rows, g_frag
+            del sets
+    del scrub_buf
     kern = {}
     for k, v in fam.items():
         avg = v["time"] / v["launches"]
@@ -307,7 +364,7 @@ def main():
     gem_peak = MFMA_FP8_PEAK_TFLOPS if fp8 else MFMA_BF16_PEAK_TFLOPS
     roofline = {"kernel": ("gemm_kernel NT e4m3 base (fp8 MFMA) + fused dequantise and bf16 LoRA expand"
                            if fp8 else "gemm_kernel NT (base GEMM + fused LoRA expand)")
-                + ", avg over the 6 block linears",
+                + ", over the 6 block linears (median launch of each, cold caches)",
                 "bound": "mfma", "achieved": round(gem_ach, 1), "peak": gem_peak, "unit": "TFLOP/s",
                 "frac": round(gem_ach / gem_peak, 4),
                 "traffic": recorded_traffic() if cfg.name == "wan13b" else None,
@@ -322,18 +379,20 @@ def main():
 
     # ---------------- vendor GEMM reference (context only): torch bf16 matmul, same shapes
     vendor = {}
+    scrub_buf = torch.ones(args.scrub_mb << 18, dtype=torch.float32, device=dev)
     with torch.no_grad():
         for L in lins[3:6]:
             x = L["x"].detach()
-            t = timed(lambda: torch.matmul(x, L["w"].T))
+            t = timed([lambda: torch.matmul(x, L["w"].T)])
             vendor[f"{L['name']} {L['K']}->{L['N']}"] = round(2 * cfg.tokens * L["K"] * L["N"] / t / 1e12, 1)
+    del scrub_buf
 
     per_role = per_role_timing(pkg, cfg, lins, scales, args, flops_step) if args.per_role else None
 
     # ---------------- CPU baseline: reference per-adapter path, fp32 torch, bounded sample
     cpu = None
     if not args.no_cpu_baseline:
-        cpu = cpu_baseline(cfg, args.cpu_seconds, args.fwd_only)
+        cpu = cpu_baseline(cfg, args.cpu_reps, args.cpu_tokens, args.fwd_only)
 
     pass_name = "fwd" if args.fwd_only else "fwd+bwd"
     shape_name = "Wan-1.3B shape" if cfg.name == "wan13b" else f"{cfg.name} shape"
@@ -345,6 +404,8 @@ def main():
         "steps": args.steps,
         "warmup": args.warmup,
         "ms_per_step": round(ms_per_step, 4),
+        "step_distribution": step_stats,
+        "peak_mem_gb": round(peak_mem / 1e9, 3),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -428,50 +489,59 @@ def per_role_timing(pkg, cfg, lins, scales, args, flops_step):
     return out
 
 
-def cpu_baseline(cfg, budget_s: float, fwd_only: bool = False):
-    """Reference per-adapter path (training/low_rank.py:26-28 per segment + autograd) in fp32 on host cores
-    (an e4m3 base is evaluated as its fp32 dequantisation: the reference has no fp8 path)."""
+def cpu_baseline(cfg, reps: int, tokens: int = 0, fwd_only: bool = False):
+    """Reference per-adapter path (training/low_rank.py:26-28 per segment + autograd) in fp32 on host
+    cores, at the configuration's shapes (all its tokens unless `tokens` is given, split over the
+    segments in proportion): each distinct linear shape timed (1 warmup + median of `reps`), the
+    block time the sum over the six linears. An e4m3 base is evaluated as its fp32 dequantisation
+    (the reference has no fp8 path)."""
     import torch
     from oracle import torch_reference as TR
     from dmd_system_amd import workloads
 
-    rows_per_seg = max(128, 2048 // len(cfg.seg_lengths))
+    full = tokens <= 0 or tokens >= cfg.tokens
+    if full:
+        lengths = cfg.seg_lengths
+    else:
+        lengths = tuple(max(1, round(m * tokens / cfg.tokens)) for m in cfg.seg_lengths)
     sample = workloads.LoraConfig(
-        name="cpu-sample", tokens=rows_per_seg * len(cfg.seg_lengths), hidden=cfg.hidden, ffn=cfg.ffn,
-        ranks=cfg.ranks, seg_lengths=(rows_per_seg,) * len(cfg.seg_lengths), seg_adapters=cfg.seg_adapters,
-        scale=cfg.scale, seed=cfg.seed)
+        name="cpu-sample", tokens=sum(lengths), hidden=cfg.hidden, ffn=cfg.ffn, ranks=cfg.ranks, seg_lengths=lengths,
+        seg_adapters=cfg.seg_adapters, scale=cfg.scale, seed=cfg.seed)
     cpu = torch.device("cpu")
-    lin = []
-    for i, (name, K, N) in enumerate(sample.linears()):
-        x, w, b, As, Bs, dy = workloads.make_linear(sample, K, N, cpu, seed=7 + i, dtype=torch.float32)
-        lin.append((K, N, x, w, b, As, Bs, dy))
-    off = sample.routing.seg_offsets
-    ids = sample.routing.adapter_ids
+    off, ids = sample.routing.seg_offsets, sample.routing.adapter_ids
     scales = [cfg.scale] * len(cfg.ranks)
+    per_shape = {}
+    t_all = time.perf_counter()
+    for i, (name, K, N) in enumerate(sample.linears()):
+        if (K, N) in per_shape:
+            continue
+        x, w, b, As, Bs, dy = workloads.make_linear(sample, K, N, cpu, seed=7 + i, dtype=torch.float32)
 
-    def one_block():
-        for K, N, x, w, b, As, Bs, dy in lin:
+        def once():
             if fwd_only:
                 with torch.no_grad():
                     TR.per_adapter_forward(x, w, b, As, Bs, scales, off, ids)
             else:
                 TR.per_adapter_step(x, w, b, As, Bs, scales, off, ids, dy)
 
-    one_block()  # warmup
-    t0 = time.perf_counter()
-    reps = 0
-    while True:
-        one_block()
-        reps += 1
-        el = time.perf_counter() - t0
-        if el >= budget_s or reps >= 50:
-            break
+        once()  # warmup
+        ts = []
+        for _ in range(max(1, reps)):
+            t0 = time.perf_counter()
+            once()
+            ts.append(time.perf_counter() - t0)
+        per_shape[(K, N)] = sorted(ts)[len(ts) // 2]
+        del x, w, b, As, Bs, dy
+    block_s = sum(per_shape[(K, N)] for _, K, N in sample.linears())
     flops = sum((sample.flops_fwd if fwd_only else sample.flops_fwd_bwd)(K, N) for _, K, N in sample.linears())
-    return {"value": round(flops * reps / el / 1e12, 4), "unit": "TFLOP/s", "cores": torch.get_num_threads(),
+    shapes = ", ".join(f"{K}->{N} {t * 1e3:.0f} ms" for (K, N), t in per_shape.items())
+    return {"value": round(flops / block_s / 1e12, 4), "unit": "TFLOP/s", "cores": torch.get_num_threads(),
             "kind": "port",
-            "sample": f"{reps} x {'fwd' if fwd_only else 'fwd+bwd'} of the 6 block linears at {sample.tokens} tokens "
-                      f"({rows_per_seg} per segment), fp32 torch per-adapter path, {el:.1f} s; "
-                      f"host os.cpu_count()={os.cpu_count()}"}
+            "sample": f"{'fwd' if fwd_only else 'fwd+bwd'} of the 6 block linears at {sample.tokens} tokens "
+                      f"({'the full configuration' if full else 'scaled-down token count'}, segments "
+                      f"{list(lengths)}), fp32 torch per-adapter path; median of {max(1, reps)} after 1 warmup per "
+                      f"linear shape ({shapes}); block {block_s * 1e3:.0f} ms; "
+                      f"{time.perf_counter() - t_all:.1f} s of CPU work; host os.cpu_count()={os.cpu_count()}"}
 
 
 if __name__ == "__main__":
