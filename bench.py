@@ -19,8 +19,9 @@ adapter, in one call), --fwd-only for a forward-only step, --per-role to time th
 same step as one call per role (this library, and the reference's unfused torch path),
 --shared-qkv to feed q, k, v one input and run them as one stacked call (the step
 with three separate calls on that input is timed beside it), and --gated-residual to end o
-and ffn.2 in the block's gated residual x + y·gate fused into the GEMM epilogue (the step
-with the residual as torch ops after the linear is timed beside it).
+and ffn.2 in the block's gated residual x + y·gate on the float32 residual stream, fused
+into the GEMM epilogue (the step with the residual as torch ops after the linear is timed
+beside it).
 
 Measurement: `value` is the whole-job throughput of exactly K steps after W warmups (one HIP
 event pair and wall clock around them, the slower of the two); `step_distribution` times
@@ -170,7 +171,8 @@ def main():
         gen.manual_seed(99)
         for L in lins:
             if L["name"] in ("o", "ffn.2"):
-                L["res"] = torch.randn(cfg.tokens, L["N"], generator=gen, device=dev).to(torch.bfloat16)
+                # the Wan block's residual stream is float32 (model.py:305-306,312-313)
+                L["res"] = torch.randn(cfg.tokens, L["N"], generator=gen, device=dev)
                 L["res"].requires_grad_(not args.fwd_only)
                 # one gate row per role segment, as Wan's per-sample e[2] / e[5]
                 L["gate"] = torch.rand(len(cfg.seg_lengths), L["N"], generator=gen, device=dev) + 0.5
@@ -180,7 +182,7 @@ def main():
     def unfused_gated(L):
         y = pkg.multi_lora_linear(L["x"], L["w"], L["b"], L["As"], L["Bs"], scales, routing, weight_t=L["wt"])
         g = L["gate"].repeat_interleave(cfg.tokens // L["gate"].shape[0], dim=0)
-        return (L["res"].float() + y.float() * g).to(torch.bfloat16)
+        return L["res"] + y.float() * g
 
     def forward(L, fuse=True):
         if "gate" in L:

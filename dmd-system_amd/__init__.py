@@ -11,6 +11,7 @@ Public API:
     RoleBatch, fuse_roles, roles_active  several roles' forwards in one pass over the shared base
     fuse_shared_inputs, SharedInputGroup, SharedInputMultiLoRAFunction   linears reading one input, stacked
     export_adapters, import_adapters, save_adapters, load_adapters   PEFT / DiffSynth adapter state
+    install_peft_multi_lora, peft_roles_active   PEFT LoRA layers (W1 / H3) on the multi-LoRA op
     kernels                              torch front end of each C-ABI entry point
     load_library()                       load libmlora.so (raises if missing)
 
@@ -27,6 +28,7 @@ from .low_rank import LoRALinear, MultiLoRALinear, TrainableLowRankLinear, insta
 from .roles import RoleBatch, fuse_roles, roles_active
 from .routing import BASE_ONLY, SegmentRouting
 from .shared_input import SharedInputGroup, fuse_shared_inputs, release_shared_inputs
+from .peft_site import install_peft_multi_lora, peft_roles_active, uninstall_peft_multi_lora
 
 
 def load_library():
@@ -40,5 +42,5 @@ __all__ = [
     "TrainableLowRankLinear", "trainable_scope", "RoleBatch", "fuse_roles", "roles_active",
     "SharedInputMultiLoRAFunction", "shared_input_multi_lora", "SharedInputGroup", "fuse_shared_inputs",
     "release_shared_inputs", "export_adapters", "import_adapters", "save_adapters", "load_adapters", "kernels",
-    "load_library",
+    "load_library", "install_peft_multi_lora", "uninstall_peft_multi_lora", "peft_roles_active",
 ]

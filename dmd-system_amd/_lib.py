@@ -41,8 +41,8 @@ SIGNATURES = {
                               _pvp, _pi32, _i32, _pi64, _pi32, _i32, _vp, _i64, _int, _vp]),
     "mlora_gemm_fwd_gated": (_int, [_vp, _i64, _i64, _i64, _vp, _i64, _i64, _vp, _int, _vp, _i64,
                                     _pvp, _pi32, _i32, _pi64, _pi32, _i32, _vp, _i64, _vp, _i64, _i64,
-                                    _vp, _i64, _vp]),
-    "mlora_gate_scale_rows": (_int, [_vp, _i64, _i64, _i64, _vp, _i64, _i64, _vp, _i64, _vp]),
+                                    _vp, _i64, _int, _vp]),
+    "mlora_gate_scale_rows": (_int, [_vp, _i64, _i64, _i64, _vp, _i64, _i64, _vp, _i64, _int, _vp]),
     "mlora_gemm_dx": (_int, [_vp, _i64, _i64, _i64, _vp, _i64, _i64, _vp, _i64,
                              _pvp, _pi32, _i32, _pi64, _pi32, _i32, _vp, _i64, _int, _vp]),
     "mlora_seg_outer": (_int, [_vp, _i64, _i64, _i64, _vp, _i32, _pvp, _int, _int, _pi32, _i32,

@@ -46,11 +46,14 @@ struct GemmArgs {
   AdapterTable ext;  // NT: B_a [Ncols, r]; NN: A_a [r, Ncols]
   SegTable seg;
   // Gated residual epilogue (gemm_kernel<C, true>): the stored value is
-  // bf16(res[m, n] + bf16(Y[m, n])·gate[m / gate_rows, n]) instead of Y.
-  const uint16_t *res;
+  // bf16(res[m, n] + bf16(Y[m, n])·gate[m / gate_rows, n]) instead of Y; with res_f32 the
+  // residual stream is float32: Yf[m, n] = res[m, n] + bf16(Y[m, n])·gate (fp32 out).
+  const void *res;
   const float *gate;
+  float *Yf;
   int64_t ldres, ldgate;
   int32_t gate_rows;
+  int32_t res_f32;
 };
 
 template <int BM_, int BN_, int WM_, int WN_, bool NN_, bool F8_ = false, int KB_ = 128, int STAGES_ = 2,
@@ -758,19 +761,40 @@ __device__ __forceinline__ void store_tile(const f32x16 (&acc)[C::TM][C::TN], co
       // the 8 bf16 values of d are bf16(Y); x and gate of the same 8 columns
       if (off != kOOB) {
         const int64_t m = m0 + r;
-        const u32x4 xv = *(const MLORA_GLOBAL u32x4 *)(args.res + m * args.ldres + n);
         const MLORA_GLOBAL f32x4 *gp = (const MLORA_GLOBAL f32x4 *)(args.gate + (m / args.gate_rows) * args.ldgate + n);
         const f32x4 g0 = gp[0], g1 = gp[1];
+        float xs[8];
+        if (args.res_f32) {
+          const MLORA_GLOBAL f32x4 *xp = (const MLORA_GLOBAL f32x4 *)((const float *)args.res + m * args.ldres + n);
+          const f32x4 x0 = xp[0], x1 = xp[1];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) xs[e] = x0[e], xs[e + 4] = x1[e];
+        } else {
+          const u32x4 xv = *(const MLORA_GLOBAL u32x4 *)((const uint16_t *)args.res + m * args.ldres + n);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            const uint32_t xw = xv[e / 2];
+            xs[e] = bf16_to_f32((uint16_t)(e % 2 ? xw >> 16 : xw & 0xffff));
+          }
+        }
         float o[8];
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
-          const uint32_t yw = d[e / 2], xw = xv[e / 2];
+          const uint32_t yw = d[e / 2];
           const float y = bf16_to_f32((uint16_t)(e % 2 ? yw >> 16 : yw & 0xffff));
-          const float x = bf16_to_f32((uint16_t)(e % 2 ? xw >> 16 : xw & 0xffff));
-          o[e] = gated_add(x, y, e < 4 ? g0[e] : g1[e - 4]);
+          o[e] = gated_add(xs[e], y, e < 4 ? g0[e] : g1[e - 4]);
+        }
+        if (args.res_f32) {
+          // float32 stream: no bf16 rounding of the sum; 32 bytes per lane
+          MLORA_GLOBAL f32x4 *op = (MLORA_GLOBAL f32x4 *)(args.Yf + m * args.ldy + n);
+          op[0] = f32x4{o[0], o[1], o[2], o[3]};
+          op[1] = f32x4{o[4], o[5], o[6], o[7]};
+          continue;
         }
 #pragma unroll
         for (int e = 0; e < 4; ++e) d[e] = pack2_bf16(o[2 * e], o[2 * e + 1]);
+      } else if (args.res_f32) {
+        continue;
       }
     }
     buf_store16(ry, off, d);
@@ -903,14 +927,24 @@ extern "C" int mlora_gemm_fwd_gated(const void *x, int64_t ldx, int64_t M, int64
                                     const void *const *b_ptrs, const int32_t *ranks, int32_t n_adapters,
                                     const int64_t *seg_offsets, const int32_t *adapter_ids, int32_t n_segments,
                                     const void *res, int64_t ldres, const float *gate, int64_t ldgate,
-                                    int64_t gate_rows, void *out, int64_t ldout, void *stream) {
+                                    int64_t gate_rows, void *out, int64_t ldout, int stream_dtype, void *stream) {
   GemmArgs a{};
   int st = fill_common(a, M, K, N, h_rows, ldh, b_ptrs, ranks, n_adapters, seg_offsets, adapter_ids, n_segments);
   if (st) return st;
+  if (stream_dtype != MLORA_BF16 && stream_dtype != MLORA_F32) return MLORA_ERR_UNSUPPORTED;
+  const bool f32 = stream_dtype == MLORA_F32;
   if ((st = check_bf16_matrix(x, ldx, M, K))) return st;
   if ((st = check_bf16_matrix(w, ldw, N, K))) return st;
-  if ((st = check_bf16_matrix(res, ldres, M, N))) return st;
-  if ((st = check_bf16_matrix(out, ldout, M, N))) return st;
+  // the residual stream (res, out): bf16, or float32 rows of 16-byte chunks
+  auto check_stream = [&](const void *p, int64_t ld) {
+    if (!f32) return check_bf16_matrix(p, ld, M, N);
+    if (M == 0 || N == 0) return (int)MLORA_OK;
+    if (p == nullptr || ld < N) return (int)MLORA_ERR_INVALID;
+    if (!aligned16(p) || ld % 4 != 0 || N % 8 != 0) return (int)MLORA_ERR_UNSUPPORTED;
+    return (int)MLORA_OK;
+  };
+  if ((st = check_stream(res, ldres))) return st;
+  if ((st = check_stream(out, ldout))) return st;
   if (M == 0 || N == 0) return MLORA_OK;
   if (out == nullptr || res == nullptr || gate == nullptr || gate_rows < 1 || gate_rows > INT32_MAX)
     return MLORA_ERR_INVALID;
@@ -919,20 +953,26 @@ extern "C" int mlora_gemm_fwd_gated(const void *x, int64_t ldx, int64_t M, int64
     if (bias_dtype != MLORA_F32 && bias_dtype != MLORA_BF16) return MLORA_ERR_UNSUPPORTED;
     if (!aligned16(bias)) return MLORA_ERR_UNSUPPORTED;
   }
-  if (!offsets_fit(ldx, 256) || !offsets_fit(ldout, 256) || !offsets_fit(ldw, 256)) return MLORA_ERR_LIMIT;
+  // byte offsets of one tile's rows stay 31-bit (fp32 rows are twice as wide)
+  if (!offsets_fit(ldx, 256) || !offsets_fit(ldout * (f32 ? 2 : 1), 256) || !offsets_fit(ldw, 256))
+    return MLORA_ERR_LIMIT;
   a.P = static_cast<const uint16_t *>(x);
   a.Q = static_cast<const uint16_t *>(w);
   a.ldp = ldx;
   a.ldq = ldw;
   a.bias = bias;
   a.bias_dtype = bias ? bias_dtype : -1;
+  // bf16 stream: Y is the output; float32 stream: the bf16 Y resource covers the same rows
+  // (its offsets only gate which lanes store) and the values go to Yf
   a.Y = static_cast<uint16_t *>(out);
   a.ldy = ldout;
-  a.res = static_cast<const uint16_t *>(res);
+  a.Yf = f32 ? static_cast<float *>(out) : nullptr;
+  a.res = res;
   a.ldres = ldres;
   a.gate = gate;
   a.ldgate = ldgate;
   a.gate_rows = (int32_t)gate_rows;
+  a.res_f32 = f32 ? 1 : 0;
   return dispatch_gemm<CfgNT256, CfgNT128, true>(a, static_cast<hipStream_t>(stream));
 }
 

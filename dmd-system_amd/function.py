@@ -235,13 +235,14 @@ class MultiLoRAGatedResidualFunction(torch.autograd.Function):
     """``apply(x, weight, weight_t, bias, routing, scales, residual, gate, *lora_as, *lora_bs)``: the linear
     that closes a DiT block branch, with the block's gated residual fused into its epilogue:
 
-        out = bf16(residual + bf16(Y)·gate[row group]),   Y = the multi-LoRA linear of x
+        out = residual + bf16(Y)·gate[row group],   Y = the multi-LoRA linear of x
 
     (reference/livewan_wan21/wan/modules/model.py:305-313, rounding as
-    runtime/helios_residual_kernel.py:66-86). residual [M, N] bf16, gate [G, N] fp32 frozen
-    (M / G consecutive rows per gate row: the tokens of one sample). Backward (frozen gate,
-    helios_residual_kernel.py:90-133): d residual = dOut; dY = bf16(dOut·gate), then the
-    linear's own backward.
+    runtime/helios_residual_kernel.py:66-86: fp32 multiply, fp32 add), in the residual
+    stream's dtype: bf16 (the sum rounded to bf16) or float32 (the Wan block's stream, not
+    rounded). residual [M, N], gate [G, N] fp32 frozen (M / G consecutive rows per gate row:
+    the tokens of one sample). Backward (frozen gate, helios_residual_kernel.py:90-133):
+    d residual = dOut; dY = bf16(dOut·gate), then the linear's own backward.
     """
 
     @staticmethod
@@ -261,7 +262,7 @@ class MultiLoRAGatedResidualFunction(torch.autograd.Function):
     def backward(ctx, dout):
         n = ctx.n
         (x, weight, weight_t, gate, *ops), h_frag = _saved(ctx)
-        dout = dout.to(torch.bfloat16).contiguous()
+        dout = dout.contiguous()
         dy = kernels.gate_scale_rows(dout, gate)
         dx_gemm = _dx_gemm(dy, weight, weight_t if ctx.has_wt else None, ops[:n], ctx.routing)
         dx, dAs, dBs = _backward(ctx, dy, x, dx_gemm, ops[:n], ops[n:], h_frag)
@@ -489,14 +490,15 @@ def multi_lora_linear_gated(x: torch.Tensor, weight: torch.Tensor, bias: torch.T
                             scales: Sequence[float], routing: SegmentRouting, residual: torch.Tensor,
                             gate: torch.Tensor, weight_t: torch.Tensor | None = None) -> torch.Tensor:
     """residual + linear(x)·gate, fused (MultiLoRAGatedResidualFunction). x [..., K]; residual
-    [..., N] bf16 with x's leading shape; gate fp32 [B, 1, N] (one row per sample of a [B, L, ...]
-    batch), [B, L, N] (per token) or [G, N]. Returns [..., N] bf16."""
+    [..., N] bf16 or float32 (the Wan block's stream) with x's leading shape; gate fp32 [B, 1, N]
+    (one row per sample of a [B, L, ...] batch), [B, L, N] (per token) or [G, N]. Returns
+    [..., N] in the residual's dtype."""
     K, N = x.shape[-1], weight.shape[0]
     lead = x.shape[:-1]
     x2 = _bf16_rows(x, weight.dtype)
     weight = weight.to(torch.bfloat16)
-    if residual.dtype != torch.bfloat16 or residual.shape != (*lead, N):
-        raise RuntimeError("gated residual: the residual stream must be bf16 with the output's shape")
+    if residual.dtype not in (torch.bfloat16, torch.float32) or residual.shape != (*lead, N):
+        raise RuntimeError("gated residual: the residual stream must be bf16 or float32 with the output's shape")
     if gate.dtype != torch.float32 or gate.shape[-1] != N:
         raise RuntimeError("gated residual: the gate must be float32 with out_features columns")
     g2 = gate.reshape(-1, N)

@@ -168,16 +168,24 @@ def _gate_rows(gate: torch.Tensor, M: int, N: int) -> int:
     return M // G
 
 
+def _check_stream(name: str, t: torch.Tensor, cols: int) -> None:
+    """A residual-stream matrix: bf16 rows, or float32 rows of 16-byte chunks."""
+    _require(t.is_cuda, f"{name} must be a ROCm device tensor")
+    _require(t.dtype in (torch.bfloat16, torch.float32), f"{name} must be bfloat16 or float32, got {t.dtype}")
+    _require(t.dim() == 2 and t.stride(1) == 1 and t.shape[1] == cols, f"{name} must be a row-major [M, {cols}] matrix")
+
+
 def gemm_fwd_gated(x: torch.Tensor, w: torch.Tensor, bias: torch.Tensor | None, h_rows: torch.Tensor | None,
                    bs: Sequence[torch.Tensor], routing: SegmentRouting, res: torch.Tensor, gate: torch.Tensor,
                    out: torch.Tensor | None = None) -> torch.Tensor:
-    """out = bf16(res + bf16(X·Wᵀ + bias + h_rows·B_aᵀ)·gate[row group]) (the block's gated residual;
-    gate [G, N] fp32, M / G consecutive rows per gate row). out may be res (in place)."""
+    """out = res + bf16(X·Wᵀ + bias + h_rows·B_aᵀ)·gate[row group] (the block's gated residual; gate
+    [G, N] fp32, M / G consecutive rows per gate row), in the residual stream's dtype: bf16 (the sum
+    rounded to bf16) or float32 (not rounded). out may be res (in place)."""
     M, K = x.shape
     N = w.shape[0]
     _check_rows("X", x, K)
     _check_rows("W", w, K)
-    _check_rows("residual", res, N)
+    _check_stream("residual", res, N)
     _require(res.shape[0] == M, "residual has the rows of X")
     per = _gate_rows(gate, M, N)
     if bias is not None:
@@ -186,8 +194,9 @@ def gemm_fwd_gated(x: torch.Tensor, w: torch.Tensor, bias: torch.Tensor | None, 
     for b in bs:
         _check_rows("lora_b", b)
         _require(b.is_contiguous() and b.shape[0] == N, "lora_b must be contiguous [N, r]")
-    y = out if out is not None else torch.empty((M, N), dtype=torch.bfloat16, device=x.device)
-    _check_rows("out", y, N)
+    y = out if out is not None else torch.empty((M, N), dtype=res.dtype, device=x.device)
+    _check_stream("out", y, N)
+    _require(y.dtype == res.dtype, "out has the residual stream's dtype")
     lib = _lib.load()
     ptrs, rk = _lib.ptr_array([_ptr(b) for b in bs]), _lib.i32_array(ranks)
     ldh = h_rows.stride(0) if h_rows is not None else 0
@@ -202,20 +211,22 @@ def gemm_fwd_gated(x: torch.Tensor, w: torch.Tensor, bias: torch.Tensor | None, 
             x[r0:r1].data_ptr(), x.stride(0), r1 - r0, K, w.data_ptr(), w.stride(0), N,
             _ptr(bias), _DT[bias.dtype] if bias is not None else 0, hr, ldh,
             ptrs, rk, len(bs), o, i, n, res[r0:r1].data_ptr(), res.stride(0),
-            gate[r0 // per:].data_ptr(), gate.stride(0), per, y[r0:r1].data_ptr(), y.stride(0), stream))
+            gate[r0 // per:].data_ptr(), gate.stride(0), per, y[r0:r1].data_ptr(), y.stride(0), _DT[res.dtype],
+            stream))
     return y
 
 
 def gate_scale_rows(dout: torch.Tensor, gate: torch.Tensor) -> torch.Tensor:
-    """dY = bf16(dOut · gate[row group]): the frozen-gate derivative of the gated residual."""
+    """dY = bf16(dOut · gate[row group]): the frozen-gate derivative of the gated residual
+    (dOut bf16 or float32, the residual stream's dtype)."""
     M, N = dout.shape
-    _check_rows("dOut", dout, N)
+    _check_stream("dOut", dout, N)
     per = _gate_rows(gate, M, N)
     dy = torch.empty((M, N), dtype=torch.bfloat16, device=dout.device)
     lib = _lib.load()
     _lib.check("mlora_gate_scale_rows", lib.mlora_gate_scale_rows(
         dout.data_ptr(), dout.stride(0), M, N, gate.data_ptr(), gate.stride(0), per, dy.data_ptr(), dy.stride(0),
-        _stream(dout)))
+        _DT[dout.dtype], _stream(dout)))
     return dy
 
 

@@ -42,17 +42,15 @@ def _drop_base_t(key: int) -> None:
     _BASE_T.pop(key, None)
 
 
-def _base_t(module: nn.Module, x: torch.Tensor) -> torch.Tensor | None:
-    """The frozen base weight transposed ([in, out] bf16, contiguous), for the NT form of the
-    dX GEMM (3-5% faster than the NN form at the Wan shapes); made on the first forward that
+def transposed_base(w: torch.Tensor, x: torch.Tensor, enabled: bool = True) -> torch.Tensor | None:
+    """The frozen base weight ``w`` transposed ([in, out] bf16, contiguous), for the NT form of
+    the dX GEMM (3-5% faster than the NN form at the Wan shapes); made on the first forward that
     will need dX and remade when the weight changes (storage, in-place version, device). It
-    costs in·out·2 bytes per distinct base weight, shared by every module over that weight;
-    not a buffer, so no state-dict entry. None when no dX will be computed, on the float32
-    path (no bf16 GEMM), or when ``module.transposed_base_for_dx`` is False (then dX runs on
-    the NN kernel and no copy is kept)."""
-    if not (torch.is_grad_enabled() and x.requires_grad) or not getattr(module, 'transposed_base_for_dx', True):
+    costs in·out·2 bytes per distinct base weight, shared by every module over that weight; not
+    a buffer, so no state-dict entry. None when no dX will be computed, on the float32 path (no
+    bf16 GEMM), or when not ``enabled`` (then dX runs on the NN kernel and no copy is kept)."""
+    if not (enabled and torch.is_grad_enabled() and x.requires_grad):
         return None
-    w = module.base.weight
     autocast = torch.is_autocast_enabled("cuda") and torch.get_autocast_dtype("cuda") == torch.bfloat16
     if not autocast and w.dtype != torch.bfloat16:
         return None
@@ -66,6 +64,12 @@ def _base_t(module: nn.Module, x: torch.Tensor) -> torch.Tensor | None:
             entry = (entry[0], key, w.detach().to(torch.bfloat16).t().contiguous())
     _BASE_T[id(w)] = entry
     return entry[2]
+
+
+def _base_t(module: nn.Module, x: torch.Tensor) -> torch.Tensor | None:
+    """transposed_base of ``module.base.weight``; ``module.transposed_base_for_dx = False`` turns
+    the copy off for that module."""
+    return transposed_base(module.base.weight, x, getattr(module, 'transposed_base_for_dx', True))
 
 
 def _init_pair(rank: int, base: nn.Linear, dtype=None) -> tuple[nn.Parameter, nn.Parameter]:

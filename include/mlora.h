@@ -145,9 +145,13 @@ int mlora_gemm_fwd(const void *x, int64_t ldx, int64_t M, int64_t K,
  * closes a branch (attention out-projection, FFN down-projection) whose output y enters
  * the residual stream as x' = x + y·gate (reference/livewan_wan21/wan/modules/model.py:305-313;
  * the exact contract of runtime/helios_residual_kernel.py:66-86):
- *   out[m, n] = bf16( RN( res[m, n] + RN( bf16(Y[m, n]) · gate[m / gate_rows, n] ) ) )
+ *   stream_dtype MLORA_BF16: out[m, n] = bf16( RN( res[m, n] + RN( bf16(Y[m, n]) · gate[m / gate_rows, n] ) ) )
+ *   stream_dtype MLORA_F32:  out[m, n] =       RN( res[m, n] + RN( bf16(Y[m, n]) · gate[m / gate_rows, n] ) )
  * with Y the value mlora_gemm_fwd would store, fp32 multiply then fp32 add, each rounded to
- * nearest (no fused multiply-add). res (x) and out are bf16 [M, N] and may be the same
+ * nearest (no fused multiply-add). The float32 stream is the Wan block's: x is float32 and
+ * `x = x + y * e[2]` runs under float32 autocast (model.py:305-306,312-313), so the bf16 y is
+ * promoted and the sum is not rounded to bf16. res (x) and out are [M, N] of the stream dtype
+ * (float32 rows: pitch a multiple of 4, 16-byte aligned, N a multiple of 8) and may be the same
  * matrix (in-place update of x); gate is fp32 with ⌈M / gate_rows⌉ rows of pitch ldgate
  * (ldgate a multiple of 4, 16-byte aligned): gate_rows = tokens per sample for a per-sample
  * gate [B, 1, N], 1 for a per-token gate. Y itself is not written. */
@@ -158,14 +162,15 @@ int mlora_gemm_fwd_gated(const void *x, int64_t ldx, int64_t M, int64_t K,
                          const void *const *b_ptrs, const int32_t *ranks, int32_t n_adapters,
                          const int64_t *seg_offsets, const int32_t *adapter_ids, int32_t n_segments,
                          const void *res, int64_t ldres, const float *gate, int64_t ldgate, int64_t gate_rows,
-                         void *out, int64_t ldout,
+                         void *out, int64_t ldout, int stream_dtype,
                          void *stream);
 /* Backward of that gated residual for a frozen gate: dY[m, n] = bf16(dOut[m, n] · gate[m / gate_rows, n])
  * (one fp32 multiply rounded to nearest: runtime/helios_residual_kernel.py:90-133); the
- * gradient of x is dOut. gate as in mlora_gemm_fwd_gated. */
+ * gradient of x is dOut. dOut is bf16 or float32 (dout_dtype, the stream's dtype); gate as in
+ * mlora_gemm_fwd_gated. */
 int mlora_gate_scale_rows(const void *dout, int64_t ldout, int64_t M, int64_t N,
                           const float *gate, int64_t ldgate, int64_t gate_rows,
-                          void *dy, int64_t lddy,
+                          void *dy, int64_t lddy, int dout_dtype,
                           void *stream);
 
 /* Input gradient with the LoRA term fused into its epilogue:

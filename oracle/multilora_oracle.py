@@ -320,9 +320,20 @@ def gated_residual(x, y, gate, gate_rows: int) -> np.ndarray:
     return bf16_round(np.add(x, p, dtype=np.float32))
 
 
+def gated_residual_f32(x, y, gate, gate_rows: int) -> np.ndarray:
+    """The Wan block's float32 residual stream (reference/livewan_wan21/wan/modules/model.py:
+    305-306,312-313: ``x = x + y * e[2]`` under float32 autocast, x and e float32, y bf16):
+    RN_f32( x + RN_f32( f32(y) · gate[m // gate_rows] ) ) — two float32 operations, no final
+    rounding. x: float32 [M, N]; y: bf16 values; gate: float32 [G, N]."""
+    x = np.asarray(x, dtype=np.float32)
+    y = np.asarray(y, dtype=np.float32)
+    g = np.repeat(np.asarray(gate, dtype=np.float32), gate_rows, axis=0)[: x.shape[0]]
+    return np.add(x, np.multiply(y, g, dtype=np.float32), dtype=np.float32)
+
+
 def gate_scale(dout, gate, gate_rows: int) -> np.ndarray:
-    """Frozen-gate backward of gated_residual (helios_residual_kernel.py:90-133):
-    dY = bf16(RN_f32(f32(dOut) · gate[m // gate_rows])); dX = dOut."""
+    """Frozen-gate backward of gated_residual / gated_residual_f32 (helios_residual_kernel.py:90-133):
+    dY = bf16(RN_f32(f32(dOut) · gate[m // gate_rows])); dX = dOut (dOut bf16 or float32)."""
     d = np.asarray(dout, dtype=np.float32)
     g = np.repeat(np.asarray(gate, dtype=np.float32), gate_rows, axis=0)[: d.shape[0]]
     return bf16_round(np.multiply(d, g, dtype=np.float32))

@@ -204,10 +204,10 @@ def test_gated_residual_entry_points_validate(lib, pkg):
     off, ids = L.i64_array([0, 64]), L.i32_array([-1])
     b, rk = L.ptr_array([0x4000]), L.i32_array([8])
 
-    def fwd(res=0x7000, gate=0x8000, ldgate=64, gate_rows=16, out=0x9000, M=64):
+    def fwd(res=0x7000, gate=0x8000, ldgate=64, gate_rows=16, out=0x9000, M=64, dt=L.BF16):
         o = L.i64_array([0, M])
         return lib.mlora_gemm_fwd_gated(0x1000, 64, M, 64, 0x2000, 64, 64, None, 1, None, 0, b, rk, 1, o, ids, 1,
-                                        res, 64, gate, ldgate, gate_rows, out, 64, None)
+                                        res, 64, gate, ldgate, gate_rows, out, 64, dt, None)
 
     assert fwd(res=None) == L.ERR_INVALID
     assert fwd(gate=None) == L.ERR_INVALID
@@ -217,9 +217,12 @@ def test_gated_residual_entry_points_validate(lib, pkg):
     assert fwd(gate=0x8004) == L.ERR_UNSUPPORTED
     assert fwd(res=0x7008) == L.ERR_UNSUPPORTED
     assert fwd(M=0) == L.OK
+    assert fwd(dt=L.FP8_E4M3) == L.ERR_UNSUPPORTED           # the stream is bf16 or float32
+    assert fwd(dt=L.F32, res=0x7008) == L.ERR_UNSUPPORTED    # float32 rows are 16-byte aligned
+    assert fwd(dt=L.F32, out=None) == L.ERR_INVALID
 
-    def gs(dout=0x1000, gate=0x8000, ldgate=64, gate_rows=4, dy=0x3000, M=8, N=64):
-        return lib.mlora_gate_scale_rows(dout, 64, M, N, gate, ldgate, gate_rows, dy, 64, None)
+    def gs(dout=0x1000, gate=0x8000, ldgate=64, gate_rows=4, dy=0x3000, M=8, N=64, dt=L.BF16):
+        return lib.mlora_gate_scale_rows(dout, 64, M, N, gate, ldgate, gate_rows, dy, 64, dt, None)
 
     assert gs(gate=None) == L.ERR_INVALID
     assert gs(gate_rows=0) == L.ERR_INVALID
@@ -227,3 +230,5 @@ def test_gated_residual_entry_points_validate(lib, pkg):
     assert gs(dy=0x3002) == L.ERR_UNSUPPORTED
     assert gs(M=0) == L.OK
     assert gs(M=-1) == L.ERR_INVALID
+    assert gs(dt=L.F32, dout=0x1004) == L.ERR_UNSUPPORTED
+    assert gs(dt=2) == L.ERR_UNSUPPORTED

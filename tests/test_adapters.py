@@ -1,8 +1,9 @@
-"""Adapter state formats on CPU: PEFT (get_peft_model_state_dict layout, scaling in the
-config; backends/training/minimax_h3/model.py:442-451) and DiffSynth (scale baked into B;
-reference/diffsynth_h3_cached/h3_dmd2.py:177-183) round trips, per-role export of a
-multi-role tree, the fail-closed checks, and what each format means numerically. No
-kernel runs."""
+"""Adapter state formats on CPU: PEFT (a PeftModel's get_peft_model_state_dict layout,
+scaling in the config), PEFT's in-module keys (training/wan_public.py:213), the diffusers
+conversion H3 saves (backends/training/minimax_h3/model.py:441-449) and DiffSynth (scale baked
+into B; reference/diffsynth_h3_cached/h3_dmd2.py:177-183): round trips, per-role export of a
+multi-role tree, the fail-closed checks, and what each format means numerically. No kernel
+runs."""
 import math
 
 import pytest
@@ -110,3 +111,68 @@ def test_safetensors_files(pkg, tmp_path, fmt):
     assert (tmp_path / "adapter_model.safetensors").exists() and (tmp_path / "adapter_config.json").exists()
     assert sorted(pkg.load_adapters(str(tmp_path), dst)) == ["ffn", "q"]
     assert torch.equal(src.q.lora_b, dst.q.lora_b) and torch.equal(src.ffn.lora_a, dst.ffn.lora_a)
+
+
+# ------------------------------------------------------------ PEFT in-module and diffusers layouts
+
+def test_peft_module_round_trip_and_real_layout(pkg):
+    """"peft_module": the keys PEFT's layers hold inside the model (wan_public.py:213, adapter
+    'default'); a state dict taken from a PEFT-layout model (tests/peft_layout.py) imports into the
+    drop-in modules over the same base, and the imported module computes what the PEFT layer does."""
+    from peft_layout import PeftLoraLinear
+    src, dst = _model(pkg, seed=0), _model(pkg, seed=1)
+    state, config = pkg.export_adapters(src, fmt="peft_module", with_base=True)
+    assert set(state) >= {"q.lora_A.default.weight", "q.lora_B.default.weight", "q.base_layer.weight",
+                          "q.base_layer.bias", "ffn.lora_A.default.weight"}
+    assert config["adapter_name"] == "default" and config["r"] == 4
+    with pytest.raises(ValueError, match="differs from the module's frozen base"):
+        pkg.import_adapters(dst, state, config, fmt="peft_module")  # dst has another base (seed 1)
+    with torch.no_grad():
+        for n in ("q", "ffn"):
+            dst.get_submodule(n).base.weight.copy_(src.get_submodule(n).base.weight)
+            dst.get_submodule(n).base.bias.copy_(src.get_submodule(n).base.bias)
+    assert sorted(pkg.import_adapters(dst, state, config, fmt="peft_module")) == ["ffn", "q"]
+    for a, b in zip(src.parameters(), dst.parameters()):
+        assert torch.equal(a, b)
+    # a PEFT-layout layer's own state dict, with a named adapter
+    torch.manual_seed(5)
+    peft = PeftLoraLinear(nn.Linear(16, 24), {"critic": (4, 8.0)})
+    with torch.no_grad():
+        peft.lora_B["critic"].weight.normal_(0, 0.1)
+    holder = nn.Module()
+    holder.q = peft
+    sd = holder.state_dict()
+    assert set(sd) == {"q.base_layer.weight", "q.base_layer.bias", "q.lora_A.critic.weight", "q.lora_B.critic.weight"}
+    mine = nn.Sequential()
+    mine.add_module("q", nn.Linear(16, 24))
+    with torch.no_grad():
+        mine.q.weight.copy_(peft.base_layer.weight)
+        mine.q.bias.copy_(peft.base_layer.bias)
+    pkg.trainable_scope(mine, {"mode": "lora", "rank": 4, "alpha": 8.0, "targets": ["q"]})
+    assert pkg.import_adapters(mine, sd, None, fmt="peft_module", adapter="critic") == ["q"]
+    x = torch.randn(5, 16)
+    m = mine.q
+    want = peft(x)
+    got = torch.nn.functional.linear(x, m.base.weight, m.base.bias) + m.scale * (x @ m.lora_a.T) @ m.lora_b.T
+    assert torch.allclose(got, want, rtol=1e-5, atol=1e-6)
+
+
+def test_diffusers_key_renames_and_round_trip(pkg, tmp_path):
+    """"diffusers" (the H3 backend's pytorch_lora_weights.safetensors, minimax_h3/model.py:441-449):
+    diffusers 0.34's PEFT -> diffusers renames, first match only, applied after ".processor." -> ".";
+    names with none of the patterns (Wan's q/k/v/o) are unchanged. Parity with diffusers itself is
+    unpinned (not installed)."""
+    from dmd_system_amd.adapters import diffusers_key
+    assert diffusers_key("blocks.0.attn1.to_q.lora_A.weight") == "blocks.0.attn1.to_q.lora.down.weight"
+    assert diffusers_key("blocks.0.attn1.to_out.0.lora_B.weight") == "blocks.0.attn1.to_out.0.lora.up.weight"
+    assert diffusers_key("text_model.layers.1.self_attn.q_proj.lora_A.weight") == \
+        "text_model.layers.1.self_attn.q_proj.lora_linear_layer.down.weight"
+    assert diffusers_key("blocks.0.self_attn.q.lora_A.weight") == "blocks.0.self_attn.q.lora_A.weight"
+    assert diffusers_key("a.processor.to_k.lora_B.weight") == "a.to_k.lora.up.weight"
+    src, dst = _model(pkg, seed=0), _model(pkg, seed=1)
+    pkg.save_adapters(str(tmp_path / "role"), src, fmt="diffusers")
+    assert sorted(p.name for p in (tmp_path / "role").iterdir()) == ["pytorch_lora_weights.safetensors"]
+    assert sorted(pkg.load_adapters(str(tmp_path / "role"), dst)) == ["ffn", "q"]
+    for a, b in zip(src.parameters(), dst.parameters()):
+        if a.requires_grad:
+            assert torch.equal(a, b)

@@ -108,3 +108,47 @@ def test_module_gated_residual_under_roles(pkg, dev):
     want = O.gated_residual(_np(xres.reshape(-1, 256)), _np(y.reshape(-1, 256)), _np(e2.reshape(B, 256)), L)
     assert np.array_equal(_np(out.reshape(-1, 256)), want)
     assert torch.equal(out_fake, out[1:2])
+
+
+@pytest.mark.parametrize("M,K,N,samples", [(1000, 320, 256, 4), (16384, 1536, 1536, 2)])
+def test_fused_gated_residual_float32_stream(pkg, dev, M, K, N, samples):
+    """The Wan block's float32 residual stream (model.py:305-306,312-313): out = x + bf16(Y)·gate
+    in float32, bit-exact against oracle.gated_residual_f32 on the unfused Y; in place too; and
+    the backward (d x = dOut float32, dY = bf16(dOut·gate)) bit-exact against torch autograd of
+    the unfused float32 composition."""
+    print(f"float32-stream gated residual M={M} K={K} N={N} gate rows {samples}", flush=True)
+    lengths = (M // 2, M // 4, M - M // 2 - M // 4)
+    ids = (0, -1, 1)
+    x, w, b, As, Bs, hidden, gate = _case(dev, M, K, N, (32, 16), lengths, ids, seed=7 * M + samples,
+                                          samples=samples)
+    g = torch.Generator().manual_seed(M)
+    stream = torch.randn(M, N, generator=g).to(dev)  # float32 residual stream
+    routing = pkg.SegmentRouting.from_lengths(lengths, ids)
+    scales = [2.0, 0.5]
+    with torch.no_grad():
+        y = pkg.multi_lora_linear(x, w, b, As, Bs, scales, routing)
+        out = pkg.multi_lora_linear_gated(x, w, b, As, Bs, scales, routing, stream, gate)
+    assert out.dtype == torch.float32
+    want = O.gated_residual_f32(_np(stream), _np(y), _np(gate), M // samples)
+    assert np.array_equal(_np(out), want)
+    A_ops = [a.contiguous() for a in As]
+    h_rows, _ = pkg.kernels.shrink(x, A_ops, 0, scales, routing, False, 32)
+    res = stream.clone()
+    pkg.kernels.gemm_fwd_gated(x, w, b, h_rows, Bs, routing, res, gate, out=res)
+    assert torch.equal(res, out)
+    # backward against autograd of the unfused composition, same kernels underneath
+    xs = [x.clone().requires_grad_(True) for _ in range(2)]
+    ss = [stream.clone().requires_grad_(True) for _ in range(2)]
+    Ag = [[a.clone().requires_grad_(True) for a in As] for _ in range(2)]
+    Bg = [[v.clone().requires_grad_(True) for v in Bs] for _ in range(2)]
+    dout = torch.randn(M, N, generator=g).to(dev)
+    fused = pkg.multi_lora_linear_gated(xs[0], w, b, Ag[0], Bg[0], scales, routing, ss[0], gate)
+    fused.backward(dout)
+    yy = pkg.multi_lora_linear(xs[1], w, b, Ag[1], Bg[1], scales, routing)
+    unfused = ss[1] + yy.float() * gate.repeat_interleave(M // samples, dim=0)
+    unfused.backward(dout)
+    assert torch.equal(fused.detach(), unfused.detach())
+    assert ss[0].grad.dtype == torch.float32 and torch.equal(ss[0].grad, ss[1].grad)
+    assert torch.equal(xs[0].grad, xs[1].grad)
+    for p0, p1 in zip(Ag[0] + Bg[0], Ag[1] + Bg[1]):
+        assert torch.equal(p0.grad, p1.grad)

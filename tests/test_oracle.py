@@ -440,6 +440,35 @@ def test_gated_residual_rounds_multiply_and_add_separately():
     assert np.array_equal(one[3:], np.tile(np.arange(8, 16, dtype=np.float32), (3, 1)))
 
 
+def test_gated_residual_f32_is_the_wan_float32_stream():
+    """The Wan block's stream (model.py:305-306): x float32, y bf16, e float32, ``x + y * e`` under
+    float32 autocast = two float32 roundings and no bf16 rounding. Against torch's float32 ops on
+    the same values (an independent evaluation), and against the fused-multiply-add form, which
+    must differ on some inputs (the order of the roundings is observable in float32)."""
+    import torch
+    rng = np.random.default_rng(33)
+    M, N = 4096, 256
+    x = rng.standard_normal((M, N)).astype(np.float32)
+    y = O.bf16_round(rng.standard_normal((M, N)).astype(np.float32))
+    g = rng.standard_normal((4, N)).astype(np.float32)
+    got = O.gated_residual_f32(x, y, g, M // 4)
+    assert got.dtype == np.float32
+    tg = torch.from_numpy(g).repeat_interleave(M // 4, dim=0)
+    want = (torch.from_numpy(x) + torch.from_numpy(y).to(torch.bfloat16).float() * tg).numpy()
+    assert np.array_equal(got, want)
+    gg = np.repeat(g, M // 4, axis=0).astype(np.float64)
+    fused = (x.astype(np.float64) + y.astype(np.float64) * gg).astype(np.float32)
+    assert (fused != got).sum() > 0
+    assert (O.bf16_round(got) != got).sum() > 0  # not rounded to bf16
+    # the gradient of y through the float32 stream is the same rounded product
+    d = rng.standard_normal((64, 32)).astype(np.float32)
+    gate = rng.standard_normal((64, 32)).astype(np.float32)
+    td = torch.from_numpy(d)
+    ty = torch.zeros(64, 32, dtype=torch.bfloat16, requires_grad=True)
+    (torch.zeros(64, 32) + ty * torch.from_numpy(gate)).backward(td)
+    assert np.array_equal(O.gate_scale(d, gate, 1), ty.grad.float().numpy())
+
+
 def test_gate_scale_is_one_rounded_product():
     import torch
     rng = np.random.default_rng(32)
