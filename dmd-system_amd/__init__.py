@@ -22,7 +22,8 @@ The directory name is not a Python identifier; importers load it as
 from . import _lib, kernels
 from .adapters import export_adapters, import_adapters, load_adapters, save_adapters
 from .function import (MultiLoRAF32Function, MultiLoRAFP8Function, MultiLoRAFunction,
-                       MultiLoRAGatedResidualFunction, SharedInputMultiLoRAFunction, multi_lora_linear,
+                       MultiLoRAGatedResidualFunction, SharedInputMultiLoRAFunction, StackedLinearsFunction,
+                       multi_lora_linear,
                        multi_lora_linear_fp8, multi_lora_linear_gated, shared_input_multi_lora)
 from .low_rank import LoRALinear, MultiLoRALinear, TrainableLowRankLinear, install_lora, trainable_scope
 from .roles import RoleBatch, fuse_roles, roles_active
@@ -40,7 +41,7 @@ __all__ = [
     "MultiLoRAF32Function", "LoRALinear", "install_lora",
     "multi_lora_linear_fp8", "MultiLoRAGatedResidualFunction", "multi_lora_linear_gated", "MultiLoRALinear",
     "TrainableLowRankLinear", "trainable_scope", "RoleBatch", "fuse_roles", "roles_active",
-    "SharedInputMultiLoRAFunction", "shared_input_multi_lora", "SharedInputGroup", "fuse_shared_inputs",
+    "SharedInputMultiLoRAFunction", "StackedLinearsFunction", "shared_input_multi_lora", "SharedInputGroup", "fuse_shared_inputs",
     "release_shared_inputs", "export_adapters", "import_adapters", "save_adapters", "load_adapters", "kernels",
     "load_library", "install_peft_multi_lora", "uninstall_peft_multi_lora", "peft_roles_active",
 ]

@@ -16,6 +16,7 @@ ABI_VERSION = 6
 MAX_SEGMENTS = 128
 MAX_ADAPTERS = 32
 MAX_RANK = 256
+MAX_STACKED = 8
 
 F32, BF16, FP8_E4M3 = 0, 1, 2
 
@@ -39,6 +40,10 @@ SIGNATURES = {
     "mlora_frag_bytes": (_i64, [_i64, _i32, _pi64, _pi32, _i32]),
     "mlora_gemm_fwd": (_int, [_vp, _i64, _i64, _i64, _vp, _i64, _i64, _vp, _int, _vp, _i64,
                               _pvp, _pi32, _i32, _pi64, _pi32, _i32, _vp, _i64, _int, _vp]),
+    "mlora_gemm_fwd_stacked": (_int, [_vp, _i64, _i64, _i64, _vp, _i64, _i64, _i64, _vp, _int, _vp, _i64, _i64,
+                                      _pvp, _pi32, _i32, _pi64, _pi32, _i32, _pvp, _i64, _vp]),
+    "mlora_gemm_dx_stacked": (_int, [_pvp, _i64, _i64, _i64, _i64, _vp, _i64, _i64, _vp, _i64,
+                                     _pvp, _pi32, _i32, _pi64, _pi32, _i32, _vp, _i64, _vp]),
     "mlora_gemm_fwd_gated": (_int, [_vp, _i64, _i64, _i64, _vp, _i64, _i64, _vp, _int, _vp, _i64,
                                     _pvp, _pi32, _i32, _pi64, _pi32, _i32, _vp, _i64, _vp, _i64, _i64,
                                     _vp, _i64, _int, _vp]),

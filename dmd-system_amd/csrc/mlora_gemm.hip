@@ -54,6 +54,16 @@ struct GemmArgs {
   int64_t ldres, ldgate;
   int32_t gate_rows;
   int32_t res_f32;
+  // Stacked linears (gemm_kernel<C, RESID, STK>), G = groups of them.
+  // STK 1 (forward): the output columns hold the G linears side by side, group_cols columns each
+  // (a multiple of the tile width), linear g's columns stored to Yg[g] (its own [M, group_cols]
+  // matrix, pitch ldy); a tile of linear g takes its LoRA rows from E's columns
+  // [g·group_ecols, g·group_ecols + r).
+  // STK 2 (dX): the main contraction runs over the G linears' dY in turn, group_cols columns each:
+  // P = Pg[g] (pitch ldp) against Q's contraction columns [g·group_cols, (g+1)·group_cols).
+  int32_t groups, group_cols, group_ecols;
+  uint16_t *Yg[MLORA_MAX_STACKED];
+  const uint16_t *Pg[MLORA_MAX_STACKED];
 };
 
 template <int BM_, int BN_, int WM_, int WN_, bool NN_, bool F8_ = false, int KB_ = 128, int STAGES_ = 2,
@@ -442,14 +452,15 @@ __device__ __forceinline__ void mma_fp8(f32x16 (&acc)[C::TM][C::TN], Frag8<C> &f
 // Finds the next LoRA source of this tile: the next segment from `seg` on that
 // overlaps rows [m0, row_end) and has an adapter. Wave-uniform scalar code.
 __device__ __forceinline__ bool next_lora_source(const GemmArgs &args, bool nn, int m0, int row_end, int &seg,
-                                                 KSource &src) {
+                                                 KSource &src, int ecol = 0) {
   while (seg < args.seg.n && args.seg.off[seg] < row_end) {
     const int a = args.seg.aid[seg];
     const int lo = max(args.seg.off[seg], m0), hi = min(args.seg.off[seg + 1], row_end);
     ++seg;
     if (a >= 0 && args.ext.rank[a] > 0 && lo < hi) {
       const int r = args.ext.rank[a];
-      src = KSource{reinterpret_cast<const char *>(args.E), reinterpret_cast<const char *>(args.ext.ptr[a]), 2 * args.lde,
+      src = KSource{reinterpret_cast<const char *>(args.E + ecol), reinterpret_cast<const char *>(args.ext.ptr[a]),
+                    2 * args.lde,
                     2 * (nn ? (int64_t)args.Ncols : (int64_t)r), lo, hi, r, 2};
       return true;
     }
@@ -476,12 +487,15 @@ __device__ __forceinline__ bool next_lora_source(const GemmArgs &args, bool nn, 
 // offset out of range (no data moves), so every step issues the same number
 // of loads and the vmcnt thresholds are constants; the phase loop is unrolled
 // so every LDS offset is a constant as well.
-template <class C>
+template <class C, int STK = 0>
 __device__ __forceinline__ void contract_tile(f32x16 (&acc)[C::TM][C::TN], const GemmArgs &args, MLORA_LDS char *lds,
                                               const FragAddr<C> &fa, int m0, int n0, int tid) {
   constexpr int S = C::PERIOD, NSUB = C::NSUB, NDMA = C::NDMA;
   const int wave = wave_id(), lane = tid & 63;
   const int row_end = min(m0 + C::BM, args.M);
+  // stacked forward: this tile's linear reads its own columns of the LoRA rows
+  const int ecol = STK == 1 ? __builtin_amdgcn_readfirstlane((n0 / args.group_cols) * args.group_ecols) : 0;
+  int grp = 0;  // stacked dX: the linear whose dY the main contraction is reading
   int seg = args.E != nullptr ? seg_of_row(args.seg, m0) : args.seg.n;
   Pipe<C> pipe;
   constexpr int esz0 = C::F8 ? 1 : 2;
@@ -494,7 +508,7 @@ __device__ __forceinline__ void contract_tile(f32x16 (&acc)[C::TM][C::TN], const
   if constexpr (C::F8) ntile = (ntile + S - 1) / S * S;
   const int n_main = ntile;  // e4m3 k-tiles (F8), before the first LoRA tile
   if (ntile == 0) {
-    if (!next_lora_source(args, C::NN, m0, row_end, seg, src)) return;
+    if (!next_lora_source(args, C::NN, m0, row_end, seg, src, ecol)) return;
     bk = C::KB / src.esz;
     ntile = (src.klim + bk - 1) / bk;
   }
@@ -511,7 +525,20 @@ __device__ __forceinline__ void contract_tile(f32x16 (&acc)[C::TM][C::TN], const
       ++n_real;
       return true;
     }
-    if (!next_lora_source(args, C::NN, m0, row_end, seg, src)) {
+    if constexpr (STK == 2) {
+      if (grp + 1 < args.groups) {  // the next linear's dY against its columns of Q
+        ++grp;
+        src = KSource{reinterpret_cast<const char *>(args.Pg[grp]),
+                      reinterpret_cast<const char *>(args.Q) + 2 * (int64_t)grp * args.group_cols, 2 * args.ldp,
+                      2 * args.ldq, 0, args.M, args.group_cols, 2};
+        kmask = src.klim % bk != 0;
+        pipe.init(src, m0, n0, args.Ncols, tid);
+        t_in_src = 0;
+        ++n_real;
+        return true;
+      }
+    }
+    if (!next_lora_source(args, C::NN, m0, row_end, seg, src, ecol)) {
       exhausted = true;
       return false;
     }
@@ -674,10 +701,13 @@ __device__ __forceinline__ float gated_add(float x, float y, float g) {
 
 template <class C, bool STAGED, bool ACCUM = true, bool RESID = false>
 __device__ __forceinline__ void store_tile(const f32x16 (&acc)[C::TM][C::TN], const GemmArgs &args, MLORA_LDS char *lds,
-                                           int m0, int n0, int wm0, int wn0, int lane, int wave) {
+                                           int m0, int n0, int wm0, int wn0, int lane, int wave,
+                                           uint16_t *Ybase, int ncol0) {
+  // Ybase: the output matrix (pitch ldy); its column 0 is tile column ncol0 (a stacked linear's
+  // first column; 0 otherwise)
   const int rows_here = min(C::BM, args.M - m0);
   const int64_t ldy_b = args.ldy * 2;
-  const __amdgpu_buffer_rsrc_t ry = make_rsrc(args.Y + (int64_t)m0 * args.ldy, rows_here * ldy_b);
+  const __amdgpu_buffer_rsrc_t ry = make_rsrc(Ybase + (int64_t)m0 * args.ldy, rows_here * ldy_b);
   constexpr int ROWB = C::BN * 2;  // bytes per staged row
   constexpr int CH = C::BN / 8;    // 16-byte chunks per staged row
   static_assert(!STAGED || C::LDS_BYTES >= C::BM * ROWB, "the staged output tile fits the operand stages");
@@ -732,9 +762,9 @@ __device__ __forceinline__ void store_tile(const f32x16 (&acc)[C::TM][C::TN], co
               u32x2{pack2_bf16(v[0], v[1]), pack2_bf16(v[2], v[3])};
         } else {
           // rows past M / columns past Ncols fall outside ry or are dropped
-          const int32_t off = (ml < rows_here && n < args.Ncols) ? (int32_t)(ml * ldy_b + n * 2) : kOOB;
+          const int32_t off = (ml < rows_here && n < args.Ncols) ? (int32_t)(ml * ldy_b + (n - ncol0) * 2) : kOOB;
           if (ACCUM && args.accumulate && off != kOOB) {
-            const u32x2 o = *(const MLORA_GLOBAL u32x2 *)(args.Y + (int64_t)(m0 + ml) * args.ldy + n);
+            const u32x2 o = *(const MLORA_GLOBAL u32x2 *)(Ybase + (int64_t)(m0 + ml) * args.ldy + (n - ncol0));
             v[0] += bf16_to_f32(o.x & 0xffff); v[1] += bf16_to_f32(o.x >> 16);
             v[2] += bf16_to_f32(o.y & 0xffff); v[3] += bf16_to_f32(o.y >> 16);
           }
@@ -756,7 +786,7 @@ __device__ __forceinline__ void store_tile(const f32x16 (&acc)[C::TM][C::TN], co
     const int q = lane % CH;
     u32x4 d = *(const lds_u4 *)(lds + r * ROWB + 16 * (q ^ (r % CH)));
     const int n = n0 + 8 * q;
-    const int32_t off = (r < rows_here && n < args.Ncols) ? (int32_t)(r * ldy_b + n * 2) : kOOB;
+    const int32_t off = (r < rows_here && n < args.Ncols) ? (int32_t)(r * ldy_b + (n - ncol0) * 2) : kOOB;
     if constexpr (RESID) {
       // the 8 bf16 values of d are bf16(Y); x and gate of the same 8 columns
       if (off != kOOB) {
@@ -802,8 +832,8 @@ __device__ __forceinline__ void store_tile(const f32x16 (&acc)[C::TM][C::TN], co
 }
 
 // One workgroup per output tile. RESID: the stored value is the block's gated
-// residual of the result (see store_tile).
-template <class C, bool RESID = false>
+// residual of the result (see store_tile). STK: stacked linears (see GemmArgs).
+template <class C, bool RESID = false, int STK = 0>
 __global__ __launch_bounds__(C::THREADS, C::WAVES_PER_SIMD) void gemm_kernel(const GemmArgs args) {
   __shared__ u32x4 smem[C::LDS_BYTES / 16];
   MLORA_LDS char *lds = (MLORA_LDS char *)smem;
@@ -821,8 +851,13 @@ __global__ __launch_bounds__(C::THREADS, C::WAVES_PER_SIMD) void gemm_kernel(con
       for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
   FragAddr<C> fa;
   fa.init(wm0, wn0, lane);
-  contract_tile<C>(acc, args, lds, fa, m0, n0, tid);
-  store_tile<C, true, true, RESID>(acc, args, lds, m0, n0, wm0, wn0, lane, wave);
+  contract_tile<C, STK>(acc, args, lds, fa, m0, n0, tid);
+  if constexpr (STK == 1) {
+    const int g = __builtin_amdgcn_readfirstlane(n0 / args.group_cols);
+    store_tile<C, true, true, RESID>(acc, args, lds, m0, n0, wm0, wn0, lane, wave, args.Yg[g], g * args.group_cols);
+  } else {
+    store_tile<C, true, true, RESID>(acc, args, lds, m0, n0, wm0, wn0, lane, wave, args.Y, 0);
+  }
 }
 
 using CfgNT256 = GemmCfg<256, 256, 4, 2, false, false, 128, 2, true, true>;
@@ -839,7 +874,7 @@ using CfgNN128 = GemmCfg<128, 128, 2, 2, true>;
 // shapes, bit-equal output.
 constexpr int kGroupM = 4;
 
-template <class C, bool RESID = false>
+template <class C, bool RESID = false, int STK = 0>
 static int launch_gemm(GemmArgs &a, hipStream_t stream) {
   a.tiles_m = (a.M + C::BM - 1) / C::BM;
   a.tiles_n = (a.Ncols + C::BN - 1) / C::BN;
@@ -847,7 +882,7 @@ static int launch_gemm(GemmArgs &a, hipStream_t stream) {
   const int64_t nblocks = (int64_t)a.tiles_m * a.tiles_n;
   if (nblocks == 0) return MLORA_OK;
   if (nblocks > INT32_MAX) return MLORA_ERR_LIMIT;
-  hipLaunchKernelGGL((gemm_kernel<C, RESID>), dim3((unsigned)nblocks), dim3(C::THREADS), 0, stream, a);
+  hipLaunchKernelGGL((gemm_kernel<C, RESID, STK>), dim3((unsigned)nblocks), dim3(C::THREADS), 0, stream, a);
   return launch_status();
 }
 
@@ -855,11 +890,11 @@ static int launch_gemm(GemmArgs &a, hipStream_t stream) {
 // whenever it still gives every CU a tile; the 4-wave 128x128 tile otherwise.
 // (A persistent form whose k-tile ring runs across output tiles, and
 // 256x128 tiles with a 3-stage ring, both measured slower.)
-template <class Big, class Small, bool RESID = false>
+template <class Big, class Small, bool RESID = false, int STK = 0>
 static int dispatch_gemm(GemmArgs &a, hipStream_t stream) {
   const int64_t big_tiles = (int64_t)((a.M + 255) / 256) * ((a.Ncols + 255) / 256);
-  if (big_tiles >= 256) return launch_gemm<Big, RESID>(a, stream);
-  return launch_gemm<Small, RESID>(a, stream);
+  if (big_tiles >= 256) return launch_gemm<Big, RESID, STK>(a, stream);
+  return launch_gemm<Small, RESID, STK>(a, stream);
 }
 
 static int fill_common(GemmArgs &a, int64_t M, int64_t Kc, int64_t Ncols, const void *e, int64_t lde,
@@ -920,6 +955,84 @@ extern "C" int mlora_gemm_fwd(const void *x, int64_t ldx, int64_t M, int64_t K, 
   a.ldy = ldy;
   a.accumulate = accumulate ? 1 : 0;
   return dispatch_gemm<CfgNT256, CfgNT128>(a, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int mlora_gemm_fwd_stacked(const void *x, int64_t ldx, int64_t M, int64_t K, const void *w, int64_t ldw,
+                                      int64_t N, int64_t group_cols, const void *bias, int bias_dtype,
+                                      const void *h_rows, int64_t ldh, int64_t group_ecols,
+                                      const void *const *b_ptrs, const int32_t *ranks, int32_t n_adapters,
+                                      const int64_t *seg_offsets, const int32_t *adapter_ids, int32_t n_segments,
+                                      void *const *y_ptrs, int64_t ldy, void *stream) {
+  GemmArgs a{};
+  int st = fill_common(a, M, K, N, h_rows, ldh, b_ptrs, ranks, n_adapters, seg_offsets, adapter_ids, n_segments);
+  if (st) return st;
+  if (group_cols <= 0 || group_cols % 256 != 0 || N % group_cols != 0 || N / group_cols > MLORA_MAX_STACKED)
+    return MLORA_ERR_UNSUPPORTED;
+  const int64_t groups = N / group_cols;
+  if ((st = check_bf16_matrix(x, ldx, M, K))) return st;
+  if ((st = check_bf16_matrix(w, ldw, N, K))) return st;
+  if (y_ptrs == nullptr) return MLORA_ERR_INVALID;
+  for (int64_t g = 0; g < groups; ++g)
+    if ((st = check_bf16_matrix(y_ptrs[g], ldy, M, group_cols))) return st;
+  const int rmax = max_used_rank(a.seg, a.ext);
+  if (group_ecols < 0 || group_ecols % 8 != 0 || rmax > group_ecols) return MLORA_ERR_INVALID;
+  if (rmax > 0 && (ldh < groups * group_ecols)) return MLORA_ERR_INVALID;  // every linear's LoRA columns
+  if (M == 0 || N == 0) return MLORA_OK;
+  for (int64_t g = 0; g < groups; ++g)
+    if (y_ptrs[g] == nullptr) return MLORA_ERR_INVALID;
+  if (bias != nullptr) {
+    if (bias_dtype != MLORA_F32 && bias_dtype != MLORA_BF16) return MLORA_ERR_UNSUPPORTED;
+    if (!aligned16(bias)) return MLORA_ERR_UNSUPPORTED;
+  }
+  if (!offsets_fit(ldx, 256) || !offsets_fit(ldy, 256) || !offsets_fit(ldw, 256)) return MLORA_ERR_LIMIT;
+  a.P = static_cast<const uint16_t *>(x);
+  a.Q = static_cast<const uint16_t *>(w);
+  a.ldp = ldx;
+  a.ldq = ldw;
+  a.bias = bias;
+  a.bias_dtype = bias ? bias_dtype : -1;
+  a.Y = static_cast<uint16_t *>(y_ptrs[0]);
+  a.ldy = ldy;
+  a.groups = (int32_t)groups;
+  a.group_cols = (int32_t)group_cols;
+  a.group_ecols = (int32_t)group_ecols;
+  for (int64_t g = 0; g < groups; ++g) a.Yg[g] = static_cast<uint16_t *>(y_ptrs[g]);
+  return dispatch_gemm<CfgNT256, CfgNT128, false, 1>(a, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int mlora_gemm_dx_stacked(const void *const *dy_ptrs, int64_t lddy, int64_t M, int64_t group_cols,
+                                     int64_t groups, const void *w_t, int64_t ldw, int64_t K, const void *g_rows,
+                                     int64_t ldg, const void *const *a_ptrs, const int32_t *ranks, int32_t n_adapters,
+                                     const int64_t *seg_offsets, const int32_t *adapter_ids, int32_t n_segments,
+                                     void *dx, int64_t lddx, void *stream) {
+  GemmArgs a{};
+  if (groups < 1 || groups > MLORA_MAX_STACKED || group_cols < 0) return MLORA_ERR_UNSUPPORTED;
+  // contraction group_cols per linear (the main source of the kernel is linear 0's), output columns K
+  int st = fill_common(a, M, group_cols, K, g_rows, ldg, a_ptrs, ranks, n_adapters, seg_offsets, adapter_ids,
+                       n_segments);
+  if (st) return st;
+  if (dy_ptrs == nullptr) return MLORA_ERR_INVALID;
+  for (int64_t g = 0; g < groups; ++g)
+    if ((st = check_bf16_matrix(dy_ptrs[g], lddy, M, group_cols))) return st;
+  if ((st = check_bf16_matrix(w_t, ldw, K, groups * group_cols))) return st;
+  if ((st = check_bf16_matrix(dx, lddx, M, K))) return st;
+  if (M == 0 || K == 0) return MLORA_OK;
+  if (dx == nullptr) return MLORA_ERR_INVALID;
+  for (int64_t g = 0; g < groups; ++g)
+    if (group_cols > 0 && dy_ptrs[g] == nullptr) return MLORA_ERR_INVALID;
+  if (!offsets_fit(lddy, 256) || !offsets_fit(lddx, 256) || !offsets_fit(ldw, 256)) return MLORA_ERR_LIMIT;
+  a.P = static_cast<const uint16_t *>(dy_ptrs[0]);
+  a.Q = static_cast<const uint16_t *>(w_t);
+  a.ldp = lddy;
+  a.ldq = ldw;
+  a.bias = nullptr;
+  a.bias_dtype = -1;
+  a.Y = static_cast<uint16_t *>(dx);
+  a.ldy = lddx;
+  a.groups = (int32_t)groups;
+  a.group_cols = (int32_t)group_cols;
+  for (int64_t g = 0; g < groups; ++g) a.Pg[g] = static_cast<const uint16_t *>(dy_ptrs[g]);
+  return dispatch_gemm<CfgNT256, CfgNT128, false, 2>(a, static_cast<hipStream_t>(stream));
 }
 
 extern "C" int mlora_gemm_fwd_gated(const void *x, int64_t ldx, int64_t M, int64_t K, const void *w, int64_t ldw,

@@ -409,6 +409,99 @@ class SharedInputMultiLoRAFunction(torch.autograd.Function):
         return (dx, None, None, None, None, None, *[d for dg in dA for d in dg], *[d for dg in dB for d in dg])
 
 
+class StackedLinearsFunction(torch.autograd.Function):
+    """``apply(x, routing, scales, groups, w_cat, b_cat, w_cat_t, *lora_as, *lora_bs)``: G multi-LoRA
+    linears that read x [M, K], as one stacked call. w_cat [G·N, K] bf16 = their frozen weights
+    stacked by rows (b_cat [G·N] or None, w_cat_t = w_cat transposed [K, G·N] or None, all frozen);
+    lora_as = [A_g,i for g < G for i < n] ([R, K] each), lora_bs likewise ([N, R]); one rank R (a
+    multiple of 16) and one output width N (a multiple of 256) for every linear. Returns the G
+    outputs [M, N], each bit-identical to that linear's own call.
+
+    Forward: one shrink of X by the stacked [A_0,i; ...; A_{G-1},i] (X read once) and one GEMM over
+    the stacked weights (mlora_gemm_fwd_stacked: X's row tiles feed all G linears' column tiles).
+    Backward: the G shrinks g_g = s·dY_g·B_g side by side into g [M, G·R]; dX = Σ_g dY_g·W_g + g·A_cat
+    as ONE GEMM whose contraction runs over the G dY in turn and then the G·R columns of g
+    (mlora_gemm_dx_stacked: no concatenated dY, no per-linear dX, one rounding of the sum); dA of
+    every linear from one reduction over X; dB_g one reduction over dY_g.
+    """
+
+    @staticmethod
+    def forward(ctx, x, routing: SegmentRouting, scales: Sequence[float], groups: int, w_cat, b_cat, w_cat_t, *ab):
+        G = int(groups)
+        n = len(ab) // (2 * G) if G > 0 else 0
+        if G < 2 or n == 0 or len(ab) != 2 * G * n or len(scales) != n:
+            raise ValueError("stacked multi-LoRA: G >= 2 linears, G·n lora_a and G·n lora_b, one scale per adapter")
+        if w_cat.requires_grad or (b_cat is not None and b_cat.requires_grad):
+            raise RuntimeError("multi-LoRA: the base weight and bias are frozen (requires_grad=False)")
+        M, K = x.shape
+        NT = w_cat.shape[0]
+        N = NT // G
+        As = [list(ab[g * n:(g + 1) * n]) for g in range(G)]
+        Bs = [list(ab[G * n + g * n:G * n + (g + 1) * n]) for g in range(G)]
+        R = int(As[0][0].shape[0])
+        routing.validate_for(M, n)
+        if (NT != G * N or N % 256 or R % 16 or G * R > _lib.MAX_RANK or G > _lib.MAX_STACKED
+                or w_cat.shape[1] != K):
+            raise ValueError(f"stacked multi-LoRA: {G} linears (at most {_lib.MAX_STACKED}) of width {N} (a multiple "
+                             f"of 256) and rank {R} (a multiple of 16, G·R <= {_lib.MAX_RANK}) over in_features {K}")
+        for g in range(G):
+            for a, b in zip(As[g], Bs[g]):
+                if a.shape != (R, K) or b.shape != (N, R):
+                    raise ValueError(f"stacked multi-LoRA: lora_a {tuple(a.shape)} / lora_b {tuple(b.shape)} of linear "
+                                     f"{g} do not match rank {R}, in {K}, out {N}")
+        A_cat = [torch.cat([_as_operand(As[g][i]) for g in range(G)]) for i in range(n)]  # [G·R, K]
+        B_cat = [torch.cat([_as_operand(Bs[g][i]) for g in range(G)]) for i in range(n)]  # [G·N, R]
+        need_b_grad = any(ctx.needs_input_grad[7 + G * n:])
+        h_rows, h_frag = kernels.shrink(x, A_cat, 0, scales, routing, want_frag=need_b_grad, width=G * R)
+        ys = kernels.gemm_fwd_stacked(x, w_cat, b_cat, h_rows, B_cat, routing, N, R)
+        _save(ctx, x, w_cat, w_cat_t, *A_cat, *B_cat, frag=list(h_frag or []))
+        ctx.routing, ctx.scales, ctx.n, ctx.G, ctx.R, ctx.N = routing, tuple(float(v) for v in scales), n, G, R, N
+        ctx.has_wt = w_cat_t is not None
+        ctx.a_dtypes = [[a.dtype for a in As[g]] for g in range(G)]
+        ctx.b_dtypes = [[b.dtype for b in Bs[g]] for g in range(G)]
+        return tuple(ys)
+
+    @staticmethod
+    def backward(ctx, *dys):
+        n, G, R, N, routing = ctx.n, ctx.G, ctx.R, ctx.N, ctx.routing
+        (x, w_cat, w_cat_t, *ops), h_frag = _saved(ctx)
+        A_cat, B_cat = ops[:n], ops[n:]
+        M = x.shape[0]
+        # an output nobody used has no gradient: it contributes zeros
+        dys = [torch.zeros((M, N), dtype=torch.bfloat16, device=x.device) if d is None
+               else d.to(torch.bfloat16).contiguous() for d in dys]
+        need_x = ctx.needs_input_grad[0]
+        need_a = any(ctx.needs_input_grad[7:7 + G * n])
+        need_b = any(ctx.needs_input_grad[7 + G * n:])
+        jt = G * R // 16
+        g_rows = g_frag = None
+        if need_x or need_a:
+            g_rows = torch.empty((M, G * R), dtype=torch.bfloat16, device=x.device)
+            g_frag = kernels.alloc_frags(routing, jt, x.device) if need_a else None
+            for g in range(G):
+                kernels.shrink(dys[g], [b[g * N:(g + 1) * N] for b in B_cat], 1, ctx.scales, routing,
+                               want_frag=need_a, width=G * R, h_out=g_rows[:, g * R:(g + 1) * R], frag_out=g_frag,
+                               frag_jt=jt, frag_t0=g * R // 16)
+        dx = None
+        if need_x:
+            if ctx.has_wt:  # one GEMM over the G dY against the stacked base held transposed
+                dx = kernels.gemm_dx_stacked(dys, w_cat_t, g_rows, [a.t().contiguous() for a in A_cat], routing)
+            else:  # NN form over the stacked base: the dY side by side
+                dx = kernels.gemm_dx(torch.cat(dys, dim=1), w_cat, g_rows, A_cat, routing)
+        dA = [[None] * n for _ in range(G)]
+        dB = [[None] * n for _ in range(G)]
+        if need_b:
+            for g in range(G):
+                outs = kernels.seg_outer(dys[g], h_frag, G * R, [R] * n, routing, 0, ctx.b_dtypes[g],
+                                         frag_jt=jt, frag_t0=g * R // 16)
+                dB[g] = [o if ctx.needs_input_grad[7 + G * n + g * n + i] else None for i, o in enumerate(outs)]
+        if need_a:
+            outs = kernels.seg_outer(x, g_frag, G * R, [G * R] * n, routing, 1, [torch.float32] * n)
+            dA = [[outs[i][g * R:(g + 1) * R].to(ctx.a_dtypes[g][i]) if ctx.needs_input_grad[7 + g * n + i] else None
+                   for i in range(n)] for g in range(G)]
+        return (dx, None, None, None, None, None, None, *[d for dg in dA for d in dg], *[d for dg in dB for d in dg])
+
+
 def _bf16_rows(x: torch.Tensor, weight_dtype: torch.dtype) -> torch.Tensor:
     """x [..., K] as contiguous bf16 rows [M, K] (under bf16 autocast the cast is done here)."""
     x2 = x.reshape(-1, x.shape[-1])
@@ -425,16 +518,30 @@ def _bf16_rows(x: torch.Tensor, weight_dtype: torch.dtype) -> torch.Tensor:
 
 def shared_input_multi_lora(x: torch.Tensor, weights: Sequence[torch.Tensor], biases: Sequence[torch.Tensor | None],
                             lora_as: Sequence[Sequence[torch.Tensor]], lora_bs: Sequence[Sequence[torch.Tensor]],
-                            scales: Sequence[float], routing: SegmentRouting) -> tuple[torch.Tensor, ...]:
-    """Functional form of SharedInputMultiLoRAFunction over x [..., K]: the G linears' outputs
-    [..., N_g]; lora_as[g][i] / lora_bs[g][i] are linear g's adapter i."""
+                            scales: Sequence[float], routing: SegmentRouting,
+                            transposed_base_for_dx: bool = True) -> tuple[torch.Tensor, ...]:
+    """Functional form over x [..., K]: the G linears' outputs [..., N_g]; lora_as[g][i] / lora_bs[g][i]
+    are linear g's adapter i. Linears of one width (a multiple of 256) run as one stacked call
+    (StackedLinearsFunction) over a cached stacked copy of their frozen bases; other widths run
+    SharedInputMultiLoRAFunction (one shrink, per-linear GEMMs)."""
+    from .low_rank import stacked_bases
     lead = x.shape[:-1]
     G = len(weights)
     x2 = _bf16_rows(x, weights[0].dtype)
-    ws = tuple(w.detach().to(torch.bfloat16) for w in weights)  # a no-op unless autocast runs fp32 bases
-    bs = tuple(None if b is None else b.detach() for b in biases)
     flat_a = [a for g in range(G) for a in lora_as[g]]
     flat_b = [b for g in range(G) for b in lora_bs[g]]
+    widths = {int(w.shape[0]) for w in weights}
+    R = int(lora_as[0][0].shape[0]) if lora_as and lora_as[0] else 0
+    if len(widths) == 1 and next(iter(widths)) % 256 == 0 and G * R <= _lib.MAX_RANK:
+        N = next(iter(widths))
+        want_t = transposed_base_for_dx and torch.is_grad_enabled() and x.requires_grad
+        w_cat, b_cat, w_cat_t = stacked_bases(list(weights), list(biases), want_t)
+        with torch.autocast("cuda", enabled=False):
+            ys = StackedLinearsFunction.apply(x2, routing, tuple(scales), G, w_cat, b_cat, w_cat_t if want_t else None,
+                                              *flat_a, *flat_b)
+        return tuple(v.reshape(*lead, N) for v in ys)
+    ws = tuple(w.detach().to(torch.bfloat16) for w in weights)  # a no-op unless autocast runs fp32 bases
+    bs = tuple(None if b is None else b.detach() for b in biases)
     with torch.autocast("cuda", enabled=False):
         ys = SharedInputMultiLoRAFunction.apply(x2, routing, tuple(scales), G, ws, bs, *flat_a, *flat_b)
     return tuple(y.reshape(*lead, w.shape[0]) for y, w in zip(ys, ws))

@@ -158,6 +158,73 @@ def gemm_fwd(x: torch.Tensor, w: torch.Tensor, bias: torch.Tensor | None, h_rows
     return y
 
 
+def gemm_fwd_stacked(x: torch.Tensor, w_cat: torch.Tensor, bias_cat: torch.Tensor | None, h_rows: torch.Tensor | None,
+                     bs_cat: Sequence[torch.Tensor], routing: SegmentRouting, group_cols: int,
+                     group_ecols: int) -> list[torch.Tensor]:
+    """G linears that read x as one GEMM: w_cat [G·N, K] (their weights stacked by rows), bias_cat
+    [G·N] or None, bs_cat[a] = [B_0,a; ...; B_{G-1},a] ([G·N, r_a]); linear g's LoRA rows are h_rows
+    columns [g·group_ecols, g·group_ecols + r_a). Returns the G outputs [M, N] (each its own tensor)."""
+    M, K = x.shape
+    NT = w_cat.shape[0]
+    G = NT // group_cols
+    _check_rows("X", x, K)
+    _check_rows("W", w_cat, K)
+    if bias_cat is not None:
+        _require(bias_cat.is_cuda and bias_cat.dtype in _DT and bias_cat.is_contiguous() and bias_cat.shape == (NT,),
+                 "bias")
+    ranks = [int(b.shape[1]) for b in bs_cat]
+    for b in bs_cat:
+        _check_rows("lora_b", b)
+        _require(b.is_contiguous() and b.shape[0] == NT, "stacked lora_b must be contiguous [G·N, r]")
+    ys = [torch.empty((M, group_cols), dtype=torch.bfloat16, device=x.device) for _ in range(G)]
+    lib = _lib.load()
+    ptrs, rk = _lib.ptr_array([_ptr(b) for b in bs_cat]), _lib.i32_array(ranks)
+    ldh = h_rows.stride(0) if h_rows is not None else 0
+    stream = _stream(x)
+    for r0, r1, off, ids in routing.groups(_lib.MAX_SEGMENTS):
+        if r1 == r0:
+            continue
+        o, i, n = _routing_arrays(off, ids)
+        hr = None if h_rows is None else h_rows[r0:r1].data_ptr()
+        _lib.check("mlora_gemm_fwd_stacked", lib.mlora_gemm_fwd_stacked(
+            x[r0:r1].data_ptr(), x.stride(0), r1 - r0, K, w_cat.data_ptr(), w_cat.stride(0), NT, group_cols,
+            _ptr(bias_cat), _DT[bias_cat.dtype] if bias_cat is not None else 0, hr, ldh, group_ecols,
+            ptrs, rk, len(bs_cat), o, i, n, _lib.ptr_array([y[r0:r1].data_ptr() for y in ys]), group_cols, stream))
+    return ys
+
+
+def gemm_dx_stacked(dys: Sequence[torch.Tensor], w_cat_t: torch.Tensor, g_rows: torch.Tensor | None,
+                    a_t_cat: Sequence[torch.Tensor], routing: SegmentRouting) -> torch.Tensor:
+    """dX of G stacked linears as one GEMM: Σ_g dY_g·W_g + g_rows·A_cat,a, with w_cat_t = the stacked
+    weights transposed [K, G·N], dys the G gradients [M, N] (contiguous), a_t_cat[a] = the stacked
+    [A_0,a; ...] transposed ([K, G·R]) and g_rows [M, G·R]."""
+    G = len(dys)
+    M, N = dys[0].shape
+    K = w_cat_t.shape[0]
+    for d in dys:
+        _check_rows("dY", d, N)
+        _require(d.shape[0] == M and d.stride(0) == dys[0].stride(0), "the dY of the stacked linears share a shape")
+    _check_rows("W_cat^T", w_cat_t, G * N)
+    ranks = [int(a.shape[1]) for a in a_t_cat]
+    for a in a_t_cat:
+        _check_rows("stacked lora_a^T", a)
+        _require(a.is_contiguous() and a.shape[0] == K, "stacked lora_a^T must be contiguous [K, G·R]")
+    dx = torch.empty((M, K), dtype=torch.bfloat16, device=dys[0].device)
+    lib = _lib.load()
+    ptrs, rk = _lib.ptr_array([_ptr(a) for a in a_t_cat]), _lib.i32_array(ranks)
+    ldg = g_rows.stride(0) if g_rows is not None else 0
+    stream = _stream(dys[0])
+    for r0, r1, off, ids in routing.groups(_lib.MAX_SEGMENTS):
+        if r1 == r0:
+            continue
+        o, i, n = _routing_arrays(off, ids)
+        _lib.check("mlora_gemm_dx_stacked", lib.mlora_gemm_dx_stacked(
+            _lib.ptr_array([d[r0:r1].data_ptr() for d in dys]), dys[0].stride(0), r1 - r0, N, G,
+            w_cat_t.data_ptr(), w_cat_t.stride(0), K, None if g_rows is None else g_rows[r0:r1].data_ptr(), ldg,
+            ptrs, rk, len(a_t_cat), o, i, n, dx[r0:r1].data_ptr(), dx.stride(0), stream))
+    return dx
+
+
 def _gate_rows(gate: torch.Tensor, M: int, N: int) -> int:
     """Rows of Y per gate row for a gate [G, N] (fp32, row pitch a multiple of 4) over M rows."""
     _require(gate.is_cuda and gate.dtype == torch.float32 and gate.dim() == 2 and gate.shape[1] == N

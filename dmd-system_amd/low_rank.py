@@ -66,6 +66,43 @@ def transposed_base(w: torch.Tensor, x: torch.Tensor, enabled: bool = True) -> t
     return entry[2]
 
 
+# Stacked copies of the frozen bases of linears that read one input (q / k / v), keyed by the
+# identities of the member weights: (weights stacked by rows [G·N, K] bf16, biases stacked [G·N]
+# or None, and the stack transposed [K, G·N] when dX needs it). Entries are remade when a
+# member weight changes and dropped when the first member weight is freed.
+_STACKED: dict[tuple, tuple] = {}
+
+
+def _drop_stacked(key: tuple) -> None:
+    _STACKED.pop(key, None)
+
+
+def stacked_bases(weights, biases, want_t: bool):
+    """(w_cat, b_cat, w_cat_t or None) for the frozen bases of stacked linears. Costs the bases'
+    bf16 size once more (twice with the transpose), per distinct set of bases."""
+    ident = tuple(id(w) for w in weights) + tuple(id(b) if b is not None else 0 for b in biases)
+    ver = tuple((w.data_ptr(), w._version) for w in weights) + tuple(
+        (b.data_ptr(), b._version) if b is not None else (0, 0) for b in biases)
+    entry = _STACKED.get(ident)
+    if entry is None or any(r() is not w for r, w in zip(entry[0], weights)):
+        entry = (tuple(weakref.ref(w) for w in weights), None, None, None, None)
+        weakref.finalize(weights[0], _drop_stacked, ident)
+    refs, v, w_cat, b_cat, w_cat_t = entry
+    if v != ver:
+        with torch.no_grad():
+            w_cat = torch.cat([w.detach().to(torch.bfloat16) for w in weights]).contiguous()
+            b_cat = None
+            if any(b is not None for b in biases):  # float32 holds bf16 and fp32 biases exactly
+                b_cat = torch.cat([b.detach().float() if b is not None else
+                                   torch.zeros(w.shape[0], device=w.device) for w, b in zip(weights, biases)])
+        w_cat_t = None
+    if want_t and w_cat_t is None:
+        with torch.no_grad():
+            w_cat_t = w_cat.t().contiguous()
+    _STACKED[ident] = (refs, ver, w_cat, b_cat, w_cat_t)
+    return w_cat, b_cat, w_cat_t
+
+
 def _base_t(module: nn.Module, x: torch.Tensor) -> torch.Tensor | None:
     """transposed_base of ``module.base.weight``; ``module.transposed_base_for_dx = False`` turns
     the copy off for that module."""

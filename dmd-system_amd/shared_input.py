@@ -15,8 +15,9 @@ object, same in-place version, same routing and grad mode), get theirs without a
 launch.
 
 The modules keep their parameters, names and state-dict keys; the stacked call reads
-the members' own frozen bases and adapter Parameters (no copies are kept), so gradients
-reach each member's ``lora_a`` / ``lora_b``. An output that nobody consumes is still
+the members' own adapter Parameters, so gradients reach each member's ``lora_a`` /
+``lora_b``, and a stacked bf16 copy of their frozen bases (and its transpose for dX), made
+once per set of bases and remade when one of them changes. An output that nobody consumes is still
 computed (and kept until the group's next call); a group is for linears that are all
 called on the tensor.
 """
@@ -109,7 +110,8 @@ class SharedInputGroup:
             return outs[idx]
         ads = [_adapters(m) for m in self.members]
         outs = shared_input_multi_lora(x, [m.base.weight for m in self.members], [m.base.bias for m in self.members],
-                                       [ad[0] for ad in ads], [ad[1] for ad in ads], ads[0][2], routing)
+                                       [ad[0] for ad in ads], [ad[1] for ad in ads], ads[0][2], routing,
+                                       all(getattr(m, 'transposed_base_for_dx', True) for m in self.members))
         self.launches += 1
         pending = set(range(len(self.members))) - {idx}
         self._out = (x, key, outs, pending) if pending else None

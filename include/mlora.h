@@ -50,6 +50,7 @@ extern "C" {
 #define MLORA_MAX_SEGMENTS 128
 #define MLORA_MAX_ADAPTERS 32
 #define MLORA_MAX_RANK 256
+#define MLORA_MAX_STACKED 8   /* linears in one stacked call (mlora_gemm_fwd_stacked / _dx_stacked) */
 
 typedef enum mlora_dtype {
   MLORA_F32 = 0,
@@ -140,6 +141,41 @@ int mlora_gemm_fwd(const void *x, int64_t ldx, int64_t M, int64_t K,
                    const int64_t *seg_offsets, const int32_t *adapter_ids, int32_t n_segments,
                    void *y, int64_t ldy, int accumulate,
                    void *stream);
+
+/* Several linears that read one input X, as one GEMM (the q / k / v projections of a DiT block,
+ * which the reference only shares one fp32 cast of X between: runtime/wan13b_lora_cast.py:265-300):
+ * the G = N / group_cols linears' frozen weights stacked by rows into w [N, K], their LoRA terms
+ * from one stacked shrink: linear g's h rows in h_rows columns [g·group_ecols, g·group_ecols + r_a)
+ * (mlora_shrink of X by [A_0,a; A_1,a; ...]) and b_ptrs[a] = [B_0,a; B_1,a; ...] ([N, r_a]):
+ *   Y_g[m, n'] = bf16( Σ_k X[m,k]·W[n,k] + bias[n] + Σ_j h_rows[m, g·group_ecols + j]·B_a[n, j] ),
+ *                n = g·group_cols + n'
+ * written to y_ptrs[g] ([M, group_cols] each, pitch ldy). group_cols a multiple of 256, N a multiple
+ * of group_cols, G <= MLORA_MAX_STACKED, r_a <= group_ecols (a multiple of 8). Each output equals
+ * mlora_gemm_fwd of its own linear bit for bit. */
+int mlora_gemm_fwd_stacked(const void *x, int64_t ldx, int64_t M, int64_t K,
+                           const void *w, int64_t ldw, int64_t N, int64_t group_cols,
+                           const void *bias, int bias_dtype,
+                           const void *h_rows, int64_t ldh, int64_t group_ecols,
+                           const void *const *b_ptrs, const int32_t *ranks, int32_t n_adapters,
+                           const int64_t *seg_offsets, const int32_t *adapter_ids, int32_t n_segments,
+                           void *const *y_ptrs, int64_t ldy,
+                           void *stream);
+
+/* The input gradient of those G linears as one GEMM whose contraction runs over their dY in turn:
+ *   dX[m, k] = bf16( Σ_g Σ_n' dY_g[m, n']·W_cat[g·group_cols + n', k] + Σ_j g_rows[m, j]·A_a[j, k] )
+ * with w_t = W_catᵀ ([K, groups·group_cols], the stacked frozen weights transposed, pitch ldw),
+ * dy_ptrs[g] = dY_g ([M, group_cols], pitch lddy), g_rows [M, groups·R] the G shrinks of dY side by
+ * side (linear g's g = s·dY_g·B_g,a in columns [g·R, (g+1)·R)) and a_ptrs[a] = the stacked
+ * [A_0,a; A_1,a; ...] transposed ([K, groups·R]). One rounding of the whole sum (autograd sums the
+ * G linears' dX in bf16). Reference: the autograd of low_rank.py:28 for each linear, summed over
+ * the linears that read X. */
+int mlora_gemm_dx_stacked(const void *const *dy_ptrs, int64_t lddy, int64_t M, int64_t group_cols, int64_t groups,
+                          const void *w_t, int64_t ldw, int64_t K,
+                          const void *g_rows, int64_t ldg,
+                          const void *const *a_ptrs, const int32_t *ranks, int32_t n_adapters,
+                          const int64_t *seg_offsets, const int32_t *adapter_ids, int32_t n_segments,
+                          void *dx, int64_t lddx,
+                          void *stream);
 
 /* mlora_gemm_fwd with the DiT block's gated residual fused into the epilogue: the linear
  * closes a branch (attention out-projection, FFN down-projection) whose output y enters

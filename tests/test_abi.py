@@ -232,3 +232,29 @@ def test_gated_residual_entry_points_validate(lib, pkg):
     assert gs(M=-1) == L.ERR_INVALID
     assert gs(dt=L.F32, dout=0x1004) == L.ERR_UNSUPPORTED
     assert gs(dt=2) == L.ERR_UNSUPPORTED
+
+
+def test_stacked_gemm_validates_before_launch(lib, pkg):
+    L = pkg._lib
+    off, ids = L.i64_array([0, 64]), L.i32_array([0])
+    b, rk = L.ptr_array([0x4000]), L.i32_array([64])
+
+    def st(N=768, group_cols=256, group_ecols=64, ldh=192, M=64):
+        o = L.i64_array([0, M])
+        ys = L.ptr_array([0x3000, 0x6000, 0x9000])
+        return lib.mlora_gemm_fwd_stacked(0x1000, 64, M, 64, 0x2000, 64, N, group_cols, None, 1, 0x5000, ldh,
+                                          group_ecols, b, rk, 1, o, ids, 1, ys, group_cols, None)
+
+    assert st(group_cols=128) == L.ERR_UNSUPPORTED   # a whole number of 256-wide tiles per linear
+    assert st(N=640) == L.ERR_UNSUPPORTED            # N a multiple of group_cols
+    assert st(group_ecols=32) == L.ERR_INVALID       # rank 64 does not fit 32 columns per linear
+    assert st(ldh=128) == L.ERR_INVALID              # h rows hold every linear's columns
+    assert st(N=9 * 256, group_cols=256) == L.ERR_UNSUPPORTED   # more than MLORA_MAX_STACKED linears
+    assert st(M=0) == L.OK
+
+    def dx(groups=3, ldw=768, dys=(0x1000, 0x2000, 0x3000)):
+        return lib.mlora_gemm_dx_stacked(L.ptr_array(list(dys)), 256, 64, 256, groups, 0x4000, ldw, 64, 0x5000, 192,
+                                         b, rk, 1, off, ids, 1, 0x6000, 64, None)
+    assert dx(groups=9) == L.ERR_UNSUPPORTED
+    assert dx(ldw=512) == L.ERR_INVALID             # W_cat^T rows hold the three linears' columns
+    assert dx(dys=(0x1000, 0x2008, 0x3000)) == L.ERR_UNSUPPORTED

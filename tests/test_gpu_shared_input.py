@@ -152,3 +152,47 @@ def test_reuse_only_for_the_same_unmodified_input(pkg, dev):
         assert torch.equal(y0, mods[0](x0, routing)) and torch.equal(y0b, y0)
         assert torch.equal(y1, mods[1](x, routing))
         assert torch.equal(y1b, mods[1](x0, routing))
+
+
+@pytest.mark.parametrize("transposed", [True, False], ids=["dx_nt", "dx_nn"])
+def test_stacked_qkv_at_the_wan_shape(pkg, dev, transposed):
+    """q / k / v of the Wan-1.3B block (1536 -> 1536, rank 64, generator + fake critic) as one stacked
+    GEMM: each output bit-identical to the member's own call; dX (one GEMM over the three dY) within
+    2e-3 of the fp64 sum of the members' dX; adapter gradients within 2e-3 of the per-member calls'."""
+    print(f"stacked qkv wan shape, transposed={transposed}", flush=True)
+    holder, mods = _members(pkg, dev, G=3, K=1536, N=1536, ranks=(64, 64), seed=5)
+    for m in mods:
+        m.transposed_base_for_dx = transposed
+    lengths, ids = (4096, 4096), (0, 1)
+    routing = pkg.SegmentRouting.from_lengths(lengths, ids)
+    M = sum(lengths)
+    x = torch.randn(M, 1536, generator=torch.Generator().manual_seed(6)).to(dev, torch.bfloat16)
+    dys = [torch.randn(M, 1536, generator=torch.Generator().manual_seed(7 + i)).to(dev, torch.bfloat16)
+           for i in range(3)]
+    params = [p for m in mods for p in (*m.lora_a, *m.lora_b)]
+
+    def run(fused):
+        for p in params:
+            p.grad = None
+        if fused:
+            pkg.fuse_shared_inputs(holder, [["m0", "m1", "m2"]])
+        xi = x.clone().requires_grad_(True)
+        ys = [m(xi, routing) for m in mods]
+        torch.autograd.backward(ys, dys)
+        if fused:
+            assert mods[0].shared_input.launches == 1
+            pkg.release_shared_inputs(holder)
+        return [y.detach() for y in ys], xi.grad, [p.grad.clone() for p in params]
+
+    ys_f, dx_f, gr_f = run(True)
+    ys_s, dx_s, gr_s = run(False)
+    for a, b in zip(ys_f, ys_s):
+        assert torch.equal(a, b)
+    rows = torch.arange(0, M, 13, device=dev)
+    ref_y, ref_dx = _reference(x[rows], mods, pkg.SegmentRouting.from_lengths(
+        (int((rows < 4096).sum()), int((rows >= 4096).sum())), ids), [d[rows] for d in dys])
+    for a, r in zip(ys_f, ref_y):
+        assert rel_l2(a[rows], r) <= 2e-3
+    assert rel_l2(dx_f[rows], ref_dx) <= 2e-3
+    for a, b in zip(gr_f, gr_s):
+        assert rel_l2(a, b) <= 2e-3
