@@ -46,6 +46,7 @@ sys.path.insert(0, str(ROOT))
 HBM_PEAK_GBS = 8000.0          # MI355X HBM3E
 MFMA_BF16_PEAK_TFLOPS = 2500.0  # dense bf16
 MFMA_FP8_PEAK_TFLOPS = 5000.0   # dense fp8
+MFMA_FP32_PEAK_TFLOPS = 157.3   # dense fp32
 
 
 def parse():
@@ -79,6 +80,10 @@ def parse():
                         "the reference's unfused torch path on the GPU")
     p.add_argument("--copy-calibration", action="store_true",
                    help="only run a plain 1 GiB device copy 4 times (scale for rocprofv3 FETCH_SIZE/WRITE_SIZE)")
+    p.add_argument("--profile-kernels", action="store_true",
+                   help="only launch each kernel of the step (and torch's bf16 matmul) --kernel-reps times per "
+                        "distinct linear shape of --config, each launch after a cache-evicting read, for "
+                        "rocprofv3 counter and trace passes; prints the launch schedule")
     return p.parse_args()
 
 
@@ -109,6 +114,62 @@ def copy_calibration():
     print(json.dumps({"copy_calibration_bytes": n, "copies": 4}), flush=True)
 
 
+def profile_kernels(args):
+    """Launches for rocprofv3: per distinct (K, N) linear shape of the configuration, each kernel
+    family `--kernel-reps` times, every launch preceded by a 512 MB read (a torch reduction) that
+    evicts L2 and the MALL. The printed schedule lists the launch groups in order (one group =
+    the kernels between two reads), so dispatches in a trace or counter file map to
+    (shape, family). Families: gemm_fwd (NT, fused LoRA expand), gemm_dx (NT against the
+    transposed base), gemm_dx_nn (NN against the base as stored), shrink_x, shrink_dy,
+    seg_outer_dB, seg_outer_dA (main pass + fixed-order reduction), torch_matmul (hipBLASLt)."""
+    import torch
+    import __graft_entry__
+    pkg = __graft_entry__.load_package()
+    pkg.load_library()
+    from dmd_system_amd import kernels, workloads
+    from dmd_system_amd.function import _as_operand
+    dev = torch.device("cuda:0")
+    cfg = workloads.CONFIGS[args.config]
+    if cfg.base_fp8 or cfg.dtype == "fp32":
+        raise SystemExit("--profile-kernels covers the bf16 kernels")
+    routing, scales = cfg.routing, [cfg.scale] * len(cfg.ranks)
+    R = kernels.padded_rank(cfg.ranks)
+    bf = [torch.bfloat16] * len(cfg.ranks)
+    scrub = torch.ones(args.scrub_mb << 18, dtype=torch.float32, device=dev)
+    schedule = []
+    shapes = []
+    for name, K, N in cfg.linears():
+        if (K, N) not in [(k, n) for _, k, n in shapes]:
+            shapes.append((name, K, N))
+    with torch.no_grad():
+        for i, (name, K, N) in enumerate(shapes):
+            x, w, b, As, Bs, dy = workloads.make_linear(cfg, K, N, dev, seed=cfg.seed * 100 + i)
+            wt = w.t().contiguous()
+            A_ops, B_ops = [_as_operand(a) for a in As], [_as_operand(v) for v in Bs]
+            A_t = [a.t().contiguous() for a in A_ops]
+            h_rows, h_frag = kernels.shrink(x, A_ops, 0, scales, routing, True, R)
+            g_rows, g_frag = kernels.shrink(dy, B_ops, 1, scales, routing, True, R)
+            fams = {
+                "gemm_fwd": lambda: kernels.gemm_fwd(x, w, b, h_rows, B_ops, routing),
+                "gemm_dx": lambda: kernels.gemm_fwd(dy, wt, None, g_rows, A_t, routing),
+                "gemm_dx_nn": lambda: kernels.gemm_dx(dy, w, g_rows, A_ops, routing),
+                "shrink_x": lambda: kernels.shrink(x, A_ops, 0, scales, routing, True, R),
+                "shrink_dy": lambda: kernels.shrink(dy, B_ops, 1, scales, routing, True, R),
+                "seg_outer_dB": lambda: kernels.seg_outer(dy, h_frag, R, cfg.ranks, routing, 0, bf),
+                "seg_outer_dA": lambda: kernels.seg_outer(x, g_frag, R, cfg.ranks, routing, 1, bf),
+                "torch_matmul": lambda: torch.matmul(x, w.T),
+            }
+            for fam, fn in fams.items():
+                for rep in range(args.kernel_reps + 1):  # the first group warms up (allocations)
+                    scrub.amax()
+                    fn()
+                    schedule.append(f"{name} {K}->{N} {fam}" + (" warm" if rep == 0 else ""))
+                torch.cuda.synchronize()
+            del x, w, b, As, Bs, dy, wt, h_rows, h_frag, g_rows, g_frag
+    print(json.dumps({"profile_kernels": cfg.name, "reps": args.kernel_reps,
+                      "marker": "torch amax reduction before every group", "schedule": schedule}), flush=True)
+
+
 def main():
     args = parse()
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -121,6 +182,9 @@ def main():
     import torch
     if args.copy_calibration:
         copy_calibration()
+        return
+    if args.profile_kernels:
+        profile_kernels(args)
         return
     import __graft_entry__
     pkg = __graft_entry__.load_package()
@@ -136,10 +200,14 @@ def main():
     scales = [cfg.scale] * len(cfg.ranks)
 
     fp8 = cfg.base_fp8
+    # a float32 configuration (config 1, the reference's precision='fp32') runs the float32 path:
+    # float32 tensors through the same op, on the fp32 MFMA kernels
+    f32 = cfg.dtype == "fp32"
     # ---------------- inputs (resident in HBM); an e4m3 base is stored quantised
     lins = []
     for i, (name, K, N) in enumerate(cfg.linears()):
-        x, w, b, As, Bs, dy = workloads.make_linear(cfg, K, N, dev, seed=cfg.seed * 100 + i)
+        x, w, b, As, Bs, dy = workloads.make_linear(cfg, K, N, dev, seed=cfg.seed * 100 + i,
+                                                    dtype=torch.float32 if f32 else torch.bfloat16)
         x.requires_grad_(not args.fwd_only)
         for t in As + Bs:
             t.requires_grad_(not args.fwd_only)
@@ -151,6 +219,8 @@ def main():
         lins.append(L)
     torch.cuda.synchronize()
 
+    if (args.shared_qkv or args.gated_residual) and f32:
+        raise SystemExit("--shared-qkv / --gated-residual run the bf16 kernels")
     if args.shared_qkv:
         if fp8:
             raise SystemExit("--shared-qkv stacks bf16 bases only")
@@ -303,14 +373,22 @@ def main():
             A_ops = [_as_operand(a) for a in L["As"]]
             B_ops = [_as_operand(v) for v in L["Bs"]]
             A_t = [a.t().contiguous() for a in A_ops]  # the NT form of dX contracts g with A_aᵀ
+            if f32:  # fp32 operands: A_a [r, K], B_a [N, r] (the dY shrink reads B_a as [K=N, r])
+                A32 = [a.detach().contiguous() for a in L["As"]]
+                B32 = [v.detach().contiguous() for v in L["Bs"]]
             sets = []
             for r in range(max(1, args.rotate)):
                 if r == 0:
                     x, dy = L["x"].detach(), L["dy"]
                 else:
                     gen.manual_seed(1000 * li + r)
-                    x = torch.randn(M, K, generator=gen, device=dev).to(torch.bfloat16)
-                    dy = torch.randn(M, N, generator=gen, device=dev).to(torch.bfloat16)
+                    dt = torch.float32 if f32 else torch.bfloat16
+                    x = torch.randn(M, K, generator=gen, device=dev).to(dt)
+                    dy = torch.randn(M, N, generator=gen, device=dev).to(dt)
+                if f32:
+                    sets.append(dict(x=x, dy=dy, h=kernels.f32_shrink(x, A32, 0, scales, routing, R),
+                                     g=kernels.f32_shrink(dy, B32, 1, scales, routing, R)))
+                    continue
                 h_rows, h_frag = kernels.shrink(x, A_ops, 0, scales, routing, True, R)
                 g_rows, g_frag = kernels.shrink(dy, B_ops, 1, scales, routing, True, R)
                 S = dict(x=x, dy=dy, h_rows=h_rows, h_frag=h_frag, g_rows=g_rows, g_frag=g_frag)
@@ -321,6 +399,7 @@ def main():
                 sets.append(S)
             lora_mr = sum(m * cfg.ranks[a] for m, a in seg if a >= 0)
             r_sum = sum(cfg.ranks)
+            ML = sum(m for m, a in seg if a >= 0)  # rows with an adapter: the LoRA kernels read only these
             bf = [torch.bfloat16] * len(cfg.ranks)
             runs = {
                 "gemm_fwd": ([lambda S=S: kernels.gemm_fwd(S["x"], L["w"], L["b"], S["h_rows"], B_ops, routing)
@@ -328,14 +407,29 @@ def main():
                 "gemm_dx": ([lambda S=S: kernels.gemm_fwd(S["dy"], L["wt"], None, S["g_rows"], A_t, routing)
                              for S in sets], 2 * M * K * N + 2 * lora_mr * K, 0),
                 "shrink_x": ([lambda S=S: kernels.shrink(S["x"], A_ops, 0, scales, routing, True, R) for S in sets],
-                             2 * lora_mr * K, M * K * 2 + r_sum * K * 2 + lora_mr * (2 + 4)),
+                             2 * lora_mr * K, ML * K * 2 + r_sum * K * 2 + lora_mr * (2 + 4)),
                 "shrink_dy": ([lambda S=S: kernels.shrink(S["dy"], B_ops, 1, scales, routing, True, R) for S in sets],
-                              2 * lora_mr * N, M * N * 2 + r_sum * N * 2 + lora_mr * (2 + 4)),
+                              2 * lora_mr * N, ML * N * 2 + r_sum * N * 2 + lora_mr * (2 + 4)),
                 "seg_outer_dB": ([lambda S=S: kernels.seg_outer(S["dy"], S["h_frag"], R, cfg.ranks, routing, 0, bf)
-                                  for S in sets], 2 * lora_mr * N, M * N * 2 + lora_mr * 4 + r_sum * N * 2),
+                                  for S in sets], 2 * lora_mr * N, ML * N * 2 + lora_mr * 4 + r_sum * N * 2),
                 "seg_outer_dA": ([lambda S=S: kernels.seg_outer(S["x"], S["g_frag"], R, cfg.ranks, routing, 1, bf)
-                                  for S in sets], 2 * lora_mr * K, M * K * 2 + lora_mr * 4 + r_sum * K * 2),
+                                  for S in sets], 2 * lora_mr * K, ML * K * 2 + lora_mr * 4 + r_sum * K * 2),
             }
+            if f32:
+                runs = {
+                    "gemm_fwd": ([lambda S=S: kernels.f32_gemm_fwd(S["x"], L["w"], L["b"], S["h"], B32, routing)
+                                  for S in sets], 2 * M * K * N + 2 * lora_mr * N, 0),
+                    "gemm_dx": ([lambda S=S: kernels.f32_gemm_dx(S["dy"], L["w"], S["g"], A32, routing)
+                                 for S in sets], 2 * M * K * N + 2 * lora_mr * K, 0),
+                    "shrink_x": ([lambda S=S: kernels.f32_shrink(S["x"], A32, 0, scales, routing, R) for S in sets],
+                                 2 * lora_mr * K, ML * K * 4 + r_sum * K * 4 + lora_mr * 4),
+                    "shrink_dy": ([lambda S=S: kernels.f32_shrink(S["dy"], B32, 1, scales, routing, R)
+                                   for S in sets], 2 * lora_mr * N, ML * N * 4 + r_sum * N * 4 + lora_mr * 4),
+                    "seg_outer_dB": ([lambda S=S: kernels.f32_seg_outer(S["dy"], S["h"], cfg.ranks, routing, 0)
+                                      for S in sets], 2 * lora_mr * N, ML * N * 4 + lora_mr * 4 + r_sum * N * 4),
+                    "seg_outer_dA": ([lambda S=S: kernels.f32_seg_outer(S["x"], S["g"], cfg.ranks, routing, 1)
+                                      for S in sets], 2 * lora_mr * K, ML * K * 4 + lora_mr * 4 + r_sum * K * 4),
+                }
             if fp8:
                 runs["gemm_fwd"] = ([lambda S=S: kernels.gemm_fwd_fp8(S["xq"], S["xs"], L["wq"], L["ws"], L["b"],
                                                                       S["h_rows"], B_ops, routing) for S in sets],
@@ -363,9 +457,10 @@ def main():
                    "gbs": round(v["bytes"] / v["time"] / 1e9, 1) if v["bytes"] else None}
     gem = fam["gemm_fwd"]
     gem_ach = gem["flops"] / gem["time"] / 1e12
-    gem_peak = MFMA_FP8_PEAK_TFLOPS if fp8 else MFMA_BF16_PEAK_TFLOPS
+    gem_peak = MFMA_FP8_PEAK_TFLOPS if fp8 else MFMA_FP32_PEAK_TFLOPS if f32 else MFMA_BF16_PEAK_TFLOPS
     roofline = {"kernel": ("gemm_kernel NT e4m3 base (fp8 MFMA) + fused dequantise and bf16 LoRA expand"
-                           if fp8 else "gemm_kernel NT (base GEMM + fused LoRA expand)")
+                           if fp8 else "f32_linear_kernel (fp32 MFMA base GEMM + fused LoRA expand)" if f32
+                           else "gemm_kernel NT (base GEMM + fused LoRA expand)")
                 + ", over the 6 block linears (median launch of each, cold caches)",
                 "bound": "mfma", "achieved": round(gem_ach, 1), "peak": gem_peak, "unit": "TFLOP/s",
                 "frac": round(gem_ach / gem_peak, 4),
@@ -411,8 +506,7 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": ("e4m3 base forward (fp32 accumulate), bf16 LoRA and backward" if fp8 else "bf16")
-        + ("" if cfg.dtype == "bf16" else f" (config specifies {cfg.dtype}; computed in bf16)"),
+        "dtype": "e4m3 base forward (fp32 accumulate), bf16 LoRA and backward" if fp8 else "fp32" if f32 else "bf16",
         "data": "synthetic (seeded N(0,1) activations, N(0,1/in) frozen base, Kaiming-uniform A, N(0,0.02) B)",
         "config": {"workload": f"{cfg.name}: {pass_name} of the 6 DiT block linears "
                                f"(q,k,v,o {cfg.hidden}->{cfg.hidden}; ffn {cfg.hidden}->{cfg.ffn}->{cfg.hidden}), "
