@@ -319,31 +319,49 @@ static void launch_shrink_rt(const ShrinkArgs &a, int nblocks, hipStream_t strea
 
 // ============================================================== seg_outer
 //
-// Work item = (row chunk of one segment, 64-wide j block, 256-wide c block).
-// The 4 waves of a workgroup walk the chunk's 32-row steps together, each wave
-// owning 64 of the 256 columns, and each item leaves one fp32 partial
-// [256 c x 64 j]; a second kernel adds an adapter's partials in chunk order.
-// Per step the workgroup moves, with direct-to-LDS loads, the P block
-// [32 rows x 256 c] (512 contiguous bytes per row) and the step's h fragments
-// (hi and lo, 64 j) into one of OUTER_STAGES LDS stages, so the next step is
-// in flight while one is multiplied. P stays in its natural layout; the gfx950
-// transposing LDS read (ds_read_b64_tr_b16) turns 4 rows x 4 columns into
-// per-column runs of rows, i.e. the A operand of v_mfma_f32_16x16x32_bf16
+// Work item = (row chunk of one segment, 64-wide j block, OUT_C-wide c block).
+// The NWO waves of a workgroup walk the chunk's 32-row steps together, each
+// wave owning 64 of the OUT_C = 64·NWO columns, and each item leaves one fp32
+// partial [OUT_C c x 64 j]; a second kernel adds an adapter's partials in chunk
+// order. Per step the workgroup moves, with direct-to-LDS loads, the P block
+// [32 rows x OUT_C c] (2·OUT_C contiguous bytes per row) and the step's h
+// fragments (hi and lo, 64 j) into one of OUTER_STAGES LDS stages, so the next
+// step is in flight while one is multiplied. P stays in its natural layout; the
+// gfx950 transposing LDS read (ds_read_b64_tr_b16) turns 4 rows x 4 columns
+// into per-column runs of rows, i.e. the A operand of v_mfma_f32_16x16x32_bf16
 // (rows <- c, contraction <- the 32 rows of the step, columns <- j). The h
 // fragments are stored by the shrink in that MFMA's B-operand order and are
 // read as they are (16 bytes per lane).
+//
+// Column block: every c block of a chunk reads the chunk's h fragments again,
+// so wider blocks read them fewer times. 8 waves (512 columns, two workgroups
+// per CU) for C <= 4096 (at C = 1536: 65 vs 73 us per reduction, the fragments
+// read 3 times instead of 6); 4 waves (256 columns, three workgroups per CU)
+// above, where the 8-wave form was slower (C = 8960: 256 vs 238 us).
 
-constexpr int OUT_C = 256;  // c per workgroup (4 waves x 64)
 constexpr int OUT_J = 64;   // j per workgroup
 constexpr int kMaxChunkRows = 32768;
-// Two stages (one step in flight while one is multiplied): 48 KB per workgroup
-// lets three workgroups share a CU, measured 7-8% faster than three stages and
-// two workgroups (and than more work items, whose partial sums cost more).
+constexpr int kWideOuterMaxC = 4096;  // C up to which the 8-wave (512-column) form runs
+// Two stages (one step in flight while one is multiplied): 48 KB (4 waves) lets three
+// workgroups share a CU, measured 7-8% faster than three stages and two workgroups
+// (and than more work items, whose partial sums cost more); 80 KB (8 waves) two.
 constexpr int OUTER_STAGES = 2;
-constexpr int OUTER_P_BYTES = 32 * OUT_C * 2;  // one step of P: 32 rows x 512 bytes
-constexpr int OUTER_H_BYTES = 8 * 1024;        // one step of h: 4 j-tiles x {hi, lo} x 1 KB
-constexpr int OUTER_STAGE_BYTES = OUTER_P_BYTES + OUTER_H_BYTES;
-constexpr int OUTER_DMA = (OUTER_P_BYTES + OUTER_H_BYTES) / 1024 / 4;  // 1 KB loads per wave and step
+constexpr int OUTER_H_BYTES = 8 * 1024;  // one step of h: 4 j-tiles x {hi, lo} x 1 KB
+
+template <int NWO>
+struct OuterCfg {
+  static constexpr int OUT_C = 64 * NWO;                          // c per workgroup
+  static constexpr int P_BYTES = 32 * OUT_C * 2;                  // one step of P: 32 rows
+  static constexpr int STAGE_BYTES = P_BYTES + OUTER_H_BYTES;
+  static constexpr int PL = P_BYTES / 1024 / NWO;                 // P loads per wave and step
+  static constexpr int HL = 8 / NWO;                              // h loads per wave and step
+  static constexpr int DMA = PL + HL;
+  static constexpr int CPR = OUT_C / 8;                           // 16-byte chunks per P row
+  static constexpr int RPL = 64 / CPR;                            // P rows per 1 KB load
+  // waves per SIMD the registers are sized for: 3 (4-wave) or 2 (8-wave) workgroups per CU
+  static constexpr int WAVES_PER_EU = NWO == 8 ? 4 : 2;
+  static_assert(PL * NWO * 1024 == P_BYTES && HL * NWO == 8, "whole 1 KB loads per wave");
+};
 
 struct OuterArgs {
   const uint16_t *P;
@@ -361,8 +379,11 @@ struct OuterArgs {
   SegTable seg;
 };
 
-__global__ __launch_bounds__(256, 2) void seg_outer_kernel(const OuterArgs args) {
-  __shared__ u32x4 smem[OUTER_STAGES * OUTER_STAGE_BYTES / 16];
+template <int NWO>
+__global__ __launch_bounds__((64 * NWO), (OuterCfg<NWO>::WAVES_PER_EU)) void seg_outer_kernel(const OuterArgs args) {
+  using OC = OuterCfg<NWO>;
+  constexpr int OUT_C = OC::OUT_C;
+  __shared__ u32x4 smem[OUTER_STAGES * OC::STAGE_BYTES / 16];
   MLORA_LDS char *lds = (MLORA_LDS char *)smem;
   const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
   const int item = blockIdx.x;
@@ -388,32 +409,41 @@ __global__ __launch_bounds__(256, 2) void seg_outer_kernel(const OuterArgs args)
   const __amdgpu_buffer_rsrc_t rh =
       make_rsrc(args.Hf + (block0 * args.jtiles) * 128, (int64_t)nsteps * args.jtiles * 2048);
 
-  // Loader. A 1 KB P load covers 2 rows (32 chunks of 16 bytes each); chunk
-  // cc of step row rr sits at LDS slot cc ^ (4 * (rr & 3)), so lane L fetches
-  // the chunk whose slot it fills: two lane patterns by the load's parity.
-  int32_t p_off[2];
+  // Loader. A 1 KB P load covers RPL rows of CPR 16-byte chunks; chunk cc of
+  // step row rr sits at LDS slot cc ^ (4 * (rr & 3)), so lane L fetches the
+  // chunk whose slot it fills. This wave's loads: P loads PL·w .. PL·w + PL - 1
+  // of the step, h loads HL·w .. HL·w + HL - 1 of the 8.
+  int32_t p_off[OC::PL], p_row[OC::PL];
 #pragma unroll
-  for (int par = 0; par < 2; ++par) {
-    const int cc = (lane & 31) ^ (4 * ((2 * par + (lane >> 5)) & 3));
-    p_off[par] = c0 + 8 * cc < args.C ? (lane >> 5) * ldp_b + 16 * cc : kOOB;
+  for (int i = 0; i < OC::PL; ++i) {
+    const int q = OC::PL * wave + i;
+    const int row = OC::RPL * q + lane / OC::CPR;
+    const int cc = (lane % OC::CPR) ^ (4 * (row & 3));
+    p_off[i] = c0 + 8 * cc < args.C ? (lane / OC::CPR) * ldp_b + 16 * cc : kOOB;
+    p_row[i] = OC::RPL * q;
   }
   const int32_t h_step = args.jtiles * 2048;
-  // this wave's loads: P loads 4w..4w+3 of the 16 per step, h loads 2w, 2w+1 of the 8
   auto issue = [&](auto st_c, int step) {
-    MLORA_LDS char *base = lds + decltype(st_c)::value * OUTER_STAGE_BYTES;
+    MLORA_LDS char *base = lds + decltype(st_c)::value * OC::STAGE_BYTES;
     const bool live = step < nsteps;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int q = 4 * wave + i;  // wave-uniform
-      const int32_t off = live ? p_off[q & 1] : kOOB;
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rp, base + q * 1024, 16, off, (32 * step + 2 * q) * ldp_b, 0, 0);
+    for (int i = 0; i < OC::PL; ++i) {
+      const int q = OC::PL * wave + i;  // wave-uniform
+      const int32_t off = live ? p_off[i] : kOOB;
+      // (operands go through variables: template-dependent expressions written inline in the
+      // builtin call make the host compilation pass drop the kernel instantiation)
+      const int32_t soff = (32 * step + p_row[i]) * ldp_b;
+      MLORA_LDS void *dst = base + q * 1024;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rp, dst, 16, off, soff, 0, 0);
     }
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const int q = 2 * wave + i;  // (j-tile, part) = (q / 2, q % 2) of this j block
+    for (int i = 0; i < OC::HL; ++i) {
+      const int q = OC::HL * wave + i;  // (j-tile, part) = (q / 2, q % 2) of this j block
       const int t = (j0 >> 4) + (q >> 1);
       const int32_t off = live && 16 * t < r ? ((t * 2 + (q & 1)) * 64 + lane) * 16 : kOOB;
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rh, base + OUTER_P_BYTES + q * 1024, 16, off, step * h_step, 0, 0);
+      const int32_t soff = step * h_step;
+      MLORA_LDS void *dst = base + OC::P_BYTES + q * 1024;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rh, dst, 16, off, soff, 0, 0);
     }
   };
 
@@ -437,12 +467,12 @@ __global__ __launch_bounds__(256, 2) void seg_outer_kernel(const OuterArgs args)
     for (int q = 0; q < 4; ++q) acc[t][q] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   auto compute = [&](auto st_c) {
-    const MLORA_LDS char *base = lds + decltype(st_c)::value * OUTER_STAGE_BYTES;
+    const MLORA_LDS char *base = lds + decltype(st_c)::value * OC::STAGE_BYTES;
     bf16x8 hi[4], lo[4], af[4];
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-      hi[q] = as_bf16x8(*(const lds_u4 *)(base + OUTER_P_BYTES + (2 * q) * 1024 + 16 * lane));
-      lo[q] = as_bf16x8(*(const lds_u4 *)(base + OUTER_P_BYTES + (2 * q + 1) * 1024 + 16 * lane));
+      hi[q] = as_bf16x8(*(const lds_u4 *)(base + OC::P_BYTES + (2 * q) * 1024 + 16 * lane));
+      lo[q] = as_bf16x8(*(const lds_u4 *)(base + OC::P_BYTES + (2 * q + 1) * 1024 + 16 * lane));
     }
     u32x4 at[4];
     lds_read_tr16_x4<4 * OUT_C * 2>(base, a_addr, at);  // rows +4: the second half of each fragment
@@ -466,7 +496,7 @@ __global__ __launch_bounds__(256, 2) void seg_outer_kernel(const OuterArgs args)
   auto step = [&](auto cur, int i) -> bool {
     if (i >= nsteps) return false;
     constexpr int refill = (decltype(cur)::value + OUTER_STAGES - 1) % OUTER_STAGES;
-    wait_vmcnt<(OUTER_STAGES - 2) * OUTER_DMA>();  // this wave's loads of step i landed
+    wait_vmcnt<(OUTER_STAGES - 2) * OC::DMA>();  // this wave's loads of step i landed
     lds_pipeline_barrier();                        // everyone's did; everyone is done with step i-1
     issue(std::integral_constant<int, refill>{}, i + OUTER_STAGES - 1);
     compute(cur);
@@ -548,6 +578,7 @@ __global__ __launch_bounds__(256) void seg_outer_reduce_kernel(const ReduceArgs 
 
 // Chunking shared by the entry point and the workspace query.
 struct OuterPlan {
+  int32_t nwo = 4;  // waves per workgroup: 64·nwo columns per work item
   int32_t chunk_rows = 0, cblocks = 0, jblocks = 0, rpad = 0, n_chunks = 0;
   int32_t chunk_start[kMaxSeg + 1];
 };
@@ -564,7 +595,9 @@ static void plan_outer(OuterPlan &pl, const SegTable &st, const int32_t *rank, i
       rmax = rank[a] > rmax ? rank[a] : rmax;
     }
   }
-  pl.cblocks = (int32_t)((C + OUT_C - 1) / OUT_C);
+  pl.nwo = C <= kWideOuterMaxC ? 8 : 4;
+  const int64_t out_c = 64 * (int64_t)pl.nwo;
+  pl.cblocks = (int32_t)((C + out_c - 1) / out_c);
   pl.jblocks = (rmax + OUT_J - 1) / OUT_J;
   pl.rpad = pl.jblocks * OUT_J;
   // aim at ~512 work items (2 per CU) with chunks of at least 512 rows
@@ -743,7 +776,10 @@ static int seg_outer_run(OuterArgs &a, const OuterPlan &pl, const void *p, int64
     for (int i = 0; i <= a.seg.n; ++i) a.chunk_start[i] = pl.chunk_start[i];
     const int64_t items = (int64_t)pl.n_chunks * pl.jblocks * pl.cblocks;
     if (items > INT32_MAX) return MLORA_ERR_LIMIT;
-    hipLaunchKernelGGL(seg_outer_kernel, dim3((unsigned)items), dim3(256), 0, s, a);
+    if (pl.nwo == 8)
+      hipLaunchKernelGGL(seg_outer_kernel<8>, dim3((unsigned)items), dim3(512), 0, s, a);
+    else
+      hipLaunchKernelGGL(seg_outer_kernel<4>, dim3((unsigned)items), dim3(256), 0, s, a);
     if ((st = launch_status())) return st;
   }
   ReduceArgs ra{};

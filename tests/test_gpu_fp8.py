@@ -201,6 +201,46 @@ def test_module_quantize_base_fp8(pkg, dev):
     assert all(p.grad is not None for p in lin.lora_a) and base.weight.grad is None
 
 
+def test_fp8_base_reloaded_from_a_state_dict(pkg, dev):
+    """load_state_dict of another quantised module into one that already ran: the forward and
+    the e4m3 dX then use the loaded base (the transposed e4m3 copy for dX is rebuilt), bit for
+    bit as the other module, and dX matches the oracle on the loaded e4m3 weights."""
+    torch.manual_seed(5)
+
+    def make():
+        base = torch.nn.Linear(256, 128).to(dev)
+        lin = pkg.MultiLoRALinear(base, ranks=[16], alphas=[16.0]).to(dev)
+        with torch.no_grad():
+            lin.lora_b[0].normal_(0, 0.02)
+        lin.quantize_base_fp8()
+        return lin
+
+    lin, other = make(), make()
+    x = torch.randn(200, 256, device=dev).to(torch.bfloat16)
+    routing = pkg.SegmentRouting.single(200, 0)
+    dy = torch.randn(200, 128, device=dev).to(torch.bfloat16)
+
+    def run(m):
+        xg = x.clone().requires_grad_(True)
+        with torch.autocast("cuda", dtype=torch.bfloat16):
+            y = m(xg, routing)
+        y.backward(dy)
+        torch.cuda.synchronize()
+        return y.detach(), xg.grad
+
+    y_before, dx_before = run(lin)  # builds lin's transposed e4m3 base
+    lin.load_state_dict(other.state_dict())
+    assert torch.equal(lin.base_wq.view(torch.uint8), other.base_wq.view(torch.uint8))
+    y, dx = run(lin)
+    y_o, dx_o = run(other)
+    assert torch.equal(y, y_o) and torch.equal(dx, dx_o)
+    assert not torch.equal(dx, dx_before)
+    bf = lambda t: f64(t.to(torch.bfloat16))  # noqa: E731
+    dx_kern = O.dx_fp8_quantized_dy(f64(dy), u8(lin.base_wq), lin.base_wscale.cpu().numpy(),
+                                    [bf(lin.lora_a[0])], [bf(lin.lora_b[0])], lin.scales, [0, 200], [0])
+    assert O.rel_l2(f64(dx), dx_kern) <= TOL
+
+
 @pytest.mark.parametrize("K,N", [(1536, 1536), (1536, 8960), (8960, 1536)])
 def test_wan13b_fp8_full_shape(pkg, dev, K, N):
     """Config 5 at full size (65520 tokens, 4 rank-64 adapters on seeded segments) at each of its

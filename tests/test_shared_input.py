@@ -71,3 +71,15 @@ def test_scales_must_agree(pkg):
     # biases may differ: one member with, one without
     holder.b = pkg.MultiLoRALinear(nn.Linear(256, 512, bias=False), ranks=[16], alphas=[16])
     assert len(pkg.fuse_shared_inputs(holder, [["a", "b"]])) == 1
+
+
+def test_stacked_rank_above_the_kernel_limit_fails_at_fuse_time(pkg):
+    """G members of rank r share one h of G·r columns: more than the kernels' 256 is a
+    ValueError when the group is made, not a kernel error on the first forward."""
+    holder = nn.Module()
+    for name in ("q", "k", "v"):
+        setattr(holder, name, pkg.MultiLoRALinear(nn.Linear(256, 256), ranks=[128], alphas=[128]))
+    with pytest.raises(ValueError, match="256"):
+        pkg.fuse_shared_inputs(holder, [["q", "k", "v"]])
+    # two members of rank 128 fit exactly
+    assert len(pkg.fuse_shared_inputs(holder, [["q", "k"]])) == 1
