@@ -147,7 +147,7 @@ class TrainableLowRankLinear(nn.Module):
 
     def gated_residual(self, value, residual, gate):
         """``residual + self(value) * gate`` of a DiT block (model.py:305-313), fused into the
-        GEMM epilogue (bf16 residual stream, frozen fp32 gate)."""
+        GEMM epilogue (bf16 or float32 residual stream, output in its dtype; frozen fp32 gate)."""
         rows = value.numel() // value.shape[-1] if value.dim() else 0
         return multi_lora_linear_gated(value, self.base.weight, self.base.bias, [self.lora_a], [self.lora_b],
                                        [self.scale], SegmentRouting.single(rows, 0), residual, gate,
@@ -343,7 +343,7 @@ class MultiLoRALinear(nn.Module):
     def gated_residual(self, x: torch.Tensor, residual: torch.Tensor, gate: torch.Tensor,
                        routing: SegmentRouting | None = None) -> torch.Tensor:
         """``residual + self(x, routing) * gate`` of a DiT block (model.py:305-313), fused into
-        the GEMM epilogue (bf16 residual stream, frozen fp32 gate)."""
+        the GEMM epilogue (bf16 or float32 residual stream, output in its dtype; frozen fp32 gate)."""
         if getattr(self, "base_wq", None) is not None:
             raise RuntimeError("gated residual: the e4m3 base is not fused; call the linear and add")
         return multi_lora_linear_gated(x, self.base.weight, self.base.bias, list(self.lora_a), list(self.lora_b),
