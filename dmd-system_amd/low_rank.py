@@ -226,6 +226,20 @@ def install_lora(model: nn.Module, task) -> list[str]:
     return [n for n, _ in found]
 
 
+def _routing_from_arrays(seg_offsets, adapter_ids) -> SegmentRouting:
+    """SegmentRouting from segment offsets [S+1] and adapter ids [S] (integer sequences or CPU
+    tensors: the routing is host data, read when the kernels are launched)."""
+    def ints(v, name):
+        if isinstance(v, torch.Tensor):
+            if v.is_cuda or v.is_floating_point() or v.dim() != 1:
+                raise ValueError(f'multi-LoRA linear: {name} must be a 1-D integer CPU tensor or a sequence')
+            v = v.tolist()
+        if v is None:
+            raise ValueError(f'multi-LoRA linear: {name} is required with adapter_ids')
+        return [int(e) for e in v]
+    return SegmentRouting(tuple(ints(seg_offsets, 'seg_offsets')), tuple(ints(adapter_ids, 'adapter_ids')))
+
+
 class MultiLoRALinear(nn.Module):
     """One frozen base nn.Linear shared by several adapters, routed by segment.
 
@@ -324,9 +338,15 @@ class MultiLoRALinear(nn.Module):
             self.__dict__['_wq_t_cache'] = cache
         return wq, self.base_wscale, cache[1]
 
-    def forward(self, x: torch.Tensor, routing: SegmentRouting | None = None) -> torch.Tensor:
-        """x [..., in] -> [..., out]. Without ``routing`` the active RoleBatch (set by
-        ``roles.roles_active``) routes x's sample-major rows."""
+    def forward(self, x: torch.Tensor, routing=None, adapter_ids=None) -> torch.Tensor:
+        """x [..., in] -> [..., out]. ``routing``: a SegmentRouting, or the segment offsets
+        [S+1] with ``adapter_ids`` [S] given too (sequences or CPU integer tensors; -1 = base
+        only). Without either, the active RoleBatch (set by ``roles.roles_active``) routes x's
+        sample-major rows."""
+        if adapter_ids is not None:
+            routing = _routing_from_arrays(routing, adapter_ids)
+        elif routing is not None and not isinstance(routing, SegmentRouting):
+            raise ValueError('multi-LoRA linear: routing is a SegmentRouting, or seg_offsets with adapter_ids')
         group = self.__dict__.get('shared_input')
         if group is not None:  # stacked with the other linears that read this input
             return group(self, x, routing)

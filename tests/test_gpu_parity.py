@@ -142,6 +142,22 @@ def test_routing_is_bit_exact(pkg, dev):
     assert not torch.equal(y[row == 0], y_base[row == 0])
 
 
+def test_module_forward_with_segment_arrays(pkg, dev):
+    """MultiLoRALinear.forward(x, seg_offsets, adapter_ids) equals the call with the same
+    SegmentRouting, bit for bit."""
+    torch.manual_seed(16)
+    m = pkg.MultiLoRALinear(torch.nn.Linear(128, 96), ranks=[8, 16], alphas=[8.0, 32.0]).to(dev)
+    with torch.no_grad():
+        for b in m.lora_b:
+            b.normal_(0, 0.05)
+    x = torch.randn(300, 128, device=dev)
+    off, ids = [0, 100, 180, 300], [1, -1, 0]
+    with torch.no_grad(), torch.autocast("cuda", dtype=torch.bfloat16):
+        y_arrays = m(x, torch.tensor(off), torch.tensor(ids))
+        y_routing = m(x, pkg.SegmentRouting(tuple(off), tuple(ids)))
+    assert torch.equal(y_arrays, y_routing)
+
+
 def test_deterministic(pkg, dev):
     lengths, ids = (300, 212), (0, 1)
     case = make_case(512, 256, 256, (8, 8), lengths, ids, seed=16)

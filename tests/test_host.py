@@ -119,6 +119,26 @@ def test_no_cpu_path(pkg):
         mixed(x.float(), pkg.SegmentRouting.single(4))
 
 
+def test_forward_takes_segment_arrays(pkg):
+    """forward(x, seg_offsets, adapter_ids): the routing as plain arrays (sequences or 1-D
+    integer CPU tensors) is the same SegmentRouting; malformed arrays fail closed before any
+    device work."""
+    from dmd_system_amd.low_rank import _routing_from_arrays
+    want = pkg.SegmentRouting.from_lengths((3, 1), (0, -1))
+    assert _routing_from_arrays([0, 3, 4], [0, -1]) == want
+    assert _routing_from_arrays(torch.tensor([0, 3, 4]), torch.tensor([0, -1], dtype=torch.int32)) == want
+    m = pkg.MultiLoRALinear(nn.Linear(16, 8).to(torch.bfloat16), ranks=[8], alphas=[8])
+    x = torch.randn(4, 16, dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="1-D integer CPU tensor"):
+        m(x, torch.tensor([0.0, 4.0]), [0])
+    with pytest.raises(ValueError, match="seg_offsets is required"):
+        m(x, None, [0])
+    with pytest.raises(ValueError, match="SegmentRouting, or seg_offsets with adapter_ids"):
+        m(x, [0, 4])
+    with pytest.raises(RuntimeError, match="ROCm device only"):  # well-formed: reaches the device check
+        m(x, [0, 4], [0])
+
+
 def test_native_lora_install_contract(pkg):
     """install_lora / LoRALinear keep native/models.py:33-64: fp32 masters `a` (Kaiming-uniform) and
     `b` (zeros) over a frozen base, scale alpha / rank, suffix matching, fail-closed messages."""
