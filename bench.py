@@ -121,7 +121,8 @@ def profile_kernels(args):
     the kernels between two reads), so dispatches in a trace or counter file map to
     (shape, family). Families: gemm_fwd (NT, fused LoRA expand), gemm_dx (NT against the
     transposed base), gemm_dx_nn (NN against the base as stored), shrink_x, shrink_dy,
-    seg_outer_dB, seg_outer_dA (main pass + fixed-order reduction), torch_matmul (hipBLASLt)."""
+    seg_outer_dB, seg_outer_dA (main pass + fixed-order reduction), torch_matmul (hipBLASLt);
+    last, a plain 1 GiB device copy as the reference rate of HBM-bound kernels."""
     import torch
     import __graft_entry__
     pkg = __graft_entry__.load_package()
@@ -166,6 +167,15 @@ def profile_kernels(args):
                     schedule.append(f"{name} {K}->{N} {fam}" + (" warm" if rep == 0 else ""))
                 torch.cuda.synchronize()
             del x, w, b, As, Bs, dy, wt, h_rows, h_frag, g_rows, g_frag
+        # reference point for the HBM-bound kernels: a plain 1 GiB device copy (torch's copy kernel)
+        src = torch.ones(1 << 29, dtype=torch.float16, device=dev)
+        dst = torch.empty_like(src)
+        for rep in range(args.kernel_reps + 1):
+            scrub.amax()
+            dst.copy_(src)
+            schedule.append("copy 1GiB copy" + (" warm" if rep == 0 else ""))
+        torch.cuda.synchronize()
+        del src, dst
     print(json.dumps({"profile_kernels": cfg.name, "reps": args.kernel_reps,
                       "marker": "torch amax reduction before every group", "schedule": schedule}), flush=True)
 
