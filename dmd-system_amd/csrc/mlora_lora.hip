@@ -319,13 +319,14 @@ static void launch_shrink_rt(const ShrinkArgs &a, int nblocks, hipStream_t strea
 
 // ============================================================== seg_outer
 //
-// Work item = (row chunk of one segment, 64-wide j block, OUT_C-wide c block).
+// Work item = (row chunk of one segment, OUT_J-wide j block, OUT_C-wide c block).
 // The NWO waves of a workgroup walk the chunk's 32-row steps together, each
 // wave owning 64 of the OUT_C = 64·NWO columns, and each item leaves one fp32
-// partial [OUT_C c x 64 j]; a second kernel adds an adapter's partials in chunk
+// partial [OUT_C c x OUT_J j] (OUT_J = 64, or 128 when most rows have an
+// adapter of rank > 64); a second kernel adds an adapter's partials in chunk
 // order. Per step the workgroup moves, with direct-to-LDS loads, the P block
 // [32 rows x OUT_C c] (2·OUT_C contiguous bytes per row) and the step's h
-// fragments (hi and lo, 64 j) into one of OUTER_STAGES LDS stages, so the next
+// fragments (hi and lo, OUT_J j) into one of OUTER_STAGES LDS stages, so the next
 // step is in flight while one is multiplied. P stays in its natural layout; the
 // gfx950 transposing LDS read (ds_read_b64_tr_b16) turns 4 rows x 4 columns
 // into per-column runs of rows, i.e. the A operand of v_mfma_f32_16x16x32_bf16
@@ -339,28 +340,32 @@ static void launch_shrink_rt(const ShrinkArgs &a, int nblocks, hipStream_t strea
 // read 3 times instead of 6); 4 waves (256 columns, three workgroups per CU)
 // above, where the 8-wave form was slower (C = 8960: 256 vs 238 us).
 
-constexpr int OUT_J = 64;   // j per workgroup
 constexpr int kMaxChunkRows = 32768;
 constexpr int kWideOuterMaxC = 4096;  // C up to which the 8-wave (512-column) form runs
-// Two stages (one step in flight while one is multiplied): 48 KB (4 waves) lets three
+// Two stages (one step in flight while one is multiplied): 48 KB (4 waves, 64 j) lets three
 // workgroups share a CU, measured 7-8% faster than three stages and two workgroups
 // (and than more work items, whose partial sums cost more); 80 KB (8 waves) two.
 constexpr int OUTER_STAGES = 2;
-constexpr int OUTER_H_BYTES = 8 * 1024;  // one step of h: 4 j-tiles x {hi, lo} x 1 KB
 
-template <int NWO>
+// NJ: 16-wide j tiles per work item (4: 64 j; 8: 128 j, for adapters of rank 65-128, so that
+// P is streamed once per chunk instead of once per 64 j).
+template <int NWO, int NJ>
 struct OuterCfg {
   static constexpr int OUT_C = 64 * NWO;                          // c per workgroup
+  static constexpr int OUT_J = 16 * NJ;                           // j per workgroup
   static constexpr int P_BYTES = 32 * OUT_C * 2;                  // one step of P: 32 rows
-  static constexpr int STAGE_BYTES = P_BYTES + OUTER_H_BYTES;
+  static constexpr int H_BYTES = NJ * 2 * 1024;                   // one step of h: NJ j-tiles x {hi, lo}
+  static constexpr int STAGE_BYTES = P_BYTES + H_BYTES;
   static constexpr int PL = P_BYTES / 1024 / NWO;                 // P loads per wave and step
-  static constexpr int HL = 8 / NWO;                              // h loads per wave and step
+  static constexpr int HL = 2 * NJ / NWO;                         // h loads per wave and step
   static constexpr int DMA = PL + HL;
   static constexpr int CPR = OUT_C / 8;                           // 16-byte chunks per P row
   static constexpr int RPL = 64 / CPR;                            // P rows per 1 KB load
-  // waves per SIMD the registers are sized for: 3 (4-wave) or 2 (8-wave) workgroups per CU
-  static constexpr int WAVES_PER_EU = NWO == 8 ? 4 : 2;
-  static_assert(PL * NWO * 1024 == P_BYTES && HL * NWO == 8, "whole 1 KB loads per wave");
+  // waves per SIMD the registers are sized for: 64 j: 3 (4-wave) or 2 (8-wave) workgroups per
+  // CU; 128 j (twice the accumulators): two 4-wave or one 8-wave workgroup
+  static constexpr int WAVES_PER_EU = NJ == 8 ? 2 : NWO == 8 ? 4 : 2;
+  static_assert(PL * NWO * 1024 == P_BYTES && HL * NWO == 2 * NJ, "whole 1 KB loads per wave");
+  static_assert(OUTER_STAGES * STAGE_BYTES <= 163840, "the stages fit the LDS");
 };
 
 struct OuterArgs {
@@ -379,9 +384,9 @@ struct OuterArgs {
   SegTable seg;
 };
 
-template <int NWO>
-__global__ __launch_bounds__((64 * NWO), (OuterCfg<NWO>::WAVES_PER_EU)) void seg_outer_kernel(const OuterArgs args) {
-  using OC = OuterCfg<NWO>;
+template <int NWO, int NJ>
+__global__ __launch_bounds__((64 * NWO), (OuterCfg<NWO, NJ>::WAVES_PER_EU)) void seg_outer_kernel(const OuterArgs args) {
+  using OC = OuterCfg<NWO, NJ>;
   constexpr int OUT_C = OC::OUT_C;
   __shared__ u32x4 smem[OUTER_STAGES * OC::STAGE_BYTES / 16];
   MLORA_LDS char *lds = (MLORA_LDS char *)smem;
@@ -394,7 +399,7 @@ __global__ __launch_bounds__((64 * NWO), (OuterCfg<NWO>::WAVES_PER_EU)) void seg
   while (s + 1 < args.seg.n && args.chunk_start[s + 1] <= chunk) ++s;
   const int a = args.seg.aid[s];
   const int r = args.rank[a];
-  const int j0 = jb * OUT_J;
+  const int j0 = jb * OC::OUT_J;
   if (j0 >= r) return;  // whole workgroup exits together
   const int rel0 = (chunk - args.chunk_start[s]) * args.chunk_rows;  // multiple of 32
   const int row0 = args.seg.off[s] + rel0;
@@ -460,17 +465,17 @@ __global__ __launch_bounds__((64 * NWO), (OuterCfg<NWO>::WAVES_PER_EU)) void seg
     a_addr[t] = row * (OUT_C * 2) + 16 * (cc ^ (4 * (row & 3))) + 8 * (li & 1);
   }
 
-  f32x4 acc[4][4];
+  f32x4 acc[4][NJ];
 #pragma unroll
   for (int t = 0; t < 4; ++t)
 #pragma unroll
-    for (int q = 0; q < 4; ++q) acc[t][q] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int q = 0; q < NJ; ++q) acc[t][q] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   auto compute = [&](auto st_c) {
     const MLORA_LDS char *base = lds + decltype(st_c)::value * OC::STAGE_BYTES;
-    bf16x8 hi[4], lo[4], af[4];
+    bf16x8 hi[NJ], lo[NJ], af[4];
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
+    for (int q = 0; q < NJ; ++q) {
       hi[q] = as_bf16x8(*(const lds_u4 *)(base + OC::P_BYTES + (2 * q) * 1024 + 16 * lane));
       lo[q] = as_bf16x8(*(const lds_u4 *)(base + OC::P_BYTES + (2 * q + 1) * 1024 + 16 * lane));
     }
@@ -481,7 +486,7 @@ __global__ __launch_bounds__((64 * NWO), (OuterCfg<NWO>::WAVES_PER_EU)) void seg
 #pragma unroll
     for (int t = 0; t < 4; ++t)
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
+      for (int q = 0; q < NJ; ++q) {
         acc[t][q] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[t], hi[q], acc[t][q], 0, 0, 0);
         acc[t][q] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[t], lo[q], acc[t][q], 0, 0, 0);
       }
@@ -519,7 +524,7 @@ __global__ __launch_bounds__((64 * NWO), (OuterCfg<NWO>::WAVES_PER_EU)) void seg
       const int c = c0 + 64 * wave + 16 * t + 4 * lg + v;
       if (c >= args.C) continue;
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
+      for (int q = 0; q < NJ; ++q) {
         const int j = j0 + 16 * q + li;
         if (j < r) dst[(int64_t)c * args.rpad + j] = acc[t][q][v];
       }
@@ -579,6 +584,7 @@ __global__ __launch_bounds__(256) void seg_outer_reduce_kernel(const ReduceArgs 
 // Chunking shared by the entry point and the workspace query.
 struct OuterPlan {
   int32_t nwo = 4;  // waves per workgroup: 64·nwo columns per work item
+  int32_t nj = 4;   // 16-wide j tiles per work item
   int32_t chunk_rows = 0, cblocks = 0, jblocks = 0, rpad = 0, n_chunks = 0;
   int32_t chunk_start[kMaxSeg + 1];
 };
@@ -586,20 +592,26 @@ struct OuterPlan {
 // chunk_floor: the smallest chunk (rows) to use; 0 for the default plan.
 static void plan_outer(OuterPlan &pl, const SegTable &st, const int32_t *rank, int64_t C, int64_t chunk_floor = 0) {
   int rmax = 0;
-  int64_t rows = 0;
+  int64_t rows = 0, rows_wide = 0;  // rows with an adapter; of them, rows of rank > 64
   for (int s = 0; s < st.n; ++s) {
     const int a = st.aid[s];
     const int len = st.off[s + 1] - st.off[s];
     if (a >= 0 && rank[a] > 0 && len > 0) {
       rows += len;
+      if (rank[a] > 64) rows_wide += len;
       rmax = rank[a] > rmax ? rank[a] : rmax;
     }
   }
   pl.nwo = C <= kWideOuterMaxC ? 8 : 4;
   const int64_t out_c = 64 * (int64_t)pl.nwo;
   pl.cblocks = (int32_t)((C + out_c - 1) / out_c);
-  pl.jblocks = (rmax + OUT_J - 1) / OUT_J;
-  pl.rpad = pl.jblocks * OUT_J;
+  // 128 j per item when most rows have an adapter of rank > 64 (their P is then streamed once
+  // instead of twice); with few such rows the 64-j items, whose second j block exits at once
+  // for the smaller ranks, are faster (config 4's mixed ranks: 3%)
+  pl.nj = 2 * rows_wide > rows ? 8 : 4;
+  const int out_j = 16 * pl.nj;
+  pl.jblocks = (rmax + out_j - 1) / out_j;
+  pl.rpad = pl.jblocks * out_j;
   // aim at ~512 work items (2 per CU) with chunks of at least 512 rows
   const int64_t target_items = 512;
   int64_t cr = rows * pl.cblocks * (pl.jblocks > 0 ? pl.jblocks : 1) / target_items;
@@ -776,10 +788,14 @@ static int seg_outer_run(OuterArgs &a, const OuterPlan &pl, const void *p, int64
     for (int i = 0; i <= a.seg.n; ++i) a.chunk_start[i] = pl.chunk_start[i];
     const int64_t items = (int64_t)pl.n_chunks * pl.jblocks * pl.cblocks;
     if (items > INT32_MAX) return MLORA_ERR_LIMIT;
-    if (pl.nwo == 8)
-      hipLaunchKernelGGL(seg_outer_kernel<8>, dim3((unsigned)items), dim3(512), 0, s, a);
+    if (pl.nwo == 8 && pl.nj == 8)
+      hipLaunchKernelGGL((seg_outer_kernel<8, 8>), dim3((unsigned)items), dim3(512), 0, s, a);
+    else if (pl.nwo == 8)
+      hipLaunchKernelGGL((seg_outer_kernel<8, 4>), dim3((unsigned)items), dim3(512), 0, s, a);
+    else if (pl.nj == 8)
+      hipLaunchKernelGGL((seg_outer_kernel<4, 8>), dim3((unsigned)items), dim3(256), 0, s, a);
     else
-      hipLaunchKernelGGL(seg_outer_kernel<4>, dim3((unsigned)items), dim3(256), 0, s, a);
+      hipLaunchKernelGGL((seg_outer_kernel<4, 4>), dim3((unsigned)items), dim3(256), 0, s, a);
     if ((st = launch_status())) return st;
   }
   ReduceArgs ra{};
