@@ -827,7 +827,7 @@ __device__ __forceinline__ void store_tile(const f32x16 (&acc)[C::TM][C::TN], co
         continue;
       }
     }
-    buf_store16(ry, off, d);
+    buf_store16_nt(ry, off, d);
   }
 }
 
