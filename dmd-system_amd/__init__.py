@@ -13,6 +13,8 @@ Public API:
     export_adapters, import_adapters, save_adapters, load_adapters   PEFT / DiffSynth adapter state
     install_peft_multi_lora, peft_roles_active   PEFT LoRA layers (W1 / H3) on the multi-LoRA op
     kernels                              torch front end of each C-ABI entry point
+    fused_modulated_norm_epilogue, fused_modulated_norm_materialization,
+    fused_bf16_layernorm_modulation, fused_layernorm_modulation   the block's modulated LayerNorm
     load_library()                       load libmlora.so (raises if missing)
 
 The directory name is not a Python identifier; importers load it as
@@ -30,6 +32,8 @@ from .roles import RoleBatch, fuse_roles, roles_active
 from .routing import BASE_ONLY, SegmentRouting
 from .shared_input import SharedInputGroup, fuse_shared_inputs, release_shared_inputs
 from .peft_site import install_peft_multi_lora, peft_roles_active, uninstall_peft_multi_lora
+from .modulated_norm import (fused_bf16_layernorm_modulation, fused_layernorm_modulation,
+                             fused_modulated_norm_epilogue, fused_modulated_norm_materialization)
 
 
 def load_library():
@@ -44,4 +48,6 @@ __all__ = [
     "SharedInputMultiLoRAFunction", "StackedLinearsFunction", "shared_input_multi_lora", "SharedInputGroup", "fuse_shared_inputs",
     "release_shared_inputs", "export_adapters", "import_adapters", "save_adapters", "load_adapters", "kernels",
     "load_library", "install_peft_multi_lora", "uninstall_peft_multi_lora", "peft_roles_active",
+    "fused_modulated_norm_epilogue", "fused_modulated_norm_materialization", "fused_bf16_layernorm_modulation",
+    "fused_layernorm_modulation",
 ]

@@ -12,7 +12,7 @@ from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "libmlora.so"
 
-ABI_VERSION = 6
+ABI_VERSION = 7
 MAX_SEGMENTS = 128
 MAX_ADAPTERS = 32
 MAX_RANK = 256
@@ -48,6 +48,8 @@ SIGNATURES = {
                                     _pvp, _pi32, _i32, _pi64, _pi32, _i32, _vp, _i64, _vp, _i64, _i64,
                                     _vp, _i64, _int, _vp]),
     "mlora_gate_scale_rows": (_int, [_vp, _i64, _i64, _i64, _vp, _i64, _i64, _vp, _i64, _int, _vp]),
+    "mlora_modulated_norm": (_int, [_vp, _int, _i64, _i64, _int, ctypes.c_float, _vp, _vp, _int, _vp, _int, _vp, _int,
+                                    _i64, _i64, _i64, _i64, _vp, _i64, _i64, _i64, _i64, _i64, _vp]),
     "mlora_gemm_dx": (_int, [_vp, _i64, _i64, _i64, _vp, _i64, _i64, _vp, _i64,
                              _pvp, _pi32, _i32, _pi64, _pi32, _i32, _vp, _i64, _int, _vp]),
     "mlora_seg_outer": (_int, [_vp, _i64, _i64, _i64, _vp, _i32, _pvp, _int, _int, _pi32, _i32,

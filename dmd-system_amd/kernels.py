@@ -297,6 +297,43 @@ def gate_scale_rows(dout: torch.Tensor, gate: torch.Tensor) -> torch.Tensor:
     return dy
 
 
+def _rows3(name: str, t: torch.Tensor, dtypes, shape) -> None:
+    _require(t.is_cuda, f"{name} must be a ROCm device tensor")
+    _require(t.dtype in dtypes, f"{name} must be one of {[str(d) for d in dtypes]}, got {t.dtype}")
+    _require(tuple(t.shape) == tuple(shape), f"{name} has shape {tuple(t.shape)}, expected {tuple(shape)}")
+    _require(t.stride(2) == 1 or t.shape[2] <= 1, f"{name} must have unit feature stride")
+
+
+def modulated_norm(x: torch.Tensor, scale: torch.Tensor, shift: torch.Tensor, out: torch.Tensor, *,
+                   eps: float | None = None, scale_row: torch.Tensor | None = None,
+                   shift_row: torch.Tensor | None = None) -> torch.Tensor:
+    """out[b,t,f] = bf16(RN(RN(v · RN(1 + s)) + h)) over [B, T, W] operands, where
+    v = LayerNorm(x) (affine-free, when eps is given; x bf16 or float32) or x itself (float32,
+    already normalized), and s / h are scale / shift, each first added (RN) to a table row
+    [W] when scale_row / shift_row are given. Operands may broadcast over tokens (stride 0)."""
+    B, T, W = x.shape
+    _rows3("x", x, (torch.bfloat16, torch.float32) if eps is not None else (torch.float32,), (B, T, W))
+    _rows3("scale", scale, (torch.bfloat16, torch.float32), (B, T, W))
+    _rows3("shift", shift, (torch.bfloat16, torch.float32), (B, T, W))
+    _rows3("output", out, (torch.bfloat16,), (B, T, W))
+    _require((scale_row is None) == (shift_row is None), "scale_row and shift_row come together")
+    if scale_row is not None:
+        for name, r in (("scale_row", scale_row), ("shift_row", shift_row)):
+            _require(r.is_cuda and r.dim() == 1 and r.shape[0] == W and r.stride(0) == 1,
+                     f"{name} must be a contiguous device vector of {W}")
+            _require(r.dtype in (torch.bfloat16, torch.float32), f"{name} must be bfloat16 or float32")
+        _require(scale_row.dtype == shift_row.dtype, "scale_row and shift_row share a dtype")
+    _require(eps is None or eps > 0, "LayerNorm epsilon must be positive")
+    lib = _lib.load()
+    tdt = _DT[scale_row.dtype] if scale_row is not None else _lib.BF16
+    _lib.check("mlora_modulated_norm", lib.mlora_modulated_norm(
+        x.data_ptr(), _DT[x.dtype], x.stride(0), x.stride(1), int(eps is not None), float(eps or 0.0),
+        _ptr(scale_row), _ptr(shift_row), tdt, scale.data_ptr(), _DT[scale.dtype], shift.data_ptr(), _DT[shift.dtype],
+        scale.stride(0), scale.stride(1), shift.stride(0), shift.stride(1),
+        out.data_ptr(), out.stride(0), out.stride(1), B, T, W, _stream(x)))
+    return out
+
+
 def gemm_dx(dy: torch.Tensor, w: torch.Tensor, g_rows: torch.Tensor | None, as_: Sequence[torch.Tensor],
             routing: SegmentRouting, out: torch.Tensor | None = None, accumulate: bool = False) -> torch.Tensor:
     """dX = dY·W + per-segment g_rows·A_a, bf16 out (accumulate: dX += ..., into `out`).

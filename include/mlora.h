@@ -43,7 +43,7 @@
 extern "C" {
 #endif
 
-#define MLORA_ABI_VERSION 6
+#define MLORA_ABI_VERSION 7
 
 /* Limits of one call (kernel-argument tables). Callers with more segments
  * split the rows into several calls; the Python host layer does this. */
@@ -208,6 +208,35 @@ int mlora_gate_scale_rows(const void *dout, int64_t ldout, int64_t M, int64_t N,
                           const float *gate, int64_t ldgate, int64_t gate_rows,
                           void *dy, int64_t lddy, int dout_dtype,
                           void *stream);
+
+/* Modulated LayerNorm that opens a DiT sublayer (the input of its next linear), bf16 out:
+ *   v[f]   = apply_ln ? (x[f] - mean)·(1 / sqrt(var + eps))   affine-free LayerNorm of the row
+ *                       (fp32, mean = Σx / W, var = Σ(x - mean)² / W)
+ *                     : x[f]                                   (x already normalized: float32)
+ *   s[f]   = scale_row ? RN(scale_row[f] + scale[b,t,f]) : scale[b,t,f]   (likewise shift)
+ *   out[f] = bf16_rne(RN(RN(v[f]·RN(1 + s[f])) + shift'[f]))
+ * for rows (b, t), b < batches, t < tokens, features f < width; every operand is addressed
+ * as base + b·stride_b + t·stride_t + f (element strides; stride_t 0 broadcasts one row over
+ * the tokens of a batch). Replaces, by apply_ln and scale_row:
+ *   apply_ln 0, no table: fused_modulated_norm_epilogue (runtime/wan13b_modulated_norm_kernel.py:207-263,
+ *                         kernel :26-97), the exact epilogue after PyTorch's fp32 LayerNorm;
+ *   apply_ln 0, table:    fused_modulated_norm_materialization (:266-353, kernel :100-204), the
+ *                         scale-shift table rows [width] added to the per-token components first;
+ *   apply_ln 1, table:    fused_bf16_layernorm_modulation (runtime/wan13b_fused_layernorm_kernel.py:135-222,
+ *                         kernel :22-132); x may also be float32 (the Wan block's residual stream).
+ * The elementwise steps are separate fp32 operations rounded to nearest (bit-exact given v).
+ * x_dtype MLORA_BF16 or MLORA_F32 (float32 when apply_ln is 0); table_dtype, scale_dtype and
+ * shift_dtype MLORA_BF16 or MLORA_F32; eps > 0 when apply_ln. width a multiple of 8 up to 8192; every
+ * pointer 16-byte aligned, strides nonnegative multiples of 8. */
+int mlora_modulated_norm(const void *x, int x_dtype, int64_t x_stride_b, int64_t x_stride_t,
+                         int apply_ln, float eps,
+                         const void *scale_row, const void *shift_row, int table_dtype,
+                         const void *scale, int scale_dtype, const void *shift, int shift_dtype,
+                         int64_t scale_stride_b, int64_t scale_stride_t,
+                         int64_t shift_stride_b, int64_t shift_stride_t,
+                         void *out, int64_t out_stride_b, int64_t out_stride_t,
+                         int64_t batches, int64_t tokens, int64_t width,
+                         void *stream);
 
 /* Input gradient with the LoRA term fused into its epilogue:
  *   dX[m, k] = bf16( Σ_n dY[m,n]·W[n,k] + Σ_j g_rows[m,j]·A_a[j,k] )

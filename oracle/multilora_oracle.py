@@ -339,6 +339,37 @@ def gate_scale(dout, gate, gate_rows: int) -> np.ndarray:
     return bf16_round(np.multiply(d, g, dtype=np.float32))
 
 
+# ------------------------------------------------------------------ modulated LayerNorm
+
+def layer_norm(x, eps: float) -> np.ndarray:
+    """Affine-free LayerNorm over the last axis (mean, biased variance), evaluated in float64
+    and rounded once to float32: the normalized values the reference's fused kernel computes in
+    float32 (runtime/wan13b_fused_layernorm_kernel.py:55-60: mean = Σx / W,
+    var = Σ(x - mean)² / W, (x - mean)·rsqrt(var + eps)), without their rounding."""
+    x = np.asarray(x, dtype=np.float64)
+    mean = x.mean(axis=-1, keepdims=True)
+    c = x - mean
+    var = (c * c).mean(axis=-1, keepdims=True)
+    return (c / np.sqrt(var + eps)).astype(np.float32)
+
+
+def modulated_norm(v, scale, shift, scale_row=None, shift_row=None) -> np.ndarray:
+    """bf16( RN(RN(v · RN(1 + s)) + h) ): runtime/wan13b_modulated_norm_kernel.py:70-97
+    (add.rn 1 + scale, mul.rn, add.rn shift, BF16 store). With table rows
+    (the materialization form, :158-174) s = RN(scale_row + scale), h = RN(shift_row + shift).
+    Inputs are float32 values (bf16 components converted exactly); numpy rounds each
+    float32 operation and never fuses a multiply-add."""
+    v = np.asarray(v, dtype=np.float32)
+    s = np.asarray(scale, dtype=np.float32)
+    h = np.asarray(shift, dtype=np.float32)
+    if scale_row is not None:
+        s = np.add(np.asarray(scale_row, dtype=np.float32), s, dtype=np.float32)
+        h = np.add(np.asarray(shift_row, dtype=np.float32), h, dtype=np.float32)
+    ops = np.add(np.float32(1.0), s, dtype=np.float32)
+    p = np.multiply(v, ops, dtype=np.float32)
+    return bf16_round(np.add(p, h, dtype=np.float32))
+
+
 def rel_l2(got, want) -> float:
     got = np.asarray(got, np.float64)
     want = np.asarray(want, np.float64)

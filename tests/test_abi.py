@@ -35,7 +35,7 @@ def test_library_exports_every_declared_symbol(lib, pkg):
 
 
 def test_abi_version_and_status_strings(lib, pkg):
-    assert lib.mlora_abi_version() == pkg._lib.ABI_VERSION == 6
+    assert lib.mlora_abi_version() == pkg._lib.ABI_VERSION == 7
     for code in (0, -1, -2, -3, -4, -5):
         assert lib.mlora_status_string(code)
     assert b"unknown" in lib.mlora_status_string(-99)
@@ -258,3 +258,32 @@ def test_stacked_gemm_validates_before_launch(lib, pkg):
     assert dx(groups=9) == L.ERR_UNSUPPORTED
     assert dx(ldw=512) == L.ERR_INVALID             # W_cat^T rows hold the three linears' columns
     assert dx(dys=(0x1000, 0x2008, 0x3000)) == L.ERR_UNSUPPORTED
+
+
+def _mnorm(lib, *, x=0x1000, x_dtype=1, apply_ln=1, eps=1e-6, srow=None, hrow=None, tdt=1,
+           scale=0x2000, sdt=0, shift=0x3000, hdt=0, out=0x4000, B=1, T=4, W=64, xst=None, ost=None):
+    xst = W if xst is None else xst
+    ost = W if ost is None else ost
+    return lib.mlora_modulated_norm(x, x_dtype, T * xst, xst, apply_ln, eps, srow, hrow, tdt,
+                                    scale, sdt, shift, hdt, 0, 0, 0, 0, out, T * ost, ost, B, T, W, None)
+
+
+def test_modulated_norm_rejects_bad_arguments(lib, pkg):
+    L = pkg._lib
+    assert _mnorm(lib, W=60) == L.ERR_UNSUPPORTED                      # width not a multiple of 8
+    assert _mnorm(lib, W=8200) == L.ERR_UNSUPPORTED                    # wider than 8192
+    assert _mnorm(lib, eps=0.0) == L.ERR_INVALID                       # LayerNorm epsilon
+    assert _mnorm(lib, eps=float("nan")) == L.ERR_INVALID
+    assert _mnorm(lib, apply_ln=0, x_dtype=1) == L.ERR_UNSUPPORTED     # normalized input is float32
+    assert _mnorm(lib, x_dtype=2) == L.ERR_UNSUPPORTED                 # e4m3 hidden state
+    assert _mnorm(lib, sdt=2) == L.ERR_UNSUPPORTED
+    assert _mnorm(lib, srow=0x5000) == L.ERR_INVALID                   # table rows come in pairs
+    assert _mnorm(lib, srow=0x5000, hrow=0x6000, tdt=2) == L.ERR_UNSUPPORTED
+    assert _mnorm(lib, x=None) == L.ERR_INVALID
+    assert _mnorm(lib, out=None) == L.ERR_INVALID
+    assert _mnorm(lib, x=0x1008) == L.ERR_UNSUPPORTED                  # 16-byte alignment
+    assert _mnorm(lib, xst=68) == L.ERR_UNSUPPORTED                    # row stride not a multiple of 8
+    assert _mnorm(lib, ost=32) == L.ERR_INVALID                        # output rows overlap
+    assert _mnorm(lib, B=-1) == L.ERR_INVALID
+    assert _mnorm(lib, B=0) == L.OK                                    # nothing to do, no launch
+    assert _mnorm(lib, W=0) == L.OK

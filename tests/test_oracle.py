@@ -477,3 +477,48 @@ def test_gate_scale_is_one_rounded_product():
     got = O.gate_scale(d, g, 1)
     want = (torch.from_numpy(d) * torch.from_numpy(g)).to(torch.bfloat16).float().numpy()
     assert np.array_equal(got, want)
+
+
+# ------------------------------------------------------------------ modulated LayerNorm
+
+def test_modulated_norm_matches_torch_float32_ops():
+    """bf16(RN(RN(v·RN(1 + s)) + h)) against torch's float32 CPU ops, one rounding per
+    operation, in the reference's order (wan13b_modulated_norm_kernel.py:70-97); the
+    materialization form adds the table rows first (:158-174)."""
+    rng = np.random.default_rng(41)
+    B, T, W = 2, 64, 96
+    v = rng.standard_normal((B, T, W)).astype(np.float32)
+    s = (0.1 * rng.standard_normal((B, T, W))).astype(np.float32)
+    h = (0.1 * rng.standard_normal((B, T, W))).astype(np.float32)
+    tv, ts, th = torch.from_numpy(v), torch.from_numpy(s), torch.from_numpy(h)
+    want = (tv * (ts + 1.0) + th).to(torch.bfloat16).float().numpy()
+    assert np.array_equal(O.modulated_norm(v, s, h), want)
+    srow = O.bf16_round(rng.standard_normal(W).astype(np.float32))
+    hrow = O.bf16_round(rng.standard_normal(W).astype(np.float32))
+    sc = torch.from_numpy(srow) + ts
+    sh = torch.from_numpy(hrow) + th
+    want = (tv * (sc + 1.0) + sh).to(torch.bfloat16).float().numpy()
+    assert np.array_equal(O.modulated_norm(v, s, h, srow, hrow), want)
+
+
+def test_modulated_norm_rounds_the_product_before_the_shift():
+    """v = 1 + 2^-12, s = 2^-12, h = -(1 + 2^-11): RN(v·(1 + s)) drops the 2^-24 of the exact
+    product (a tie, to even), so the separately rounded result is 0, while a fused
+    multiply-add would keep 2^-24."""
+    v = np.float32(1 + 2.0 ** -12)
+    s = np.float32(2.0 ** -12)
+    h = np.float32(-(1 + 2.0 ** -11))
+    assert O.modulated_norm(np.array([v]), np.array([s]), np.array([h]))[0] == 0.0
+    fused = float(v) * (1 + float(s)) + float(h)
+    assert fused == 2.0 ** -24
+
+
+def test_layer_norm_is_torch_layer_norm():
+    """Affine-free LayerNorm with the biased variance: torch's layer_norm in float64."""
+    rng = np.random.default_rng(43)
+    x = (3 + 2 * rng.standard_normal((5, 7, 1536))).astype(np.float32)
+    want = torch.nn.functional.layer_norm(torch.from_numpy(x).double(), (1536,), eps=1e-6).float().numpy()
+    np.testing.assert_allclose(O.layer_norm(x, 1e-6), want, rtol=0, atol=2e-7)
+    got = O.layer_norm(x, 1e-6).astype(np.float64)
+    np.testing.assert_allclose(got.mean(-1), 0, atol=1e-6)
+    np.testing.assert_allclose((got ** 2).mean(-1), 1, atol=1e-5)
