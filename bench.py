@@ -29,7 +29,10 @@ max(50, K) further steps one by one. Per-kernel rates (roofline, lora_hbm) are t
 --kernel-reps launches, each reading one of --rotate input sets after a 512 MB read that evicts
 L2 and the MALL.
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--config wan13b] [--fwd-only] [--per-role] [--shared-qkv] [--gated-residual]
+--modulated-norm times only the block's modulated LayerNorm kernel (fused LayerNorm + modulation) at
+the configuration's tokens and width, on the float32 residual stream and a bf16 hidden state.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--config wan13b] [--fwd-only] [--per-role] [--shared-qkv] [--gated-residual] [--modulated-norm]
 """
 from __future__ import annotations
 
@@ -78,6 +81,10 @@ def parse():
     p.add_argument("--per-role", action="store_true",
                    help="also time the same step as one call per segment (role), with this library and with "
                         "the reference's unfused torch path on the GPU")
+    p.add_argument("--modulated-norm", action="store_true",
+                   help="only time the block's modulated LayerNorm (fused LayerNorm + modulation into the next "
+                        "sublayer's bf16 input) at the configuration's tokens and hidden width, on the float32 "
+                        "residual stream and on a bf16 hidden state, beside torch's LayerNorm + ops")
     p.add_argument("--copy-calibration", action="store_true",
                    help="only run a plain 1 GiB device copy 4 times (scale for rocprofv3 FETCH_SIZE/WRITE_SIZE)")
     p.add_argument("--profile-kernels", action="store_true",
@@ -112,6 +119,70 @@ def copy_calibration():
         dst.copy_(src)
     torch.cuda.synchronize()
     print(json.dumps({"copy_calibration_bytes": n, "copies": 4}), flush=True)
+
+
+def modulated_norm_bench(args, pkg, cfg, dev):
+    """Per-launch time of the fused LayerNorm + modulation (mlora_modulated_norm) at the
+    configuration's shape: B samples (one per segment when the segments are equal, as the
+    wan13b roles are) of T tokens, width = the block's hidden size. The modulation is Wan's:
+    a [1, 6, W] table plus a per-sample [B, 6, W] time embedding (token stride 0). Medians of
+    --kernel-reps launches, each after a cache-evicting read, cycling --rotate input sets."""
+    import statistics
+    import torch
+    lengths = cfg.routing.lengths()
+    M = sum(lengths)
+    B = len(lengths) if len(set(lengths)) == 1 else 1
+    T = M // B
+    W = cfg.hidden
+    scrub = torch.ones(args.scrub_mb << 18, dtype=torch.float32, device=dev)
+    table = 0.1 * torch.randn(1, 6, W, device=dev)
+    e = 0.1 * torch.randn(B, 6, W, device=dev)
+    scale_c, shift_c = e[:, 1:2].expand(B, T, W), e[:, 0:1].expand(B, T, W)
+
+    def time_launches(fn, inputs):
+        ts = []
+        for i in range(args.kernel_reps + 2):
+            x = inputs[i % len(inputs)]
+            scrub.amax()
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record()
+            fn(x)
+            b.record()
+            torch.cuda.synchronize()
+            if i >= 2:
+                ts.append(a.elapsed_time(b) * 1e3)
+        return statistics.median(ts)
+
+    res = {}
+    for name, dt in (("float32_stream", torch.float32), ("bf16_hidden", torch.bfloat16)):
+        inputs = [(3 + 2 * torch.randn(B, T, W, device=dev)).to(dt) for _ in range(args.rotate)]
+        out = torch.empty(B, T, W, dtype=torch.bfloat16, device=dev)
+
+        def ours(x):
+            pkg.fused_layernorm_modulation(x, table, 1, 0, scale_c, shift_c, out, eps=1e-6)
+
+        def torch_path(x):
+            n = torch.nn.functional.layer_norm(x.float(), (W,), eps=1e-6)
+            s = (table[:, 1] + e[:, 1]).unsqueeze(1)
+            h = (table[:, 0] + e[:, 0]).unsqueeze(1)
+            return (n * (1 + s) + h).to(torch.bfloat16)
+
+        us = time_launches(ours, inputs)
+        tus = time_launches(torch_path, inputs)
+        nbytes = M * W * (inputs[0].element_size() + 2) + 2 * B * W * 4 + 2 * W * 4
+        res[name] = {"avg_us": round(us, 2), "bytes_per_launch": nbytes, "achieved_gbs": round(nbytes / us / 1e3, 1),
+                     "frac_hbm": round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4), "torch_us": round(tus, 2),
+                     "speedup_vs_torch": round(tus / us, 2)}
+    f = res["float32_stream"]
+    print(json.dumps({
+        "metric": f"modulated LayerNorm GB/s at {cfg.name} shape", "value": f["achieved_gbs"], "unit": "GB/s",
+        "higher_is_better": True, "dtype": "f32 -> bf16",
+        "config": {"workload": f"fused LayerNorm + Wan modulation into the next sublayer's bf16 input, {B} x {T} "
+                               f"tokens, width {W}", "tokens": M},
+        "roofline": {"kernel": "modulated_norm_kernel (float32 stream)", "bound": "hbm",
+                     "achieved": f["achieved_gbs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": f["frac_hbm"], "avg_launch_us": f["avg_us"]},
+        "variants": res}), flush=True)
 
 
 def profile_kernels(args):
@@ -206,6 +277,9 @@ def main():
     dev = torch.device("cuda:0")
     props = torch.cuda.get_device_properties(dev)
     cfg = workloads.CONFIGS[args.config]
+    if args.modulated_norm:
+        modulated_norm_bench(args, pkg, cfg, dev)
+        return
     routing = cfg.routing
     scales = [cfg.scale] * len(cfg.ranks)
 
