@@ -173,6 +173,45 @@ def modulated_norm_bench(args, pkg, cfg, dev):
         res[name] = {"avg_us": round(us, 2), "bytes_per_launch": nbytes, "achieved_gbs": round(nbytes / us / 1e3, 1),
                      "frac_hbm": round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4), "torch_us": round(tus, 2),
                      "speedup_vs_torch": round(tus / us, 2)}
+    # backward on the float32 stream (the Wan block): the hidden gradient with the row statistics,
+    # the per-sample component gradient, and the whole autograd op (forward + backward) beside torch's
+    hidden = [(3 + 2 * torch.randn(B, T, W, device=dev)) for _ in range(args.rotate)]
+    up = torch.randn(B, T, W, device=dev).to(torch.bfloat16)
+    dx = torch.empty(B, T, W, device=dev)
+    mean = torch.empty(B, T, device=dev)
+    rstd = torch.empty(B, T, device=dev)
+    dcomp = torch.zeros(B, 6, W, device=dev)
+    scale4 = e[:, 4:5].expand(B, T, W)
+
+    def hidden_bwd(x):
+        pkg.fused_layernorm_modulation_hidden_backward(x, up, table, 4, scale4, dx, mean, rstd, eps=1e-6)
+
+    def comp_bwd(x):
+        pkg.fused_reduced_component_gradient(x, up, mean, rstd, dcomp, 4, 3)
+
+    tab_p = table.clone().requires_grad_(True)
+    e_p = e.clone().requires_grad_(True)
+
+    def op_fwd_bwd(x):
+        x = x.detach().requires_grad_(True)
+        pkg.modulated_layer_norm(x, tab_p, e_p, 4, 3, 1e-6).backward(up)
+
+    def torch_fwd_bwd(x):
+        x = x.detach().requires_grad_(True)
+        mod = tab_p + e_p
+        n = torch.nn.functional.layer_norm(x, (W,), eps=1e-6)
+        (n * (1 + mod[:, 4:5]) + mod[:, 3:4]).to(torch.bfloat16).backward(up)
+
+    hidden_bwd(hidden[0])
+    bus, cus = time_launches(hidden_bwd, hidden), time_launches(comp_bwd, hidden)
+    ous, tous = time_launches(op_fwd_bwd, hidden), time_launches(torch_fwd_bwd, hidden)
+    hb = M * W * (4 + 2 + 4) + M * 8
+    cb = M * W * (4 + 2) + M * 8
+    res["backward_float32_stream"] = {
+        "hidden_backward_us": round(bus, 2), "hidden_backward_gbs": round(hb / bus / 1e3, 1),
+        "component_gradient_us": round(cus, 2), "component_gradient_gbs": round(cb / cus / 1e3, 1),
+        "autograd_fwd_bwd_us": round(ous, 2), "torch_autograd_fwd_bwd_us": round(tous, 2),
+        "speedup_vs_torch": round(tous / ous, 2)}
     f = res["float32_stream"]
     print(json.dumps({
         "metric": f"modulated LayerNorm GB/s at {cfg.name} shape", "value": f["achieved_gbs"], "unit": "GB/s",

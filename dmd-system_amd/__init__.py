@@ -15,6 +15,9 @@ Public API:
     kernels                              torch front end of each C-ABI entry point
     fused_modulated_norm_epilogue, fused_modulated_norm_materialization,
     fused_bf16_layernorm_modulation, fused_layernorm_modulation   the block's modulated LayerNorm
+    fused_bf16_layernorm_modulation_hidden_backward, fused_reduced_component_gradient,
+    fused_tensor4d_component_gradient      its fused backward
+    ModulatedLayerNormFunction, modulated_layer_norm   the same as one autograd op
     load_library()                       load libmlora.so (raises if missing)
 
 The directory name is not a Python identifier; importers load it as
@@ -32,8 +35,11 @@ from .roles import RoleBatch, fuse_roles, roles_active
 from .routing import BASE_ONLY, SegmentRouting
 from .shared_input import SharedInputGroup, fuse_shared_inputs, release_shared_inputs
 from .peft_site import install_peft_multi_lora, peft_roles_active, uninstall_peft_multi_lora
-from .modulated_norm import (fused_bf16_layernorm_modulation, fused_layernorm_modulation,
-                             fused_modulated_norm_epilogue, fused_modulated_norm_materialization)
+from .modulated_norm import (ModulatedLayerNormFunction, fused_bf16_layernorm_modulation,
+                             fused_bf16_layernorm_modulation_hidden_backward, fused_layernorm_modulation,
+                             fused_layernorm_modulation_hidden_backward, fused_modulated_norm_epilogue,
+                             fused_modulated_norm_materialization, fused_reduced_component_gradient,
+                             fused_tensor4d_component_gradient, modulated_layer_norm)
 
 
 def load_library():
@@ -49,5 +55,7 @@ __all__ = [
     "release_shared_inputs", "export_adapters", "import_adapters", "save_adapters", "load_adapters", "kernels",
     "load_library", "install_peft_multi_lora", "uninstall_peft_multi_lora", "peft_roles_active",
     "fused_modulated_norm_epilogue", "fused_modulated_norm_materialization", "fused_bf16_layernorm_modulation",
-    "fused_layernorm_modulation",
+    "fused_layernorm_modulation", "fused_bf16_layernorm_modulation_hidden_backward",
+    "fused_layernorm_modulation_hidden_backward", "fused_reduced_component_gradient",
+    "fused_tensor4d_component_gradient", "ModulatedLayerNormFunction", "modulated_layer_norm",
 ]

@@ -50,6 +50,13 @@ SIGNATURES = {
     "mlora_gate_scale_rows": (_int, [_vp, _i64, _i64, _i64, _vp, _i64, _i64, _vp, _i64, _int, _vp]),
     "mlora_modulated_norm": (_int, [_vp, _int, _i64, _i64, _int, ctypes.c_float, _vp, _vp, _int, _vp, _int, _vp, _int,
                                     _i64, _i64, _i64, _i64, _vp, _i64, _i64, _i64, _i64, _i64, _vp]),
+    "mlora_modulated_norm_backward": (_int, [_vp, _int, _i64, _i64, _vp, _int, _i64, _i64, _vp, _int,
+                                             _vp, _int, _i64, _i64, _vp, _int, _i64, _i64, _vp, _vp, ctypes.c_float,
+                                             _i64, _i64, _i64, _vp]),
+    "mlora_modulated_norm_component_workspace_bytes": (_i64, [_i64, _i64, _i64]),
+    "mlora_modulated_norm_component_grad": (_int, [_vp, _int, _i64, _i64, _vp, _int, _i64, _i64, _vp, _vp,
+                                                   _vp, _int, _i64, _i64, _i64, _int, _int, _int, _vp, _i64,
+                                                   _i64, _i64, _i64, _vp]),
     "mlora_gemm_dx": (_int, [_vp, _i64, _i64, _i64, _vp, _i64, _i64, _vp, _i64,
                              _pvp, _pi32, _i32, _pi64, _pi32, _i32, _vp, _i64, _int, _vp]),
     "mlora_seg_outer": (_int, [_vp, _i64, _i64, _i64, _vp, _i32, _pvp, _int, _int, _pi32, _i32,

@@ -334,6 +334,66 @@ def modulated_norm(x: torch.Tensor, scale: torch.Tensor, shift: torch.Tensor, ou
     return out
 
 
+def modulated_norm_backward(x: torch.Tensor, g: torch.Tensor, scale: torch.Tensor, dx: torch.Tensor,
+                            mean: torch.Tensor, rstd: torch.Tensor, *, eps: float,
+                            scale_row: torch.Tensor | None = None) -> torch.Tensor:
+    """dx of out = bf16(LN(x)·RN(1 + s) + h) for the upstream gradient g ([B, T, W] each; s =
+    RN(scale_row + scale) with a table row); writes the rows' mean and rstd ([B, T] float32)."""
+    B, T, W = x.shape
+    fl = (torch.bfloat16, torch.float32)
+    _rows3("hidden", x, fl, (B, T, W))
+    _rows3("grad_output", g, fl, (B, T, W))
+    _rows3("scale_component", scale, fl, (B, T, W))
+    _rows3("hidden_gradient", dx, fl, (B, T, W))
+    for name, t in (("mean", mean), ("rstd", rstd)):
+        _require(t.is_cuda and t.dtype == torch.float32 and tuple(t.shape) == (B, T) and t.is_contiguous(),
+                 f"{name} must be a contiguous float32 [{B}, {T}] device tensor")
+    if scale_row is not None:
+        _require(scale_row.is_cuda and scale_row.dim() == 1 and scale_row.shape[0] == W and scale_row.stride(0) == 1
+                 and scale_row.dtype in fl, f"scale_row must be a contiguous device vector of {W}")
+    _require(eps > 0, "LayerNorm epsilon must be positive")
+    lib = _lib.load()
+    _lib.check("mlora_modulated_norm_backward", lib.mlora_modulated_norm_backward(
+        x.data_ptr(), _DT[x.dtype], x.stride(0), x.stride(1), g.data_ptr(), _DT[g.dtype], g.stride(0), g.stride(1),
+        _ptr(scale_row), _DT[scale_row.dtype] if scale_row is not None else _lib.BF16,
+        scale.data_ptr(), _DT[scale.dtype], scale.stride(0), scale.stride(1),
+        dx.data_ptr(), _DT[dx.dtype], dx.stride(0), dx.stride(1), mean.data_ptr(), rstd.data_ptr(), float(eps),
+        B, T, W, _stream(x)))
+    return dx
+
+
+def modulated_norm_component_grad(x: torch.Tensor, g: torch.Tensor, mean: torch.Tensor, rstd: torch.Tensor,
+                                  out: torch.Tensor, scale_index: int, shift_index: int) -> torch.Tensor:
+    """Scale / shift component gradients into out: [B, 6, W] (summed over tokens: Σ g·n, Σ g)
+    or [B, T, 6, W] (per token: g·n, g); n from the row statistics. Other slots untouched."""
+    B, T, W = x.shape
+    fl = (torch.bfloat16, torch.float32)
+    _rows3("hidden", x, fl, (B, T, W))
+    _rows3("grad_output", g, fl, (B, T, W))
+    for name, t in (("mean", mean), ("rstd", rstd)):
+        _require(t.is_cuda and t.dtype == torch.float32 and tuple(t.shape) == (B, T) and t.is_contiguous(),
+                 f"{name} must be a contiguous float32 [{B}, {T}] device tensor")
+    _require(out.is_cuda and out.dtype in fl, "component gradient must be a bfloat16 or float32 device tensor")
+    reduce = out.dim() == 3
+    _require(tuple(out.shape) == ((B, 6, W) if reduce else (B, T, 6, W)),
+             f"component gradient must be [{B}, 6, {W}] or [{B}, {T}, 6, {W}], got {tuple(out.shape)}")
+    _require(out.stride(-1) == 1, "component gradient must have unit feature stride")
+    lib = _lib.load()
+    if reduce:
+        sb, st, sc = out.stride(0), 0, out.stride(1)
+        nbytes = lib.mlora_modulated_norm_component_workspace_bytes(B, T, W)
+        _lib.check("mlora_modulated_norm_component_workspace_bytes", nbytes if nbytes < 0 else 0)
+        ws = torch.empty((max(nbytes, 16) + 15) // 16 * 4, dtype=torch.float32, device=x.device)
+    else:
+        sb, st, sc = out.stride(0), out.stride(1), out.stride(2)
+        ws, nbytes = None, 0
+    _lib.check("mlora_modulated_norm_component_grad", lib.mlora_modulated_norm_component_grad(
+        x.data_ptr(), _DT[x.dtype], x.stride(0), x.stride(1), g.data_ptr(), _DT[g.dtype], g.stride(0), g.stride(1),
+        mean.data_ptr(), rstd.data_ptr(), out.data_ptr(), _DT[out.dtype], sb, st, sc, int(scale_index),
+        int(shift_index), int(reduce), _ptr(ws), nbytes, B, T, W, _stream(x)))
+    return out
+
+
 def gemm_dx(dy: torch.Tensor, w: torch.Tensor, g_rows: torch.Tensor | None, as_: Sequence[torch.Tensor],
             routing: SegmentRouting, out: torch.Tensor | None = None, accumulate: bool = False) -> torch.Tensor:
     """dX = dY·W + per-segment g_rows·A_a, bf16 out (accumulate: dX += ..., into `out`).

@@ -238,6 +238,42 @@ int mlora_modulated_norm(const void *x, int x_dtype, int64_t x_stride_b, int64_t
                          int64_t batches, int64_t tokens, int64_t width,
                          void *stream);
 
+/* Backward of mlora_modulated_norm with apply_ln (the reference's fused backward,
+ * runtime/wan13b_fused_layernorm_backward_kernel.py), for the upstream gradient g of out:
+ *   fused_bf16_layernorm_modulation_hidden_backward (:337-393, kernel :27-134): per row,
+ *     n = LN(x), s' = RN(1 + (scale_row ? RN(scale_row + scale) : scale)), gn = RN(g·s'),
+ *     dx = RN(RN(RN(gn - Σgn / W) - RN(n·(Σ(gn·n) / W)))·rstd), and the row's mean and rstd
+ *     (float32 [batches·tokens], row b·tokens + t).
+ * x, g, scale and dx are bf16 or float32 (dx in dx_dtype); width a multiple of 8 up to 5120. */
+int mlora_modulated_norm_backward(const void *x, int x_dtype, int64_t x_stride_b, int64_t x_stride_t,
+                                  const void *g, int g_dtype, int64_t g_stride_b, int64_t g_stride_t,
+                                  const void *scale_row, int table_dtype,
+                                  const void *scale, int scale_dtype, int64_t scale_stride_b, int64_t scale_stride_t,
+                                  void *dx, int dx_dtype, int64_t dx_stride_b, int64_t dx_stride_t,
+                                  float *mean, float *rstd, float eps,
+                                  int64_t batches, int64_t tokens, int64_t width,
+                                  void *stream);
+/* Gradients of the two modulation components from the same x, g and the row statistics
+ * above, with n = RN(RN(x - mean)·rstd):
+ *   reduce 1: fused_reduced_component_gradient (:396-447, kernel :137-212):
+ *             out[b, scale_index, f] = Σ_t g·n, out[b, shift_index, f] = Σ_t g  (out [batches, 6, width]
+ *             with strides out_stride_b, out_stride_c; float32 partial sums over 64-token chunks,
+ *             added in a fixed order, in a caller workspace of
+ *             mlora_modulated_norm_component_workspace_bytes(batches, tokens, width) bytes);
+ *   reduce 0: fused_tensor4d_component_gradient (:450-502, kernel :215-270):
+ *             out[b, t, scale_index, :] = RN(g·n), out[b, t, shift_index, :] = g  (out [batches, tokens, 6,
+ *             width]; no workspace).
+ * The other four component slots are not written. out_dtype MLORA_BF16 or MLORA_F32. */
+int64_t mlora_modulated_norm_component_workspace_bytes(int64_t batches, int64_t tokens, int64_t width);
+int mlora_modulated_norm_component_grad(const void *x, int x_dtype, int64_t x_stride_b, int64_t x_stride_t,
+                                        const void *g, int g_dtype, int64_t g_stride_b, int64_t g_stride_t,
+                                        const float *mean, const float *rstd,
+                                        void *out, int out_dtype, int64_t out_stride_b, int64_t out_stride_t,
+                                        int64_t out_stride_c, int scale_index, int shift_index, int reduce,
+                                        void *workspace, int64_t workspace_bytes,
+                                        int64_t batches, int64_t tokens, int64_t width,
+                                        void *stream);
+
 /* Input gradient with the LoRA term fused into its epilogue:
  *   dX[m, k] = bf16( Σ_n dY[m,n]·W[n,k] + Σ_j g_rows[m,j]·A_a[j,k] )
  * g_rows = s_a·dY·B_a from mlora_shrink(op_layout=1). a_ptrs[i]: bf16 [r_i, K].

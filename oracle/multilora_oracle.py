@@ -370,6 +370,28 @@ def modulated_norm(v, scale, shift, scale_row=None, shift_row=None) -> np.ndarra
     return bf16_round(np.add(p, h, dtype=np.float32))
 
 
+def modulated_norm_backward(x, g, scale, eps: float, scale_row=None):
+    """Closed-form gradients of out = LN(x)·(1 + s) + h (s = scale_row + scale) for the upstream
+    gradient g, in float64 — what the reference's fused backward evaluates in float32
+    (runtime/wan13b_fused_layernorm_backward_kernel.py:27-270):
+      n = (x - mean)·rstd, gn = g·(1 + s),
+      dx = (gn - mean_f(gn) - n·mean_f(gn·n))·rstd,   d_scale = g·n,   d_shift = g
+    (per element; the reduced component gradient sums d_scale and d_shift over tokens).
+    Returns (dx, d_scale, d_shift, mean, rstd)."""
+    x = np.asarray(x, dtype=np.float64)
+    g = np.asarray(g, dtype=np.float64)
+    s = np.asarray(scale, dtype=np.float64)
+    if scale_row is not None:
+        s = np.asarray(scale_row, dtype=np.float64) + s
+    mean = x.mean(axis=-1, keepdims=True)
+    c = x - mean
+    rstd = 1.0 / np.sqrt((c * c).mean(axis=-1, keepdims=True) + eps)
+    n = c * rstd
+    gn = g * (1.0 + s)
+    dx = (gn - gn.mean(axis=-1, keepdims=True) - n * (gn * n).mean(axis=-1, keepdims=True)) * rstd
+    return dx, g * n, g, mean[..., 0], rstd[..., 0]
+
+
 def rel_l2(got, want) -> float:
     got = np.asarray(got, np.float64)
     want = np.asarray(want, np.float64)

@@ -287,3 +287,34 @@ def test_modulated_norm_rejects_bad_arguments(lib, pkg):
     assert _mnorm(lib, B=-1) == L.ERR_INVALID
     assert _mnorm(lib, B=0) == L.OK                                    # nothing to do, no launch
     assert _mnorm(lib, W=0) == L.OK
+
+
+def test_modulated_norm_backward_rejects_bad_arguments(lib, pkg):
+    L = pkg._lib
+
+    def bwd(x=0x1000, g=0x2000, sc=0x3000, dx=0x4000, mean=0x5000, rstd=0x6000, eps=1e-6, W=64, T=4, dt=1):
+        return lib.mlora_modulated_norm_backward(x, dt, T * W, W, g, dt, T * W, W, None, 1, sc, 0, 0, 0,
+                                                 dx, dt, T * W, W, mean, rstd, eps, 1, T, W, None)
+
+    assert bwd(W=5128) == L.ERR_UNSUPPORTED          # the backward keeps rows up to 5120 in registers
+    assert bwd(W=12) == L.ERR_UNSUPPORTED
+    assert bwd(eps=0.0) == L.ERR_INVALID
+    assert bwd(dt=2) == L.ERR_UNSUPPORTED
+    assert bwd(mean=None) == L.ERR_INVALID
+    assert bwd(g=0x2004) == L.ERR_UNSUPPORTED        # 16-byte alignment
+    assert bwd(T=0) == L.OK
+
+    def comp(reduce=1, si=4, hi=3, ws=None, wsb=0, out=0x7000, sb=6 * 64, st=0, sc=64, W=64, T=4):
+        return lib.mlora_modulated_norm_component_grad(0x1000, 1, T * W, W, 0x2000, 1, T * W, W, 0x5000, 0x6000,
+                                                       out, 0, sb, st, sc, si, hi, reduce, ws, wsb, 1, T, W, None)
+
+    need = lib.mlora_modulated_norm_component_workspace_bytes(1, 4, 64)
+    assert need == 1 * 1 * 2 * 64 * 4
+    assert comp() == L.ERR_WORKSPACE                 # the reduced form needs its partial-sum workspace
+    assert comp(ws=0x8000, wsb=need - 4) == L.ERR_WORKSPACE
+    assert comp(si=3, hi=3) == L.ERR_INVALID         # two different slots
+    assert comp(si=6) == L.ERR_INVALID
+    assert comp(sc=32) == L.ERR_INVALID              # slots overlap
+    assert comp(out=None) == L.ERR_INVALID
+    assert comp(reduce=0, st=100) == L.ERR_INVALID   # [B, T, 6, W] rows overlap
+    assert comp(reduce=0, sb=4 * 6 * 64, st=6 * 64, out=0x7004) == L.ERR_UNSUPPORTED

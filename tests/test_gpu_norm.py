@@ -162,3 +162,111 @@ def test_contract_violations_raise(pkg, dev):
         pkg.fused_modulated_norm_epilogue(odd, odd, odd, torch.zeros(B, T, 60, device=dev, dtype=torch.bfloat16))
     empty = torch.zeros(0, T, W, device=dev)
     assert pkg.fused_modulated_norm_epilogue(empty, empty, empty, empty.bfloat16()).numel() == 0
+
+
+# ------------------------------------------------------------------ backward
+
+def _bwd_case(dev, B, T, W, hidden_dtype, seed):
+    g = torch.Generator().manual_seed(seed)
+    hidden = (3 + 2 * torch.randn(B, T, W, generator=g)).to(dev, hidden_dtype)
+    grad = torch.randn(B, T, W, generator=g).to(dev, hidden_dtype)
+    table = (0.1 * torch.randn(1, 6, W, generator=g)).to(dev)
+    e = (0.1 * torch.randn(B, 6, W, generator=g)).to(dev)
+    return hidden, grad, table, e
+
+
+def _rel(got, want):
+    return O.rel_l2(got, want)
+
+
+@pytest.mark.parametrize("hidden_dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("B,T,W", [(3, 700, 1536), (2, 129, 5120), (1, 64, 520), (1, 5, 8)])
+def test_hidden_backward_matches_closed_form(pkg, dev, hidden_dtype, B, T, W):
+    """dx and the row statistics against the oracle's float64 closed form. float32 dx: rel-L2
+    ≤ 1e-5 (fp32 evaluation); bf16 dx: every element within one bf16 ulp plus 1e-4·|dx|max
+    (the cancellation in gn - mean(gn) - n·mean(gn·n) is evaluated in fp32)."""
+    print(f"modulated-norm hidden backward {hidden_dtype} B={B} T={T} W={W}", flush=True)
+    hidden, grad, table, e = _bwd_case(dev, B, T, W, hidden_dtype, seed=B * T + W)
+    scale_c = e[:, 1:2].expand(B, T, W)
+    dx = torch.empty_like(hidden)
+    mean = torch.empty(B, T, device=dev)
+    rstd = torch.empty(B, T, device=dev)
+    if hidden_dtype == torch.bfloat16:
+        pkg.fused_bf16_layernorm_modulation_hidden_backward(hidden, grad, table, 1, scale_c, dx, mean, rstd, eps=1e-6)
+    else:
+        pkg.fused_layernorm_modulation_hidden_backward(hidden, grad, table, 1, scale_c, dx, mean, rstd, eps=1e-6)
+    want, _, _, wmean, wrstd = O.modulated_norm_backward(_np(hidden), _np(grad), _np(scale_c), 1e-6, _np(table[0, 1]))
+    np.testing.assert_allclose(_np(mean), wmean, rtol=1e-6, atol=1e-6)
+    np.testing.assert_allclose(_np(rstd), wrstd, rtol=1e-5)
+    got = _np(dx)
+    if hidden_dtype == torch.float32:
+        assert _rel(got, want) <= 1e-5
+    else:
+        bound = _bf16_ulp(want) + 1e-4 * np.abs(want).max()
+        assert (np.abs(got - want) <= bound).all()
+
+
+@pytest.mark.parametrize("hidden_dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("out_dtype", [torch.float32, torch.bfloat16])
+def test_component_gradients(pkg, dev, hidden_dtype, out_dtype):
+    """Reduced [B, 6, W] (Σ_t g·n, Σ_t g) and per-token [B, T, 6, W] (g·n, g) gradients against
+    the oracle; the four other slots stay untouched. float32 out: rel-L2 ≤ 1e-5 (sums of 1000
+    tokens in float32); bf16 out: ≤ 4e-3 (one rounding)."""
+    print(f"modulated-norm component gradients {hidden_dtype} -> {out_dtype}", flush=True)
+    B, T, W = 2, 1000, 1536
+    hidden, grad, table, e = _bwd_case(dev, B, T, W, hidden_dtype, seed=99)
+    scale_c = e[:, 4:5].expand(B, T, W)
+    dx = torch.empty_like(hidden)
+    mean = torch.empty(B, T, device=dev)
+    rstd = torch.empty(B, T, device=dev)
+    pkg.fused_layernorm_modulation_hidden_backward(hidden, grad, table, 4, scale_c, dx, mean, rstd, eps=1e-6)
+    _, ds, dh, _, _ = O.modulated_norm_backward(_np(hidden), _np(grad), _np(scale_c), 1e-6, _np(table[0, 4]))
+    tol = 1e-5 if out_dtype == torch.float32 else 4e-3
+    red = torch.full((B, 6, W), 7.0, device=dev, dtype=out_dtype)
+    pkg.fused_reduced_component_gradient(hidden, grad, mean, rstd, red, 4, 3)
+    assert _rel(_np(red[:, 4]), ds.sum(axis=1)) <= tol
+    assert _rel(_np(red[:, 3]), dh.sum(axis=1)) <= tol
+    assert (_np(red[:, [0, 1, 2, 5]]) == 7.0).all()
+    per = torch.full((B, T, 6, W), 7.0, device=dev, dtype=out_dtype)
+    pkg.fused_tensor4d_component_gradient(hidden, grad, mean, rstd, per, 4, 3)
+    assert _rel(_np(per[:, :, 4]), ds) <= tol
+    assert _rel(_np(per[:, :, 3]), dh) <= (0 if out_dtype == hidden_dtype else tol)
+    assert (_np(per[:, :, [0, 1, 2, 5]]) == 7.0).all()
+
+
+@pytest.mark.parametrize("per_token", [False, True])
+def test_autograd_op_matches_torch_float64(pkg, dev, per_token):
+    """modulated_layer_norm (fused forward + fused backward) against torch autograd of
+    layer_norm(x)·(1 + (table + e)[si]) + (table + e)[hi] in float64: the gradients of the
+    float32 hidden state, the table and the time embedding. Two backward passes are
+    bit-identical (fixed-order reductions)."""
+    print(f"modulated layer norm autograd, per_token={per_token}", flush=True)
+    B, T, W, eps = 2, 512, 1536, 1e-6
+    g = torch.Generator().manual_seed(5)
+    hidden = (3 + 2 * torch.randn(B, T, W, generator=g)).to(dev).requires_grad_(True)
+    table = (0.1 * torch.randn(1, 6, W, generator=g)).to(dev).requires_grad_(True)
+    shape = (B, T, 6, W) if per_token else (B, 6, W)
+    e = (0.1 * torch.randn(*shape, generator=g)).to(dev).requires_grad_(True)
+    up = torch.randn(B, T, W, generator=g).to(dev, torch.bfloat16)
+    out = pkg.modulated_layer_norm(hidden, table, e, 4, 3, eps)
+    assert out.dtype == torch.bfloat16
+    out.backward(up)
+    grads = [t.grad.clone() for t in (hidden, table, e)]
+    for t in (hidden, table, e):
+        t.grad = None
+    pkg.modulated_layer_norm(hidden, table, e, 4, 3, eps).backward(up)
+    for a, t in zip(grads, (hidden, table, e)):
+        assert torch.equal(a, t.grad)
+    # float64 reference on the CPU
+    h64 = hidden.detach().double().cpu().requires_grad_(True)
+    t64 = table.detach().double().cpu().requires_grad_(True)
+    e64 = e.detach().double().cpu().requires_grad_(True)
+    mod = t64.unsqueeze(1) + e64 if per_token else t64 + e64  # [B, (T,) 6, W]
+    s_ = mod[..., 4, :] if per_token else mod[:, 4:5, :]
+    h_ = mod[..., 3, :] if per_token else mod[:, 3:4, :]
+    ref = torch.nn.functional.layer_norm(h64, (W,), eps=eps) * (1 + s_) + h_
+    assert O.rel_l2(_np(out), ref.detach().numpy()) <= 4e-3  # one bf16 rounding
+    ref.backward(up.double().cpu())
+    assert O.rel_l2(_np(grads[0]), h64.grad.numpy()) <= 1e-5
+    assert O.rel_l2(_np(grads[1]), t64.grad.numpy()) <= 1e-5
+    assert O.rel_l2(_np(grads[2]), e64.grad.numpy()) <= 1e-5

@@ -522,3 +522,27 @@ def test_layer_norm_is_torch_layer_norm():
     got = O.layer_norm(x, 1e-6).astype(np.float64)
     np.testing.assert_allclose(got.mean(-1), 0, atol=1e-6)
     np.testing.assert_allclose((got ** 2).mean(-1), 1, atol=1e-5)
+
+
+def test_modulated_norm_backward_is_torch_autograd():
+    """The closed-form gradients of LN(x)·(1 + s) + h against torch autograd in float64, for
+    the hidden state, the per-element scale and shift, and the row statistics."""
+    rng = np.random.default_rng(47)
+    B, T, W, eps = 2, 5, 64, 1e-6
+    x = 3 + 2 * rng.standard_normal((B, T, W))
+    g = rng.standard_normal((B, T, W))
+    s = 0.1 * rng.standard_normal((B, T, W))
+    srow = 0.1 * rng.standard_normal(W)
+    h = 0.1 * rng.standard_normal((B, T, W))
+    tx = torch.tensor(x, requires_grad=True)
+    ts = torch.tensor(s, requires_grad=True)
+    th = torch.tensor(h, requires_grad=True)
+    n = torch.nn.functional.layer_norm(tx, (W,), eps=eps)
+    out = n * (1 + (torch.tensor(srow) + ts)) + th
+    out.backward(torch.tensor(g))
+    dx, ds, dh, mean, rstd = O.modulated_norm_backward(x, g, s, eps, srow)
+    np.testing.assert_allclose(dx, tx.grad.numpy(), rtol=1e-10, atol=1e-12)
+    np.testing.assert_allclose(ds, ts.grad.numpy(), rtol=1e-10, atol=1e-12)
+    np.testing.assert_allclose(dh, th.grad.numpy(), rtol=0, atol=0)
+    np.testing.assert_allclose(mean, x.mean(-1), rtol=1e-12)
+    np.testing.assert_allclose(rstd, 1 / np.sqrt(x.var(-1) + eps), rtol=1e-12)
