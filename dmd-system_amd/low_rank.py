@@ -301,14 +301,17 @@ class MultiLoRALinear(nn.Module):
     def num_adapters(self) -> int:
         return len(self.scales)
 
-    def quantize_base_fp8(self) -> "MultiLoRALinear":
+    def quantize_base_fp8(self, dx_bf16: bool | None = None) -> "MultiLoRALinear":
         """Store the frozen base weight as e4m3 with one fp32 scale per output
         channel (buffers ``base_wq`` [out, in], ``base_wscale`` [out]); forward and dX
         then run on the e4m3 MFMA. The bf16/fp32 ``base.weight`` is left in place for
         its other users (shared construction aliases it). The e4m3 copy follows the
         weight: if ``base.weight`` changes (in place, or by a state-dict load) it is
         quantised again on the next call; ``base_wq`` transposed (for the e4m3 dX) is
-        remade whenever ``base_wq`` changes."""
+        remade whenever ``base_wq`` changes. ``dx_bf16=True`` runs dX on the bf16 MFMA
+        against the dequantised base instead (dY not quantised; ~1.4× the dX time)."""
+        if dx_bf16 is not None:
+            self.__dict__['_fp8_dx_bf16'] = bool(dx_bf16)
         w = self.base.weight.detach().to(torch.bfloat16).contiguous()
         wq, ws = quantize_rows_fp8(w)
         if getattr(self, "base_wq", None) is None:
@@ -375,6 +378,7 @@ class MultiLoRALinear(nn.Module):
         if getattr(self, "base_wq", None) is not None:
             wq, ws, wq_t = self._fp8_base()
             return multi_lora_linear_fp8(x, wq, ws, self.base.bias, list(self.lora_a), list(self.lora_b),
-                                         self.scales, routing, wq_t=wq_t)
+                                         self.scales, routing, wq_t=wq_t,
+                                         dx_bf16=self.__dict__.get('_fp8_dx_bf16', False))
         return multi_lora_linear(x, self.base.weight, self.base.bias, list(self.lora_a), list(self.lora_b),
                                  self.scales, routing, weight_t=_base_t(self, x))
