@@ -235,6 +235,10 @@ class ModulatedLayerNormFunction(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, hidden, table, component, scale_index: int, shift_index: int, eps: float):
+        if hidden.dim() != 3:
+            _fail(f"hidden must be [batch, tokens, width], got {tuple(hidden.shape)}")
+        if int(scale_index) == int(shift_index):
+            _fail("scale and shift must be two different components")
         B, T, W = hidden.shape
         if component.dim() == 3:
             scale_c = component[:, scale_index].unsqueeze(1).expand(B, T, W)
