@@ -81,6 +81,9 @@ def parse():
     p.add_argument("--per-role", action="store_true",
                    help="also time the same step as one call per segment (role), with this library and with "
                         "the reference's unfused torch path on the GPU")
+    p.add_argument("--fp8-dx-bf16", action="store_true",
+                   help="with an e4m3 base: dX on the bf16 MFMA against the dequantised base instead of the "
+                        "e4m3 MFMA with a quantised dY (closer to the exact dX, slower)")
     p.add_argument("--modulated-norm", action="store_true",
                    help="only time the block's modulated LayerNorm (fused LayerNorm + modulation into the next "
                         "sublayer's bf16 input) at the configuration's tokens and hidden width, on the float32 "
@@ -323,6 +326,8 @@ def main():
     scales = [cfg.scale] * len(cfg.ranks)
 
     fp8 = cfg.base_fp8
+    if args.fp8_dx_bf16 and not fp8:
+        raise SystemExit("--fp8-dx-bf16 needs a configuration with an e4m3 base (wan13b_fp8)")
     # a float32 configuration (config 1, the reference's precision='fp32') runs the float32 path:
     # float32 tensors through the same op, on the fp32 MFMA kernels
     f32 = cfg.dtype == "fp32"
@@ -385,7 +390,7 @@ def main():
             return unfused_gated(L)
         if fp8:
             return pkg.multi_lora_linear_fp8(L["x"], L["wq"], L["ws"], L["b"], L["As"], L["Bs"], scales, routing,
-                                             wq_t=L["wqt"])
+                                             wq_t=L["wqt"], dx_bf16=args.fp8_dx_bf16)
         return pkg.multi_lora_linear(L["x"], L["w"], L["b"], L["As"], L["Bs"], scales, routing, weight_t=L["wt"])
 
     def step(stack=args.shared_qkv, fuse=True):
@@ -629,7 +634,9 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "e4m3 base forward (fp32 accumulate), bf16 LoRA and backward" if fp8 else "fp32" if f32 else "bf16",
+        "dtype": (("e4m3 base forward (fp32 accumulate), " + ("bf16 dX against the dequantised base"
+                                                               if args.fp8_dx_bf16 else "e4m3 dX")
+                   + ", bf16 LoRA") if fp8 else "fp32" if f32 else "bf16"),
         "data": "synthetic (seeded N(0,1) activations, N(0,1/in) frozen base, Kaiming-uniform A, N(0,0.02) B)",
         "config": {"workload": f"{cfg.name}: {pass_name} of the 6 DiT block linears "
                                f"(q,k,v,o {cfg.hidden}->{cfg.hidden}; ffn {cfg.hidden}->{cfg.ffn}->{cfg.hidden}), "
