@@ -656,40 +656,23 @@ __device__ __forceinline__ void tile_origin(const GemmArgs &args, int p, int &m0
   n0 = tn * C::BN;
 }
 
-// Entries c + 4 * hi .. c + 4 * hi + 3 of a per-column vector (f32, or bf16
-// when BF16) as f32: the eight entries c..c+7 come through the scalar data
-// cache (c is wave-uniform; Ncols is a multiple of 8, so they are all in
-// range or all past Ncols: zeros) and each lane picks its half. Scalar loads
-// are waited for with lgkmcnt, so the epilogue does not wait for
-// direct-to-LDS loads still in flight.
-typedef const __attribute__((address_space(4))) float cf32;
-typedef const __attribute__((address_space(4))) uint32_t cu32;
-__device__ __forceinline__ f32x4 col4(const void *p, bool bf16, int c, int ncols, bool hi) {
-  c = __builtin_amdgcn_readfirstlane(c);  // uniform by construction; keeps the loads scalar
-  if (c >= ncols) return f32x4{0.f, 0.f, 0.f, 0.f};
-  f32x4 lo4, hi4;
-  if (bf16) {
-    const cu32 *q = (const cu32 *)((const uint16_t *)p + c);
-    const uint32_t w0 = q[0], w1 = q[1], w2 = q[2], w3 = q[3];
-    lo4 = f32x4{bf16_to_f32(w0 & 0xffff), bf16_to_f32(w0 >> 16), bf16_to_f32(w1 & 0xffff), bf16_to_f32(w1 >> 16)};
-    hi4 = f32x4{bf16_to_f32(w2 & 0xffff), bf16_to_f32(w2 >> 16), bf16_to_f32(w3 & 0xffff), bf16_to_f32(w3 >> 16)};
+// This lane's 4 entries of a per-column vector (bf16 when BF16, else f32) at columns c .. c + 3
+// (c a multiple of 4): one 8- or 16-byte load; past the vector's end (Ncols is a multiple of 8,
+// so a group of 4 is all in range or all past it) the buffer reads zeros.
+template <bool BF16>
+__device__ __forceinline__ f32x4 cols4(__amdgpu_buffer_rsrc_t r, int c) {
+  if constexpr (BF16) {
+    const uint2 w = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(r, 2 * c, 0, 0));
+    return f32x4{bf16_to_f32(w.x & 0xffff), bf16_to_f32(w.x >> 16), bf16_to_f32(w.y & 0xffff), bf16_to_f32(w.y >> 16)};
   } else {
-    const cf32 *q = (const cf32 *)((const float *)p + c);
-    lo4 = f32x4{q[0], q[1], q[2], q[3]};
-    hi4 = f32x4{q[4], q[5], q[6], q[7]};
+    return __builtin_bit_cast(f32x4, buf_load16(r, 4 * c));
   }
-  return hi ? hi4 : lo4;
 }
 
-// Epilogue of one output tile, column tile by column tile: (fp8:
-// x_scale[m]·w_scale[n]), + bias, (+ Y), round to bf16. Register 4g + e of
-// tile (i, j) holds row m = m0 + wm0 + 32i + lane%32 and column
-// n = n0 + wn0 + 32j + 8g + 4(lane/32) + e.
-// STAGED: the rounded tile is staged in LDS (whose operand stages must be
-// free), row-major with 16-byte chunk q of row r at slot q ^ (r % CH), and
-// leaves in 16-byte stores that cover whole rows. Otherwise (and always when
-// accumulating into Y, which adds the old value in fp32 before the one
-// rounding) each lane stores its 4 consecutive columns directly.
+// Epilogue of one output tile: (fp8: x_scale[m]·w_scale[n]), + bias, (+ Y), round to bf16.
+// Register 4g + e of tile (i, j) holds row m = m0 + wm0 + 32i + lane%32 and column
+// n = n0 + wn0 + 32j + 8g + 4(lane/32) + e. BK: the bias (0: none, 1: bf16, 2: f32).
+// The bias and column scales come in as this lane's own 4-column groups (vector loads).
 // x + y·g of the reference's gated residual: fp32 multiply, then fp32 add, each
 // rounded to nearest (no fused multiply-add), as runtime/helios_residual_kernel.py:66-86
 // states it.
@@ -699,83 +682,94 @@ __device__ __forceinline__ float gated_add(float x, float y, float g) {
   return x + p;
 }
 
-template <class C, bool STAGED, bool ACCUM = true, bool RESID = false>
-__device__ __forceinline__ void store_tile(const f32x16 (&acc)[C::TM][C::TN], const GemmArgs &args, MLORA_LDS char *lds,
-                                           int m0, int n0, int wm0, int wn0, int lane, int wave,
-                                           uint16_t *Ybase, int ncol0) {
-  // Ybase: the output matrix (pitch ldy); its column 0 is tile column ncol0 (a stacked linear's
-  // first column; 0 otherwise)
+template <class C>
+struct EpiVectors {
+  __amdgpu_buffer_rsrc_t rb, rq;
+  bool has_qs;
+  float ps[C::TM];  // fp8: x_scale of each row tile's row
+  __device__ __forceinline__ void init(const GemmArgs &args, int bk, int m0, int wm0, int lane) {
+    rb = make_rsrc(args.bias, bk ? (int64_t)args.Ncols * (bk == 1 ? 2 : 4) : 0);
+    has_qs = C::F8 && args.qsc != nullptr;
+    rq = make_rsrc(args.qsc, has_qs ? (int64_t)args.Ncols * 4 : 0);
+#pragma unroll
+    for (int i = 0; i < C::TM; ++i) {
+      const int m = m0 + wm0 + 32 * i + (lane & 31);
+      ps[i] = 1.f;
+      if constexpr (C::F8) ps[i] = m < args.M ? args.psc[m] : 0.f;
+    }
+  }
+  // the 4 values of tile (i, j), group g, scaled (fp8) and biased, as fp32
+  template <int BK>
+  __device__ __forceinline__ void apply(float (&v)[4], const f32x16 &a, int g, int i, const f32x4 &b4,
+                                        const f32x4 &q4) const {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      v[e] = a[4 * g + e];
+      // e4m3: acc = Σ xq·wq + Σ (h/x_scale)·(B/w_scale): one scaling restores both
+      if constexpr (C::F8) v[e] *= ps[i] * q4[e];
+      if constexpr (BK != 0) v[e] += b4[e];
+    }
+  }
+  template <int BK>
+  __device__ __forceinline__ void load(f32x4 &b4, f32x4 &q4, int c) const {
+    b4 = f32x4{0.f, 0.f, 0.f, 0.f};
+    if constexpr (BK != 0) b4 = cols4<BK == 1>(rb, c);
+    q4 = f32x4{1.f, 1.f, 1.f, 1.f};
+    if constexpr (C::F8) {
+      if (has_qs) q4 = cols4<false>(rq, c);
+    }
+  }
+};
+
+// Staged store: the rounded tile goes to LDS (whose operand stages must be free), row-major with
+// 16-byte chunk q of row r at slot q ^ (r % CH), and leaves in 16-byte stores that cover whole
+// rows. Lane l writes its 8 bytes of (i, j, g) to row wm0 + 32i + l%32, slot
+// (wn0/8 + 4j + g) ^ (l%32 % CH): one XOR per (j, g), the row part an immediate offset.
+template <class C, int BK, bool RESID>
+__device__ __forceinline__ void store_staged(const f32x16 (&acc)[C::TM][C::TN], const GemmArgs &args,
+                                             MLORA_LDS char *lds, int m0, int n0, int wm0, int wn0, int lane, int wave,
+                                             uint16_t *Ybase, int ncol0) {
+  constexpr int ROWB = C::BN * 2;  // bytes per staged row
+  constexpr int CH = C::BN / 8;    // 16-byte chunks per staged row
+  static_assert(C::LDS_BYTES >= C::BM * ROWB, "the staged output tile fits the operand stages");
+  static_assert(C::WM * 32 * C::TM == C::BM && (C::BM / C::WM) % 32 == 0, "row tiles of 32 rows");
+  const int l31 = lane & 31, hh = lane >> 5;
+  const int ncol = n0 + wn0 + 4 * hh;  // this lane's first column of tile 0, group 0
+  EpiVectors<C> ev;
+  ev.init(args, BK, m0, wm0, lane);
+  // bf16 bias: every entry this lane needs (TN x 4 groups), loaded before the barrier
+  f32x4 b0[BK == 1 ? C::TN * 4 : 1];
+  if constexpr (BK == 1) {
+#pragma unroll
+    for (int q = 0; q < C::TN * 4; ++q) b0[q] = cols4<true>(ev.rb, ncol + 8 * q);
+  }
+  lds_pipeline_barrier();  // every wave's operand loads have landed and been read
+  const int rowb = (wm0 + l31) * ROWB + 8 * hh;
+  const int w8 = wn0 >> 3;
+  const int z = l31 % CH;
+#pragma unroll
+  for (int j = 0; j < C::TN; ++j) {
+    f32x4 b4[4], q4[4];
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      ev.template load<BK == 1 ? 0 : BK>(b4[g], q4[g], ncol + 32 * j + 8 * g);
+      if constexpr (BK == 1) b4[g] = b0[4 * j + g];
+    }
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      MLORA_LDS char *dst = lds + rowb + 16 * ((w8 + 4 * j + g) ^ z);
+#pragma unroll
+      for (int i = 0; i < C::TM; ++i) {
+        float v[4];
+        ev.template apply<BK>(v, acc[i][j], g, i, b4[g], q4[g]);
+        *(MLORA_LDS u32x2 *)(dst + i * 32 * ROWB) = u32x2{pack2_bf16(v[0], v[1]), pack2_bf16(v[2], v[3])};
+      }
+    }
+  }
+  lds_pipeline_barrier();
   const int rows_here = min(C::BM, args.M - m0);
   const int64_t ldy_b = args.ldy * 2;
   const __amdgpu_buffer_rsrc_t ry = make_rsrc(Ybase + (int64_t)m0 * args.ldy, rows_here * ldy_b);
-  constexpr int ROWB = C::BN * 2;  // bytes per staged row
-  constexpr int CH = C::BN / 8;    // 16-byte chunks per staged row
-  static_assert(!STAGED || C::LDS_BYTES >= C::BM * ROWB, "the staged output tile fits the operand stages");
-  const bool staged = STAGED && !(ACCUM && args.accumulate);
-  if (staged) lds_pipeline_barrier();  // every wave's operand loads have landed and been read
-  float ps[C::TM];  // fp8: x_scale of each row tile's row
-#pragma unroll
-  for (int i = 0; i < C::TM; ++i) {
-    const int m = m0 + wm0 + 32 * i + (lane & 31);
-    ps[i] = 1.f;
-    if constexpr (C::F8) ps[i] = m < args.M ? args.psc[m] : 0.f;
-  }
-#pragma unroll
-  for (int j = 0; j < C::TN; ++j) {
-    // bias and (fp8) w_scale of this lane's 16 columns of tile j, zero past Ncols
-    float bias[16], qs[16];
-#pragma unroll
-    for (int v = 0; v < 16; ++v) bias[v] = 0.f, qs[v] = 1.f;
-#pragma unroll
-    for (int g = 0; g < 4; ++g) {
-      const int c = n0 + wn0 + 32 * j + 8 * g;  // wave-uniform: this lane takes c + 4 * (lane / 32) + e
-      const bool hi = lane >= 32;
-      if (args.bias_dtype >= 0) {
-        const f32x4 b4 = col4(args.bias, args.bias_dtype == MLORA_BF16, c, args.Ncols, hi);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) bias[4 * g + e] = b4[e];
-      }
-      if (C::F8 && args.qsc != nullptr) {
-        const f32x4 q4 = col4(args.qsc, false, c, args.Ncols, hi);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) qs[4 * g + e] = q4[e];
-      }
-    }
-#pragma unroll
-    for (int i = 0; i < C::TM; ++i) {
-      const int ml = wm0 + 32 * i + (lane & 31);
-#pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const int nl = wn0 + 32 * j + 8 * g + 4 * (lane >> 5);  // tile-local column
-        const int n = n0 + nl;
-        float v[4];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          v[e] = acc[i][j][4 * g + e];
-          // e4m3: acc = Σ xq·wq + Σ (h/x_scale)·(B/w_scale): one scaling restores both
-          if constexpr (C::F8) v[e] *= ps[i] * qs[4 * g + e];
-          v[e] += bias[4 * g + e];
-        }
-        if (staged) {
-          const int slot = (nl >> 3) ^ (ml % CH);
-          *(MLORA_LDS u32x2 *)(lds + ml * ROWB + 16 * slot + 8 * ((nl >> 2) & 1)) =
-              u32x2{pack2_bf16(v[0], v[1]), pack2_bf16(v[2], v[3])};
-        } else {
-          // rows past M / columns past Ncols fall outside ry or are dropped
-          const int32_t off = (ml < rows_here && n < args.Ncols) ? (int32_t)(ml * ldy_b + (n - ncol0) * 2) : kOOB;
-          if (ACCUM && args.accumulate && off != kOOB) {
-            const u32x2 o = *(const MLORA_GLOBAL u32x2 *)(Ybase + (int64_t)(m0 + ml) * args.ldy + (n - ncol0));
-            v[0] += bf16_to_f32(o.x & 0xffff); v[1] += bf16_to_f32(o.x >> 16);
-            v[2] += bf16_to_f32(o.y & 0xffff); v[3] += bf16_to_f32(o.y >> 16);
-          }
-          buf_store8(ry, off, make_uint2(pack2_bf16(v[0], v[1]), pack2_bf16(v[2], v[3])));
-        }
-      }
-      __builtin_amdgcn_sched_barrier(0);  // one accumulator tile at a time
-    }
-  }
-  if (!staged) return;
-  lds_pipeline_barrier();
   // each wave stores BM / NW rows, 1 KB (1024 / ROWB rows) per instruction
   constexpr int RPI = 1024 / ROWB;
   constexpr int ROWS_W = C::BM / C::NW;
@@ -831,6 +825,62 @@ __device__ __forceinline__ void store_tile(const f32x16 (&acc)[C::TM][C::TN], co
   }
 }
 
+// Direct store (accumulating into Y, which adds the old value in fp32 before the one rounding):
+// each lane stores its 4 consecutive columns of (i, j, g).
+template <class C, int BK>
+__device__ __forceinline__ void store_direct(const f32x16 (&acc)[C::TM][C::TN], const GemmArgs &args, int m0, int n0,
+                                             int wm0, int wn0, int lane, uint16_t *Ybase, int ncol0) {
+  const int rows_here = min(C::BM, args.M - m0);
+  const int64_t ldy_b = args.ldy * 2;
+  const __amdgpu_buffer_rsrc_t ry = make_rsrc(Ybase + (int64_t)m0 * args.ldy, rows_here * ldy_b);
+  const int ncol = n0 + wn0 + 4 * (lane >> 5);
+  EpiVectors<C> ev;
+  ev.init(args, BK, m0, wm0, lane);
+#pragma unroll
+  for (int j = 0; j < C::TN; ++j) {
+    f32x4 b4[4], q4[4];
+#pragma unroll
+    for (int g = 0; g < 4; ++g) ev.template load<BK>(b4[g], q4[g], ncol + 32 * j + 8 * g);
+#pragma unroll
+    for (int i = 0; i < C::TM; ++i) {
+      const int ml = wm0 + 32 * i + (lane & 31);
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int n = ncol + 32 * j + 8 * g;
+        float v[4];
+        ev.template apply<BK>(v, acc[i][j], g, i, b4[g], q4[g]);
+        // rows past M / columns past Ncols fall outside ry or are dropped
+        const int32_t off = (ml < rows_here && n < args.Ncols) ? (int32_t)(ml * ldy_b + (n - ncol0) * 2) : kOOB;
+        if (args.accumulate && off != kOOB) {
+          const u32x2 o = *(const MLORA_GLOBAL u32x2 *)(Ybase + (int64_t)(m0 + ml) * args.ldy + (n - ncol0));
+          v[0] += bf16_to_f32(o.x & 0xffff); v[1] += bf16_to_f32(o.x >> 16);
+          v[2] += bf16_to_f32(o.y & 0xffff); v[3] += bf16_to_f32(o.y >> 16);
+        }
+        buf_store8(ry, off, make_uint2(pack2_bf16(v[0], v[1]), pack2_bf16(v[2], v[3])));
+      }
+      __builtin_amdgcn_sched_barrier(0);  // one accumulator tile at a time
+    }
+  }
+}
+
+// Ybase: the output matrix (pitch ldy); its column 0 is tile column ncol0 (a stacked linear's
+// first column; 0 otherwise). RESID: the stored value is the block's gated residual of bf16(Y)
+// (staged path only: the gated-residual entry points never accumulate).
+template <class C, bool RESID>
+__device__ __forceinline__ void store_tile(const f32x16 (&acc)[C::TM][C::TN], const GemmArgs &args, MLORA_LDS char *lds,
+                                           int m0, int n0, int wm0, int wn0, int lane, int wave, uint16_t *Ybase,
+                                           int ncol0) {
+  if (!RESID && args.accumulate) {
+    if (args.bias_dtype == MLORA_BF16) store_direct<C, 1>(acc, args, m0, n0, wm0, wn0, lane, Ybase, ncol0);
+    else if (args.bias_dtype == MLORA_F32) store_direct<C, 2>(acc, args, m0, n0, wm0, wn0, lane, Ybase, ncol0);
+    else store_direct<C, 0>(acc, args, m0, n0, wm0, wn0, lane, Ybase, ncol0);
+    return;
+  }
+  if (args.bias_dtype == MLORA_BF16) store_staged<C, 1, RESID>(acc, args, lds, m0, n0, wm0, wn0, lane, wave, Ybase, ncol0);
+  else if (args.bias_dtype == MLORA_F32) store_staged<C, 2, RESID>(acc, args, lds, m0, n0, wm0, wn0, lane, wave, Ybase, ncol0);
+  else store_staged<C, 0, RESID>(acc, args, lds, m0, n0, wm0, wn0, lane, wave, Ybase, ncol0);
+}
+
 // One workgroup per output tile. RESID: the stored value is the block's gated
 // residual of the result (see store_tile). STK: stacked linears (see GemmArgs).
 template <class C, bool RESID = false, int STK = 0>
@@ -854,9 +904,9 @@ __global__ __launch_bounds__(C::THREADS, C::WAVES_PER_SIMD) void gemm_kernel(con
   contract_tile<C, STK>(acc, args, lds, fa, m0, n0, tid);
   if constexpr (STK == 1) {
     const int g = __builtin_amdgcn_readfirstlane(n0 / args.group_cols);
-    store_tile<C, true, true, RESID>(acc, args, lds, m0, n0, wm0, wn0, lane, wave, args.Yg[g], g * args.group_cols);
+    store_tile<C, RESID>(acc, args, lds, m0, n0, wm0, wn0, lane, wave, args.Yg[g], g * args.group_cols);
   } else {
-    store_tile<C, true, true, RESID>(acc, args, lds, m0, n0, wm0, wn0, lane, wave, args.Y, 0);
+    store_tile<C, RESID>(acc, args, lds, m0, n0, wm0, wn0, lane, wave, args.Y, 0);
   }
 }
 
