@@ -257,54 +257,78 @@ shrink_kernel(const ShrinkArgs args) {
   for (int kc = 0; kc < nk; kc += ST) static_for<ST>([&](auto k) { return step(k, kc + decltype(k)::value); });
   wait_vmcnt<0>();
   lds_pipeline_barrier();  // the epilogue reuses the stages as its re-layout buffer
-  MLORA_LDS float *ebuf = (MLORA_LDS float *)lds;
 
-  // ---- epilogue 1: scaled bf16 rows (lane holds j = l%32, m = 8(v/4) + 4(l/32) + v%4)
-  MLORA_GLOBAL uint16_t *hr = gp(args.Hr);
+  // ---- epilogue: one 32-wide j tile at a time, each wave re-lays out its 32 rows through its
+  // own LDS block (fp32, 16-byte aligned rows of WS floats), then stores the scaled bf16 rows in
+  // 16-byte chunks and, if asked, the hi/lo fragments. The acc layout: lane holds j = l%32,
+  // m = 8(v/4) + 4(l/32) + v%4.
+  constexpr int WS = 36;
+  static_assert(NW * 32 * WS * 4 <= ST * C::STAGE_BYTES, "the re-layout blocks fit the stages");
+  MLORA_LDS float *wb = (MLORA_LDS float *)lds + wave * 32 * WS;
   const int wrow = m0 + 32 * wave;  // first row of this wave
+  const int vrows = min(32, mend - wrow);  // this wave's rows in the segment (<= 0: none)
+  // rows past the segment end fall outside rh: their stores are dropped
+  const __amdgpu_buffer_rsrc_t rh =
+      make_rsrc(args.Hr + (int64_t)(vrows > 0 ? wrow : 0) * args.ldh, (int64_t)max(vrows, 0) * args.ldh * 2);
+  // h rows: lane L stores row 16p + L/4, columns 8(L%4) .. +7 of the j tile (pass p = 0, 1)
+  const int hr_row = lane >> 2, hr_c8 = 8 * (lane & 3);
+  float rdiv[2] = {1.f, 1.f};
+  if (args.row_div != nullptr) {
 #pragma unroll
-  for (int j = 0; j < RT; ++j) {
-    const int col = 32 * j + (lane & 31);
-    if (col >= r) continue;
-#pragma unroll
-    for (int v = 0; v < 16; ++v) {
-      const int row = wrow + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
-      if (row < mend) {
-        const float h = acc[j][v] * scale;
-        hr[(int64_t)row * args.ldh + col] = f32_to_bf16_rne(args.row_div ? h / args.row_div[row] : h);
-      }
+    for (int p = 0; p < 2; ++p) {
+      const int row = wrow + 16 * p + hr_row;
+      if (row < mend) rdiv[p] = args.row_div[row];
     }
   }
-  // ---- epilogue 2: hi/lo fragments, re-laid out through LDS one 32-wide j tile at a time
-  if (args.Hf == nullptr) return;  // uniform over the workgroup
-  const bool wave_rows = wrow < mend;  // a wave past the segment end owns no block
+  const bool frag = args.Hf != nullptr && wrow < mend;  // a wave past the segment end owns no block
   const int64_t block = (args.pad.start[s] + rel0 + 32 * wave) / 32;
-  MLORA_LDS float *wb = ebuf + wave * 32 * 33;
   MLORA_GLOBAL u32x4 *hf = gp(args.Hf);
+  auto wave_lds_sync = [] {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  };
 #pragma unroll
   for (int j = 0; j < RT; ++j) {
     if (32 * j >= r) break;  // uniform
 #pragma unroll
     for (int v = 0; v < 16; ++v) {
       const int ml = 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
-      wb[ml * 33 + (lane & 31)] = acc[j][v] * scale;
+      wb[ml * WS + (lane & 31)] = acc[j][v] * scale;
     }
-    __syncthreads();
+    wave_lds_sync();
+    if (32 * j + hr_c8 < r) {
 #pragma unroll
-    for (int sub = 0; sub < 2; ++sub) {
-      const int t = 2 * j + sub;
-      if (16 * t < r && wave_rows) {
-        float v8[8];
+      for (int p = 0; p < 2; ++p) {
+        const int rl = 16 * p + hr_row;
+        const MLORA_LDS f32x4 *src = (const MLORA_LDS f32x4 *)(wb + rl * WS + hr_c8);
+        const f32x4 x0 = src[0], x1 = src[1];
+        float h[8] = {x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]};
+        if (args.row_div != nullptr) {
 #pragma unroll
-        for (int e = 0; e < 8; ++e) v8[e] = wb[(8 * (lane >> 4) + e) * 33 + 16 * sub + (lane & 15)];
-        u32x4 hi, lo;
-        split_hi_lo(v8, hi, lo);
-        const int64_t base = ((block * args.jtiles + t) * 2) * 64 + lane;
-        hf[base] = hi;
-        hf[base + 64] = lo;
+          for (int e = 0; e < 8; ++e) h[e] = h[e] / rdiv[p];
+        }
+        const u32x4 d = {pack2_bf16(h[0], h[1]), pack2_bf16(h[2], h[3]), pack2_bf16(h[4], h[5]), pack2_bf16(h[6], h[7])};
+        buf_store16(rh, (int32_t)((rl * args.ldh + 32 * j + hr_c8) * 2), d);
       }
     }
-    __syncthreads();
+    if (frag) {
+#pragma unroll
+      for (int sub = 0; sub < 2; ++sub) {
+        const int t = 2 * j + sub;
+        if (16 * t < r) {
+          float v8[8];
+#pragma unroll
+          for (int e = 0; e < 8; ++e) v8[e] = wb[(8 * (lane >> 4) + e) * WS + 16 * sub + (lane & 15)];
+          u32x4 hi, lo;
+          split_hi_lo(v8, hi, lo);
+          const int64_t base = ((block * args.jtiles + t) * 2) * 64 + lane;
+          hf[base] = hi;
+          hf[base + 64] = lo;
+        }
+      }
+    }
+    wave_lds_sync();  // every lane has read the block before the next j tile overwrites it
   }
 }
 
@@ -673,8 +697,8 @@ extern "C" int mlora_shrink(const void *p, int64_t ldp, int64_t M, int64_t K, co
   if (rmax == 0 || M == 0) return MLORA_OK;
   if ((st = check_bf16_matrix(p, ldp, M, K))) return st;
   if ((st = check_bf16_matrix(h_rows, ldh, M, rmax))) return st;
-  // 31-bit byte offsets inside the buffer resources of one tile / one operand
-  if (ldp * 2 * 256 >= kOOB || K * 2 * (int64_t)kMaxRank >= kOOB) return MLORA_ERR_LIMIT;
+  // 31-bit byte offsets inside the buffer resources of one tile / one operand / 32 h rows
+  if (ldp * 2 * 256 >= kOOB || K * 2 * (int64_t)kMaxRank >= kOOB || ldh * 2 * 32 >= kOOB) return MLORA_ERR_LIMIT;
   if (h_frag != nullptr) {
     if (frag_jtiles * 16 < rmax || frag_jtiles > kMaxRank / 16) return MLORA_ERR_INVALID;
     if (!aligned16(h_frag)) return MLORA_ERR_UNSUPPORTED;
