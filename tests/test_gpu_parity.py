@@ -229,6 +229,32 @@ def test_expand_standalone_accumulates(pkg, dev):
     assert O.rel_l2(f64(y), want) <= TOL
 
 
+@pytest.mark.parametrize("accumulate", [False, True], ids=["store", "accumulate"])
+@pytest.mark.parametrize("bias_dtype", [None, torch.bfloat16, torch.float32], ids=["no_bias", "bias_bf16", "bias_f32"])
+@pytest.mark.parametrize("M,N", [(300, 200), (4096, 4096)], ids=["tile128", "tile256"])
+def test_gemm_epilogue_forms(pkg, dev, M, N, bias_dtype, accumulate):
+    """Every epilogue form of the fused forward GEMM: no, bf16 or fp32 bias; Y stored, or the
+    old Y added before the one rounding; on the 128x128 and on the 256x256 tile."""
+    K, r = 136, 16
+    g = torch.Generator().manual_seed(M + N + (7 if accumulate else 0))
+    x = torch.randn(M, K, generator=g).to(torch.bfloat16)
+    w = (torch.randn(N, K, generator=g) / math.sqrt(K)).to(torch.bfloat16)
+    b = None if bias_dtype is None else (torch.randn(N, generator=g) / math.sqrt(K)).to(bias_dtype)
+    h = torch.randn(M, r, generator=g).to(torch.bfloat16)
+    B = (torch.randn(N, r, generator=g) * 0.1).to(torch.bfloat16)
+    y0 = torch.randn(M, N, generator=g).to(torch.bfloat16)
+    routing = pkg.SegmentRouting.single(M, 0)
+    out = y0.to(dev).clone() if accumulate else None
+    y = pkg.kernels.gemm_fwd(x.to(dev), w.to(dev), None if b is None else b.to(dev), h.to(dev), [B.to(dev)],
+                             routing, out=out, accumulate=accumulate)
+    want = f64(x) @ f64(w).T + f64(h) @ f64(B).T
+    if b is not None:
+        want = want + f64(b)[None, :]
+    if accumulate:
+        want = want + f64(y0)
+    assert O.rel_l2(f64(y), want) <= TOL
+
+
 @pytest.mark.parametrize("transposed", [False, True], ids=["dx_nn", "dx_nt"])
 @pytest.mark.parametrize("name,K,N", [("q", 1536, 1536), ("ffn.0", 1536, 8960), ("ffn.2", 8960, 1536)])
 def test_wan13b_full_shape(pkg, dev, name, K, N, transposed):
