@@ -284,8 +284,8 @@ class MultiLoRAFP8Function(torch.autograd.Function):
     scaled by dy_scale[m] in the epilogue; dA, dB as in the bf16 path. With
     ``dx_bf16`` the dX runs instead on the bf16 MFMA against the base dequantised
     to bf16 (bf16(w_scale[n]·wq[n, k]), made per call): dY is not quantised, so dX
-    carries bf16 rounding only (2.3e-3 rel-L2 against 2.6e-2 at config 5), at ~1.4× the
-    e4m3 dX's time (+12% per fwd+bwd step at config 5).
+    carries bf16 rounding only (2.3e-3 rel-L2 against 2.6e-2 at config 5), at the cost of
+    a slower dX (+17% per fwd+bwd step at config 5).
     """
 
     @staticmethod
