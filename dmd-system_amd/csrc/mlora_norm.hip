@@ -493,6 +493,7 @@ extern "C" int mlora_modulated_norm(const void *x, int x_dtype, int64_t x_sb, in
   if (rows == 0 || width == 0) return MLORA_OK;
   if (x == nullptr || scale == nullptr || shift == nullptr || out == nullptr) return MLORA_ERR_INVALID;
   if (tokens > 1 && (x_st < width || out_st < width)) return MLORA_ERR_INVALID;  // rows of one batch overlap
+  if (batches > 1 && out_sb < (tokens - 1) * out_st + width) return MLORA_ERR_INVALID;  // batches overlap
   if (!rows_aligned(x, x_sb, x_st) || !rows_aligned(out, out_sb, out_st) || !rows_aligned(scale, scale_sb, scale_st) ||
       !rows_aligned(shift, shift_sb, shift_st))
     return MLORA_ERR_UNSUPPORTED;
@@ -531,6 +532,7 @@ extern "C" int mlora_modulated_norm_backward(const void *x, int x_dtype, int64_t
   if (x == nullptr || g == nullptr || scale == nullptr || dx == nullptr || mean == nullptr || rstd == nullptr)
     return MLORA_ERR_INVALID;
   if (tokens > 1 && dx_st < width) return MLORA_ERR_INVALID;  // rows of one batch overlap
+  if (batches > 1 && dx_sb < (tokens - 1) * dx_st + width) return MLORA_ERR_INVALID;  // batches overlap
   if (!rows_aligned(x, x_sb, x_st) || !rows_aligned(g, g_sb, g_st) || !rows_aligned(scale, scale_sb, scale_st) ||
       !rows_aligned(dx, dx_sb, dx_st))
     return MLORA_ERR_UNSUPPORTED;
@@ -607,6 +609,7 @@ extern "C" int mlora_modulated_norm_component_grad(const void *x, int x_dtype, i
   if (tokens == 0) return MLORA_OK;
   if (x == nullptr || g == nullptr || mean == nullptr || rstd == nullptr) return MLORA_ERR_INVALID;
   if (out_sc < width || out_st < 6 * out_sc) return MLORA_ERR_INVALID;  // [B, T, 6, W] rows do not overlap
+  if (batches > 1 && out_sb < (tokens - 1) * out_st + 6 * out_sc) return MLORA_ERR_INVALID;  // nor batches
   if (!rows_aligned(x, x_sb, x_st) || !rows_aligned(g, g_sb, g_st) || !aligned16(out) || out_sb % 8 != 0 ||
       out_st % 8 != 0 || out_sc % 8 != 0)
     return MLORA_ERR_UNSUPPORTED;

@@ -261,11 +261,12 @@ def test_stacked_gemm_validates_before_launch(lib, pkg):
 
 
 def _mnorm(lib, *, x=0x1000, x_dtype=1, apply_ln=1, eps=1e-6, srow=None, hrow=None, tdt=1,
-           scale=0x2000, sdt=0, shift=0x3000, hdt=0, out=0x4000, B=1, T=4, W=64, xst=None, ost=None):
+           scale=0x2000, sdt=0, shift=0x3000, hdt=0, out=0x4000, B=1, T=4, W=64, xst=None, ost=None, osb=None):
     xst = W if xst is None else xst
     ost = W if ost is None else ost
+    osb = T * ost if osb is None else osb
     return lib.mlora_modulated_norm(x, x_dtype, T * xst, xst, apply_ln, eps, srow, hrow, tdt,
-                                    scale, sdt, shift, hdt, 0, 0, 0, 0, out, T * ost, ost, B, T, W, None)
+                                    scale, sdt, shift, hdt, 0, 0, 0, 0, out, osb, ost, B, T, W, None)
 
 
 def test_modulated_norm_rejects_bad_arguments(lib, pkg):
@@ -284,6 +285,7 @@ def test_modulated_norm_rejects_bad_arguments(lib, pkg):
     assert _mnorm(lib, x=0x1008) == L.ERR_UNSUPPORTED                  # 16-byte alignment
     assert _mnorm(lib, xst=68) == L.ERR_UNSUPPORTED                    # row stride not a multiple of 8
     assert _mnorm(lib, ost=32) == L.ERR_INVALID                        # output rows overlap
+    assert _mnorm(lib, B=2, osb=3 * 64) == L.ERR_INVALID               # the two samples' rows overlap
     assert _mnorm(lib, B=-1) == L.ERR_INVALID
     assert _mnorm(lib, B=0) == L.OK                                    # nothing to do, no launch
     assert _mnorm(lib, W=0) == L.OK
@@ -292,9 +294,11 @@ def test_modulated_norm_rejects_bad_arguments(lib, pkg):
 def test_modulated_norm_backward_rejects_bad_arguments(lib, pkg):
     L = pkg._lib
 
-    def bwd(x=0x1000, g=0x2000, sc=0x3000, dx=0x4000, mean=0x5000, rstd=0x6000, eps=1e-6, W=64, T=4, dt=1):
+    def bwd(x=0x1000, g=0x2000, sc=0x3000, dx=0x4000, mean=0x5000, rstd=0x6000, eps=1e-6, W=64, T=4, dt=1, B=1,
+            dxsb=None):
+        dxsb = T * W if dxsb is None else dxsb
         return lib.mlora_modulated_norm_backward(x, dt, T * W, W, g, dt, T * W, W, None, 1, sc, 0, 0, 0,
-                                                 dx, dt, T * W, W, mean, rstd, eps, 1, T, W, None)
+                                                 dx, dt, dxsb, W, mean, rstd, eps, B, T, W, None)
 
     assert bwd(W=5128) == L.ERR_UNSUPPORTED          # the backward keeps rows up to 5120 in registers
     assert bwd(W=12) == L.ERR_UNSUPPORTED
@@ -303,10 +307,11 @@ def test_modulated_norm_backward_rejects_bad_arguments(lib, pkg):
     assert bwd(mean=None) == L.ERR_INVALID
     assert bwd(g=0x2004) == L.ERR_UNSUPPORTED        # 16-byte alignment
     assert bwd(T=0) == L.OK
+    assert bwd(B=2, dxsb=3 * 64) == L.ERR_INVALID    # the two samples' dx rows overlap
 
-    def comp(reduce=1, si=4, hi=3, ws=None, wsb=0, out=0x7000, sb=6 * 64, st=0, sc=64, W=64, T=4):
+    def comp(reduce=1, si=4, hi=3, ws=None, wsb=0, out=0x7000, sb=6 * 64, st=0, sc=64, W=64, T=4, B=1):
         return lib.mlora_modulated_norm_component_grad(0x1000, 1, T * W, W, 0x2000, 1, T * W, W, 0x5000, 0x6000,
-                                                       out, 0, sb, st, sc, si, hi, reduce, ws, wsb, 1, T, W, None)
+                                                       out, 0, sb, st, sc, si, hi, reduce, ws, wsb, B, T, W, None)
 
     need = lib.mlora_modulated_norm_component_workspace_bytes(1, 4, 64)
     assert need == 1 * 1 * 2 * 64 * 4
@@ -317,4 +322,5 @@ def test_modulated_norm_backward_rejects_bad_arguments(lib, pkg):
     assert comp(sc=32) == L.ERR_INVALID              # slots overlap
     assert comp(out=None) == L.ERR_INVALID
     assert comp(reduce=0, st=100) == L.ERR_INVALID   # [B, T, 6, W] rows overlap
+    assert comp(reduce=0, st=6 * 64, sb=3 * 6 * 64, B=2) == L.ERR_INVALID  # the two samples overlap
     assert comp(reduce=0, sb=4 * 6 * 64, st=6 * 64, out=0x7004) == L.ERR_UNSUPPORTED
