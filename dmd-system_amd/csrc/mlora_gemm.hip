@@ -496,7 +496,12 @@ __device__ __forceinline__ void contract_tile(f32x16 (&acc)[C::TM][C::TN], const
   // stacked forward: this tile's linear reads its own columns of the LoRA rows
   const int ecol = STK == 1 ? __builtin_amdgcn_readfirstlane((n0 / args.group_cols) * args.group_ecols) : 0;
   int grp = 0;  // stacked dX: the linear whose dY the main contraction is reading
-  int seg = args.E != nullptr ? seg_of_row(args.seg, m0) : args.seg.n;
+  // the first segment that may overlap the tile: looked up when the LoRA sources start, so that
+  // the scalar loads of the search do not delay the first k-tile loads
+  int seg = -1;
+  auto first_seg = [&]() {
+    if (seg < 0) seg = args.E != nullptr ? seg_of_row(args.seg, m0) : args.seg.n;
+  };
   Pipe<C> pipe;
   constexpr int esz0 = C::F8 ? 1 : 2;
   KSource src{static_cast<const char *>(args.P), static_cast<const char *>(args.Q), esz0 * args.ldp, esz0 * args.ldq,
@@ -508,6 +513,7 @@ __device__ __forceinline__ void contract_tile(f32x16 (&acc)[C::TM][C::TN], const
   if constexpr (C::F8) ntile = (ntile + S - 1) / S * S;
   const int n_main = ntile;  // e4m3 k-tiles (F8), before the first LoRA tile
   if (ntile == 0) {
+    first_seg();
     if (!next_lora_source(args, C::NN, m0, row_end, seg, src, ecol)) return;
     bk = C::KB / src.esz;
     ntile = (src.klim + bk - 1) / bk;
@@ -538,6 +544,7 @@ __device__ __forceinline__ void contract_tile(f32x16 (&acc)[C::TM][C::TN], const
         return true;
       }
     }
+    first_seg();
     if (!next_lora_source(args, C::NN, m0, row_end, seg, src, ecol)) {
       exhausted = true;
       return false;
@@ -888,6 +895,10 @@ __global__ __launch_bounds__(C::THREADS, C::WAVES_PER_SIMD) void gemm_kernel(con
   __shared__ u32x4 smem[C::LDS_BYTES / 16];
   MLORA_LDS char *lds = (MLORA_LDS char *)smem;
   const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
+  // the scalar arguments of the tile order and the first k-tile loads, fetched together (one
+  // wait) instead of one dependent fetch after another
+  asm volatile("" ::"s"(args.tiles_m), "s"(args.tiles_n), "s"(args.group_m), "s"(args.M), "s"(args.Ncols),
+               "s"(args.Kc), "s"(args.ldp), "s"(args.ldq), "s"(args.P), "s"(args.Q));
   const int wm0 = (wave / C::WN) * (C::BM / C::WM);
   const int wn0 = (wave % C::WN) * (C::BN / C::WN);
   int m0, n0;
