@@ -773,18 +773,22 @@ __device__ __forceinline__ void store_staged(const f32x16 (&acc)[C::TM][C::TN], 
       }
     }
   }
-  lds_pipeline_barrier();
+  // Each wave stores the block it staged itself: (BM / WM) rows of (BN / WN) columns, in 1 KB
+  // instructions of whole 16-byte chunks. It reads only its own LDS writes, so a wave-level
+  // ordering suffices (no workgroup barrier).
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
   const int rows_here = min(C::BM, args.M - m0);
   const int64_t ldy_b = args.ldy * 2;
   const __amdgpu_buffer_rsrc_t ry = make_rsrc(Ybase + (int64_t)m0 * args.ldy, rows_here * ldy_b);
-  // each wave stores BM / NW rows, 1 KB (1024 / ROWB rows) per instruction
-  constexpr int RPI = 1024 / ROWB;
-  constexpr int ROWS_W = C::BM / C::NW;
-  static_assert(ROWS_W % RPI == 0, "whole store instructions per wave");
+  constexpr int WROWS = C::BM / C::WM, WCH = C::BN / C::WN / 8;  // the wave's rows; its 16-byte chunks per row
+  constexpr int RPI = 64 / WCH;                                  // rows per 1 KB instruction
+  static_assert(64 % WCH == 0 && WROWS % RPI == 0, "whole store instructions per wave");
 #pragma unroll
-  for (int it = 0; it < ROWS_W / RPI; ++it) {
-    const int r = wave * ROWS_W + it * RPI + lane / CH;
-    const int q = lane % CH;
+  for (int it = 0; it < WROWS / RPI; ++it) {
+    const int r = wm0 + it * RPI + lane / WCH;
+    const int q = w8 + lane % WCH;
     u32x4 d = *(const lds_u4 *)(lds + r * ROWB + 16 * (q ^ (r % CH)));
     const int n = n0 + 8 * q;
     const int32_t off = (r < rows_here && n < args.Ncols) ? (int32_t)(r * ldy_b + (n - ncol0) * 2) : kOOB;
