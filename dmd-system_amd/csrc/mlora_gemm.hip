@@ -676,10 +676,6 @@ __device__ __forceinline__ f32x4 cols4(__amdgpu_buffer_rsrc_t r, int c) {
   }
 }
 
-// Epilogue of one output tile: (fp8: x_scale[m]·w_scale[n]), + bias, (+ Y), round to bf16.
-// Register 4g + e of tile (i, j) holds row m = m0 + wm0 + 32i + lane%32 and column
-// n = n0 + wn0 + 32j + 8g + 4(lane/32) + e. BK: the bias (0: none, 1: bf16, 2: f32).
-// The bias and column scales come in as this lane's own 4-column groups (vector loads).
 // x + y·g of the reference's gated residual: fp32 multiply, then fp32 add, each
 // rounded to nearest (no fused multiply-add), as runtime/helios_residual_kernel.py:66-86
 // states it.
@@ -689,6 +685,10 @@ __device__ __forceinline__ float gated_add(float x, float y, float g) {
   return x + p;
 }
 
+// Epilogue of one output tile: (fp8: x_scale[m]·w_scale[n]), + bias, (+ Y), round to bf16.
+// Register 4g + e of tile (i, j) holds row m = m0 + wm0 + 32i + lane%32 and column
+// n = n0 + wn0 + 32j + 8g + 4(lane/32) + e. BK: the bias (0: none, 1: bf16, 2: f32).
+// The bias and column scales come in as this lane's own 4-column groups (vector loads).
 template <class C>
 struct EpiVectors {
   __amdgpu_buffer_rsrc_t rb, rq;
@@ -734,7 +734,7 @@ struct EpiVectors {
 // (wn0/8 + 4j + g) ^ (l%32 % CH): one XOR per (j, g), the row part an immediate offset.
 template <class C, int BK, bool RESID>
 __device__ __forceinline__ void store_staged(const f32x16 (&acc)[C::TM][C::TN], const GemmArgs &args,
-                                             MLORA_LDS char *lds, int m0, int n0, int wm0, int wn0, int lane, int wave,
+                                             MLORA_LDS char *lds, int m0, int n0, int wm0, int wn0, int lane,
                                              uint16_t *Ybase, int ncol0) {
   constexpr int ROWB = C::BN * 2;  // bytes per staged row
   constexpr int CH = C::BN / 8;    // 16-byte chunks per staged row
@@ -879,17 +879,16 @@ __device__ __forceinline__ void store_direct(const f32x16 (&acc)[C::TM][C::TN], 
 // (staged path only: the gated-residual entry points never accumulate).
 template <class C, bool RESID>
 __device__ __forceinline__ void store_tile(const f32x16 (&acc)[C::TM][C::TN], const GemmArgs &args, MLORA_LDS char *lds,
-                                           int m0, int n0, int wm0, int wn0, int lane, int wave, uint16_t *Ybase,
-                                           int ncol0) {
+                                           int m0, int n0, int wm0, int wn0, int lane, uint16_t *Ybase, int ncol0) {
   if (!RESID && args.accumulate) {
     if (args.bias_dtype == MLORA_BF16) store_direct<C, 1>(acc, args, m0, n0, wm0, wn0, lane, Ybase, ncol0);
     else if (args.bias_dtype == MLORA_F32) store_direct<C, 2>(acc, args, m0, n0, wm0, wn0, lane, Ybase, ncol0);
     else store_direct<C, 0>(acc, args, m0, n0, wm0, wn0, lane, Ybase, ncol0);
     return;
   }
-  if (args.bias_dtype == MLORA_BF16) store_staged<C, 1, RESID>(acc, args, lds, m0, n0, wm0, wn0, lane, wave, Ybase, ncol0);
-  else if (args.bias_dtype == MLORA_F32) store_staged<C, 2, RESID>(acc, args, lds, m0, n0, wm0, wn0, lane, wave, Ybase, ncol0);
-  else store_staged<C, 0, RESID>(acc, args, lds, m0, n0, wm0, wn0, lane, wave, Ybase, ncol0);
+  if (args.bias_dtype == MLORA_BF16) store_staged<C, 1, RESID>(acc, args, lds, m0, n0, wm0, wn0, lane, Ybase, ncol0);
+  else if (args.bias_dtype == MLORA_F32) store_staged<C, 2, RESID>(acc, args, lds, m0, n0, wm0, wn0, lane, Ybase, ncol0);
+  else store_staged<C, 0, RESID>(acc, args, lds, m0, n0, wm0, wn0, lane, Ybase, ncol0);
 }
 
 // One workgroup per output tile. RESID: the stored value is the block's gated
@@ -919,9 +918,9 @@ __global__ __launch_bounds__(C::THREADS, C::WAVES_PER_SIMD) void gemm_kernel(con
   contract_tile<C, STK>(acc, args, lds, fa, m0, n0, tid);
   if constexpr (STK == 1) {
     const int g = __builtin_amdgcn_readfirstlane(n0 / args.group_cols);
-    store_tile<C, RESID>(acc, args, lds, m0, n0, wm0, wn0, lane, wave, args.Yg[g], g * args.group_cols);
+    store_tile<C, RESID>(acc, args, lds, m0, n0, wm0, wn0, lane, args.Yg[g], g * args.group_cols);
   } else {
-    store_tile<C, RESID>(acc, args, lds, m0, n0, wm0, wn0, lane, wave, args.Y, 0);
+    store_tile<C, RESID>(acc, args, lds, m0, n0, wm0, wn0, lane, args.Y, 0);
   }
 }
 
