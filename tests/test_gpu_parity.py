@@ -122,7 +122,37 @@ def test_more_segments_than_one_call(pkg, dev):
     check_against_oracle(pkg, dev, case, [1.0, 0.5, 2.0], routing)
 
 
-def test_routing_is_bit_exact(pkg, dev):
+@pytest.mark.parametrize("rank,lengths,ids", [
+    (64, (20001, 333, 16000, 4097, 30000), (0, -1, 1, 2, 0)),   # 256-row tiles
+    (128, (9000, 77, 31000, 641), (1, 0, -1, 1)),                # 128-row tiles
+], ids=["rank64", "rank128"])
+def test_shrink_segments_match_single_segment_calls(pkg, dev, rank, lengths, ids):
+    """Ragged segments (tiles ending inside a segment's last 32 rows, a base-only segment between
+    adapter segments, more tiles than the GPU runs at once): each segment's h rows and fragments
+    equal those of a call on that segment alone, bit for bit, and h matches the fp64 product."""
+    from dmd_system_amd import kernels
+    K, M = 96, sum(lengths)
+    g = torch.Generator().manual_seed(21)
+    x = torch.randn(M, K, generator=g).to(torch.bfloat16)
+    As = [((torch.rand(rank, K, generator=g) * 2 - 1) / math.sqrt(K)).to(torch.bfloat16) for _ in range(3)]
+    scales = [1.0, 0.5, 2.0]
+    xg, Ag = x.to(dev), [a.to(dev) for a in As]
+    routing = pkg.SegmentRouting.from_lengths(lengths, ids)
+    h, frags = kernels.shrink(xg, Ag, 0, scales, routing, True, rank)
+    torch.cuda.synchronize()
+    (frag,) = frags
+    fb = kernels.frag_jtiles(rank) * 2048 // 2  # bf16 elements per 32-row fragment block
+    off, block = 0, 0
+    for n, a in zip(lengths, ids):
+        nb = (n + 31) // 32
+        if a >= 0:
+            h1, (f1,) = kernels.shrink(xg[off:off + n], Ag, 0, scales, pkg.SegmentRouting.single(n, a), True, rank)
+            torch.cuda.synchronize()
+            assert torch.equal(h[off:off + n], h1), (n, a)
+            assert torch.equal(frag[block * fb:(block + nb) * fb], f1[:nb * fb]), (n, a)
+            ref = scales[a] * (f64(x[off:off + n]) @ f64(As[a]).T)
+            assert O.rel_l2(f64(h1), ref) <= 4e-3
+        off, block = off + n, block + nb
     """Rows of base-only segments equal an adapter-free launch bit for bit, and
     adapter rows equal the launch with that adapter on all rows."""
     lengths, ids = (130, 70, 200, 112), (0, -1, 1, -1)
