@@ -286,6 +286,17 @@ def test_gemm_epilogue_forms(pkg, dev, M, N, bias_dtype, accumulate):
 
 
 @pytest.mark.parametrize("transposed", [False, True], ids=["dx_nn", "dx_nt"])
+def test_big_tiles_with_ragged_edges(pkg, dev, transposed):
+    """The 256x256 tile (>= 256 output tiles) with partial tiles on both edges: M and N off
+    multiples of 256 (N a multiple of 8), K off a multiple of 64, a segment boundary and a
+    base-only segment inside row tiles, ranks 64 and 40; Y, dX, dA, dB vs the fp64 oracle."""
+    lengths, ids = (3001, 200, 4999), (0, -1, 1)
+    case = make_case(sum(lengths), 520, 4104, (64, 40), lengths, ids, seed=22)
+    routing = pkg.SegmentRouting.from_lengths(lengths, ids)
+    check_against_oracle(pkg, dev, case, [1.0, 2.0], routing, transposed=transposed)
+
+
+@pytest.mark.parametrize("transposed", [False, True], ids=["dx_nn", "dx_nt"])
 @pytest.mark.parametrize("name,K,N", [("q", 1536, 1536), ("ffn.0", 1536, 8960), ("ffn.2", 8960, 1536)])
 def test_wan13b_full_shape(pkg, dev, name, K, N, transposed):
     """BASELINE config 2 (65520 tokens, 2 adapters rank 64) at full size:
