@@ -285,6 +285,50 @@ def test_gemm_epilogue_forms(pkg, dev, M, N, bias_dtype, accumulate):
     assert O.rel_l2(f64(y), want) <= TOL
 
 
+@pytest.mark.parametrize("M", [3000, 9000], ids=["tile128", "tile256"])
+def test_pitched_operands_equal_contiguous(pkg, dev, M):
+    """Every matrix given as a view with a wider row pitch and a 16-byte offset (X, W, dY, h,
+    the output): shrink, forward GEMM, NN and NT dX GEMMs and the dA / dB reductions give the
+    same bits as on contiguous copies."""
+    from dmd_system_amd import kernels
+    K, N, r = 264, 392, 32
+    routing = pkg.SegmentRouting.from_lengths((M // 3, 200, M - M // 3 - 200), (0, -1, 1))
+    g = torch.Generator().manual_seed(23)
+
+    def pitched(rows, cols, std=1.0):
+        big = (torch.randn(rows, cols + 24, generator=g) * std).to(torch.bfloat16).to(dev)
+        return big[:, 8:8 + cols]
+
+    x, w, dy = pitched(M, K), pitched(N, K, 1 / math.sqrt(K)), pitched(M, N)
+    b = (torch.randn(N, generator=g) / math.sqrt(K)).to(torch.bfloat16).to(dev)
+    As = [((torch.rand(r, K, generator=g) * 2 - 1) / math.sqrt(K)).to(torch.bfloat16).to(dev) for _ in range(2)]
+    Bs = [(torch.randn(N, r, generator=g) * 0.05).to(torch.bfloat16).to(dev) for _ in range(2)]
+    scales, bf = [1.0, 0.5], [torch.bfloat16] * 2
+    At = [a.t().contiguous() for a in As]
+    wt = pitched(K, N)
+    with torch.no_grad():
+        wt.copy_(w.t())
+
+    def run(x, w, wt, dy, h_out, y_out):
+        h, hf = kernels.shrink(x, As, 0, scales, routing, True, r, h_out=h_out)
+        gr, gf = kernels.shrink(dy, Bs, 1, scales, routing, True, r)
+        y = kernels.gemm_fwd(x, w, b, h, Bs, routing, out=y_out)
+        dx_nn = kernels.gemm_dx(dy, w, gr, As, routing)
+        dx_nt = kernels.gemm_fwd(dy, wt, None, gr, At, routing)
+        dB = kernels.seg_outer(dy, hf, r, [r, r], routing, 0, bf)
+        dA = kernels.seg_outer(x, gf, r, [r, r], routing, 1, bf)
+        torch.cuda.synchronize()
+        return [h, y, dx_nn, dx_nt, *dB, *dA]
+
+    h_pitched = pitched(M, r)
+    h_pitched.zero_()  # the shrink writes only the rows that have an adapter
+    got = run(x, w, wt, dy, h_pitched, pitched(M, N))
+    want = run(x.contiguous(), w.contiguous(), wt.contiguous(), dy.contiguous(),
+               torch.zeros(M, r, dtype=torch.bfloat16, device=dev), None)
+    for i, (a, c) in enumerate(zip(got, want)):
+        assert torch.equal(a, c), i
+
+
 @pytest.mark.parametrize("transposed", [False, True], ids=["dx_nn", "dx_nt"])
 def test_big_tiles_with_ragged_edges(pkg, dev, transposed):
     """The 256x256 tile (>= 256 output tiles) with partial tiles on both edges: M and N off
