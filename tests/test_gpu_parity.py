@@ -285,6 +285,25 @@ def test_gemm_epilogue_forms(pkg, dev, M, N, bias_dtype, accumulate):
     assert O.rel_l2(f64(y), want) <= TOL
 
 
+@pytest.mark.parametrize("transposed", [False, True], ids=["dx_nn", "dx_nt"])
+def test_empty_batch(pkg, dev, transposed):
+    """No tokens, as torch's F.linear path gives it: Y [0, N], dX [0, K], zero adapter gradients."""
+    K, N, r = 128, 96, 16
+    g = torch.Generator().manual_seed(24)
+    w = (torch.randn(N, K, generator=g) / math.sqrt(K)).to(torch.bfloat16).to(dev)
+    b = torch.randn(N, generator=g).to(torch.bfloat16).to(dev)
+    As = [torch.randn(r, K, generator=g).to(torch.bfloat16).to(dev).requires_grad_(True)]
+    Bs = [torch.randn(N, r, generator=g).to(torch.bfloat16).to(dev).requires_grad_(True)]
+    x = torch.empty(0, K, dtype=torch.bfloat16, device=dev, requires_grad=True)
+    wt = w.t().contiguous() if transposed else None
+    y = pkg.multi_lora_linear(x, w, b, As, Bs, [1.0], pkg.SegmentRouting.from_lengths((0,), (0,)), weight_t=wt)
+    y.backward(torch.empty(0, N, dtype=torch.bfloat16, device=dev))
+    torch.cuda.synchronize()
+    assert y.shape == (0, N) and x.grad.shape == (0, K)
+    for t in As + Bs:
+        assert t.grad is not None and t.grad.shape == t.shape and not t.grad.any()
+
+
 @pytest.mark.parametrize("M", [3000, 9000], ids=["tile128", "tile256"])
 def test_pitched_operands_equal_contiguous(pkg, dev, M):
     """Every matrix given as a view with a wider row pitch and a 16-byte offset (X, W, dY, h,
