@@ -324,3 +324,61 @@ def test_modulated_norm_backward_rejects_bad_arguments(lib, pkg):
     assert comp(reduce=0, st=100) == L.ERR_INVALID   # [B, T, 6, W] rows overlap
     assert comp(reduce=0, st=6 * 64, sb=3 * 6 * 64, B=2) == L.ERR_INVALID  # the two samples overlap
     assert comp(reduce=0, sb=4 * 6 * 64, st=6 * 64, out=0x7004) == L.ERR_UNSUPPORTED
+
+
+# ---------------------------------------------------------------- host-side sizing, random routings
+
+from hypothesis import given, settings, strategies as st  # noqa: E402
+
+_segments = st.lists(st.tuples(st.integers(0, 300), st.integers(-1, 3)), min_size=1, max_size=128)
+
+
+@settings(max_examples=300, deadline=None)
+@given(segs=_segments, jt=st.integers(0, 16))
+def test_frag_bytes_is_padded_blocks_times_jtiles(lib, pkg, segs, jt):
+    """One 2 KB fragment tile per 32-row block of every segment (each padded to whole blocks) and
+    j-tile, whatever the routing."""
+    L = pkg._lib
+    off = [0]
+    for n, _ in segs:
+        off.append(off[-1] + n)
+    got = lib.mlora_frag_bytes(off[-1], jt, L.i64_array(off), L.i32_array([a for _, a in segs]), len(segs))
+    assert got == sum((n + 31) // 32 for n, _ in segs) * jt * 2048
+
+
+@settings(max_examples=200, deadline=None)
+@given(segs=_segments, bad=st.sampled_from(["start", "decrease", "end", "id"]))
+def test_malformed_routings_are_rejected(lib, pkg, segs, bad):
+    L = pkg._lib
+    off = [0]
+    for n, _ in segs:
+        off.append(off[-1] + n)
+    ids = [a for _, a in segs]
+    M = off[-1]
+    if bad == "start":
+        off[0] = 1
+    elif bad == "decrease":
+        if len(off) < 3:
+            off.insert(1, 5)
+            ids.append(0)
+        off[1] = off[2] + 1
+    elif bad == "end":
+        M += 1
+    else:
+        ids[0] = -2
+    assert lib.mlora_frag_bytes(M, 4, L.i64_array(off), L.i32_array(ids), len(ids)) == L.ERR_INVALID
+
+
+@settings(max_examples=200, deadline=None)
+@given(segs=_segments, C=st.sampled_from([8, 72, 1536, 8960]))
+def test_seg_outer_workspace_follows_the_adapter_rows(lib, pkg, segs, C):
+    """fp32 partials of whole C-wide rows; none at all when no adapter owns a row."""
+    L = pkg._lib
+    off = [0]
+    for n, _ in segs:
+        off.append(off[-1] + n)
+    ids = [a for _, a in segs]
+    ranks = L.i32_array([64, 16, 128, 8])
+    ws = lib.mlora_seg_outer_workspace_bytes(off[-1], C, ranks, 4, L.i64_array(off), L.i32_array(ids), len(ids))
+    assert ws >= 0 and ws % (C * 4) == 0
+    assert (ws > 0) == any(n > 0 and a >= 0 for n, a in segs)

@@ -39,6 +39,24 @@ def test_routing_groups_cover_rows_exactly(pkg):
     assert nseg == 300 and rows == r.row_adapter()
 
 
+from hypothesis import given, settings, strategies as st  # noqa: E402
+
+
+@settings(max_examples=300, deadline=None)
+@given(segs=st.lists(st.tuples(st.integers(0, 20), st.integers(-1, 5)), min_size=1, max_size=700),
+       per_call=st.integers(1, 200))
+def test_routing_groups_property(pkg, segs, per_call):
+    """Any routing split into calls of at most `per_call` segments: the calls tile the rows in order,
+    each with local offsets from 0, and give every row its adapter."""
+    r = pkg.SegmentRouting.from_lengths([n for n, _ in segs], [a for _, a in segs])
+    rows, nseg, end = [], 0, 0
+    for r0, r1, off, gids in r.groups(per_call):
+        assert r0 == end and 1 <= len(gids) <= per_call and off[0] == 0 and off[-1] == r1 - r0
+        rows.extend(pkg.SegmentRouting(off, gids).row_adapter())
+        nseg, end = nseg + len(gids), r1
+    assert nseg == len(segs) and end == r.num_rows and rows == r.row_adapter()
+
+
 # ---------------------------------------------------------------- drop-in trainable scope
 
 class Native(nn.Module):
