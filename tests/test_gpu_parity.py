@@ -10,6 +10,7 @@ import math
 import numpy as np
 import pytest
 import torch
+from hypothesis import given, settings, strategies as st
 
 from oracle import multilora_oracle as O
 
@@ -120,6 +121,26 @@ def test_more_segments_than_one_call(pkg, dev):
     case = make_case(sum(lengths), 64, 72, (8, 16, 8), lengths, ids, seed=14)
     routing = pkg.SegmentRouting.from_lengths(lengths, ids)
     check_against_oracle(pkg, dev, case, [1.0, 0.5, 2.0], routing)
+
+
+_RANKS = (8, 16, 24, 64, 128)
+
+
+@settings(max_examples=25, deadline=None, derandomize=True)
+@given(segs=st.lists(st.tuples(st.integers(0, 300), st.integers(-1, 3)), min_size=1, max_size=12),
+       rank_idx=st.lists(st.integers(0, len(_RANKS) - 1), min_size=4, max_size=4),
+       transposed=st.booleans())
+def test_random_routings_vs_oracle(pkg, dev, segs, rank_idx, transposed):
+    """Random segment lengths (empty ones included), adapter ids (base-only ones included) and
+    ranks, a fixed set of examples: Y, dX, dA and dB against the fp64 oracle."""
+    lengths, ids = [n for n, _ in segs], [a for _, a in segs]
+    M = sum(lengths)
+    if M == 0:
+        return
+    ranks = tuple(_RANKS[i] for i in rank_idx)
+    case = make_case(M, 136, 200, ranks, lengths, ids, seed=M)
+    routing = pkg.SegmentRouting.from_lengths(lengths, ids)
+    check_against_oracle(pkg, dev, case, [1.0, 0.5, 2.0, 0.25], routing, transposed=transposed)
 
 
 @pytest.mark.parametrize("rank,lengths,ids", [
