@@ -21,25 +21,39 @@ def _tensors(dev, seed, M=4096, K=512, N=768, ranks=(64, 32)):
     return [t.to(dev) for t in (x, *As, *Bs, dy)]
 
 
-def _eager(pkg, w, wt, b, routing, x, As, Bs, dy):
+def _eager(op, x, As, Bs, dy):
     """y, dX, dA, dB of one eager step on fresh leaves holding the given values."""
     xl = x.detach().clone().requires_grad_(True)
     Al = [a.detach().clone().requires_grad_(True) for a in As]
     Bl = [v.detach().clone().requires_grad_(True) for v in Bs]
-    y = pkg.multi_lora_linear(xl, w, b, Al, Bl, [1.0, 0.5], routing, weight_t=wt)
+    y = op(xl, Al, Bl)
     y.backward(dy)
     torch.cuda.synchronize()
     return [y.detach(), xl.grad] + [a.grad for a in Al] + [v.grad for v in Bl]
 
 
-@pytest.mark.parametrize("transposed", [False, True], ids=["dx_nn", "dx_nt"])
-def test_graph_replays_equal_eager(pkg, dev, transposed):
+@pytest.mark.parametrize("path", ["bf16_dx_nn", "bf16_dx_nt", "e4m3", "e4m3_dx_bf16"])
+def test_graph_replays_equal_eager(pkg, dev, path):
+    """bf16 base (dX on the NN kernel or against the transposed base) and e4m3 base (e4m3 dX, or
+    bf16 dX against the dequantised base): forward, backward and the per-row quantisations."""
     M, K, N = 4096, 512, 768
     g = torch.Generator().manual_seed(30)
     w = (torch.randn(N, K, generator=g) / math.sqrt(K)).to(torch.bfloat16).to(dev)
     b = (torch.randn(N, generator=g) / math.sqrt(K)).to(torch.bfloat16).to(dev)
-    wt = w.t().contiguous() if transposed else None
     routing = pkg.SegmentRouting.from_lengths((1500, 96, 2500), (0, -1, 1))
+    if path.startswith("bf16"):
+        wt = w.t().contiguous() if path == "bf16_dx_nt" else None
+
+        def op(x, As, Bs):
+            return pkg.multi_lora_linear(x, w, b, As, Bs, [1.0, 0.5], routing, weight_t=wt)
+    else:
+        from dmd_system_amd import kernels
+        wq, ws = kernels.quantize_rows_fp8(w)
+        wqt = wq.t().contiguous()
+
+        def op(x, As, Bs):
+            return pkg.multi_lora_linear_fp8(x, wq, ws, b, As, Bs, [1.0, 0.5], routing, wq_t=wqt,
+                                             dx_bf16=path == "e4m3_dx_bf16")
 
     x0, a0, a1, b0, b1, dy0 = _tensors(dev, 31)
     x = x0.clone().requires_grad_(True)
@@ -49,7 +63,7 @@ def test_graph_replays_equal_eager(pkg, dev, transposed):
     leaves = [x, *As, *Bs]
 
     def step():
-        y = pkg.multi_lora_linear(x, w, b, As, Bs, [1.0, 0.5], routing, weight_t=wt)
+        y = op(x, As, Bs)
         y.backward(dy)
         return y
 
@@ -71,7 +85,7 @@ def test_graph_replays_equal_eager(pkg, dev, transposed):
     def outputs():
         return [y_static, x.grad] + [t.grad for t in As] + [t.grad for t in Bs]
 
-    want = _eager(pkg, w, wt, b, routing, x0, [a0, a1], [b0, b1], dy0)
+    want = _eager(op, x0, [a0, a1], [b0, b1], dy0)
     for rep in range(3):
         graph.replay()
         torch.cuda.synchronize()
@@ -84,7 +98,7 @@ def test_graph_replays_equal_eager(pkg, dev, transposed):
     with torch.no_grad():
         for t, v in zip([x, *As, *Bs, dy], [x1, c0, c1, d0, d1, dy1]):
             t.copy_(v)
-    want = _eager(pkg, w, wt, b, routing, x1, [c0, c1], [d0, d1], dy1)
+    want = _eager(op, x1, [c0, c1], [d0, d1], dy1)
     for rep in range(2):
         graph.replay()
         torch.cuda.synchronize()
