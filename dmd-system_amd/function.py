@@ -285,7 +285,7 @@ class MultiLoRAFP8Function(torch.autograd.Function):
     ``dx_bf16`` the dX runs instead on the bf16 MFMA against the base dequantised
     to bf16 (bf16(w_scale[n]·wq[n, k]), made per call): dY is not quantised, so dX
     carries bf16 rounding only (2.3e-3 rel-L2 against 2.6e-2 at config 5), at the cost of
-    a slower dX (+17% per fwd+bwd step at config 5).
+    a slower dX (+16-17% per fwd+bwd step at config 5).
     """
 
     @staticmethod
@@ -638,7 +638,7 @@ def multi_lora_linear_fp8(x: torch.Tensor, wq: torch.Tensor, w_scale: torch.Tens
 
     wq_t: wq transposed ([K, N], contiguous) for the e4m3 dX; made here when not given (a frozen
     base keeps it, see MultiLoRALinear.quantize_base_fp8). dx_bf16: dX on the bf16 MFMA against
-    the dequantised base (no quantisation of dY; +17% per fwd+bwd step at config 5)."""
+    the dequantised base (no quantisation of dY; +16-17% per fwd+bwd step at config 5)."""
     K = x.shape[-1]
     lead = x.shape[:-1]
     x2 = x.reshape(-1, K)

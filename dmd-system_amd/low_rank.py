@@ -309,7 +309,7 @@ class MultiLoRALinear(nn.Module):
         weight: if ``base.weight`` changes (in place, or by a state-dict load) it is
         quantised again on the next call; ``base_wq`` transposed (for the e4m3 dX) is
         remade whenever ``base_wq`` changes. ``dx_bf16=True`` runs dX on the bf16 MFMA
-        against the dequantised base instead (dY not quantised; +17% per fwd+bwd step at config 5)."""
+        against the dequantised base instead (dY not quantised; +16-17% per fwd+bwd step at config 5)."""
         if dx_bf16 is not None:
             self.__dict__['_fp8_dx_bf16'] = bool(dx_bf16)
         w = self.base.weight.detach().to(torch.bfloat16).contiguous()
