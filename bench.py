@@ -3,7 +3,7 @@
 One step = forward + backward of the six LoRA linears of one Wan-1.3B DiT
 block (q, k, v, o: 1536->1536; ffn.0: 1536->8960; ffn.2: 8960->1536) over
 65520 tokens = two roles (generator, fake critic) of 32760 tokens, each with
-its own rank-64 adapter on the shared frozen bf16 base,
+its own rank-64 adapter on the shared frozen bf16 base (config 2, `wan13b`),
 through the drop-in autograd op with inputs resident in HBM.
 
 Prints one JSON line: metric/value (TFLOP/s of the whole step), the roofline

@@ -72,7 +72,7 @@ def errors(pkg, got, case_, scales, routing):
 @pytest.mark.parametrize("lengths,ids", [((256, 256), (0, 1)), ((200, 56, 256), (0, -1, 1)),
                                          ((0, 300, 212), (1, 0, -1))])
 def test_tiny_config_fp32(pkg, dev, bias, lengths, ids):
-    """BASELINE config 1 as specified: fp32, X [2x256 tokens, 256], W [256, 256] ~ N(0, 1/256), two
+    """Config 1 (`tiny`) as specified: fp32, X [2x256 tokens, 256], W [256, 256] ~ N(0, 1/256), two
     rank-8 adapters (Kaiming-uniform A, B ~ N(0, 0.02)), scale 1; plus null and empty segments."""
     from dmd_system_amd import workloads as W
     cfg = W.CONFIGS["tiny"]

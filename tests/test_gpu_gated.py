@@ -1,4 +1,4 @@
-"""GPU parity of the gated residual fused into the GEMM epilogue (SURVEY row: downstream
+"""GPU parity of the gated residual fused into the GEMM epilogue (downstream
 epilogue fusion): out = bf16(x + bf16(Y)·gate) with the rounding contract of
 runtime/helios_residual_kernel.py:66-86, and its frozen-gate backward (:90-133).
 

@@ -1,5 +1,5 @@
-"""GPU parity of the modulated LayerNorm that opens a DiT sublayer (the
-modulated norm), through the reference-named host functions in ``modulated_norm.py``.
+"""GPU parity of the modulated LayerNorm that opens a DiT sublayer (the downstream
+fusion on the linear's output), through the reference-named host functions in ``modulated_norm.py``.
 
 Oracle: ``oracle.multilora_oracle.modulated_norm`` and ``layer_norm``. Bars:
 

@@ -71,7 +71,7 @@ def check_against_oracle(pkg, dev, case, scales, routing, tol=TOL, transposed=Fa
 @pytest.mark.parametrize("lengths,ids", [((256, 256), (0, 1)), ((200, 56, 256), (0, -1, 1)),
                                          ((0, 300, 212), (1, 0, -1))])
 def test_tiny_config_vs_oracle(pkg, dev, bias, lengths, ids):
-    """BASELINE config 1 shape: 512 tokens, 256 -> 256, two rank-8 adapters."""
+    """Config 1 shape: 512 tokens, 256 -> 256, two rank-8 adapters."""
     case = make_case(512, 256, 256, (8, 8), lengths, ids, seed=11, bias=bias)
     routing = pkg.SegmentRouting.from_lengths(lengths, ids)
     check_against_oracle(pkg, dev, case, [1.0, 1.0], routing)
@@ -383,7 +383,7 @@ def test_big_tiles_with_ragged_edges(pkg, dev, transposed):
 @pytest.mark.parametrize("transposed", [False, True], ids=["dx_nn", "dx_nt"])
 @pytest.mark.parametrize("name,K,N", [("q", 1536, 1536), ("ffn.0", 1536, 8960), ("ffn.2", 8960, 1536)])
 def test_wan13b_full_shape(pkg, dev, name, K, N, transposed):
-    """BASELINE config 2 (65520 tokens, 2 adapters rank 64) at full size:
+    """Config 2 (65520 tokens, 2 adapters rank 64) at full size:
     Y and dX on 512 sampled rows vs the fp64 oracle, adapter gradients vs torch
     fp32 on the GPU, frozen W untouched. dX both on the NN kernel and on the NT kernel
     against the frozen base held transposed (the modules' default and the benchmarked path)."""
@@ -420,7 +420,7 @@ def test_wan13b_full_shape(pkg, dev, name, K, N, transposed):
 @pytest.mark.parametrize("cfg_name,lin", [("wan22_5b", "ffn.0"), ("wan22_5b", "ffn.2"), ("flux", "q"),
                                           ("flux", "ffn.0"), ("flux", "ffn.2")])
 def test_config_3_4_full_shape(pkg, dev, cfg_name, lin, transposed):
-    """BASELINE configs 3 (27280 tokens, 3 rank-128 adapters on seeded segments, scale 2) and
+    """Configs 3 (27280 tokens, 3 rank-128 adapters on seeded segments, scale 2) and
     4 (16 samples x 4608 tokens, one adapter each, ranks from {16,32,64,128}) at full size:
     Y and dX on 384 sampled rows vs the fp64 oracle, every adapter's gradients vs torch fp32
     on the GPU; dX on the NN kernel and on the NT kernel against the transposed base."""

@@ -187,7 +187,7 @@ def test_workload_flops_match_baseline_table(pkg):
     from dmd_system_amd import workloads as W
     cfg = W.CONFIGS["wan13b"]
     total = sum(cfg.flops_fwd_bwd(K, N) for _, K, N in cfg.linears())
-    assert abs(total / 1e12 - 10.524) < 0.001  # 10.524 TFLOP per 6-linear block (BASELINE table)
+    assert abs(total / 1e12 - 10.524) < 0.001  # 10.524 TFLOP per 6-linear block (the headline metric's figure)
     lora = total - sum(4 * cfg.tokens * K * N for _, K, N in cfg.linears())
     assert abs(lora / 1e12 - 0.837) < 0.001
     for c in W.CONFIGS.values():
