@@ -92,7 +92,7 @@ def inputs(batch: int, tokens: int, ctx_tokens: int, hidden: int, device, dtype,
 
 
 def rel_l2(a, b):
-    a, b = a.double(), b.double()
+    a, b = a.detach().double(), b.detach().double()
     return float((a - b).norm() / b.norm().clamp_min(1e-30))
 
 
