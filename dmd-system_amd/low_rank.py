@@ -67,9 +67,10 @@ def transposed_base(w: torch.Tensor, x: torch.Tensor, enabled: bool = True) -> t
 
 
 # Stacked copies of the frozen bases of linears that read one input (q / k / v), keyed by the
-# identities of the member weights: (weights stacked by rows [G·N, K] bf16, biases stacked [G·N]
-# or None, and the stack transposed [K, G·N] when dX needs it). Entries are remade when a
-# member weight changes and dropped when the first member weight is freed.
+# identities of the member weights and biases: (weights stacked by rows [G·N, K] bf16, biases
+# stacked [G·N] or None, and the stack transposed [K, G·N] when dX needs it). Entries are remade
+# when a member tensor changes (storage or in-place version) or is replaced by another object,
+# and dropped as soon as any member weight or bias is freed.
 _STACKED: dict[tuple, tuple] = {}
 
 
@@ -80,13 +81,16 @@ def _drop_stacked(key: tuple) -> None:
 def stacked_bases(weights, biases, want_t: bool):
     """(w_cat, b_cat, w_cat_t or None) for the frozen bases of stacked linears. Costs the bases'
     bf16 size once more (twice with the transpose), per distinct set of bases."""
+    members = [*weights, *(b for b in biases if b is not None)]
     ident = tuple(id(w) for w in weights) + tuple(id(b) if b is not None else 0 for b in biases)
     ver = tuple((w.data_ptr(), w._version) for w in weights) + tuple(
         (b.data_ptr(), b._version) if b is not None else (0, 0) for b in biases)
     entry = _STACKED.get(ident)
-    if entry is None or any(r() is not w for r, w in zip(entry[0], weights)):
-        entry = (tuple(weakref.ref(w) for w in weights), None, None, None, None)
-        weakref.finalize(weights[0], _drop_stacked, ident)
+    if entry is None or len(entry[0]) != len(members) or any(r() is not t for r, t in zip(entry[0], members)):
+        # a new set of tensors (an id can be reused by a later object: compare the objects themselves)
+        entry = (tuple(weakref.ref(t) for t in members), None, None, None, None)
+        for t in members:
+            weakref.finalize(t, _drop_stacked, ident)
     refs, v, w_cat, b_cat, w_cat_t = entry
     if v != ver:
         with torch.no_grad():

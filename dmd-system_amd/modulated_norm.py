@@ -204,8 +204,8 @@ def _component_gradient(hidden, grad_output, mean, rstd, component_gradient, sca
     if grad_output.shape != hidden.shape:
         _fail("grad_output shape differs from the hidden state's")
     _check_stats(hidden, mean, rstd)
-    if B == 0 or (rank == 4 and T == 0):
-        return component_gradient
+    if B == 0 or T == 0:  # nothing to sum: the buffer is returned untouched (as the reference does
+        return component_gradient  # for an empty token interval, so earlier intervals' sums survive)
     return kernels.modulated_norm_component_grad(hidden, grad_output, mean, rstd, component_gradient, si, hi)
 
 

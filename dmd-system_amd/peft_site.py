@@ -122,12 +122,15 @@ def _peft_forward(self: nn.Module, x: torch.Tensor, *args, **kwargs) -> torch.Te
         _fail("extra forward arguments (variant keyword arguments) are outside the fused contract")
     base = self.base_layer
     roles = self.__dict__.get("peft_roles")
+    # merged first: a merged base carries the adapter, so even the disabled (base-only) branch
+    # would include it; the reference's installed forward rejects merged layers whatever
+    # disable_adapters says (runtime/wan13b_lora_cast.py:185-189)
+    if getattr(self, "merged", False):
+        _fail("merged adapters (the base already carries them): unmerge first")
     if getattr(self, "disable_adapters", False):
         if adapter_names is not None:
             _fail("adapter_names cannot be used while the adapters are disabled")
         names, routing = [], SegmentRouting.single(_rows(x), BASE_ONLY)
-    elif getattr(self, "merged", False):
-        _fail("merged adapters (the base already carries them): unmerge first")
     elif adapter_names is not None:
         names, routing = _mixed_routing(x, adapter_names)
     elif roles is not None:

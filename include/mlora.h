@@ -31,7 +31,9 @@
  *   - Return MLORA_OK (0) or a negative mlora_status; no exceptions cross the
  *     ABI. Argument errors are detected before any launch.
  *   - Reentrant: no global mutable state; safe to call from several host
- *     threads on different streams.
+ *     threads on different streams. The one exception is
+ *     mlora_seg_outer_noalloc: it keeps its partial sums in one file-scope
+ *     device array per GPU, so its calls on one GPU must be serialised.
  *   - Results are deterministic: fixed-order reductions, no float atomics.
  */
 #ifndef MLORA_H_

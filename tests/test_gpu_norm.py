@@ -227,6 +227,12 @@ def test_component_gradients(pkg, dev, hidden_dtype, out_dtype):
     assert _rel(_np(red[:, 4]), ds.sum(axis=1)) <= tol
     assert _rel(_np(red[:, 3]), dh.sum(axis=1)) <= tol
     assert (_np(red[:, [0, 1, 2, 5]]) == 7.0).all()
+    # an empty token interval leaves the reduced buffer untouched (wan13b_fused_layernorm_backward_kernel.py:420-421)
+    kept = red.clone()
+    pkg.fused_reduced_component_gradient(hidden[:, :0], grad[:, :0], torch.empty(B, 0, device=dev),
+                                         torch.empty(B, 0, device=dev), red, 4, 3)
+    torch.cuda.synchronize()
+    assert torch.equal(red, kept)
     per = torch.full((B, T, 6, W), 7.0, device=dev, dtype=out_dtype)
     pkg.fused_tensor4d_component_gradient(hidden, grad, mean, rstd, per, 4, 3)
     assert _rel(_np(per[:, :, 4]), ds) <= tol

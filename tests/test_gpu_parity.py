@@ -174,6 +174,9 @@ def test_shrink_segments_match_single_segment_calls(pkg, dev, rank, lengths, ids
             ref = scales[a] * (f64(x[off:off + n]) @ f64(As[a]).T)
             assert O.rel_l2(f64(h1), ref) <= 4e-3
         off, block = off + n, block + nb
+
+
+def test_routing_is_bit_exact(pkg, dev):
     """Rows of base-only segments equal an adapter-free launch bit for bit, and
     adapter rows equal the launch with that adapter on all rows."""
     lengths, ids = (130, 70, 200, 112), (0, -1, 1, -1)

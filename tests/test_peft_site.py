@@ -60,6 +60,11 @@ def test_fail_closed_before_any_device_work(pkg):
     layer.enable_adapters(False)
     with pytest.raises(RuntimeError, match="disabled"):
         layer(x, adapter_names=["generator", "critic"])
+    # disabled AND merged: the base weight carries the adapter, so the base-only branch would
+    # silently include it; the merged check comes first (wan13b_lora_cast.py:185-189)
+    layer.merged_adapters = ["generator"]
+    with pytest.raises(RuntimeError, match="merged"):
+        layer(x)
 
 
 def test_roles_need_known_names(pkg):

@@ -2,6 +2,7 @@
 fail-closed checks, and that grouping leaves parameters and state-dict keys alone.
 No kernel runs."""
 import pytest
+import torch
 from torch import nn
 
 from toy_dit import make_roles
@@ -83,3 +84,22 @@ def test_stacked_rank_above_the_kernel_limit_fails_at_fuse_time(pkg):
         pkg.fuse_shared_inputs(holder, [["q", "k", "v"]])
     # two members of rank 128 fit exactly
     assert len(pkg.fuse_shared_inputs(holder, [["q", "k"]])) == 1
+
+
+def test_stacked_bases_follow_replaced_biases_and_free_with_any_member(pkg):
+    """The stacked-base cache compares member weights AND biases by identity: a bias replaced by
+    a new Parameter (which may reuse the freed one's id and storage, at in-place version 0) is
+    stacked again; freeing any member drops the entry."""
+    import gc
+    from dmd_system_amd import low_rank as L
+    ws = [torch.nn.Parameter(torch.randn(16, 8), requires_grad=False) for _ in range(3)]
+    bs = [torch.nn.Parameter(torch.randn(16), requires_grad=False) for _ in range(3)]
+    _, b_cat, _ = L.stacked_bases(ws, bs, want_t=False)
+    assert torch.equal(b_cat, torch.cat([b.float() for b in bs]))
+    bs[1] = torch.nn.Parameter(torch.full((16,), 5.0), requires_grad=False)
+    _, b_cat2, _ = L.stacked_bases(ws, bs, want_t=False)
+    assert torch.equal(b_cat2[16:32], torch.full((16,), 5.0))
+    keys_before = set(L._STACKED)
+    del bs[2]
+    gc.collect()
+    assert not (set(L._STACKED) & keys_before), "freeing one member bias must drop the cached stack"
