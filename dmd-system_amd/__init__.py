@@ -12,6 +12,8 @@ Public API:
     fuse_shared_inputs, SharedInputGroup, SharedInputMultiLoRAFunction   linears reading one input, stacked
     export_adapters, import_adapters, save_adapters, load_adapters   PEFT / DiffSynth adapter state
     install_peft_multi_lora, peft_roles_active   PEFT LoRA layers (W1 / H3) on the multi-LoRA op
+    livewan, LiveWanLoRALinear, install_livewan_multi_lora   LiveWan's critic LoRA (wanstreamer/lora.py)
+    restore_identity()                   kernel / source identity for the run's model metadata
     kernels                              torch front end of each C-ABI entry point
     fused_modulated_norm_epilogue, fused_modulated_norm_materialization,
     fused_bf16_layernorm_modulation, fused_layernorm_modulation   the block's modulated LayerNorm
@@ -35,6 +37,9 @@ from .roles import RoleBatch, fuse_roles, roles_active
 from .routing import BASE_ONLY, SegmentRouting
 from .shared_input import SharedInputGroup, fuse_shared_inputs, release_shared_inputs
 from .peft_site import install_peft_multi_lora, peft_roles_active, uninstall_peft_multi_lora
+from . import livewan
+from .livewan import LiveWanLoRALinear, install_livewan_multi_lora, uninstall_livewan_multi_lora
+from ._lib import restore_identity
 from .modulated_norm import (ModulatedLayerNormFunction, fused_bf16_layernorm_modulation,
                              fused_bf16_layernorm_modulation_hidden_backward, fused_layernorm_modulation,
                              fused_layernorm_modulation_hidden_backward, fused_modulated_norm_epilogue,
@@ -54,6 +59,8 @@ __all__ = [
     "SharedInputMultiLoRAFunction", "StackedLinearsFunction", "shared_input_multi_lora", "SharedInputGroup", "fuse_shared_inputs",
     "release_shared_inputs", "export_adapters", "import_adapters", "save_adapters", "load_adapters", "kernels",
     "load_library", "install_peft_multi_lora", "uninstall_peft_multi_lora", "peft_roles_active",
+    "livewan", "LiveWanLoRALinear", "install_livewan_multi_lora", "uninstall_livewan_multi_lora",
+    "restore_identity",
     "fused_modulated_norm_epilogue", "fused_modulated_norm_materialization", "fused_bf16_layernorm_modulation",
     "fused_layernorm_modulation", "fused_bf16_layernorm_modulation_hidden_backward",
     "fused_layernorm_modulation_hidden_backward", "fused_reduced_component_gradient",

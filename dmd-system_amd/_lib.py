@@ -143,3 +143,34 @@ def i64_array(values) -> ctypes.Array:
 
 def f32_array(values) -> ctypes.Array:
     return (ctypes.c_float * max(1, len(values)))(*values)
+
+
+def python_source_hash() -> str:
+    """SHA-256 over this package's Python modules (name and bytes of each, in name order)."""
+    import hashlib
+    h = hashlib.sha256()
+    for f in sorted(LIB_PATH.parent.glob("*.py")):
+        h.update(f.name.encode())
+        h.update(b"\0")
+        h.update(f.read_bytes())
+        h.update(b"\0")
+    return h.hexdigest()
+
+
+def restore_identity() -> dict:
+    """The entries a model factory adds to ``ModelComponents.metadata`` so that the reference's
+    restore identity follows this op's arithmetic. session.construct stores the metadata as
+    ``model_metadata`` in the run identity (training/session.py:164-169), and a resume is refused
+    when the identity differs. The reference's source-derived semantics
+    (training/semantics.py:466-474) binds Python it reaches through static imports; the HIP
+    sources and the library are not Python, and a by-path import of this package is not static,
+    so they enter here: the C ABI version, the hash of the sources the loaded libmlora.so was
+    built from (csrc/ and include/, the value it returns from mlora_source_hash), the hash of the
+    package's Python modules, and the GPU architecture the kernels are compiled for."""
+    lib = load()
+    return {"mi355x_multi_lora": {
+        "abi_version": int(lib.mlora_abi_version()),
+        "kernel_source_sha256": lib.mlora_source_hash().decode(),
+        "python_source_sha256": python_source_hash(),
+        "arch": "gfx950",
+    }}

@@ -122,6 +122,22 @@ def _init_pair(rank: int, base: nn.Linear, dtype=None) -> tuple[nn.Parameter, nn
     return a, b
 
 
+def lora_pair(m: nn.Module):
+    """(A [r, in], B [out, r], scale) of a single-adapter LoRA wrapper over ``m.base``: a
+    TrainableLowRankLinear (``lora_a`` / ``lora_b``), a native LoRALinear or a module of LiveWan's
+    layout (``a`` / ``b``); None for anything else."""
+    base = getattr(m, 'base', None)
+    if not isinstance(base, nn.Linear):
+        return None
+    for an, bn in (('lora_a', 'lora_b'), ('a', 'b')):
+        a, b = getattr(m, an, None), getattr(m, bn, None)
+        if (isinstance(a, nn.Parameter) and isinstance(b, nn.Parameter) and a.dim() == 2 and b.dim() == 2
+                and a.shape[1] == base.in_features and b.shape == (base.out_features, a.shape[0])
+                and isinstance(getattr(m, 'scale', None), (int, float))):
+            return a, b, float(m.scale)
+    return None
+
+
 class TrainableLowRankLinear(nn.Module):
     """Frozen W*x + (alpha/rank)*B(A*x), with separately owned trainable A/B.
 
@@ -269,23 +285,30 @@ class MultiLoRALinear(nn.Module):
         self.active_roles = None             # RoleBatch routing calls without an explicit routing
 
     @classmethod
-    def from_roles(cls, roles: Sequence[TrainableLowRankLinear], *, base: nn.Linear | None = None,
+    def from_roles(cls, roles: Sequence[nn.Module], *, base: nn.Linear | None = None,
                    role_names: Sequence[str] | None = None) -> "MultiLoRALinear":
-        """Batch per-role TrainableLowRankLinear modules that alias one frozen base.
+        """Batch per-role LoRA wrappers that alias one frozen base.
 
-        The adapters are the roles' own Parameters (not copies), so each role's
-        optimizer keeps owning exactly its trainables (open_workload/dmd.py:266-275);
-        the base must be the same Parameter object in every role, as
-        construction_sharing.place_frozen_role arranges (construction_sharing.py:105-118).
-        ``base`` (default: the first role's) may be a base-only role's own nn.Linear over
-        the same Parameters; ``role_names`` names the roles in order, adapter i being
-        role_names[i] (used by a RoleBatch routing).
+        A wrapper is a TrainableLowRankLinear (``lora_a`` / ``lora_b``), a native-model
+        LoRALinear (``a`` / ``b`` fp32 masters) or a module of LiveWan's LoRA layout (``a`` /
+        ``b`` and an ``enabled`` flag, wanstreamer/lora.py:8-27). The adapters are the roles'
+        own Parameters (not copies), so each role's optimizer keeps owning exactly its
+        trainables (open_workload/dmd.py:266-275); the base must be the same Parameter object
+        in every role, as construction_sharing.place_frozen_role arranges
+        (construction_sharing.py:105-118). ``base`` (default: the first role's) may be a
+        base-only role's own nn.Linear over the same Parameters; ``role_names`` names the roles
+        in order, adapter i being role_names[i] (used by a RoleBatch routing); with no roles the
+        module is the base alone (every role base-only). A wrapper with
+        an ``enabled`` flag that is False when a RoleBatch routes a call leaves its role's rows
+        base-only (LiveWan's ``lora_enabled(model, False)``).
         """
-        _require(len(roles) > 0, 'at least one role module required')
+        _require(len(roles) > 0 or base is not None, 'at least one role module (or the base) required')
+        pairs = [lora_pair(m) for m in roles]
+        _require(all(p is not None for p in pairs),
+                 'roles must be LoRA wrappers (TrainableLowRankLinear, LoRALinear or LiveWan LoRA)')
         base = roles[0].base if base is None else base
         _require(type(base) is nn.Linear, 'multi-LoRA base must be an actual native Linear')
         for m in roles:
-            _require(isinstance(m, TrainableLowRankLinear), 'roles must be TrainableLowRankLinear modules')
             _require(m.base.weight is base.weight and m.base.bias is base.bias,
                      'roles must alias one frozen base (shared construction)')
         names = list(role_names) if role_names is not None else []
@@ -294,11 +317,13 @@ class MultiLoRALinear(nn.Module):
         obj = cls.__new__(cls)
         nn.Module.__init__(obj)
         obj.base = base
-        obj.lora_a = nn.ParameterList([m.lora_a for m in roles])
-        obj.lora_b = nn.ParameterList([m.lora_b for m in roles])
-        obj.scales = [m.scale for m in roles]
+        obj.lora_a = nn.ParameterList([a for a, _, _ in pairs])
+        obj.lora_b = nn.ParameterList([b for _, b, _ in pairs])
+        obj.scales = [s for _, _, s in pairs]
         obj.role_ids = {n: i for i, n in enumerate(names)}
         obj.active_roles = None
+        # the source wrappers (not submodules: no second state-dict entry), for their enabled flags
+        obj.__dict__['_role_wrappers'] = list(roles)
         return obj
 
     @property
@@ -359,12 +384,21 @@ class MultiLoRALinear(nn.Module):
             return group(self, x, routing)
         return self._single(x, routing)
 
+    def role_routing(self, rows: int) -> SegmentRouting:
+        """The active RoleBatch's routing of ``rows`` sample-major rows: each role to its
+        adapter, roles without one (or whose source wrapper is disabled) to the base alone."""
+        if self.active_roles is None:
+            raise ValueError('multi-LoRA linear: no routing given and no role batch active')
+        role_ids = self.role_ids
+        wrappers = self.__dict__.get('_role_wrappers')
+        if wrappers is not None:
+            role_ids = {n: i for n, i in role_ids.items() if getattr(wrappers[i], 'enabled', True)}
+        return self.active_roles.routing(rows, role_ids)
+
     def _routing(self, x: torch.Tensor, routing: SegmentRouting | None) -> SegmentRouting:
         if routing is None:
-            if self.active_roles is None:
-                raise ValueError('multi-LoRA linear: no routing given and no role batch active')
             rows = x.numel() // x.shape[-1] if x.dim() and x.shape[-1] else 0
-            routing = self.active_roles.routing(rows, self.role_ids)
+            routing = self.role_routing(rows)
         return routing
 
     def gated_residual(self, x: torch.Tensor, residual: torch.Tensor, gate: torch.Tensor,

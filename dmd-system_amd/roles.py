@@ -37,7 +37,7 @@ from typing import Iterator, Mapping, Sequence
 import torch
 from torch import nn
 
-from .low_rank import MultiLoRALinear, TrainableLowRankLinear
+from .low_rank import MultiLoRALinear, lora_pair
 from .routing import BASE_ONLY, SegmentRouting
 
 
@@ -128,22 +128,40 @@ def _canonical(name: str, wrappers: Sequence[str]) -> str:
     return name
 
 
-def fuse_roles(roles: Mapping[str, nn.Module]) -> nn.Module:
+def _is_wrapper(mod: nn.Module) -> bool:
+    return not isinstance(mod, MultiLoRALinear) and lora_pair(mod) is not None
+
+
+def fuse_roles(roles: Mapping[str, nn.Module], base_roles: Sequence[str] = ()) -> nn.Module:
     """One module tree running every role of ``roles`` (name -> role model) in one pass.
+
+    LoRA wrappers are TrainableLowRankLinear modules, native-model LoRALinear modules or
+    modules of LiveWan's LoRA layout (``a`` / ``b`` / ``enabled``, wanstreamer/lora.py:8-27).
+    Roles named in ``base_roles`` use the frozen base alone at every target even where their
+    model holds wrappers: LiveWan's teacher pass is the critic model under
+    ``lora_enabled(model, False)`` (runtime/livewan_crossscale_worker.py:2614-2632), so
+    ``fuse_roles({'teacher': critic, 'critic': critic}, base_roles=('teacher',))`` runs both
+    passes in one call per linear. One model object may serve several roles only if all but
+    one of them are base roles.
 
     Fail-closed checks (``ValueError('multi-role call: …')``): the roles have the same
     module structure up to LoRA wrappers; every frozen Parameter is the same object in
     every role (the shared construction aliases them); every trainable Parameter is a
-    wrapper's ``lora_a`` / ``lora_b``; buffers are equal in dtype, shape and value.
+    wrapper's adapter; buffers are equal in dtype, shape and value.
     The result shares all of these tensors; it holds no copy of any of them.
     """
     _require(isinstance(roles, Mapping) and len(roles) > 0, 'a mapping of role name -> module is required')
     names = list(roles)
     models = [roles[n] for n in names]
     _require(all(isinstance(m, nn.Module) for m in models), 'roles must be nn.Module trees')
+    base_roles = tuple(base_roles)
+    _require(all(r in names for r in base_roles), f'base roles {base_roles} must name roles of the mapping')
+    adapter_models = [m for n, m in zip(names, models) if n not in base_roles]
+    _require(len({id(m) for m in adapter_models}) == len(adapter_models),
+             'one model object serves two adapter roles (make all but one of them base roles)')
 
-    wrappers = [sorted((k for k, mod in m.named_modules() if isinstance(mod, TrainableLowRankLinear)),
-                       key=len, reverse=True) for m in models]
+    wrappers = [sorted((k for k, mod in m.named_modules() if _is_wrapper(mod)), key=len, reverse=True)
+                for m in models]
     targets = sorted(set().union(*wrappers))
 
     # module structure: same names and types, a wrapper where another role has its plain Linear
@@ -154,7 +172,7 @@ def fuse_roles(roles: Mapping[str, nn.Module]) -> nn.Module:
         for k, mod in m.named_modules():
             if k in inner:
                 continue
-            mods[k] = nn.Linear if isinstance(mod, TrainableLowRankLinear) else type(mod)
+            mods[k] = nn.Linear if _is_wrapper(mod) else type(mod)
         if ref_mods is None:
             ref_mods = mods
         _require(mods == ref_mods, f'role {name!r} has a different module structure')
@@ -164,8 +182,7 @@ def fuse_roles(roles: Mapping[str, nn.Module]) -> nn.Module:
     # parameters: frozen ones aliased by canonical name, trainable ones only LoRA
     frozen_ref: dict[str, nn.Parameter] | None = None
     for name, m, wr in zip(names, models, wrappers):
-        lora = {id(w.lora_a) for k in wr for w in [m.get_submodule(k)]} | \
-               {id(w.lora_b) for k in wr for w in [m.get_submodule(k)]}
+        lora = {id(p) for k in wr for p in lora_pair(m.get_submodule(k))[:2]}
         frozen: dict[str, nn.Parameter] = {}
         for pname, p in m.named_parameters(remove_duplicate=False):
             if id(p) in lora:
@@ -197,11 +214,12 @@ def fuse_roles(roles: Mapping[str, nn.Module]) -> nn.Module:
     fused = copy.deepcopy(template, memo)
     for t in targets:
         base_linear = None
-        adapters: list[tuple[str, TrainableLowRankLinear]] = []
+        adapters: list[tuple[str, nn.Module]] = []
         for name, m in zip(names, models):
             mod = m.get_submodule(t)
-            if isinstance(mod, TrainableLowRankLinear):
-                adapters.append((name, mod))
+            if _is_wrapper(mod):
+                if name not in base_roles:
+                    adapters.append((name, mod))
                 base_linear = base_linear or mod.base
             elif base_linear is None:
                 base_linear = mod
