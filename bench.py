@@ -81,6 +81,12 @@ def parse():
     p.add_argument("--per-role", action="store_true",
                    help="also time the same step as one call per segment (role), with this library and with "
                         "the reference's unfused torch path on the GPU")
+    p.add_argument("--rank", type=int, default=0,
+                   help="every adapter of --config at this rank instead of the configuration's (the reference's "
+                        "Wan LoRA runs use 128 and 256)")
+    p.add_argument("--fp32-masters", action="store_true",
+                   help="fp32 adapter masters over the bf16 base outside autocast (the W1 / native layout): the "
+                        "shrinks use them at fp32-class precision (hi + lo bf16 parts)")
     p.add_argument("--fp8-dx-bf16", action="store_true",
                    help="with an e4m3 base: dX on the bf16 MFMA against the dequantised base instead of the "
                         "e4m3 MFMA with a quantised dY (closer to the exact dX, slower)")
@@ -232,10 +238,13 @@ def profile_kernels(args):
     family `--kernel-reps` times, every launch preceded by a 512 MB read (a torch reduction) that
     evicts L2 and the MALL. The printed schedule lists the launch groups in order (one group =
     the kernels between two reads), so dispatches in a trace or counter file map to
-    (shape, family). Families: gemm_fwd (NT, fused LoRA expand), gemm_dx (NT against the
+    (shape, family); beside it, each group's algorithmic work ("flop", or "byte": what the
+    kernel must move once). Families: gemm_fwd (NT, fused LoRA expand), gemm_dx (NT against the
     transposed base), gemm_dx_nn (NN against the base as stored), shrink_x, shrink_dy,
-    seg_outer_dB, seg_outer_dA (main pass + fixed-order reduction), torch_matmul (hipBLASLt);
-    last, a plain 1 GiB device copy as the reference rate of HBM-bound kernels."""
+    seg_outer_dB, seg_outer_dA (main pass + fixed-order reduction), torch_matmul (hipBLASLt, bf16);
+    with an e4m3 base instead of the bf16 GEMMs: quantize_x, gemm_fwd_fp8, quantize_dy (dY times
+    the channel scales), gemm_dx_fp8 (the e4m3 dX); last, a plain 1 GiB device copy as the
+    reference rate of HBM-bound kernels."""
     import torch
     import __graft_entry__
     pkg = __graft_entry__.load_package()
@@ -244,13 +253,37 @@ def profile_kernels(args):
     from dmd_system_amd.function import _as_operand
     dev = torch.device("cuda:0")
     cfg = workloads.CONFIGS[args.config]
-    if cfg.base_fp8 or cfg.dtype == "fp32":
-        raise SystemExit("--profile-kernels covers the bf16 kernels")
+    if args.rank:
+        import dataclasses
+        cfg = dataclasses.replace(cfg, ranks=(args.rank,) * len(cfg.ranks))
+    if cfg.dtype == "fp32":
+        raise SystemExit("--profile-kernels covers the bf16 and e4m3 kernels")
+    fp8 = cfg.base_fp8
     routing, scales = cfg.routing, [cfg.scale] * len(cfg.ranks)
     R = kernels.padded_rank(cfg.ranks)
     bf = [torch.bfloat16] * len(cfg.ranks)
+    M = cfg.tokens
+    segs = [(n, a) for n, a in zip(cfg.seg_lengths, cfg.seg_adapters)]
+    m_a = sum(n for n, a in segs if a >= 0)                     # rows with an adapter
+    mr = sum(n * cfg.ranks[a] for n, a in segs if a >= 0)        # Σ rows·rank
+    r_sum = sum(cfg.ranks[a] for a in {a for _, a in segs if a >= 0})
+
+    def algorithmic(fam, K, N):
+        return {"gemm_fwd": ("flop", 2 * M * K * N + 2 * mr * N), "gemm_fwd_fp8": ("flop", 2 * M * K * N + 2 * mr * N),
+                "gemm_dx": ("flop", 2 * M * K * N + 2 * mr * K), "gemm_dx_nn": ("flop", 2 * M * K * N + 2 * mr * K),
+                "gemm_dx_fp8": ("flop", 2 * M * K * N + 2 * mr * K), "torch_matmul": ("flop", 2 * M * K * N),
+                # P rows read once, the adapter operands once, h rows (2 B) and hi/lo fragments (4 B) written
+                "shrink_x": ("byte", m_a * K * 2 + r_sum * K * 2 + mr * 6),
+                "shrink_dy": ("byte", m_a * N * 2 + r_sum * N * 2 + mr * 6),
+                # P rows and the fragments read once, the bf16 gradients written
+                "seg_outer_dB": ("byte", m_a * N * 2 + mr * 4 + r_sum * N * 2),
+                "seg_outer_dA": ("byte", m_a * K * 2 + mr * 4 + r_sum * K * 2),
+                # bf16 rows read, e4m3 rows and one fp32 scale per row written (+ the channel scales)
+                "quantize_x": ("byte", M * K * 3 + M * 4), "quantize_dy": ("byte", M * N * 3 + M * 4 + N * 4),
+                }[fam]
+
     scrub = torch.ones(args.scrub_mb << 18, dtype=torch.float32, device=dev)
-    schedule = []
+    schedule, algo = [], {}
     shapes = []
     for name, K, N in cfg.linears():
         if (K, N) not in [(k, n) for _, k, n in shapes]:
@@ -258,28 +291,49 @@ def profile_kernels(args):
     with torch.no_grad():
         for i, (name, K, N) in enumerate(shapes):
             x, w, b, As, Bs, dy = workloads.make_linear(cfg, K, N, dev, seed=cfg.seed * 100 + i)
-            wt = w.t().contiguous()
             A_ops, B_ops = [_as_operand(a) for a in As], [_as_operand(v) for v in Bs]
             A_t = [a.t().contiguous() for a in A_ops]
-            h_rows, h_frag = kernels.shrink(x, A_ops, 0, scales, routing, True, R)
-            g_rows, g_frag = kernels.shrink(dy, B_ops, 1, scales, routing, True, R)
-            fams = {
-                "gemm_fwd": lambda: kernels.gemm_fwd(x, w, b, h_rows, B_ops, routing),
-                "gemm_dx": lambda: kernels.gemm_fwd(dy, wt, None, g_rows, A_t, routing),
-                "gemm_dx_nn": lambda: kernels.gemm_dx(dy, w, g_rows, A_ops, routing),
-                "shrink_x": lambda: kernels.shrink(x, A_ops, 0, scales, routing, True, R),
-                "shrink_dy": lambda: kernels.shrink(dy, B_ops, 1, scales, routing, True, R),
+            if fp8:
+                wq, ws = kernels.quantize_rows_fp8(w)
+                wqt = wq.t().contiguous()
+                xq, xs = kernels.quantize_rows_fp8(x)
+                dyq, dys = kernels.quantize_rows_fp8(dy, col_scale=ws)
+                B_div = [kernels.div_rows_bf16(v, ws) for v in B_ops]
+                h_rows, h_frag = kernels.shrink(x, A_ops, 0, scales, routing, True, R, row_div=xs)
+                g_rows, g_frag = kernels.shrink(dy, B_ops, 1, scales, routing, True, R, row_div=dys)
+                fams = {
+                    "quantize_x": lambda: kernels.quantize_rows_fp8(x),
+                    "gemm_fwd_fp8": lambda: kernels.gemm_fwd_fp8(xq, xs, wq, ws, b, h_rows, B_div, routing),
+                    "quantize_dy": lambda: kernels.quantize_rows_fp8(dy, col_scale=ws),
+                    "gemm_dx_fp8": lambda: kernels.gemm_fwd_fp8(dyq, dys, wqt, None, None, g_rows, A_t, routing),
+                    "shrink_x": lambda: kernels.shrink(x, A_ops, 0, scales, routing, True, R, row_div=xs),
+                    "shrink_dy": lambda: kernels.shrink(dy, B_ops, 1, scales, routing, True, R, row_div=dys),
+                }
+            else:
+                wt = w.t().contiguous()
+                h_rows, h_frag = kernels.shrink(x, A_ops, 0, scales, routing, True, R)
+                g_rows, g_frag = kernels.shrink(dy, B_ops, 1, scales, routing, True, R)
+                fams = {
+                    "gemm_fwd": lambda: kernels.gemm_fwd(x, w, b, h_rows, B_ops, routing),
+                    "gemm_dx": lambda: kernels.gemm_fwd(dy, wt, None, g_rows, A_t, routing),
+                    "gemm_dx_nn": lambda: kernels.gemm_dx(dy, w, g_rows, A_ops, routing),
+                    "shrink_x": lambda: kernels.shrink(x, A_ops, 0, scales, routing, True, R),
+                    "shrink_dy": lambda: kernels.shrink(dy, B_ops, 1, scales, routing, True, R),
+                }
+            fams.update({
                 "seg_outer_dB": lambda: kernels.seg_outer(dy, h_frag, R, cfg.ranks, routing, 0, bf),
                 "seg_outer_dA": lambda: kernels.seg_outer(x, g_frag, R, cfg.ranks, routing, 1, bf),
                 "torch_matmul": lambda: torch.matmul(x, w.T),
-            }
+            })
             for fam, fn in fams.items():
+                label = f"{name} {K}->{N} {fam}"
+                algo[label] = algorithmic(fam, K, N)
                 for rep in range(args.kernel_reps + 1):  # the first group warms up (allocations)
                     scrub.amax()
                     fn()
-                    schedule.append(f"{name} {K}->{N} {fam}" + (" warm" if rep == 0 else ""))
+                    schedule.append(label + (" warm" if rep == 0 else ""))
                 torch.cuda.synchronize()
-            del x, w, b, As, Bs, dy, wt, h_rows, h_frag, g_rows, g_frag
+            del x, w, b, As, Bs, dy, A_ops, B_ops, A_t, h_rows, h_frag, g_rows, g_frag, fams
         # reference point for the HBM-bound kernels: a plain 1 GiB device copy (torch's copy kernel)
         src = torch.ones(1 << 29, dtype=torch.float16, device=dev)
         dst = torch.empty_like(src)
@@ -287,10 +341,12 @@ def profile_kernels(args):
             scrub.amax()
             dst.copy_(src)
             schedule.append("copy 1GiB copy" + (" warm" if rep == 0 else ""))
+        algo["copy 1GiB copy"] = ("byte", 2 << 30)
         torch.cuda.synchronize()
         del src, dst
-    print(json.dumps({"profile_kernels": cfg.name, "reps": args.kernel_reps,
-                      "marker": "torch amax reduction before every group", "schedule": schedule}), flush=True)
+    print(json.dumps({"profile_kernels": cfg.name, "ranks": list(cfg.ranks), "tokens": M, "reps": args.kernel_reps,
+                      "marker": "torch amax reduction before every group", "schedule": schedule,
+                      "algorithmic": algo}), flush=True)
 
 
 def main():
@@ -319,6 +375,9 @@ def main():
     dev = torch.device("cuda:0")
     props = torch.cuda.get_device_properties(dev)
     cfg = workloads.CONFIGS[args.config]
+    if args.rank:
+        import dataclasses
+        cfg = dataclasses.replace(cfg, ranks=(args.rank,) * len(cfg.ranks))
     if args.modulated_norm:
         modulated_norm_bench(args, pkg, cfg, dev)
         return
@@ -336,6 +395,10 @@ def main():
     for i, (name, K, N) in enumerate(cfg.linears()):
         x, w, b, As, Bs, dy = workloads.make_linear(cfg, K, N, dev, seed=cfg.seed * 100 + i,
                                                     dtype=torch.float32 if f32 else torch.bfloat16)
+        if args.fp32_masters:
+            if f32 or fp8:
+                raise SystemExit("--fp32-masters is for the bf16 base")
+            As, Bs = [a.float() for a in As], [b.float() for b in Bs]
         x.requires_grad_(not args.fwd_only)
         for t in As + Bs:
             t.requires_grad_(not args.fwd_only)
@@ -642,6 +705,7 @@ def main():
                                f"(q,k,v,o {cfg.hidden}->{cfg.hidden}; ffn {cfg.hidden}->{cfg.ffn}->{cfg.hidden}), "
                                f"{cfg.tokens} tokens in segments {list(cfg.seg_lengths)}, ranks {list(cfg.ranks)}, "
                                f"scale {cfg.scale}, bias on" + (", frozen base e4m3 + per-channel scale" if fp8 else "")
+                               + (", fp32 adapter masters (hi + lo bf16 parts)" if args.fp32_masters else "")
                                + ("; q, k, v read one input and run as one stacked call" if args.shared_qkv else "")
                                + ("; o and ffn.2 end in the block's gated residual, fused" if args.gated_residual
                                   else ""),

@@ -12,11 +12,12 @@ from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "libmlora.so"
 
-ABI_VERSION = 7
+ABI_VERSION = 8
 MAX_SEGMENTS = 128
 MAX_ADAPTERS = 32
 MAX_RANK = 256
 MAX_STACKED = 8
+MAX_GEMM_RANK = MAX_RANK * MAX_STACKED  # the GEMM entry points: the stacked LoRA term of up to 8 linears
 
 F32, BF16, FP8_E4M3 = 0, 1, 2
 

@@ -74,6 +74,7 @@ __device__ __forceinline__ void buf_store16_nt(__amdgpu_buffer_rsrc_t r, int32_t
 constexpr int kMaxSeg = MLORA_MAX_SEGMENTS;
 constexpr int kMaxAdapters = MLORA_MAX_ADAPTERS;
 constexpr int kMaxRank = MLORA_MAX_RANK;
+constexpr int kMaxGemmRank = MLORA_MAX_GEMM_RANK;
 
 // Routing for one call. off[] are row offsets (int32: one call covers < 2^31 rows).
 struct SegTable {

@@ -968,7 +968,7 @@ static int fill_common(GemmArgs &a, int64_t M, int64_t Kc, int64_t Ncols, const 
   if (M > INT32_MAX - 1024 || Kc > INT32_MAX - 1024 || Ncols > INT32_MAX - 1024) return MLORA_ERR_LIMIT;
   int st = build_segtable(a.seg, M, seg_offsets, adapter_ids, n_segments, n_adapters);
   if (st) return st;
-  st = build_adapters(a.ext, a.seg, ext_ptrs, ranks, nullptr, n_adapters);
+  st = build_adapters(a.ext, a.seg, ext_ptrs, ranks, nullptr, n_adapters, kMaxGemmRank);
   if (st) return st;
   const int rmax = max_used_rank(a.seg, a.ext);
   if (rmax > 0) {
@@ -1166,7 +1166,7 @@ extern "C" int mlora_gemm_dx(const void *dy, int64_t lddy, int64_t M, int64_t N,
   if ((st = check_bf16_matrix(dx, lddx, M, K))) return st;
   if (M == 0 || K == 0) return MLORA_OK;
   if (dx == nullptr) return MLORA_ERR_INVALID;
-  if (!offsets_fit(lddy, 256) || !offsets_fit(lddx, 256) || !offsets_fit(ldw, N) || !offsets_fit(K, kMaxRank))
+  if (!offsets_fit(lddy, 256) || !offsets_fit(lddx, 256) || !offsets_fit(ldw, N) || !offsets_fit(K, kMaxGemmRank))
     return MLORA_ERR_LIMIT;
   a.P = static_cast<const uint16_t *>(dy);
   a.Q = static_cast<const uint16_t *>(w);

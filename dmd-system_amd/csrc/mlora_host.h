@@ -36,9 +36,10 @@ inline bool adapter_used(const SegTable &st, int a) {
 }
 
 // Validate the adapter table. A used adapter with rank > 0 needs a 16-byte
-// aligned operand pointer; ranks are 0 or multiples of 8 in [8, kMaxRank].
+// aligned operand pointer; ranks are 0 or multiples of 8 in [8, max_rank] (kMaxRank, or
+// kMaxGemmRank for the GEMMs, whose LoRA term is any number of extra k-tiles).
 inline int build_adapters(AdapterTable &at, const SegTable &st, const void *const *ptrs, const int32_t *ranks,
-                          const float *scales, int32_t n) {
+                          const float *scales, int32_t n, int32_t max_rank = kMaxRank) {
   if (n < 0) return MLORA_ERR_INVALID;
   if (n > kMaxAdapters) return MLORA_ERR_LIMIT;
   if (n > 0 && ranks == nullptr) return MLORA_ERR_INVALID;
@@ -49,8 +50,8 @@ inline int build_adapters(AdapterTable &at, const SegTable &st, const void *cons
   }
   for (int a = 0; a < n; ++a) {
     const int r = ranks[a];
-    if (r < 0 || (r > 0 && r < 8) || (r % 8) != 0) return r > kMaxRank ? MLORA_ERR_LIMIT : MLORA_ERR_INVALID;
-    if (r > kMaxRank) return MLORA_ERR_LIMIT;
+    if (r < 0 || (r > 0 && r < 8) || (r % 8) != 0) return r > max_rank ? MLORA_ERR_LIMIT : MLORA_ERR_INVALID;
+    if (r > max_rank) return MLORA_ERR_LIMIT;
     at.rank[a] = r;
     at.scale[a] = scales ? scales[a] : 1.f;
     if (r > 0 && adapter_used(st, a)) {

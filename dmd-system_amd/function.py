@@ -328,25 +328,129 @@ class MultiLoRAFP8Function(torch.autograd.Function):
         return (dx, None, None, None, None, None, None, None, *dAs, *dBs)
 
 
+def _stack_slices(G: int, R: int) -> list[tuple[int, int]]:
+    """Member ranges [g0, g1) of G stacked linears of rank R whose side-by-side LoRA rows fit one
+    shrink / reduction call (at most MAX_RANK columns: 2 members of rank 128, 1 of rank 256); the
+    GEMMs take all G·R columns at once (MAX_GEMM_RANK)."""
+    per = max(1, _lib.MAX_RANK // R)
+    return [(g0, min(G, g0 + per)) for g0 in range(0, G, per)]
+
+
+def _stacked_operand(mats: Sequence[torch.Tensor], split: bool) -> tuple[torch.Tensor, torch.Tensor | None]:
+    """The matrices stacked by rows as one bf16 operand: (hi, None), or with ``split`` (fp32
+    masters at fp32-class precision) the (hi, lo) parts of the fp32 stack."""
+    if split:
+        return kernels.split_hi_lo(torch.cat([m.detach().to(torch.float32) for m in mats]))
+    if len(mats) == 1:
+        return _as_operand(mats[0]), None
+    return torch.cat([_as_operand(m) for m in mats]), None
+
+
+def _stacked_shrink(x, A_hi, A_lo, scales, routing: SegmentRouting, G: int, R: int, want_frag: bool):
+    """h [M, G·R] of G stacked linears (linear g at columns g·R) from the stacked A ([G·R, K] per
+    adapter), by one shrink per member slice (_stack_slices); returns (h_rows, the fragments of
+    each slice, or empty lists)."""
+    h_rows = torch.empty((x.shape[0], G * R), dtype=torch.bfloat16, device=x.device)
+    frags = []
+    for g0, g1 in _stack_slices(G, R):
+        c = slice(g0 * R, g1 * R)
+        _, f = kernels.shrink(x, [a[c] for a in A_hi], 0, scales, routing, want_frag=want_frag, width=(g1 - g0) * R,
+                              h_out=h_rows[:, c], ops_lo=None if A_lo is None else [a[c] for a in A_lo])
+        frags.append(list(f or []))
+    return h_rows, frags
+
+
+def _save_stacked(ctx, tensors, frags) -> None:
+    """save_for_backward of the call's tensors and the per-slice fragments."""
+    ctx.frag_counts = [len(f) for f in frags]
+    _save(ctx, *tensors, frag=[t for f in frags for t in f])
+
+
+def _saved_stacked(ctx):
+    tensors, flat = _saved(ctx)
+    frags, k = [], 0
+    for c in ctx.frag_counts:
+        frags.append(flat[k:k + c])
+        k += c
+    return tensors, frags
+
+
+def _stacked_grads(ctx, x, dys, b_hi, b_lo, h_frags, dx_fn, a0: int, b0: int):
+    """Backward of G stacked linears of rank R (ctx.G, ctx.R, ctx.n adapters): g_g = s·dY_g·B_g
+    side by side into g [M, G·R] (fragments per member slice), dX = dx_fn(g_rows), dA of each
+    slice's members from one reduction over X, dB_g from one reduction over dY_g. b_hi[g] /
+    b_lo[g]: linear g's B operands ([N_g, R] per adapter; lo None unless split); a0 / b0: the
+    autograd input index of the first lora_a / lora_b."""
+    G, R, n, routing = ctx.G, ctx.R, ctx.n, ctx.routing
+    need_x = ctx.needs_input_grad[0]
+    need_a = [[ctx.needs_input_grad[a0 + g * n + i] for i in range(n)] for g in range(G)]
+    need_b = [[ctx.needs_input_grad[b0 + g * n + i] for i in range(n)] for g in range(G)]
+    any_a = any(map(any, need_a))
+    slices = _stack_slices(G, R)
+    g_rows, g_frags = None, [None] * len(slices)
+    if need_x or any_a:
+        g_rows = torch.empty((x.shape[0], G * R), dtype=torch.bfloat16, device=x.device)
+        for s, (g0, g1) in enumerate(slices):
+            jt = (g1 - g0) * R // 16
+            g_frags[s] = kernels.alloc_frags(routing, jt, x.device) if any_a else None
+            for g in range(g0, g1):
+                kernels.shrink(dys[g], b_hi[g], 1, ctx.scales, routing, want_frag=any_a, width=(g1 - g0) * R,
+                               h_out=g_rows[:, g * R:(g + 1) * R], frag_out=g_frags[s], frag_jt=jt,
+                               frag_t0=(g - g0) * R // 16, ops_lo=b_lo[g])
+    dx = dx_fn(g_rows) if need_x else None
+    dA = [[None] * n for _ in range(G)]
+    dB = [[None] * n for _ in range(G)]
+    for s, (g0, g1) in enumerate(slices):
+        w = (g1 - g0) * R
+        for g in range(g0, g1):
+            if any(need_b[g]):
+                outs = kernels.seg_outer(dys[g], h_frags[s], w, [R] * n, routing, 0, ctx.b_dtypes[g],
+                                         frag_jt=w // 16, frag_t0=(g - g0) * R // 16)
+                dB[g] = [o if need_b[g][i] else None for i, o in enumerate(outs)]
+        if any(any(need_a[g]) for g in range(g0, g1)):
+            outs = kernels.seg_outer(x, g_frags[s], w, [w] * n, routing, 1, [torch.float32] * n)
+            for g in range(g0, g1):
+                dA[g] = [outs[i][(g - g0) * R:(g - g0 + 1) * R].to(ctx.a_dtypes[g][i]) if need_a[g][i] else None
+                         for i in range(n)]
+    return dx, dA, dB
+
+
+def _check_stack(what: str, As, Bs, K: int, widths: Sequence[int]) -> int:
+    """One rank R (a multiple of 16) for every linear and adapter; returns R."""
+    R = int(As[0][0].shape[0])
+    if R % 16 or R > _lib.MAX_RANK:
+        raise ValueError(f"{what}: the rank must be a multiple of 16, at most {_lib.MAX_RANK} (got {R})")
+    for g, N in enumerate(widths):
+        for a, b in zip(As[g], Bs[g]):
+            if a.shape != (R, K) or b.shape != (N, R):
+                raise ValueError(f"{what}: lora_a {tuple(a.shape)} / lora_b {tuple(b.shape)} of linear {g} do not "
+                                 f"match rank {R}, in {K}, out {N}")
+    return R
+
+
 class SharedInputMultiLoRAFunction(torch.autograd.Function):
-    """``apply(x, routing, scales, groups, weights, biases, *lora_as, *lora_bs)``: G = ``groups``
-    multi-LoRA linears that read the same input x [M, K].
+    """``apply(x, routing, scales, groups, weights, biases, split, *lora_as, *lora_bs)``: G =
+    ``groups`` multi-LoRA linears that read the same input x [M, K].
 
     weights / biases: tuples of the G frozen bases ([N_g, K] bf16; bias [N_g] or None);
     lora_as = [A_g,i for g < G for i < n] ([R, K] each), lora_bs likewise ([N_g, R]): one rank R
-    (a multiple of 16) for every linear and adapter, adapter i's scale scales[i] in every
-    linear. Returns the G outputs [M, N_g], each equal to its own multi-LoRA linear's.
+    (a multiple of 16, at most 256) for every linear and adapter, adapter i's scale scales[i] in
+    every linear. split: fp32 adapter masters used at fp32-class precision (hi + lo bf16 parts in
+    the shrinks), as MultiLoRAFunction does. Returns the G outputs [M, N_g], each equal to its own
+    multi-LoRA linear's.
 
-    Forward: one shrink of X by the stacked [A_0,i; …; A_{G-1},i] (X read once instead of G
-    times), then each linear's fused GEMM reading its R columns of the stacked h. Backward:
-    the G shrinks g_g = s·dY_g·B_g write side by side into one g [M, G·R] and its fragments;
-    dX accumulates the G linears' dY_g·W_g + g_g·A_g in the dX GEMM's epilogue (fp32 sum,
-    one bf16 rounding per call, instead of autograd's G-1 separate bf16 additions); dA of
-    every linear is one reduction over X (X read once); dB_g one reduction per dY_g.
+    Forward: shrinks of X by the stacked [A_0,i; …; A_{G-1},i], 256 columns per call (X read once
+    per call instead of once per linear), then each linear's fused GEMM reading its R columns of
+    the stacked h. Backward: the G shrinks g_g = s·dY_g·B_g write side by side into one g
+    [M, G·R] and its fragments; dX accumulates the G linears' dY_g·W_g + g_g·A_g in the dX GEMM's
+    epilogue (fp32 sum, one bf16 rounding per call, instead of autograd's G-1 separate bf16
+    additions); dA of the linears of one 256-column slice is one reduction over X; dB_g one
+    reduction per dY_g.
     """
 
     @staticmethod
-    def forward(ctx, x, routing: SegmentRouting, scales: Sequence[float], groups: int, weights, biases, *ab):
+    def forward(ctx, x, routing: SegmentRouting, scales: Sequence[float], groups: int, weights, biases, split: bool,
+                *ab):
         G = int(groups)
         n = len(ab) // (2 * G) if G > 0 else 0
         if G < 2 or n == 0 or len(ab) != 2 * G * n or len(scales) != n or len(weights) != G or len(biases) != G:
@@ -356,27 +460,25 @@ class SharedInputMultiLoRAFunction(torch.autograd.Function):
         M, K = x.shape
         As = [list(ab[g * n:(g + 1) * n]) for g in range(G)]
         Bs = [list(ab[G * n + g * n:G * n + (g + 1) * n]) for g in range(G)]
-        R = int(As[0][0].shape[0])
         routing.validate_for(M, n)
         for g in range(G):
-            N = weights[g].shape[0]
             if weights[g].shape[1] != K:
                 raise ValueError(f"shared-input multi-LoRA: linear {g} has in_features {weights[g].shape[1]}, "
                                  f"the input has {K}")
-            for a, b in zip(As[g], Bs[g]):
-                if a.shape != (R, K) or b.shape != (N, R):
-                    raise ValueError(f"shared-input multi-LoRA: lora_a {tuple(a.shape)} / lora_b {tuple(b.shape)} "
-                                     f"of linear {g} do not match rank {R}, in {K}, out {N}")
-        if R % 16:
-            raise ValueError("shared-input multi-LoRA: the rank must be a multiple of 16")
-        A_cat = [torch.cat([_as_operand(As[g][i]) for g in range(G)]) for i in range(n)]  # [G·R, K]
-        B_ops = [[_as_operand(b) for b in Bs[g]] for g in range(G)]
-        need_b_grad = any(ctx.needs_input_grad[6 + G * n:])
-        h_rows, h_frag = kernels.shrink(x, A_cat, 0, scales, routing, want_frag=need_b_grad, width=G * R)
-        ys = [kernels.gemm_fwd(x, weights[g], biases[g], h_rows[:, g * R:(g + 1) * R], B_ops[g], routing)
+        R = _check_stack("shared-input multi-LoRA", As, Bs, K, [w.shape[0] for w in weights])
+        split = bool(split)
+        A_hi, A_lo = zip(*[_stacked_operand([As[g][i] for g in range(G)], split) for i in range(n)])  # [G·R, K]
+        B_parts = [[_stacked_operand([b], split) for b in Bs[g]] for g in range(G)]
+        B_hi = [[p[0] for p in bp] for bp in B_parts]
+        B_lo = [[p[1] for p in bp] for bp in B_parts] if split else []
+        need_b_grad = any(ctx.needs_input_grad[7 + G * n:])
+        h_rows, frags = _stacked_shrink(x, A_hi, A_lo if split else None, scales, routing, G, R, need_b_grad)
+        ys = [kernels.gemm_fwd(x, weights[g], biases[g], h_rows[:, g * R:(g + 1) * R], B_hi[g], routing)
               for g in range(G)]
-        _save(ctx, x, *weights, *A_cat, *[b for bg in B_ops for b in bg], frag=list(h_frag or []))
+        _save_stacked(ctx, [x, *weights, *A_hi, *[b for bg in B_hi for b in bg], *[b for bg in B_lo for b in bg]],
+                      frags)
         ctx.routing, ctx.scales, ctx.n, ctx.G, ctx.R = routing, tuple(float(v) for v in scales), n, G, R
+        ctx.split = split
         ctx.a_dtypes = [[a.dtype for a in As[g]] for g in range(G)]
         ctx.b_dtypes = [[b.dtype for b in Bs[g]] for g in range(G)]
         return tuple(ys)
@@ -384,62 +486,49 @@ class SharedInputMultiLoRAFunction(torch.autograd.Function):
     @staticmethod
     def backward(ctx, *dys):
         n, G, R, routing = ctx.n, ctx.G, ctx.R, ctx.routing
-        (x, *ops), h_frag = _saved(ctx)
+        (x, *ops), h_frags = _saved_stacked(ctx)
         ws, ops = ops[:G], ops[G:]
-        A_cat = ops[:n]
-        B_ops = [ops[n + g * n:n + (g + 1) * n] for g in range(G)]
+        A_hi = ops[:n]
+        B_hi = [ops[n + g * n:n + (g + 1) * n] for g in range(G)]
+        B_lo = ([ops[n + G * n + g * n:n + G * n + (g + 1) * n] for g in range(G)] if ctx.split
+                else [None] * G)
         M = x.shape[0]
         # an output nobody used has no gradient: it contributes zeros
         dys = [torch.zeros((M, ws[g].shape[0]), dtype=torch.bfloat16, device=x.device) if d is None
                else d.to(torch.bfloat16).contiguous() for g, d in enumerate(dys)]
-        need_x = ctx.needs_input_grad[0]
-        need_a = any(ctx.needs_input_grad[6:6 + G * n])
-        need_b = any(ctx.needs_input_grad[6 + G * n:])
-        jt = G * R // 16
-        g_rows = g_frag = None
-        if need_x or need_a:
-            g_rows = torch.empty((M, G * R), dtype=torch.bfloat16, device=x.device)
-            g_frag = kernels.alloc_frags(routing, jt, x.device) if need_a else None
-            for g in range(G):
-                kernels.shrink(dys[g], B_ops[g], 1, ctx.scales, routing, want_frag=need_a, width=G * R,
-                               h_out=g_rows[:, g * R:(g + 1) * R], frag_out=g_frag, frag_jt=jt, frag_t0=g * R // 16)
-        dx = None
-        if need_x:
+
+        def dx_fn(g_rows):
+            dx = None
             for g in range(G):
                 dx = kernels.gemm_dx(dys[g], ws[g], g_rows[:, g * R:(g + 1) * R],
-                                     [a[g * R:(g + 1) * R] for a in A_cat], routing, out=dx, accumulate=g > 0)
-        dA = [[None] * n for _ in range(G)]
-        dB = [[None] * n for _ in range(G)]
-        if need_b:
-            for g in range(G):
-                outs = kernels.seg_outer(dys[g], h_frag, G * R, [R] * n, routing, 0, ctx.b_dtypes[g],
-                                         frag_jt=jt, frag_t0=g * R // 16)
-                dB[g] = [o if ctx.needs_input_grad[6 + G * n + g * n + i] else None for i, o in enumerate(outs)]
-        if need_a:
-            outs = kernels.seg_outer(x, g_frag, G * R, [G * R] * n, routing, 1, [torch.float32] * n)
-            dA = [[outs[i][g * R:(g + 1) * R].to(ctx.a_dtypes[g][i]) if ctx.needs_input_grad[6 + g * n + i] else None
-                   for i in range(n)] for g in range(G)]
-        return (dx, None, None, None, None, None, *[d for dg in dA for d in dg], *[d for dg in dB for d in dg])
+                                     [a[g * R:(g + 1) * R] for a in A_hi], routing, out=dx, accumulate=g > 0)
+            return dx
+
+        dx, dA, dB = _stacked_grads(ctx, x, dys, B_hi, B_lo, h_frags, dx_fn, a0=7, b0=7 + G * n)
+        return (dx, None, None, None, None, None, None, *[d for dg in dA for d in dg], *[d for dg in dB for d in dg])
 
 
 class StackedLinearsFunction(torch.autograd.Function):
-    """``apply(x, routing, scales, groups, w_cat, b_cat, w_cat_t, *lora_as, *lora_bs)``: G multi-LoRA
-    linears that read x [M, K], as one stacked call. w_cat [G·N, K] bf16 = their frozen weights
-    stacked by rows (b_cat [G·N] or None, w_cat_t = w_cat transposed [K, G·N] or None, all frozen);
-    lora_as = [A_g,i for g < G for i < n] ([R, K] each), lora_bs likewise ([N, R]); one rank R (a
-    multiple of 16) and one output width N (a multiple of 256) for every linear. Returns the G
-    outputs [M, N], each bit-identical to that linear's own call.
+    """``apply(x, routing, scales, groups, w_cat, b_cat, w_cat_t, split, *lora_as, *lora_bs)``: G
+    multi-LoRA linears that read x [M, K], as one stacked call. w_cat [G·N, K] bf16 = their frozen
+    weights stacked by rows (b_cat [G·N] or None, w_cat_t = w_cat transposed [K, G·N] or None, all
+    frozen); lora_as = [A_g,i for g < G for i < n] ([R, K] each), lora_bs likewise ([N, R]); one
+    rank R (a multiple of 16, at most 256) and one output width N (a multiple of 256) for every
+    linear. split: fp32 adapter masters at fp32-class precision (hi + lo bf16 parts in the
+    shrinks). Returns the G outputs [M, N], each bit-identical to that linear's own call.
 
-    Forward: one shrink of X by the stacked [A_0,i; ...; A_{G-1},i] (X read once) and one GEMM over
-    the stacked weights (mlora_gemm_fwd_stacked: X's row tiles feed all G linears' column tiles).
-    Backward: the G shrinks g_g = s·dY_g·B_g side by side into g [M, G·R]; dX = Σ_g dY_g·W_g + g·A_cat
-    as ONE GEMM whose contraction runs over the G dY in turn and then the G·R columns of g
-    (mlora_gemm_dx_stacked: no concatenated dY, no per-linear dX, one rounding of the sum); dA of
-    every linear from one reduction over X; dB_g one reduction over dY_g.
+    Forward: shrinks of X by the stacked [A_0,i; ...; A_{G-1},i], 256 columns per call (X read
+    once per call), and one GEMM over the stacked weights (mlora_gemm_fwd_stacked: X's row tiles
+    feed all G linears' column tiles). Backward: the G shrinks g_g = s·dY_g·B_g side by side into
+    g [M, G·R]; dX = Σ_g dY_g·W_g + g·A_cat as ONE GEMM whose contraction runs over the G dY in
+    turn and then the G·R columns of g (mlora_gemm_dx_stacked: no concatenated dY, no per-linear
+    dX, one rounding of the sum); dA of each 256-column slice's linears from one reduction over
+    X; dB_g one reduction over dY_g.
     """
 
     @staticmethod
-    def forward(ctx, x, routing: SegmentRouting, scales: Sequence[float], groups: int, w_cat, b_cat, w_cat_t, *ab):
+    def forward(ctx, x, routing: SegmentRouting, scales: Sequence[float], groups: int, w_cat, b_cat, w_cat_t,
+                split: bool, *ab):
         G = int(groups)
         n = len(ab) // (2 * G) if G > 0 else 0
         if G < 2 or n == 0 or len(ab) != 2 * G * n or len(scales) != n:
@@ -451,68 +540,46 @@ class StackedLinearsFunction(torch.autograd.Function):
         N = NT // G
         As = [list(ab[g * n:(g + 1) * n]) for g in range(G)]
         Bs = [list(ab[G * n + g * n:G * n + (g + 1) * n]) for g in range(G)]
-        R = int(As[0][0].shape[0])
         routing.validate_for(M, n)
-        if (NT != G * N or N % 256 or R % 16 or G * R > _lib.MAX_RANK or G > _lib.MAX_STACKED
-                or w_cat.shape[1] != K):
+        if NT != G * N or N % 256 or G > _lib.MAX_STACKED or w_cat.shape[1] != K:
             raise ValueError(f"stacked multi-LoRA: {G} linears (at most {_lib.MAX_STACKED}) of width {N} (a multiple "
-                             f"of 256) and rank {R} (a multiple of 16, G·R <= {_lib.MAX_RANK}) over in_features {K}")
-        for g in range(G):
-            for a, b in zip(As[g], Bs[g]):
-                if a.shape != (R, K) or b.shape != (N, R):
-                    raise ValueError(f"stacked multi-LoRA: lora_a {tuple(a.shape)} / lora_b {tuple(b.shape)} of linear "
-                                     f"{g} do not match rank {R}, in {K}, out {N}")
-        A_cat = [torch.cat([_as_operand(As[g][i]) for g in range(G)]) for i in range(n)]  # [G·R, K]
-        B_cat = [torch.cat([_as_operand(Bs[g][i]) for g in range(G)]) for i in range(n)]  # [G·N, R]
-        need_b_grad = any(ctx.needs_input_grad[7 + G * n:])
-        h_rows, h_frag = kernels.shrink(x, A_cat, 0, scales, routing, want_frag=need_b_grad, width=G * R)
-        ys = kernels.gemm_fwd_stacked(x, w_cat, b_cat, h_rows, B_cat, routing, N, R)
-        _save(ctx, x, w_cat, w_cat_t, *A_cat, *B_cat, frag=list(h_frag or []))
+                             f"of 256) over in_features {K}")
+        R = _check_stack("stacked multi-LoRA", As, Bs, K, [N] * G)
+        split = bool(split)
+        A_hi, A_lo = zip(*[_stacked_operand([As[g][i] for g in range(G)], split) for i in range(n)])  # [G·R, K]
+        B_hi, B_lo = zip(*[_stacked_operand([Bs[g][i] for g in range(G)], split) for i in range(n)])  # [G·N, R]
+        need_b_grad = any(ctx.needs_input_grad[8 + G * n:])
+        h_rows, frags = _stacked_shrink(x, A_hi, A_lo if split else None, scales, routing, G, R, need_b_grad)
+        ys = kernels.gemm_fwd_stacked(x, w_cat, b_cat, h_rows, B_hi, routing, N, R)
+        _save_stacked(ctx, [x, w_cat, w_cat_t, *A_hi, *B_hi, *(B_lo if split else ())], frags)
         ctx.routing, ctx.scales, ctx.n, ctx.G, ctx.R, ctx.N = routing, tuple(float(v) for v in scales), n, G, R, N
-        ctx.has_wt = w_cat_t is not None
+        ctx.has_wt, ctx.split = w_cat_t is not None, split
         ctx.a_dtypes = [[a.dtype for a in As[g]] for g in range(G)]
         ctx.b_dtypes = [[b.dtype for b in Bs[g]] for g in range(G)]
         return tuple(ys)
 
     @staticmethod
     def backward(ctx, *dys):
-        n, G, R, N, routing = ctx.n, ctx.G, ctx.R, ctx.N, ctx.routing
-        (x, w_cat, w_cat_t, *ops), h_frag = _saved(ctx)
-        A_cat, B_cat = ops[:n], ops[n:]
+        n, G, N, routing = ctx.n, ctx.G, ctx.N, ctx.routing
+        (x, w_cat, w_cat_t, *ops), h_frags = _saved_stacked(ctx)
+        A_hi, B_hi, B_lo = ops[:n], ops[n:2 * n], ops[2 * n:]
         M = x.shape[0]
         # an output nobody used has no gradient: it contributes zeros
         dys = [torch.zeros((M, N), dtype=torch.bfloat16, device=x.device) if d is None
                else d.to(torch.bfloat16).contiguous() for d in dys]
-        need_x = ctx.needs_input_grad[0]
-        need_a = any(ctx.needs_input_grad[7:7 + G * n])
-        need_b = any(ctx.needs_input_grad[7 + G * n:])
-        jt = G * R // 16
-        g_rows = g_frag = None
-        if need_x or need_a:
-            g_rows = torch.empty((M, G * R), dtype=torch.bfloat16, device=x.device)
-            g_frag = kernels.alloc_frags(routing, jt, x.device) if need_a else None
-            for g in range(G):
-                kernels.shrink(dys[g], [b[g * N:(g + 1) * N] for b in B_cat], 1, ctx.scales, routing,
-                               want_frag=need_a, width=G * R, h_out=g_rows[:, g * R:(g + 1) * R], frag_out=g_frag,
-                               frag_jt=jt, frag_t0=g * R // 16)
-        dx = None
-        if need_x:
+        member = lambda parts, g: [b[g * N:(g + 1) * N] for b in parts]  # noqa: E731
+
+        def dx_fn(g_rows):
             if ctx.has_wt:  # one GEMM over the G dY against the stacked base held transposed
-                dx = kernels.gemm_dx_stacked(dys, w_cat_t, g_rows, [a.t().contiguous() for a in A_cat], routing)
-            else:  # NN form over the stacked base: the dY side by side
-                dx = kernels.gemm_dx(torch.cat(dys, dim=1), w_cat, g_rows, A_cat, routing)
-        dA = [[None] * n for _ in range(G)]
-        dB = [[None] * n for _ in range(G)]
-        if need_b:
-            for g in range(G):
-                outs = kernels.seg_outer(dys[g], h_frag, G * R, [R] * n, routing, 0, ctx.b_dtypes[g],
-                                         frag_jt=jt, frag_t0=g * R // 16)
-                dB[g] = [o if ctx.needs_input_grad[7 + G * n + g * n + i] else None for i, o in enumerate(outs)]
-        if need_a:
-            outs = kernels.seg_outer(x, g_frag, G * R, [G * R] * n, routing, 1, [torch.float32] * n)
-            dA = [[outs[i][g * R:(g + 1) * R].to(ctx.a_dtypes[g][i]) if ctx.needs_input_grad[7 + g * n + i] else None
-                   for i in range(n)] for g in range(G)]
-        return (dx, None, None, None, None, None, None, *[d for dg in dA for d in dg], *[d for dg in dB for d in dg])
+                return kernels.gemm_dx_stacked(dys, w_cat_t, g_rows, [a.t().contiguous() for a in A_hi], routing)
+            # NN form over the stacked base: the dY side by side
+            return kernels.gemm_dx(torch.cat(dys, dim=1), w_cat, g_rows, list(A_hi), routing)
+
+        dx, dA, dB = _stacked_grads(ctx, x, dys, [member(B_hi, g) for g in range(G)],
+                                    [member(B_lo, g) if ctx.split else None for g in range(G)], h_frags, dx_fn,
+                                    a0=8, b0=8 + G * n)
+        return (dx, None, None, None, None, None, None, None, *[d for dg in dA for d in dg],
+                *[d for dg in dB for d in dg])
 
 
 def _bf16_rows(x: torch.Tensor, weight_dtype: torch.dtype) -> torch.Tensor:
@@ -534,29 +601,32 @@ def shared_input_multi_lora(x: torch.Tensor, weights: Sequence[torch.Tensor], bi
                             scales: Sequence[float], routing: SegmentRouting,
                             transposed_base_for_dx: bool = True) -> tuple[torch.Tensor, ...]:
     """Functional form over x [..., K]: the G linears' outputs [..., N_g]; lora_as[g][i] / lora_bs[g][i]
-    are linear g's adapter i. Linears of one width (a multiple of 256) run as one stacked call
-    (StackedLinearsFunction) over a cached stacked copy of their frozen bases; other widths run
-    SharedInputMultiLoRAFunction (one shrink, per-linear GEMMs)."""
+    are linear g's adapter i (one rank, a multiple of 16, for all). Linears of one width (a multiple
+    of 256, at most MAX_STACKED of them) run as one stacked call (StackedLinearsFunction) over a
+    cached stacked copy of their frozen bases; other widths run SharedInputMultiLoRAFunction (shared
+    shrinks, per-linear GEMMs). Arithmetic as multi_lora_linear's for bf16 x: under bf16 autocast
+    the adapters are rounded to bf16; outside it fp32 adapter masters are used at fp32-class
+    precision."""
     from .low_rank import stacked_bases
     lead = x.shape[:-1]
     G = len(weights)
     x2 = _bf16_rows(x, weights[0].dtype)
     flat_a = [a for g in range(G) for a in lora_as[g]]
     flat_b = [b for g in range(G) for b in lora_bs[g]]
+    split = not _autocast_bf16() and any(t.dtype == torch.float32 for t in (*flat_a, *flat_b))
     widths = {int(w.shape[0]) for w in weights}
-    R = int(lora_as[0][0].shape[0]) if lora_as and lora_as[0] else 0
-    if len(widths) == 1 and next(iter(widths)) % 256 == 0 and G * R <= _lib.MAX_RANK:
+    if len(widths) == 1 and next(iter(widths)) % 256 == 0 and G <= _lib.MAX_STACKED:
         N = next(iter(widths))
         want_t = transposed_base_for_dx and torch.is_grad_enabled() and x.requires_grad
         w_cat, b_cat, w_cat_t = stacked_bases(list(weights), list(biases), want_t)
         with torch.autocast("cuda", enabled=False):
             ys = StackedLinearsFunction.apply(x2, routing, tuple(scales), G, w_cat, b_cat, w_cat_t if want_t else None,
-                                              *flat_a, *flat_b)
+                                              split, *flat_a, *flat_b)
         return tuple(v.reshape(*lead, N) for v in ys)
     ws = tuple(w.detach().to(torch.bfloat16) for w in weights)  # a no-op unless autocast runs fp32 bases
     bs = tuple(None if b is None else b.detach() for b in biases)
     with torch.autocast("cuda", enabled=False):
-        ys = SharedInputMultiLoRAFunction.apply(x2, routing, tuple(scales), G, ws, bs, *flat_a, *flat_b)
+        ys = SharedInputMultiLoRAFunction.apply(x2, routing, tuple(scales), G, ws, bs, split, *flat_a, *flat_b)
     return tuple(y.reshape(*lead, w.shape[0]) for y, w in zip(ys, ws))
 
 

@@ -223,6 +223,12 @@ class LoRALinear(nn.Module):
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         if self.use_fused and not torch.is_grad_enabled():
             self.fused_calls += 1
+        group = self.__dict__.get('shared_input')
+        if group is not None:  # stacked with the other linears that read this input
+            return group(self, x)
+        return self._single(x)
+
+    def _single(self, x: torch.Tensor, routing=None) -> torch.Tensor:
         rows = x.numel() // x.shape[-1] if x.dim() else 0
         return multi_lora_linear(x, self.base.weight, self.base.bias, [self.a], [self.b], [self.scale],
                                  SegmentRouting.single(rows, 0), weight_t=_base_t(self, x))

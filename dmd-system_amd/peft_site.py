@@ -115,12 +115,10 @@ def _mixed_routing(x: torch.Tensor, adapter_names: Sequence[str]) -> tuple[list[
     return names, SegmentRouting.from_lengths(lengths, ids)
 
 
-def _peft_forward(self: nn.Module, x: torch.Tensor, *args, **kwargs) -> torch.Tensor:
-    """The installed forward (a method of each layer)."""
-    adapter_names = kwargs.pop("adapter_names", None)
-    if args or any(v is not None for v in kwargs.values()):
-        _fail("extra forward arguments (variant keyword arguments) are outside the fused contract")
-    base = self.base_layer
+def peft_plan(self: nn.Module, x: torch.Tensor, adapter_names: Sequence[str] | None = None):
+    """(adapter names, routing) of one installed layer's call on x, with the fail-closed checks of
+    the module doc: the disabled layer routes every row to the base alone, a mixed batch by
+    sample, an active role batch by role, otherwise the one active adapter over every row."""
     roles = self.__dict__.get("peft_roles")
     # merged first: a merged base carries the adapter, so even the disabled (base-only) branch
     # would include it; the reference's installed forward rejects merged layers whatever
@@ -145,11 +143,36 @@ def _peft_forward(self: nn.Module, x: torch.Tensor, *args, **kwargs) -> torch.Te
         names, routing = act, SegmentRouting.single(_rows(x), 0)
     for n in names:
         _check_adapter(self, n)
+    return names, routing
+
+
+def _peft_single(self: nn.Module, x: torch.Tensor, adapter_names: Sequence[str] | None = None) -> torch.Tensor:
+    """One layer's own call on the multi-LoRA op."""
+    names, routing = peft_plan(self, x, adapter_names)
+    base = self.base_layer
     As = [self.lora_A[n].weight for n in names]
     Bs = [self.lora_B[n].weight for n in names]
     scales = [float(self.scaling[n]) for n in names]
     return multi_lora_linear(x, base.weight, base.bias, As, Bs, scales, routing,
                              weight_t=transposed_base(base.weight, x, getattr(self, "transposed_base_for_dx", True)))
+
+
+def _peft_forward(self: nn.Module, x: torch.Tensor, *args, **kwargs) -> torch.Tensor:
+    """The installed forward (a method of each layer). A layer in a shared-input group
+    (fuse_shared_inputs) runs stacked with the group's other linears when its adapters are on
+    and no mixed batch is given."""
+    adapter_names = kwargs.pop("adapter_names", None)
+    if args or any(v is not None for v in kwargs.values()):
+        _fail("extra forward arguments (variant keyword arguments) are outside the fused contract")
+    group = self.__dict__.get("shared_input")
+    if group is not None and adapter_names is None and not getattr(self, "disable_adapters", False):
+        return group(self, x)
+    return _peft_single(self, x, adapter_names)
+
+
+def is_installed(m: nn.Module) -> bool:
+    """The layer's forward is the multi-LoRA one (install_peft_multi_lora)."""
+    return "_peft_original_forward" in m.__dict__
 
 
 def install_peft_multi_lora(model: nn.Module) -> list[str]:
@@ -178,7 +201,7 @@ def uninstall_peft_multi_lora(model: nn.Module) -> None:
 
 
 def _installed(model: nn.Module) -> Iterable[nn.Module]:
-    return (m for m in model.modules() if "_peft_original_forward" in m.__dict__)
+    return (m for m in model.modules() if is_installed(m))
 
 
 @contextmanager

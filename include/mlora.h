@@ -45,7 +45,7 @@
 extern "C" {
 #endif
 
-#define MLORA_ABI_VERSION 7
+#define MLORA_ABI_VERSION 8
 
 /* Limits of one call (kernel-argument tables). Callers with more segments
  * split the rows into several calls; the Python host layer does this. */
@@ -53,6 +53,10 @@ extern "C" {
 #define MLORA_MAX_ADAPTERS 32
 #define MLORA_MAX_RANK 256
 #define MLORA_MAX_STACKED 8   /* linears in one stacked call (mlora_gemm_fwd_stacked / _dx_stacked) */
+/* The GEMM entry points take adapter ranks up to this: the LoRA term of stacked linears that read
+ * one input is the side-by-side h (or g) of up to MLORA_MAX_STACKED members, each of rank at most
+ * MLORA_MAX_RANK (the GEMM runs the LoRA term as extra k-tiles, so any length fits). */
+#define MLORA_MAX_GEMM_RANK (MLORA_MAX_RANK * MLORA_MAX_STACKED)
 
 typedef enum mlora_dtype {
   MLORA_F32 = 0,
@@ -75,7 +79,8 @@ typedef enum mlora_status {
  *                              seg_offsets[n_segments] == M.
  *   adapter_ids[n_segments]:   -1 (base only) or 0 <= id < n_adapters.
  * Adapter table (host arrays, length n_adapters):
- *   ranks[i] in {0} ∪ [8, MLORA_MAX_RANK], multiple of 8; scales[i] = alpha_i / rank_i.
+ *   ranks[i] in {0} ∪ [8, MLORA_MAX_RANK], multiple of 8 (GEMM entry points: up to
+ *   MLORA_MAX_GEMM_RANK); scales[i] = alpha_i / rank_i.
  * The reference builds one role per module call (training/dmd.py:301-353);
  * here each role is a segment of one call over the shared frozen base
  * (training/construction_sharing.py:105-118). */

@@ -35,7 +35,7 @@ def test_library_exports_every_declared_symbol(lib, pkg):
 
 
 def test_abi_version_and_status_strings(lib, pkg):
-    assert lib.mlora_abi_version() == pkg._lib.ABI_VERSION == 7
+    assert lib.mlora_abi_version() == pkg._lib.ABI_VERSION == 8
     for code in (0, -1, -2, -3, -4, -5):
         assert lib.mlora_status_string(code)
     assert b"unknown" in lib.mlora_status_string(-99)
@@ -44,8 +44,11 @@ def test_abi_version_and_status_strings(lib, pkg):
 def test_header_limits_match_python(pkg):
     text = HEADER.read_text()
     for name, val in (("MLORA_MAX_SEGMENTS", pkg._lib.MAX_SEGMENTS), ("MLORA_MAX_ADAPTERS", pkg._lib.MAX_ADAPTERS),
-                      ("MLORA_MAX_RANK", pkg._lib.MAX_RANK), ("MLORA_ABI_VERSION", pkg._lib.ABI_VERSION)):
+                      ("MLORA_MAX_RANK", pkg._lib.MAX_RANK), ("MLORA_ABI_VERSION", pkg._lib.ABI_VERSION),
+                      ("MLORA_MAX_STACKED", pkg._lib.MAX_STACKED)):
         assert re.search(rf"#define {name} {val}\b", text), name
+    assert "#define MLORA_MAX_GEMM_RANK (MLORA_MAX_RANK * MLORA_MAX_STACKED)" in text
+    assert pkg._lib.MAX_GEMM_RANK == pkg._lib.MAX_RANK * pkg._lib.MAX_STACKED
 
 
 def _gemm_fwd(lib, L, *, M=64, K=64, N=64, x=0x1000, w=0x2000, y=0x3000, ldx=None, off=None, ids=None,
@@ -67,7 +70,9 @@ def test_gemm_fwd_rejects_bad_routing_and_layout(lib, pkg):
     assert _gemm_fwd(lib, L, x=0x1008) == L.ERR_UNSUPPORTED           # misaligned X
     assert _gemm_fwd(lib, L, K=60, ldx=60) == L.ERR_UNSUPPORTED       # K not a multiple of 8
     assert _gemm_fwd(lib, L, ranks=(5,)) == L.ERR_INVALID             # rank not a multiple of 8
-    assert _gemm_fwd(lib, L, ranks=(264,)) == L.ERR_LIMIT             # rank above the limit
+    assert _gemm_fwd(lib, L, ranks=(L.MAX_GEMM_RANK + 8,)) == L.ERR_LIMIT  # rank above the GEMM limit
+    # a stacked rank above the shrink's limit is a GEMM rank: validated against h's width
+    assert _gemm_fwd(lib, L, ranks=(L.MAX_RANK + 8,), ldh=8) == L.ERR_INVALID
     assert _gemm_fwd(lib, L, bptr=(0,)) == L.ERR_INVALID              # used adapter without B
     assert _gemm_fwd(lib, L, h=0) == L.ERR_INVALID                    # adapter rows without h
     assert _gemm_fwd(lib, L, bias=0x6000, bias_dtype=2) == L.ERR_UNSUPPORTED
@@ -117,6 +122,7 @@ def test_shrink_validation(lib, pkg):
         off, ids, 1, h, 64, None, 0, None, None)
     assert args(3, [8], 0x3000) == L.ERR_INVALID
     assert args(0, [12], 0x3000) == L.ERR_INVALID
+    assert args(0, [L.MAX_RANK + 8], 0x3000) == L.ERR_LIMIT  # the shrink's rank limit stays 256
     assert args(0, [8], 0) == L.ERR_INVALID
     # split (fp32-master) operands: every used operand needs an aligned lo part
     assert args(0, [8], 0x3000, lo=L.ptr_array([0])) == L.ERR_INVALID

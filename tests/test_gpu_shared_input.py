@@ -196,3 +196,154 @@ def test_stacked_qkv_at_the_wan_shape(pkg, dev, transposed):
     assert rel_l2(dx_f[rows], ref_dx) <= 2e-3
     for a, b in zip(gr_f, gr_s):
         assert rel_l2(a, b) <= 2e-3
+
+
+def _wan_qkv(pkg, dev, family, rank, seed):
+    """q / k / v of the Wan-1.3B block (1536 -> 1536, bf16 base). family 'multi': MultiLoRALinear with
+    two bf16 adapters (generator, fake critic); 'peft': PEFT layers of the W1 layout (one adapter
+    'default', r = alpha, fp32 masters, training/wan_public.py:213) after install_peft_multi_lora."""
+    from peft_layout import PeftLoraLinear
+    g = torch.Generator().manual_seed(seed)
+    holder = nn.Module()
+    for name in ("q", "k", "v"):
+        base = nn.Linear(1536, 1536)
+        with torch.no_grad():
+            base.weight.copy_(torch.randn(1536, 1536, generator=g) / 1536 ** 0.5)
+            base.bias.copy_(torch.randn(1536, generator=g) * 0.1)
+        if family == "multi":
+            m = pkg.MultiLoRALinear(base, ranks=[rank, rank], alphas=[rank, rank])
+            with torch.no_grad():
+                for b in m.lora_b:
+                    b.copy_(torch.randn(b.shape, generator=g) * 0.02)
+            m = m.to(dev, torch.bfloat16)
+        else:
+            m = PeftLoraLinear(base.to(torch.bfloat16), {"default": (rank, float(rank))}, dtype=torch.float32)
+            with torch.no_grad():
+                m.lora_B["default"].weight.copy_(torch.randn(1536, rank, generator=g) * 0.02)
+            m = m.to(dev)
+        holder.add_module(name, m)
+    if family == "peft":
+        pkg.install_peft_multi_lora(holder)
+    return holder, [holder.q, holder.k, holder.v]
+
+
+def _adapters(m):
+    if hasattr(m, "lora_A"):
+        return [m.lora_A["default"].weight], [m.lora_B["default"].weight], [float(m.scaling["default"])]
+    return list(m.lora_a), list(m.lora_b), list(m.scales)
+
+
+@pytest.mark.parametrize("family,rank", [("multi", 128), ("peft", 256)], ids=["bf16_r128", "peft_fp32_r256"])
+def test_stacked_qkv_at_the_reference_ranks(pkg, dev, family, rank):
+    """q / k / v at the Wan shape (65520 tokens, 1536 -> 1536) and the reference's ranks: rank 128
+    (two bf16 adapters on the generator / critic segments; the shrinks run two members, then one)
+    and rank 256 with fp32 masters in the PEFT layout (one member per shrink, hi + lo parts).
+    Forward: each output bit-identical to the member's own call, and within 2e-3 of the fp64
+    oracle on 512 sampled rows; dX (one GEMM over the three dY and the 3·rank LoRA columns)
+    within 2e-3 of the fp64 oracle's sum of the members' dX; adapter gradients against fp64
+    products of the whole batch: 2e-3 for bf16 adapters (their bf16 rounding), 5e-5 for fp32
+    masters (fp32-class)."""
+    import numpy as np
+    from oracle import multilora_oracle as O
+    print(f"stacked qkv at the reference ranks: {family} rank {rank}", flush=True)
+    holder, mods = _wan_qkv(pkg, dev, family, rank, seed=41)
+    M = 65520
+    if family == "multi":
+        lengths, ids = (32760, 32760), (0, 1)
+    else:
+        lengths, ids = (M,), (0,)
+    routing = pkg.SegmentRouting.from_lengths(lengths, ids)
+    gen = torch.Generator().manual_seed(42)
+    x = torch.randn(M, 1536, generator=gen).to(dev, torch.bfloat16)
+    dys = [torch.randn(M, 1536, generator=gen).to(dev, torch.bfloat16) for _ in range(3)]
+    params = [p for m in mods for ab in _adapters(m)[:2] for p in ab]
+
+    def run(fused):
+        for p in params:
+            p.grad = None
+        if fused:
+            pkg.fuse_shared_inputs(holder, [["q", "k", "v"]])
+        xi = x.clone().requires_grad_(True)
+        ys = [m(xi, routing) if family == "multi" else m(xi) for m in mods]
+        torch.autograd.backward(ys, dys)
+        if fused:
+            assert mods[0].shared_input.launches == 1
+            pkg.release_shared_inputs(holder)
+        torch.cuda.synchronize()
+        return [y.detach() for y in ys], xi.grad, [p.grad.clone() for p in params]
+
+    ys_f, dx_f, gr_f = run(True)
+    ys_s, _, _ = run(False)
+    for a, b in zip(ys_f, ys_s):
+        assert torch.equal(a, b)
+    rows = np.sort(np.random.default_rng(43).choice(M, 512, replace=False))
+    rows[0], rows[-1] = 0, M - 1
+    ad = O.row_adapters(routing.seg_offsets, routing.adapter_ids)[rows]
+    loff = [0] + [i for i in range(1, len(ad)) if ad[i] != ad[i - 1]] + [len(ad)]
+    lids = [int(ad[i]) for i in loff[:-1]]
+    f64 = lambda t: t.detach().double().cpu().numpy()  # noqa: E731
+    xr, dx_ref = f64(x[rows]), 0.0
+    for m, y, dy in zip(mods, ys_f, dys):
+        As, Bs, scales = _adapters(m)
+        base = m.base_layer if hasattr(m, "base_layer") else m.base
+        Af, Bf = [f64(a) for a in As], [f64(b) for b in Bs]
+        y_ref = O.forward_rows(np.arange(len(rows)), xr, f64(base.weight), f64(base.bias), Af, Bf, scales, loff, lids)
+        assert O.rel_l2(f64(y[rows]), y_ref) <= 2e-3
+        dx_ref = dx_ref + O.dx_rows(np.arange(len(rows)), f64(base.weight), Af, Bf, scales, loff, lids,
+                                    f64(dy[rows]))
+    assert O.rel_l2(f64(dx_f[rows]), dx_ref) <= 2e-3
+    # adapter gradients against fp64 products over the whole batch (on the device)
+    tol = 5e-5 if family == "peft" else 2e-3
+    k = 0
+    xd = x.double()
+    for m, dy in zip(mods, dys):
+        As, Bs, scales = _adapters(m)
+        n = len(As)
+        got_a, got_b = gr_f[k:k + n], gr_f[k + n:k + 2 * n]
+        k += 2 * n
+        for (lo, hi), a in zip(zip(routing.seg_offsets, routing.seg_offsets[1:]), routing.adapter_ids):
+            xs, gu = xd[lo:hi], scales[a] * dy[lo:hi].double()
+            dB_ref = gu.T @ (xs @ As[a].detach().double().T)
+            dA_ref = (gu @ Bs[a].detach().double()).T @ xs
+            assert got_a[a].dtype == As[a].dtype and got_b[a].dtype == Bs[a].dtype
+            assert float((got_b[a].double() - dB_ref).norm() / dB_ref.norm()) <= tol
+            assert float((got_a[a].double() - dA_ref).norm() / dA_ref.norm()) <= tol
+
+
+def test_stacked_peft_roles_and_disabled_members(pkg, dev):
+    """PEFT layers in a group: members on different active adapters (of one rank and scaling) still
+    stack, each with its own adapter; with the adapters disabled every member runs the base alone
+    on its own (bit-exact with an adapter-free launch). Every output equals the member's own call."""
+    from peft_layout import PeftLoraLinear
+    print("stacked peft disabled / different adapters", flush=True)
+    holder = nn.Module()
+    g = torch.Generator().manual_seed(44)
+    for name in ("q", "k"):
+        m = PeftLoraLinear(nn.Linear(256, 256).to(torch.bfloat16), {"a": (16, 16.0), "b": (16, 16.0)},
+                           dtype=torch.bfloat16)
+        with torch.no_grad():
+            for n in ("a", "b"):
+                m.lora_B[n].weight.copy_(torch.randn(256, 16, generator=g) * 0.05)
+        holder.add_module(name, m.to(dev))
+    pkg.install_peft_multi_lora(holder)
+    group = pkg.fuse_shared_inputs(holder, [["q", "k"]])[0]
+    x = torch.randn(2, 64, 256, generator=g).to(dev, torch.bfloat16)
+    with torch.no_grad():
+        yq, yk = holder.q(x), holder.k(x)
+        assert group.launches == 1
+        holder.k.set_adapter("b")
+        yq2, yk2 = holder.q(x), holder.k(x)
+        assert group.launches == 2  # q on 'a', k on 'b': one stacked call, each member its adapter
+        for m in (holder.q, holder.k):
+            m.enable_adapters(False)
+        zq = holder.q(x)
+        assert group.launches == 2  # disabled: the base alone, per member
+        pkg.release_shared_inputs(holder)
+        assert torch.equal(zq, pkg.multi_lora_linear(x, holder.q.base_layer.weight, holder.q.base_layer.bias,
+                                                     [], [], [], pkg.SegmentRouting.single(128, pkg.BASE_ONLY)))
+        for m in (holder.q, holder.k):
+            m.enable_adapters(True)
+        holder.k.set_adapter("a")
+        assert torch.equal(yq, holder.q(x)) and torch.equal(yk, holder.k(x)) and torch.equal(yq2, yq)
+        holder.k.set_adapter("b")
+        assert torch.equal(yk2, holder.k(x)) and not torch.equal(yk2, yk)

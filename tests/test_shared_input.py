@@ -74,16 +74,67 @@ def test_scales_must_agree(pkg):
     assert len(pkg.fuse_shared_inputs(holder, [["a", "b"]])) == 1
 
 
-def test_stacked_rank_above_the_kernel_limit_fails_at_fuse_time(pkg):
-    """G members of rank r share one h of G·r columns: more than the kernels' 256 is a
-    ValueError when the group is made, not a kernel error on the first forward."""
+def test_wan_ranks_stack(pkg):
+    """G members of rank r share h of G·r columns: the shrinks and reductions take 256 of them
+    per call, the GEMMs all of them, so q/k/v at the reference's ranks 128 and 256 stack."""
+    for rank in (128, 256):
+        holder = nn.Module()
+        for name in ("q", "k", "v"):
+            setattr(holder, name, pkg.MultiLoRALinear(nn.Linear(256, 256), ranks=[rank], alphas=[rank]))
+        assert pkg.fuse_shared_inputs(holder, [["q", "k", "v"]])[0].rank == rank
+    from dmd_system_amd.function import _stack_slices
+    assert _stack_slices(3, 128) == [(0, 2), (2, 3)]
+    assert _stack_slices(3, 256) == [(0, 1), (1, 2), (2, 3)]
+    assert _stack_slices(3, 64) == [(0, 3)]
+    assert _stack_slices(8, 32) == [(0, 8)]
+
+
+def test_every_call_site_layout_groups(pkg):
+    """PEFT layers (after install_peft_multi_lora), the native LoRALinear and LiveWan's layout
+    group; an uninstalled PEFT layer or reference-layout module, or a mixture of families, fails
+    closed with the reason."""
+    from types import SimpleNamespace
+
+    from livewan_layout import RefLayoutLoRA
+    from peft_layout import PeftLoraLinear
     holder = nn.Module()
     for name in ("q", "k", "v"):
-        setattr(holder, name, pkg.MultiLoRALinear(nn.Linear(256, 256), ranks=[128], alphas=[128]))
-    with pytest.raises(ValueError, match="256"):
+        setattr(holder, name, PeftLoraLinear(nn.Linear(256, 256), {"default": (128, 128)}))
+    with pytest.raises(ValueError, match="install_peft_multi_lora first"):
         pkg.fuse_shared_inputs(holder, [["q", "k", "v"]])
-    # two members of rank 128 fit exactly
-    assert len(pkg.fuse_shared_inputs(holder, [["q", "k"]])) == 1
+    pkg.install_peft_multi_lora(holder)
+    g = pkg.fuse_shared_inputs(holder, [["q", "k", "v"]])[0]
+    assert g.family == "peft" and g.rank == 128 and g.n == 1
+    pkg.release_shared_inputs(holder)
+    # PEFT layers whose adapters differ by name or scaling do not stack
+    holder.v = PeftLoraLinear(nn.Linear(256, 256), {"other": (128, 128)})
+    pkg.install_peft_multi_lora(holder)
+    with pytest.raises(ValueError, match="same adapters"):
+        pkg.fuse_shared_inputs(holder, [["q", "v"]])
+    holder.v = PeftLoraLinear(nn.Linear(256, 256), {"default": (128, 64)})
+    pkg.install_peft_multi_lora(holder)
+    with pytest.raises(ValueError, match="different scales"):
+        pkg.fuse_shared_inputs(holder, [["q", "v"]])
+
+    task = SimpleNamespace(lora_rank=256, lora_alpha=256)
+    native = nn.Module()
+    for name in ("q", "k", "v"):
+        setattr(native, name, pkg.LoRALinear(nn.Linear(256, 256), task))
+    assert pkg.fuse_shared_inputs(native, [["q", "k", "v"]])[0].family == "pair"
+
+    lw = nn.Module()
+    for name in ("q", "k"):
+        setattr(lw, name, RefLayoutLoRA(nn.Linear(256, 256), rank=32))
+    with pytest.raises(ValueError, match="install_livewan_multi_lora first"):
+        pkg.fuse_shared_inputs(lw, [["q", "k"]])
+    pkg.install_livewan_multi_lora(lw)
+    assert pkg.fuse_shared_inputs(lw, [["q", "k"]])[0].family == "pair"
+
+    mixed = nn.Module()
+    mixed.q = pkg.LoRALinear(nn.Linear(256, 256), task)
+    mixed.k = pkg.MultiLoRALinear(nn.Linear(256, 256), ranks=[256], alphas=[256])
+    with pytest.raises(ValueError, match="all MultiLoRALinear"):
+        pkg.fuse_shared_inputs(mixed, [["q", "k"]])
 
 
 def test_stacked_bases_follow_replaced_biases_and_free_with_any_member(pkg):
