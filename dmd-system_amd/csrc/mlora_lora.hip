@@ -714,25 +714,49 @@ extern "C" int mlora_shrink(const void *p, int64_t ldp, int64_t M, int64_t K, co
   a.op_layout = op_layout;
   a.jtiles = frag_jtiles;
   build_pad(a.pad, a.seg);
-  const int rt = (rmax + 31) / 32;
-  // ranks 33-64: 256-row workgroups of 8 waves (more of P in flight per CU)
-  const int kTileRows = rt == 2 ? ShrinkCfg<2, 8>::BMS : 128;
-  int64_t n = 0;
-  for (int s = 0; s < a.seg.n; ++s) {
-    a.tile_start[s] = (int32_t)n;
-    const int ad = a.seg.aid[s];
-    const int len = a.seg.off[s + 1] - a.seg.off[s];
-    if (ad >= 0 && a.op.rank[ad] > 0 && len > 0) n += (len + kTileRows - 1) / kTileRows;
-  }
-  a.tile_start[a.seg.n] = (int32_t)n;
-  if (n == 0) return MLORA_OK;
   hipStream_t s = static_cast<hipStream_t>(stream);
+  // tiles of every segment with an adapter of rank > 0 (tile_rows rows each); false: no tile
+  auto plan_tiles = [](ShrinkArgs &b, int tile_rows, int64_t &n) {
+    n = 0;
+    for (int sg = 0; sg < b.seg.n; ++sg) {
+      b.tile_start[sg] = (int32_t)n;
+      const int ad = b.seg.aid[sg];
+      const int len = b.seg.off[sg + 1] - b.seg.off[sg];
+      if (ad >= 0 && b.op.rank[ad] > 0 && len > 0) n += (len + tile_rows - 1) / tile_rows;
+    }
+    b.tile_start[b.seg.n] = (int32_t)n;
+    return n > 0;
+  };
+  const int rt = (rmax + 31) / 32;
+  int64_t n = 0;
+  if (split && op_layout == 0 && rt > 4) {
+    // fp32 masters [r, K] of rank > 128: two passes of the 128-column kernel, columns [0, 128)
+    // and [128, r) (operand rows 128.., h columns 128.., fragment j-tiles 8..). One pass over
+    // all columns would hold the P tile and both 256-row operand tiles in every stage (80 KB:
+    // two stages only), and measured 6-11x slower than the two passes.
+    ShrinkArgs hi_cols = a;
+    for (int i = 0; i < n_adapters; ++i) {
+      a.op.rank[i] = a.op.rank[i] < 128 ? a.op.rank[i] : 128;
+      const bool more = hi_cols.op.rank[i] > 128;
+      hi_cols.op.rank[i] = more ? hi_cols.op.rank[i] - 128 : 0;
+      hi_cols.op.ptr[i] = more ? hi_cols.op.ptr[i] + (int64_t)128 * K : nullptr;
+      hi_cols.op_lo[i] = more ? hi_cols.op_lo[i] + (int64_t)128 * K : nullptr;
+    }
+    hi_cols.Hr = a.Hr + 128;
+    hi_cols.Hf = a.Hf != nullptr ? a.Hf + 8 * 2 * 64 : nullptr;
+    if (plan_tiles(a, 128, n)) hipLaunchKernelGGL((shrink_kernel<4, 0, 4, true>), dim3((int)n), dim3(256), 0, s, a);
+    if (plan_tiles(hi_cols, 128, n))
+      hipLaunchKernelGGL((shrink_kernel<4, 0, 4, true>), dim3((int)n), dim3(256), 0, s, hi_cols);
+    return launch_status();
+  }
+  // ranks 33-64: 256-row workgroups of 8 waves (more of P in flight per CU)
+  if (!plan_tiles(a, rt == 2 ? ShrinkCfg<2, 8>::BMS : 128, n)) return MLORA_OK;
   if (split) {
     // fp32 masters: the same tile shapes with both operand parts in each stage
     if (rt <= 1) launch_shrink_rt<1, 4, true>(a, (int)n, s);
     else if (rt == 2) launch_shrink_rt<2, 8, true>(a, (int)n, s);
     else if (rt <= 4) launch_shrink_rt<4, 4, true>(a, (int)n, s);
-    else launch_shrink_rt<8, 4, true>(a, (int)n, s);
+    else hipLaunchKernelGGL((shrink_kernel<8, 1, 4, true>), dim3((int)n), dim3(256), 0, s, a);  // layout 1
     return launch_status();
   }
   if (rt <= 1) launch_shrink_rt<1>(a, (int)n, s);

@@ -149,14 +149,18 @@ def test_trainable_scope_in_fp32_precision(pkg, dev):
     assert m0.base.weight.grad is None
 
 
-@pytest.mark.parametrize("K,N,rank", [(1536, 1536, 64), (512, 1024, 256), (136, 200, 24)])
-def test_fp32_masters_over_bf16_base(pkg, dev, K, N, rank):
+@pytest.mark.parametrize("K,N,ranks,lengths,ids", [
+    (1536, 1536, (64, 64), (1500, 548), (0, 1)), (512, 1024, (256, 256), (1500, 548), (0, 1)),
+    (136, 200, (24, 24), (1500, 548), (0, 1)),
+    # ranks above 128 run the forward shrink in two column passes: one adapter above, one below,
+    # and a base-only segment between
+    (1536, 768, (200, 96), (700, 300, 548), (0, -1, 1))])
+def test_fp32_masters_over_bf16_base(pkg, dev, K, N, ranks, lengths, ids):
     """native/models.py:44-51 with fp32 masters (models.py:150-156): bf16 x and base, fp32 A / B.
     dA / dB against the exact gradients of the unrounded masters (5e-5), Y / dX (bf16) within
     one rounding; the same oracle on bf16-rounded masters is far outside 5e-5 (so the check
     tells fp32 masters from rounded ones)."""
-    lengths, ids = (1500, 548), (0, 1)
-    x, w, b, As, Bs, dy = case(sum(lengths), K, N, (rank, rank), seed=45, dtype=torch.bfloat16)
+    x, w, b, As, Bs, dy = case(sum(lengths), K, N, ranks, seed=45, dtype=torch.bfloat16)
     routing = pkg.SegmentRouting.from_lengths(lengths, ids)
     scales = [1.0, 0.5]
     y, dx, dAs, dBs = run(pkg, dev, x, w, b, As, Bs, dy, scales, routing)
