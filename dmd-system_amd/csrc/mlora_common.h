@@ -298,4 +298,13 @@ __device__ __forceinline__ int xcd_remap(int bid, int nblocks) {
   return (bid % kXcd) * (nblocks / kXcd) + bid / kXcd;
 }
 
+// The same for any grid size: XCD x (bids x, x + 8, ...) takes the contiguous logical ids
+// [x·q + min(x, m), ...) of its share (q = nblocks / 8, m = nblocks % 8; the first m XCDs take
+// one more). A bijection on [0, nblocks).
+__device__ __forceinline__ int xcd_contiguous(int bid, int nblocks) {
+  constexpr int kXcd = 8;
+  const int x = bid % kXcd, q = nblocks / kXcd, m = nblocks % kXcd;
+  return x * q + (x < m ? x : m) + bid / kXcd;
+}
+
 }  // namespace mlora

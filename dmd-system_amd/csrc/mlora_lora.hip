@@ -74,17 +74,27 @@ struct ShrinkCfg {
   // used for ranks <= 32); larger ranks as many stages as 160 KB allows. 8 waves
   // (256 rows, used for ranks 33-64): 4 stages of 40 KB, one workgroup per CU,
   // 96 KB of P in flight instead of 64 KB (3-7% faster at rank 64; slower at 128).
+  // 9 waves (288 rows, ranks <= 64): the row count that puts one tile on each CU when 256-row
+  // tiles would leave a few for a second round (65520 rows in four segments: 259 tiles of
+  // 256 rows, 230 of 288); 3 stages of 40-44 KB.
   // SPLIT: as many stages (at most 3) as fit.
-  static constexpr int STAGES_PLAIN = NW == 8 ? 4 : RT <= 2 ? 3 : RT <= 4 ? 4 : 3;
+  static constexpr int STAGES_PLAIN = NW == 8 ? 4 : NW == 9 ? 3 : RT <= 2 ? 3 : RT <= 4 ? 4 : 3;
   static constexpr int STAGES_FIT = 163840 / STAGE_BYTES;
   static constexpr int STAGES = SPLIT ? (STAGES_FIT < 3 ? STAGES_FIT : 3) : STAGES_PLAIN;
-  static constexpr int WG_PER_CU = NW == 8 ? 1 : (RT <= 2 && 2 * STAGES * STAGE_BYTES <= 163840) ? 2 : 1;
+  static constexpr int WG_PER_CU = NW >= 8 ? 1 : (RT <= 2 && 2 * STAGES * STAGE_BYTES <= 163840) ? 2 : 1;
   static constexpr int THREADS = 64 * NW;
   static constexpr int P_DMA = P_BYTES / 1024 / NW;    // per wave per tile
-  static constexpr int OP_DMA = OP_BYTES / 1024 / NW;  // per wave per tile (layout 0 and 1 alike)
+  // The operand tile(s) of a stage take OP_BLOCKS 1 KB loads, OP_DMA per wave; when NW does not
+  // divide them, the last waves issue loads out of range into a 1 KB dummy block after the
+  // stages (no data read; every wave issues the same count, so the vmcnt thresholds hold).
+  static constexpr int OP_BLOCKS = OP_BYTES / 1024;
+  static constexpr int OP_DMA = (OP_BLOCKS + NW - 1) / NW;  // per wave per tile (layout 0 and 1 alike)
+  static constexpr bool OP_DUMMY = OP_DMA * NW != OP_BLOCKS;
+  static constexpr int LDS_BYTES = STAGES * STAGE_BYTES + (OP_DUMMY ? 1024 : 0);
   static constexpr int OP_HALF_DMA = OP_HALF / 1024;   // 1 KB loads of one operand tile (whole workgroup)
-  static_assert(P_DMA * NW * 1024 == P_BYTES && OP_DMA * NW * 1024 == OP_BYTES, "whole 1 KB loads per wave");
-  static_assert(STAGES >= 2 && STAGES * (P_BYTES + OP_BYTES) <= 163840, "the ring fits the LDS");
+  static_assert(P_DMA * NW * 1024 == P_BYTES && OP_BLOCKS * 1024 == OP_BYTES, "whole 1 KB loads");
+  static_assert(!(SPLIT && OP_DUMMY), "the split operand's two tiles divide over the waves");
+  static_assert(STAGES >= 2 && LDS_BYTES <= 163840, "the ring fits the LDS");
   static constexpr int DMA = P_DMA + OP_DMA;
   static constexpr int OPROW_B = OPROWS * 2;          // layout 1: bytes per k row
   static_assert(OP_DMA >= 1 && (STAGES - 2) * DMA < 64, "vmcnt field");
@@ -112,7 +122,7 @@ shrink_kernel(const ShrinkArgs args) {
   using C = ShrinkCfg<RT, NW, SPLIT>;
   constexpr int BMS = C::BMS;
   constexpr int ST = C::STAGES;
-  __shared__ u32x4 smem[ST * C::STAGE_BYTES / 16];  // the epilogue reuses it
+  __shared__ u32x4 smem[C::LDS_BYTES / 16];  // the epilogue reuses the stages
   MLORA_LDS char *lds = (MLORA_LDS char *)smem;
   const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
 
@@ -166,7 +176,8 @@ shrink_kernel(const ShrinkArgs args) {
 #pragma unroll
     for (int i = 0; i < C::OP_DMA; ++i) {
       const int qa = wave * C::OP_DMA + i;  // 1 KB block of the stage's operand tiles (wave-uniform)
-      MLORA_LDS char *dst = base + C::P_BYTES + qa * 1024;
+      const bool dummy = C::OP_DUMMY && qa >= C::OP_BLOCKS;
+      MLORA_LDS char *dst = dummy ? lds + ST * C::STAGE_BYTES : base + C::P_BYTES + qa * 1024;
       // SPLIT: blocks past the first operand tile fill the lo tile from the lo matrix
       const bool lo_half = SPLIT && qa >= C::OP_HALF_DMA;
       const int q = lo_half ? qa - C::OP_HALF_DMA : qa;  // block within its operand tile
@@ -174,12 +185,12 @@ shrink_kernel(const ShrinkArgs args) {
       if constexpr (OPL == 0) {
         const int j = 8 * q + (lane >> 3);
         int32_t off = j < r ? p_off[q & 1] - (lane >> 3) * ldp_b + j * K * 2 : kOOB;
-        if (!live || (kmask && k0 + p_kc[q & 1] >= K)) off = kOOB;
+        if (!live || dummy || (kmask && k0 + p_kc[q & 1] >= K)) off = kOOB;
         __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, dst, 16, off, 2 * k0, 0, 0);
       } else {
         const int krow = q * (1024 / C::OPROW_B) + o1_row;  // k row within the tile
         int32_t off = o1_off;
-        if (!live || k0 + krow >= K) off = kOOB;
+        if (!live || dummy || k0 + krow >= K) off = kOOB;
         // (the scalar offset goes through a variable: written inline in the builtin call,
         // this expression made the host compilation pass drop the kernel instantiation)
         const int32_t soff = (k0 + q * (1024 / C::OPROW_B)) * r * 2;
@@ -403,6 +414,7 @@ struct OuterArgs {
   int32_t rpad;              // 64 * jblocks: partial row length
   int32_t jtiles;            // fragment j-tiles per block
   int32_t chunk_start[kMaxSeg + 1];
+  int32_t item_start[kMaxSeg + 1];  // first work item of each segment
   int32_t rank[kMaxAdapters];
   PadTable pad;
   SegTable seg;
@@ -415,16 +427,20 @@ __global__ __launch_bounds__((64 * NWO), (OuterCfg<NWO, NJ>::WAVES_PER_EU)) void
   __shared__ u32x4 smem[OUTER_STAGES * OC::STAGE_BYTES / 16];
   MLORA_LDS char *lds = (MLORA_LDS char *)smem;
   const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
-  const int item = blockIdx.x;
-  const int cb = item % args.cblocks;
-  const int jb = (item / args.cblocks) % args.jblocks;
-  const int chunk = item / (args.cblocks * args.jblocks);
+  // Work items: per segment with an adapter, its chunks x its j blocks (ceil(r / OUT_J), so no
+  // item is empty) x the c blocks, c fastest. The items of one chunk are consecutive logical ids,
+  // and these run on one XCD, whose L2 then serves the chunk's h fragments to all of them.
+  const int item = xcd_contiguous(blockIdx.x, gridDim.x);
   int s = 0;
-  while (s + 1 < args.seg.n && args.chunk_start[s + 1] <= chunk) ++s;
+  while (s + 1 < args.seg.n && args.item_start[s + 1] <= item) ++s;
   const int a = args.seg.aid[s];
   const int r = args.rank[a];
+  const int local = item - args.item_start[s];
+  const int jbs = (r + OC::OUT_J - 1) / OC::OUT_J;
+  const int cb = local % args.cblocks;
+  const int jb = (local / args.cblocks) % jbs;
+  const int chunk = args.chunk_start[s] + local / (args.cblocks * jbs);
   const int j0 = jb * OC::OUT_J;
-  if (j0 >= r) return;  // whole workgroup exits together
   const int rel0 = (chunk - args.chunk_start[s]) * args.chunk_rows;  // multiple of 32
   const int row0 = args.seg.off[s] + rel0;
   const int rend = min(row0 + args.chunk_rows, args.seg.off[s + 1]);
@@ -610,11 +626,12 @@ struct OuterPlan {
   int32_t nwo = 4;  // waves per workgroup: 64·nwo columns per work item
   int32_t nj = 4;   // 16-wide j tiles per work item
   int32_t chunk_rows = 0, cblocks = 0, jblocks = 0, rpad = 0, n_chunks = 0;
+  int64_t n_items = 0;
   int32_t chunk_start[kMaxSeg + 1];
+  int64_t item_start[kMaxSeg + 1];
 };
 
-// chunk_floor: the smallest chunk (rows) to use; 0 for the default plan.
-static void plan_outer(OuterPlan &pl, const SegTable &st, const int32_t *rank, int64_t C, int64_t chunk_floor = 0) {
+static void plan_outer(OuterPlan &pl, const SegTable &st, const int32_t *rank, int64_t C) {
   int rmax = 0;
   int64_t rows = 0, rows_wide = 0;  // rows with an adapter; of them, rows of rank > 64
   for (int s = 0; s < st.n; ++s) {
@@ -636,22 +653,76 @@ static void plan_outer(OuterPlan &pl, const SegTable &st, const int32_t *rank, i
   const int out_j = 16 * pl.nj;
   pl.jblocks = (rmax + out_j - 1) / out_j;
   pl.rpad = pl.jblocks * out_j;
-  // aim at ~512 work items (2 per CU) with chunks of at least 512 rows
-  const int64_t target_items = 512;
-  int64_t cr = rows * pl.cblocks * (pl.jblocks > 0 ? pl.jblocks : 1) / target_items;
-  cr = cr < 512 ? 512 : cr;
-  cr = cr < chunk_floor ? chunk_floor : cr;
-  cr = (cr + 127) / 128 * 128;
-  pl.chunk_rows = (int32_t)(cr > kMaxChunkRows ? kMaxChunkRows : cr);
+  // Chunk rows: the candidate (a multiple of 64 from 256 rows) of least modelled time. The model,
+  // calibrated on MI355X at the Wan / FLUX shapes: a work item moves cr·(2·OUT_C + 4·OUT_J) bytes
+  // of P and h fragments and writes its OUT_C x OUT_J partial sums; a CU running k items at once
+  // streams about 24 / 38 / 50 KB per us (k = 1 / 2 / 3), the chip about 5.8 MB per us; the
+  // fragments come from HBM once (the items of a chunk share an XCD's L2); the reduction reads
+  // the partial sums once more. A plan whose items exceed the CUs' slots pays a whole extra
+  // round, so the model favours chunks that give every item a slot.
+  const int w = pl.nj == 8 ? (pl.nwo == 8 ? 1 : 2) : (pl.nwo == 8 ? 2 : 3);  // workgroups per CU
+  constexpr double kRate[4] = {0.0, 24e3, 38e3, 50e3};  // bytes per us per CU, k workgroups
+  constexpr double kChip = 5.8e6;                       // bytes per us
+  constexpr int kCUs = 256;
+  int64_t max_len = 0, frag = 0;
+  for (int s = 0; s < st.n; ++s) {
+    const int a = st.aid[s];
+    const int64_t len = st.off[s + 1] - st.off[s];
+    if (a >= 0 && rank[a] > 0 && len > 0) {
+      max_len = len > max_len ? len : max_len;
+      frag += (len + 31) / 32 * 32 * ((rank[a] + 15) / 16 * 16) * 4;
+    }
+  }
+  int64_t best_cr = 512;
+  double best_t = -1.0;
+  const int64_t cr_hi = max_len < kMaxChunkRows ? (max_len + 63) / 64 * 64 : kMaxChunkRows;
+  for (int64_t cr = 256; cr <= (cr_hi > 256 ? cr_hi : 256); cr += 64) {
+    int64_t items = 0, nch = 0;
+    for (int s = 0; s < st.n; ++s) {
+      const int a = st.aid[s];
+      const int64_t len = st.off[s + 1] - st.off[s];
+      if (a >= 0 && rank[a] > 0 && len > 0) {
+        const int64_t c = (len + cr - 1) / cr;
+        nch += c;
+        items += c * pl.cblocks * ((rank[a] + out_j - 1) / out_j);
+      }
+    }
+    const double part = (double)nch * C * pl.rpad * 4;
+    const double total = (double)rows * C * 2 + (double)frag + part;
+    const double rows_item = (double)(cr < max_len ? cr : max_len);
+    const double item_b = rows_item * (2.0 * out_c + 4.0 * out_j) + 4.0 * out_c * out_j;
+    double t_cu;
+    if (items <= (int64_t)kCUs * w) {
+      const int k = (int)((items + kCUs - 1) / kCUs);
+      t_cu = item_b * k / kRate[k < 1 ? 1 : k];
+    } else {
+      const int64_t rounds = (items + (int64_t)kCUs * w - 1) / ((int64_t)kCUs * w);
+      t_cu = (double)rounds * item_b * w / kRate[w];
+    }
+    const double t = (total / kChip > t_cu ? total / kChip : t_cu) + part / kChip;
+    if (best_t < 0.0 || t < best_t) {
+      best_t = t;
+      best_cr = cr;
+    }
+  }
+  pl.chunk_rows = (int32_t)best_cr;
   int32_t n = 0;
+  int64_t items = 0;
   for (int s = 0; s < st.n; ++s) {
     pl.chunk_start[s] = n;
+    pl.item_start[s] = items;
     const int a = st.aid[s];
     const int len = st.off[s + 1] - st.off[s];
-    if (a >= 0 && rank[a] > 0 && len > 0) n += (len + pl.chunk_rows - 1) / pl.chunk_rows;
+    if (a >= 0 && rank[a] > 0 && len > 0) {
+      const int c = (len + pl.chunk_rows - 1) / pl.chunk_rows;
+      n += c;
+      items += (int64_t)c * pl.cblocks * ((rank[a] + out_j - 1) / out_j);
+    }
   }
   pl.chunk_start[st.n] = n;
+  pl.item_start[st.n] = items;
   pl.n_chunks = n;
+  pl.n_items = items;
 }
 
 static int64_t frag_bytes(const SegTable &st, int jtiles) {
@@ -751,6 +822,23 @@ extern "C" int mlora_shrink(const void *p, int64_t ldp, int64_t M, int64_t K, co
   }
   // ranks 33-64: 256-row workgroups of 8 waves (more of P in flight per CU)
   if (!plan_tiles(a, rt == 2 ? ShrinkCfg<2, 8>::BMS : 128, n)) return MLORA_OK;
+  if (!split && rt <= 2) {
+    // 288-row workgroups of 9 waves when they give every CU at most one tile and the default
+    // tiles would not: cost = rounds x rows a CU takes per round (256 CUs; the 4-wave tiles of
+    // ranks <= 32 run two workgroups per CU)
+    constexpr int64_t kCUs = 256;
+    const int64_t wg = rt <= 1 ? 2 : 1, rows = rt <= 1 ? 128 : 256;
+    const int64_t cost_default = (n + kCUs * wg - 1) / (kCUs * wg) * rows * wg;
+    int64_t n9 = 0;
+    plan_tiles(a, ShrinkCfg<2, 9>::BMS, n9);
+    const int64_t cost9 = (n9 + kCUs - 1) / kCUs * ShrinkCfg<2, 9>::BMS;
+    if (cost9 < cost_default) {
+      if (rt <= 1) launch_shrink_rt<1, 9>(a, (int)n9, s);
+      else launch_shrink_rt<2, 9>(a, (int)n9, s);
+      return launch_status();
+    }
+    plan_tiles(a, rows, n);
+  }
   if (split) {
     // fp32 masters: the same tile shapes with both operand parts in each stage
     if (rt <= 1) launch_shrink_rt<1, 4, true>(a, (int)n, s);
@@ -833,9 +921,12 @@ static int seg_outer_run(OuterArgs &a, const OuterPlan &pl, const void *p, int64
     a.rpad = pl.rpad;
     a.jtiles = frag_jtiles;
     build_pad(a.pad, a.seg);
-    for (int i = 0; i <= a.seg.n; ++i) a.chunk_start[i] = pl.chunk_start[i];
-    const int64_t items = (int64_t)pl.n_chunks * pl.jblocks * pl.cblocks;
+    const int64_t items = pl.n_items;
     if (items > INT32_MAX) return MLORA_ERR_LIMIT;
+    for (int i = 0; i <= a.seg.n; ++i) {
+      a.chunk_start[i] = pl.chunk_start[i];
+      a.item_start[i] = (int32_t)pl.item_start[i];
+    }
     if (pl.nwo == 8 && pl.nj == 8)
       hipLaunchKernelGGL((seg_outer_kernel<8, 8>), dim3((unsigned)items), dim3(512), 0, s, a);
     else if (pl.nwo == 8)

@@ -143,23 +143,31 @@ def test_random_routings_vs_oracle(pkg, dev, segs, rank_idx, transposed):
     check_against_oracle(pkg, dev, case, [1.0, 0.5, 2.0, 0.25], routing, transposed=transposed)
 
 
-@pytest.mark.parametrize("rank,lengths,ids", [
-    (64, (20001, 333, 16000, 4097, 30000), (0, -1, 1, 2, 0)),   # 256-row tiles
-    (128, (9000, 77, 31000, 641), (1, 0, -1, 1)),                # 128-row tiles
-], ids=["rank64", "rank128"])
-def test_shrink_segments_match_single_segment_calls(pkg, dev, rank, lengths, ids):
+_CFG5_SEGS = (16997, 24338, 8047, 16138)  # config 5's segments: 259 tiles of 256 rows, 230 of 288
+
+
+@pytest.mark.parametrize("rank,lengths,ids,layout", [
+    (64, (20001, 333, 16000, 4097, 30000), (0, -1, 1, 2, 0), 0),   # 256-row tiles
+    (128, (9000, 77, 31000, 641), (1, 0, -1, 1), 0),                # 128-row tiles
+    # 288-row tiles of 9 waves in the four-segment call, the default tiles in each segment's own
+    (64, _CFG5_SEGS, (0, 1, 2, 0), 0), (64, _CFG5_SEGS, (0, 1, 2, 0), 1),
+    (32, _CFG5_SEGS, (2, 0, 1, 1), 0), (32, _CFG5_SEGS, (2, 0, 1, 1), 1),
+], ids=["rank64", "rank128", "rank64_9waves", "rank64_9waves_layout1", "rank32_9waves", "rank32_9waves_layout1"])
+def test_shrink_segments_match_single_segment_calls(pkg, dev, rank, lengths, ids, layout):
     """Ragged segments (tiles ending inside a segment's last 32 rows, a base-only segment between
     adapter segments, more tiles than the GPU runs at once): each segment's h rows and fragments
-    equal those of a call on that segment alone, bit for bit, and h matches the fp64 product."""
+    equal those of a call on that segment alone, bit for bit, and h matches the fp64 product.
+    Layout 1 takes the operand as [K, r] (lora_b of the backward shrink)."""
     from dmd_system_amd import kernels
     K, M = 96, sum(lengths)
     g = torch.Generator().manual_seed(21)
     x = torch.randn(M, K, generator=g).to(torch.bfloat16)
     As = [((torch.rand(rank, K, generator=g) * 2 - 1) / math.sqrt(K)).to(torch.bfloat16) for _ in range(3)]
+    ops = As if layout == 0 else [a.t().contiguous() for a in As]
     scales = [1.0, 0.5, 2.0]
-    xg, Ag = x.to(dev), [a.to(dev) for a in As]
+    xg, Ag = x.to(dev), [o.to(dev) for o in ops]
     routing = pkg.SegmentRouting.from_lengths(lengths, ids)
-    h, frags = kernels.shrink(xg, Ag, 0, scales, routing, True, rank)
+    h, frags = kernels.shrink(xg, Ag, layout, scales, routing, True, rank)
     torch.cuda.synchronize()
     (frag,) = frags
     fb = kernels.frag_jtiles(rank) * 2048 // 2  # bf16 elements per 32-row fragment block
@@ -167,7 +175,8 @@ def test_shrink_segments_match_single_segment_calls(pkg, dev, rank, lengths, ids
     for n, a in zip(lengths, ids):
         nb = (n + 31) // 32
         if a >= 0:
-            h1, (f1,) = kernels.shrink(xg[off:off + n], Ag, 0, scales, pkg.SegmentRouting.single(n, a), True, rank)
+            h1, (f1,) = kernels.shrink(xg[off:off + n], Ag, layout, scales, pkg.SegmentRouting.single(n, a), True,
+                                       rank)
             torch.cuda.synchronize()
             assert torch.equal(h[off:off + n], h1), (n, a)
             assert torch.equal(frag[block * fb:(block + nb) * fb], f1[:nb * fb]), (n, a)
