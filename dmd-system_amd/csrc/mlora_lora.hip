@@ -369,14 +369,15 @@ static void launch_shrink_rt(const ShrinkArgs &a, int nblocks, hipStream_t strea
 // fragments are stored by the shrink in that MFMA's B-operand order and are
 // read as they are (16 bytes per lane).
 //
-// Column block: every c block of a chunk reads the chunk's h fragments again,
-// so wider blocks read them fewer times. 8 waves (512 columns, two workgroups
-// per CU) for C <= 4096 (at C = 1536: 65 vs 73 us per reduction, the fragments
-// read 3 times instead of 6); 4 waves (256 columns, three workgroups per CU)
-// above, where the 8-wave form was slower (C = 8960: 256 vs 238 us).
+// Column block: every c block of a chunk reads the chunk's h fragments again. The
+// items of a chunk run on one XCD, so after the first read they come from its L2.
+// 4 waves (256 columns, three workgroups per CU with 64 j) by default; 8 waves
+// (512 columns) for 128 j at C <= 4096, where the wider block was faster
+// (C = 3072, rank 128: 67 vs 72 us; with 64 j the 4-wave form was faster: C = 1536
+// 58.5 vs 63 us, C = 3072 106 vs 111 us).
 
 constexpr int kMaxChunkRows = 32768;
-constexpr int kWideOuterMaxC = 4096;  // C up to which the 8-wave (512-column) form runs
+constexpr int kWideOuterMaxC = 4096;  // C up to which the 8-wave (512-column) form runs with 128 j
 // Two stages (one step in flight while one is multiplied): 48 KB (4 waves, 64 j) lets three
 // workgroups share a CU, measured 7-8% faster than three stages and two workgroups
 // (and than more work items, whose partial sums cost more); 80 KB (8 waves) two.
@@ -643,14 +644,14 @@ static void plan_outer(OuterPlan &pl, const SegTable &st, const int32_t *rank, i
       rmax = rank[a] > rmax ? rank[a] : rmax;
     }
   }
-  pl.nwo = C <= kWideOuterMaxC ? 8 : 4;
-  const int64_t out_c = 64 * (int64_t)pl.nwo;
-  pl.cblocks = (int32_t)((C + out_c - 1) / out_c);
   // 128 j per item when most rows have an adapter of rank > 64 (their P is then streamed once
   // instead of twice); with few such rows the 64-j items, whose second j block exits at once
   // for the smaller ranks, are faster (config 4's mixed ranks: 3%)
   pl.nj = 2 * rows_wide > rows ? 8 : 4;
   const int out_j = 16 * pl.nj;
+  pl.nwo = C <= kWideOuterMaxC && pl.nj == 8 ? 8 : 4;
+  const int64_t out_c = 64 * (int64_t)pl.nwo;
+  pl.cblocks = (int32_t)((C + out_c - 1) / out_c);
   pl.jblocks = (rmax + out_j - 1) / out_j;
   pl.rpad = pl.jblocks * out_j;
   // Chunk rows: the candidate (a multiple of 64 from 256 rows) of least modelled time. The model,
@@ -825,7 +826,11 @@ extern "C" int mlora_shrink(const void *p, int64_t ldp, int64_t M, int64_t K, co
   if (!split && rt <= 2) {
     // 288-row workgroups of 9 waves when they give every CU at most one tile and the default
     // tiles would not: cost = rounds x rows a CU takes per round (256 CUs; the 4-wave tiles of
-    // ranks <= 32 run two workgroups per CU)
+    // ranks <= 32 run two workgroups per CU). At ranks <= 64 a tile's time hardly depends on its
+    // rows (its k-steps stream at a latency-bound pace): 65520 rows in four segments take 259
+    // tiles of 256 rows (two rounds) or 230 of 288 (one), and the shrink 47 instead of 67 us at
+    // K = 1536. (256-row tiles for ranks 65-128, in two rounds instead of three of 128 rows,
+    // measured 3-12% slower at config 4's shapes: there the rows do set the time.)
     constexpr int64_t kCUs = 256;
     const int64_t wg = rt <= 1 ? 2 : 1, rows = rt <= 1 ? 128 : 256;
     const int64_t cost_default = (n + kCUs * wg - 1) / (kCUs * wg) * rows * wg;

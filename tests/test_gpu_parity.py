@@ -152,7 +152,10 @@ _CFG5_SEGS = (16997, 24338, 8047, 16138)  # config 5's segments: 259 tiles of 25
     # 288-row tiles of 9 waves in the four-segment call, the default tiles in each segment's own
     (64, _CFG5_SEGS, (0, 1, 2, 0), 0), (64, _CFG5_SEGS, (0, 1, 2, 0), 1),
     (32, _CFG5_SEGS, (2, 0, 1, 1), 0), (32, _CFG5_SEGS, (2, 0, 1, 1), 1),
-], ids=["rank64", "rank128", "rank64_9waves", "rank64_9waves_layout1", "rank32_9waves", "rank32_9waves_layout1"])
+    # config 4's sixteen 4608-row samples at rank 128 (three rounds of 128-row tiles)
+    (128, (4608,) * 16, (0, 1, 2, 0) * 4, 0), (128, (4608,) * 16, (0, 1, 2, 0) * 4, 1),
+], ids=["rank64", "rank128", "rank64_9waves", "rank64_9waves_layout1", "rank32_9waves", "rank32_9waves_layout1",
+        "rank128_16segments", "rank128_16segments_layout1"])
 def test_shrink_segments_match_single_segment_calls(pkg, dev, rank, lengths, ids, layout):
     """Ragged segments (tiles ending inside a segment's last 32 rows, a base-only segment between
     adapter segments, more tiles than the GPU runs at once): each segment's h rows and fragments
