@@ -243,8 +243,9 @@ def profile_kernels(args):
     transposed base), gemm_dx_nn (NN against the base as stored), shrink_x, shrink_dy,
     seg_outer_dB, seg_outer_dA (main pass + fixed-order reduction), torch_matmul (hipBLASLt, bf16);
     with an e4m3 base instead of the bf16 GEMMs: quantize_x, gemm_fwd_fp8, quantize_dy (dY times
-    the channel scales), gemm_dx_fp8 (the e4m3 dX); last, a plain 1 GiB device copy as the
-    reference rate of HBM-bound kernels."""
+    the channel scales), gemm_dx_fp8 (the e4m3 dX), torch_scaled_mm (hipBLASLt's e4m3 GEMM, where
+    torch takes row-wise scales); last, a plain 1 GiB device copy as the reference rate of
+    HBM-bound kernels."""
     import torch
     import __graft_entry__
     pkg = __graft_entry__.load_package()
@@ -272,6 +273,7 @@ def profile_kernels(args):
         return {"gemm_fwd": ("flop", 2 * M * K * N + 2 * mr * N), "gemm_fwd_fp8": ("flop", 2 * M * K * N + 2 * mr * N),
                 "gemm_dx": ("flop", 2 * M * K * N + 2 * mr * K), "gemm_dx_nn": ("flop", 2 * M * K * N + 2 * mr * K),
                 "gemm_dx_fp8": ("flop", 2 * M * K * N + 2 * mr * K), "torch_matmul": ("flop", 2 * M * K * N),
+                "torch_scaled_mm": ("flop", 2 * M * K * N),
                 # P rows read once, the adapter operands once, h rows (2 B) and hi/lo fragments (4 B) written
                 "shrink_x": ("byte", m_a * K * 2 + r_sum * K * 2 + mr * 6),
                 "shrink_dy": ("byte", m_a * N * 2 + r_sum * N * 2 + mr * 6),
@@ -309,6 +311,16 @@ def profile_kernels(args):
                     "shrink_x": lambda: kernels.shrink(x, A_ops, 0, scales, routing, True, R, row_div=xs),
                     "shrink_dy": lambda: kernels.shrink(dy, B_ops, 1, scales, routing, True, R, row_div=dys),
                 }
+                # hipBLASLt's e4m3 GEMM (torch._scaled_mm, row-wise scales) on the same operands, context
+                # only; left out where this torch build does not take it
+                scaled = lambda: torch._scaled_mm(xq, wq.t(), scale_a=xs[:, None], scale_b=ws[None, :],  # noqa: E731
+                                                  out_dtype=torch.bfloat16)
+                try:
+                    scaled()
+                    torch.cuda.synchronize()
+                    fams["torch_scaled_mm"] = scaled
+                except (RuntimeError, TypeError):
+                    pass
             else:
                 wt = w.t().contiguous()
                 h_rows, h_frag = kernels.shrink(x, A_ops, 0, scales, routing, True, R)
@@ -667,12 +679,32 @@ def main():
 
     # ---------------- vendor GEMM reference (context only): torch bf16 matmul, same shapes
     vendor = {}
+    vendor_fp8 = {}
     scrub_buf = torch.ones(args.scrub_mb << 18, dtype=torch.float32, device=dev)
     with torch.no_grad():
         for L in lins[3:6]:
             x = L["x"].detach()
             t = timed([lambda: torch.matmul(x, L["w"].T)])
             vendor[f"{L['name']} {L['K']}->{L['N']}"] = round(2 * cfg.tokens * L["K"] * L["N"] / t / 1e12, 1)
+            if fp8:
+                # hipBLASLt's e4m3 GEMM through torch._scaled_mm on the same quantised operands, with
+                # row-wise scales (X per token, W per channel) where this torch build takes them
+                xq, xs = kernels.quantize_rows_fp8(x)
+                key = f"{L['name']} {L['K']}->{L['N']}"
+                for form, sa, sb in (("rowwise", xs[:, None], L["ws"][None, :]),
+                                     ("tensorwise", xs.max(), L["ws"].max())):
+                    try:
+                        fn = lambda: torch._scaled_mm(xq, L["wq"].t(), scale_a=sa, scale_b=sb,  # noqa: E731
+                                                      out_dtype=torch.bfloat16)
+                        fn()
+                        torch.cuda.synchronize()
+                    except (RuntimeError, TypeError) as exc:
+                        vendor_fp8[key + " " + form] = f"unsupported: {str(exc).splitlines()[0][:120]}"
+                        continue
+                    t = timed([fn])
+                    vendor_fp8[key + " " + form] = round(2 * cfg.tokens * L["K"] * L["N"] / t / 1e12, 1)
+                    break
+                del xq, xs
     del scrub_buf
 
     per_role = per_role_timing(pkg, cfg, lins, scales, args, flops_step) if args.per_role else None
@@ -716,6 +748,7 @@ def main():
         "lora_hbm": lora,
         "kernels": kern,
         "vendor_gemm_tflops": vendor,
+        **({"vendor_fp8_gemm_tflops": vendor_fp8} if fp8 else {}),
         **({"per_role": per_role} if per_role is not None else {}),
         **({"qkv_unstacked": unstacked} if unstacked is not None else {}),
         **({"gated_residual_unfused": unfused} if unfused is not None else {}),

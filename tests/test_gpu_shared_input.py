@@ -347,3 +347,126 @@ def test_stacked_peft_roles_and_disabled_members(pkg, dev):
         assert torch.equal(yq, holder.q(x)) and torch.equal(yk, holder.k(x)) and torch.equal(yq2, yq)
         holder.k.set_adapter("b")
         assert torch.equal(yk2, holder.k(x)) and not torch.equal(yk2, yk)
+
+
+def _grads_close(a, b, tol):
+    for x, y in zip(a, b):
+        assert float((x.double() - y.double()).norm() / y.double().norm()) <= tol
+
+
+def test_livewan_self_attention_group(pkg, dev):
+    """LiveWan's layout (the reference's module after install_livewan_multi_lora, fp32 a / b over the
+    bf16 critic) with self_attn.q / k / v stacked: the model's output bit-identical to the unstacked
+    model's, every adapter gradient within 1e-4 (the stacked reductions sum in another order);
+    with the adapters off (lora_enabled(model, False)) every member runs the base alone on its own."""
+    from livewan_layout import WanLike, wrap_reference_layout
+    print("livewan self-attention group", flush=True)
+    model = WanLike(hidden=256, ffn=512, heads=4, layers=1).to(torch.bfloat16)
+    wrap_reference_layout(model, rank=32)
+    model = model.to(dev)
+    pkg.install_livewan_multi_lora(model)
+    gen = torch.Generator().manual_seed(71)
+    x = torch.randn(2, 64, 256, generator=gen).to(dev, torch.bfloat16)
+    w = torch.randn(2, 64, 256, generator=gen).to(dev, torch.bfloat16)
+    params = [p for p in model.parameters() if p.requires_grad]
+    names = [["blocks.0.self_attn.q", "blocks.0.self_attn.k", "blocks.0.self_attn.v"]]
+
+    def run(stacked):
+        for p in params:
+            p.grad = None
+        groups = pkg.fuse_shared_inputs(model, names) if stacked else []
+        y = model(x)
+        (y.float() * w.float()).sum().backward()
+        with torch.no_grad(), pkg.livewan.lora_enabled(model, False):
+            y_off = model(x)
+        launches = [g.launches for g in groups]
+        pkg.release_shared_inputs(model)
+        return y.detach(), y_off, [p.grad.clone() for p in params], launches
+
+    y_s, off_s, g_s, launches = run(True)
+    y_u, off_u, g_u, _ = run(False)
+    assert launches == [1]  # the disabled pass ran its members on their own
+    assert torch.equal(y_s, y_u) and torch.equal(off_s, off_u) and not torch.equal(y_s, off_s)
+    _grads_close(g_s, g_u, 1e-4)
+
+
+def test_native_lora_linear_group(pkg, dev):
+    """The native LoRALinear (install_lora: fp32 masters over a bf16 base) at rank 128, q / k / v
+    stacked: outputs bit-identical to the members' own calls, gradients within 1e-4."""
+    from types import SimpleNamespace
+    print("native LoRALinear group rank 128", flush=True)
+    holder = nn.Module()
+    gen = torch.Generator().manual_seed(72)
+    for name in ("q", "k", "v"):
+        lin = nn.Linear(512, 512)
+        with torch.no_grad():
+            lin.weight.copy_(torch.randn(512, 512, generator=gen) / 512 ** 0.5)
+        setattr(holder, name, lin.to(torch.bfloat16))
+    pkg.install_lora(holder, SimpleNamespace(lora_rank=128, lora_alpha=64, target_modules=["q", "k", "v"]))
+    for name in ("q", "k", "v"):
+        with torch.no_grad():
+            m = getattr(holder, name)
+            m.b.copy_(torch.randn(m.b.shape, generator=gen) * 0.02)
+    holder = holder.to(dev)
+    mods = [holder.q, holder.k, holder.v]
+    x = torch.randn(4096, 512, generator=gen).to(dev, torch.bfloat16)
+    dys = [torch.randn(4096, 512, generator=gen).to(dev, torch.bfloat16) for _ in range(3)]
+    params = [p for m in mods for p in (m.a, m.b)]
+
+    def run(stacked):
+        for p in params:
+            p.grad = None
+        group = pkg.fuse_shared_inputs(holder, [["q", "k", "v"]])[0] if stacked else None
+        xi = x.clone().requires_grad_(True)
+        ys = [m(xi) for m in mods]
+        torch.autograd.backward(ys, dys)
+        if stacked:
+            assert group.launches == 1
+            pkg.release_shared_inputs(holder)
+        return [y.detach() for y in ys], xi.grad, [p.grad.clone() for p in params]
+
+    ys_s, dx_s, g_s = run(True)
+    ys_u, dx_u, g_u = run(False)
+    assert all(torch.equal(a, b) for a, b in zip(ys_s, ys_u))
+    assert all(g.dtype == torch.float32 for g in g_s)
+    _grads_close(g_s, g_u, 1e-4)
+    assert float((dx_s.double() - dx_u.double()).norm() / dx_u.double().norm()) <= 4e-3
+
+
+def test_peft_role_batch_group(pkg, dev):
+    """PEFT layers routed by a role batch (peft_roles_active: the teacher's rows on the base alone,
+    the critic's on its adapter, H3's pattern) with q / k / v stacked: outputs bit-identical to the
+    unstacked layers', adapter gradients within 2e-3 (bf16 adapters)."""
+    from peft_layout import PeftLoraLinear
+    print("peft role batch group", flush=True)
+    holder = nn.Module()
+    gen = torch.Generator().manual_seed(73)
+    for name in ("q", "k", "v"):
+        m = PeftLoraLinear(nn.Linear(512, 512).to(torch.bfloat16), {"critic": (64, 64.0)}, dtype=torch.bfloat16)
+        with torch.no_grad():
+            m.lora_B["critic"].weight.copy_(torch.randn(512, 64, generator=gen) * 0.05)
+        holder.add_module(name, m.to(dev))
+    pkg.install_peft_multi_lora(holder)
+    mods = [holder.q, holder.k, holder.v]
+    x = torch.randn(3, 200, 512, generator=gen).to(dev, torch.bfloat16)
+    dys = [torch.randn(3, 200, 512, generator=gen).to(dev, torch.bfloat16) for _ in range(3)]
+    params = [p for m in mods for p in (m.lora_A["critic"].weight, m.lora_B["critic"].weight)]
+    rb = pkg.RoleBatch([("teacher", 2), ("critic", 1)])
+
+    def run(stacked):
+        for p in params:
+            p.grad = None
+        group = pkg.fuse_shared_inputs(holder, [["q", "k", "v"]])[0] if stacked else None
+        xi = x.clone().requires_grad_(True)
+        with pkg.peft_roles_active(holder, rb, base_roles=("teacher",)):
+            ys = [m(xi) for m in mods]
+        torch.autograd.backward(ys, dys)
+        if stacked:
+            assert group.launches == 1
+            pkg.release_shared_inputs(holder)
+        return [y.detach() for y in ys], [p.grad.clone() for p in params]
+
+    ys_s, g_s = run(True)
+    ys_u, g_u = run(False)
+    assert all(torch.equal(a, b) for a, b in zip(ys_s, ys_u))
+    _grads_close(g_s, g_u, 2e-3)
