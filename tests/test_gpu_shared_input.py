@@ -470,3 +470,72 @@ def test_peft_role_batch_group(pkg, dev):
     ys_u, g_u = run(False)
     assert all(torch.equal(a, b) for a, b in zip(ys_s, ys_u))
     _grads_close(g_s, g_u, 2e-3)
+
+
+@pytest.mark.parametrize("split", [False, True], ids=["bf16", "fp32_masters"])
+@pytest.mark.parametrize("widths", [(256, 512, 768), (512, 512, 512)], ids=["mixed_widths", "stacked"])
+def test_rank128_many_segments(pkg, dev, split, widths):
+    """Rank 128 with 131 segments (two calls of the kernels' 128-segment tables, base-only segments
+    between), for members of different widths (SharedInputMultiLoRAFunction: the shared shrinks in
+    256-column slices, one GEMM per member, the members' dX accumulated in the dX GEMMs'
+    epilogues) and of one width (StackedLinearsFunction): each output bit-identical to the
+    member's own call; dX within 2e-3 (one stacked GEMM) or √G·2e-3 (G accumulating GEMMs) of the
+    fp64 sum of the members' dX; adapter gradients within 2e-3 (bf16) / 1e-4 (fp32 masters) of
+    the per-member calls'."""
+    print(f"rank 128, 131 segments, widths {widths}, split={split}", flush=True)
+    g = torch.Generator().manual_seed(74)
+    holder = nn.Module()
+    mods = []
+    for i, N in enumerate(widths):
+        base = nn.Linear(512, N)
+        with torch.no_grad():
+            base.weight.copy_(torch.randn(N, 512, generator=g) / 512 ** 0.5)
+        m = pkg.MultiLoRALinear(base, ranks=[128, 128], alphas=[64, 256])
+        with torch.no_grad():
+            for b in m.lora_b:
+                b.copy_(torch.randn(b.shape, generator=g) * 0.03)
+        m = m.to(dev, torch.bfloat16)
+        if split:
+            for p in (*m.lora_a, *m.lora_b):
+                p.data = p.data.float()
+        holder.add_module(f"m{i}", m)
+        mods.append(m)
+    lengths = tuple(32 + (7 * i) % 50 for i in range(131))
+    ids = tuple(-1 if i % 5 == 4 else i % 2 for i in range(131))
+    routing = pkg.SegmentRouting.from_lengths(lengths, ids)
+    M = sum(lengths)
+    x = torch.randn(M, 512, generator=g).to(dev, torch.bfloat16)
+    dys = [torch.randn(M, N, generator=g).to(dev, torch.bfloat16) for N in widths]
+    params = [p for m in mods for p in (*m.lora_a, *m.lora_b)]
+
+    def run(fused):
+        for p in params:
+            p.grad = None
+        if fused:
+            pkg.fuse_shared_inputs(holder, [["m0", "m1", "m2"]])
+        xi = x.clone().requires_grad_(True)
+        ys = [m(xi, routing) for m in mods]
+        torch.autograd.backward(ys, dys)
+        if fused:
+            assert mods[0].shared_input.launches == 1
+            pkg.release_shared_inputs(holder)
+        return [y.detach() for y in ys], xi.grad, [p.grad.clone() for p in params]
+
+    ys_f, dx_f, gr_f = run(True)
+    ys_s, dx_s, gr_s = run(False)
+    for a, b in zip(ys_f, ys_s):
+        assert torch.equal(a, b)
+    with torch.no_grad():
+        dx_ref = torch.zeros(M, 512, dtype=torch.float64, device=dev)
+        for m, dy in zip(mods, dys):
+            dyd = dy.double()
+            dx_ref += dyd @ m.base.weight.double()
+            for (r0, r1), a in zip(zip(routing.seg_offsets, routing.seg_offsets[1:]), routing.adapter_ids):
+                if a >= 0 and r1 > r0:
+                    dx_ref[r0:r1] += m.scales[a] * (dyd[r0:r1] @ m.lora_b[a].double()) @ m.lora_a[a].double()
+    # one rounding of the sum in the stacked dX GEMM; one per accumulating call (G of them) when
+    # the members' widths differ
+    tol = 2e-3 if len(set(widths)) == 1 else 2e-3 * len(widths) ** 0.5
+    assert float((dx_f.double() - dx_ref).norm() / dx_ref.norm()) <= tol
+    _grads_close(gr_f, gr_s, 1e-4 if split else 2e-3)
+    assert all(p.dtype == (torch.float32 if split else torch.bfloat16) for p in gr_f)
