@@ -390,25 +390,26 @@ def _stacked_grads(ctx, x, dys, b_hi, b_lo, h_frags, dx_fn, a0: int, b0: int):
     any_a = any(map(any, need_a))
     slices = _stack_slices(G, R)
     g_rows, g_frags = None, [None] * len(slices)
-    if need_x or any_a:
-        g_rows = torch.empty((x.shape[0], G * R), dtype=torch.bfloat16, device=x.device)
-        for s, (g0, g1) in enumerate(slices):
-            jt = (g1 - g0) * R // 16
-            g_frags[s] = kernels.alloc_frags(routing, jt, x.device) if any_a else None
-            for g in range(g0, g1):
-                kernels.shrink(dys[g], b_hi[g], 1, ctx.scales, routing, want_frag=any_a, width=(g1 - g0) * R,
-                               h_out=g_rows[:, g * R:(g + 1) * R], frag_out=g_frags[s], frag_jt=jt,
-                               frag_t0=(g - g0) * R // 16, ops_lo=b_lo[g])
-    dx = dx_fn(g_rows) if need_x else None
     dA = [[None] * n for _ in range(G)]
     dB = [[None] * n for _ in range(G)]
+    if need_x or any_a:
+        g_rows = torch.empty((x.shape[0], G * R), dtype=torch.bfloat16, device=x.device)
     for s, (g0, g1) in enumerate(slices):
         w = (g1 - g0) * R
+        if need_x or any_a:
+            g_frags[s] = kernels.alloc_frags(routing, w // 16, x.device) if any_a else None
         for g in range(g0, g1):
-            if any(need_b[g]):
+            if need_x or any_a:
+                kernels.shrink(dys[g], b_hi[g], 1, ctx.scales, routing, want_frag=any_a, width=w,
+                               h_out=g_rows[:, g * R:(g + 1) * R], frag_out=g_frags[s], frag_jt=w // 16,
+                               frag_t0=(g - g0) * R // 16, ops_lo=b_lo[g])
+            if any(need_b[g]):  # right after the shrink of dY_g, while dY_g is still cached
                 outs = kernels.seg_outer(dys[g], h_frags[s], w, [R] * n, routing, 0, ctx.b_dtypes[g],
                                          frag_jt=w // 16, frag_t0=(g - g0) * R // 16)
                 dB[g] = [o if need_b[g][i] else None for i, o in enumerate(outs)]
+    dx = dx_fn(g_rows) if need_x else None
+    for s, (g0, g1) in enumerate(slices):
+        w = (g1 - g0) * R
         if any(any(need_a[g]) for g in range(g0, g1)):
             outs = kernels.seg_outer(x, g_frags[s], w, [w] * n, routing, 1, [torch.float32] * n)
             for g in range(g0, g1):
