@@ -154,3 +154,45 @@ def test_stacked_bases_follow_replaced_biases_and_free_with_any_member(pkg):
     del bs[2]
     gc.collect()
     assert not (set(L._STACKED) & keys_before), "freeing one member bias must drop the cached stack"
+
+
+def test_more_fuse_time_refusals(pkg):
+    """An e4m3 base, a PEFT adapter above the kernels' rank limit, and ranks that are not one
+    multiple of 16 are refused when the group is made."""
+    from peft_layout import PeftLoraLinear
+    holder = nn.Module()
+    holder.q = pkg.MultiLoRALinear(nn.Linear(256, 256), ranks=[16], alphas=[16])
+    holder.k = pkg.MultiLoRALinear(nn.Linear(256, 256), ranks=[16], alphas=[16])
+    holder.k.base_wq = torch.zeros(1)  # stands in for a quantised base
+    with pytest.raises(ValueError, match="e4m3 bases are not stacked"):
+        pkg.fuse_shared_inputs(holder, [["q", "k"]])
+    peft = nn.Module()
+    for name in ("q", "k"):
+        setattr(peft, name, PeftLoraLinear(nn.Linear(512, 512), {"default": (320, 320)}))
+    pkg.install_peft_multi_lora(peft)
+    with pytest.raises(ValueError, match="above the kernels' 256"):
+        pkg.fuse_shared_inputs(peft, [["q", "k"]])
+    mixed = nn.Module()
+    mixed.q = pkg.MultiLoRALinear(nn.Linear(256, 256), ranks=[16], alphas=[16])
+    mixed.k = pkg.MultiLoRALinear(nn.Linear(256, 256), ranks=[32], alphas=[32])
+    with pytest.raises(ValueError, match="one LoRA rank"):
+        pkg.fuse_shared_inputs(mixed, [["q", "k"]])
+
+
+def test_call_time_plans_that_do_not_stack(pkg):
+    """At call time the members stack only with one routing, adapter count, scales and rank (a
+    multiple of 16); otherwise each runs its own call. Checked on the plans alone (no kernel)."""
+    from dmd_system_amd.shared_input import SharedInputGroup
+    R = pkg.SegmentRouting
+    a16, b16 = torch.zeros(16, 8), torch.zeros(8, 16)
+    a32 = torch.zeros(32, 8)
+    one = R.single(10, 0)
+    ok = [([a16], [b16], [1.0], one), ([a16], [b16], [1.0], R.single(10, 0))]
+    assert SharedInputGroup._plans_stack(ok)
+    assert not SharedInputGroup._plans_stack([ok[0], ([a16], [b16], [2.0], one)])           # scales
+    assert not SharedInputGroup._plans_stack([ok[0], ([a16], [b16], [1.0], R.single(10, -1))])  # routing
+    assert not SharedInputGroup._plans_stack([ok[0], ([a32], [b16], [1.0], one)])           # rank
+    assert not SharedInputGroup._plans_stack([ok[0], ([], [], [], one)])                    # a disabled member
+    assert not SharedInputGroup._plans_stack([([], [], [], one), ([], [], [], one)])        # no adapter at all
+    a8 = torch.zeros(8, 8)
+    assert not SharedInputGroup._plans_stack([([a8], [b16], [1.0], one), ([a8], [b16], [1.0], one)])  # rank 8
