@@ -670,6 +670,9 @@ def main():
                 "traffic": recorded_traffic() if cfg.name == "wan13b" else None,
                 "avg_launch_us": round(gem["time"] / gem["launches"] * 1e6, 2),
                 "flops_per_launch": gem["flops"] // gem["launches"]}
+    # the LoRA-side kernels of one step (one launch of each family per linear), from the same
+    # per-kernel medians (cold caches; inside a step some operands are still cached)
+    lora_side_ms = sum(fam[k]["time"] for k in ("shrink_x", "shrink_dy", "seg_outer_dB", "seg_outer_dA")) * 1e3
     lora = {}
     for k in ("shrink_x", "shrink_dy", "seg_outer_dB", "seg_outer_dA") + (("quantize_x", "quantize_dy") if fp8 else ()):
         v = fam[k]
@@ -746,6 +749,7 @@ def main():
         "roofline": roofline,
         "cpu_baseline": cpu,
         "lora_hbm": lora,
+        "lora_side_ms_per_step": round(lora_side_ms, 3),
         "kernels": kern,
         "vendor_gemm_tflops": vendor,
         **({"vendor_fp8_gemm_tflops": vendor_fp8} if fp8 else {}),
