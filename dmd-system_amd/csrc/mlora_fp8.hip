@@ -103,11 +103,18 @@ __global__ __launch_bounds__(256) void quantize_rows_kernel(const QuantArgs a) {
 
 // Row held in registers: NI 16-byte chunks per lane (K <= 512 * NI). With
 // column factors (CS) the products are formed once, in the absmax pass, and
-// kept as fp32 for the conversion pass.
+// kept as fp32 for the conversion pass; the factors are first copied to LDS by
+// the whole workgroup (its four rows share them), so the absmax pass reads
+// them at LDS latency instead of waiting on a global load per chunk.
 template <int NI, bool CS>
 __global__ __launch_bounds__(256) void quantize_rows_reg_kernel(const QuantArgs a) {
   const int lane = threadIdx.x & 63;
   const int m = blockIdx.x * 4 + wave_id();
+  __shared__ f32x4 cs_lds[CS ? 128 * NI : 1];  // K <= 512 * NI factors
+  if constexpr (CS) {
+    for (int i = (int)threadIdx.x; i < a.K / 4; i += 256) cs_lds[i] = *(const MLORA_GLOBAL f32x4 *)(a.cs + 4 * i);
+    __syncthreads();  // before any wave leaves: every wave of the workgroup reaches it
+  }
   if (m >= a.M) return;
   const __amdgpu_buffer_rsrc_t rx = make_rsrc(a.x + (int64_t)m * a.ldx, (int64_t)a.K * 2);
   u32x4 v[NI];
@@ -118,7 +125,18 @@ __global__ __launch_bounds__(256) void quantize_rows_reg_kernel(const QuantArgs 
 #pragma unroll
   for (int it = 0; it < NI; ++it) {
     float t[8];
-    chunk_values<CS>(v[it], a, 8 * lane + 512 * it, t);
+    const int k = 8 * lane + 512 * it;
+    chunk_values<false>(v[it], a, k, t);
+    if constexpr (CS) {
+      if (k < a.K) {  // K is a multiple of 8: a chunk is all in range or all past K
+        const f32x4 c0 = cs_lds[k / 4], c1 = cs_lds[k / 4 + 1];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          t[e] *= c0[e];
+          t[4 + e] *= c1[e];
+        }
+      }
+    }
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
       amax = fmaxf(amax, fabsf(t[e]));
