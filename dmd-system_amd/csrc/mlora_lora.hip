@@ -74,9 +74,9 @@ struct ShrinkCfg {
   // used for ranks <= 32); larger ranks as many stages as 160 KB allows. 8 waves
   // (256 rows, used for ranks 33-64): 4 stages of 40 KB, one workgroup per CU,
   // 96 KB of P in flight instead of 64 KB (3-7% faster at rank 64; slower at 128).
-  // 9 waves (288 rows, ranks <= 64): the row count that puts one tile on each CU when 256-row
+  // 9 waves (288 rows, ranks <= 128): the row count that puts one tile on each CU when 256-row
   // tiles would leave a few for a second round (65520 rows in four segments: 259 tiles of
-  // 256 rows, 230 of 288); 3 stages of 40-44 KB.
+  // 256 rows, 230 of 288); 3 stages of 40-52 KB.
   // SPLIT: as many stages (at most 3) as fit.
   static constexpr int STAGES_PLAIN = NW == 8 ? 4 : NW == 9 ? 3 : RT <= 2 ? 3 : RT <= 4 ? 4 : 3;
   static constexpr int STAGES_FIT = 163840 / STAGE_BYTES;
@@ -823,23 +823,26 @@ extern "C" int mlora_shrink(const void *p, int64_t ldp, int64_t M, int64_t K, co
   }
   // ranks 33-64: 256-row workgroups of 8 waves (more of P in flight per CU)
   if (!plan_tiles(a, rt == 2 ? ShrinkCfg<2, 8>::BMS : 128, n)) return MLORA_OK;
-  if (!split && rt <= 2) {
+  if (!split && rt <= 4) {
     // 288-row workgroups of 9 waves when they give every CU at most one tile and the default
     // tiles would not: cost = rounds x rows a CU takes per round (256 CUs; the 4-wave tiles of
     // ranks <= 32 run two workgroups per CU). At ranks <= 64 a tile's time hardly depends on its
     // rows (its k-steps stream at a latency-bound pace): 65520 rows in four segments take 259
     // tiles of 256 rows (two rounds) or 230 of 288 (one), and the shrink 47 instead of 67 us at
-    // K = 1536. (256-row tiles for ranks 65-128, in two rounds instead of three of 128 rows,
-    // measured 3-12% slower at config 4's shapes: there the rows do set the time.)
+    // K = 1536. At ranks 65-128 the rows do set a tile's time (256-row tiles of 8 waves, in two
+    // rounds instead of three of 128 rows, measured 3-12% slower at 16 x 4608 rows), so the
+    // 288-row tiles are taken only where they save rows per CU: 16 x 4608 rows are 576 tiles of
+    // 128 rows (three rounds, 384 rows per CU) or 256 of 288 (one round, 288 rows per CU).
     constexpr int64_t kCUs = 256;
-    const int64_t wg = rt <= 1 ? 2 : 1, rows = rt <= 1 ? 128 : 256;
+    const int64_t wg = rt <= 1 ? 2 : 1, rows = rt == 2 ? 256 : 128;
     const int64_t cost_default = (n + kCUs * wg - 1) / (kCUs * wg) * rows * wg;
     int64_t n9 = 0;
     plan_tiles(a, ShrinkCfg<2, 9>::BMS, n9);
     const int64_t cost9 = (n9 + kCUs - 1) / kCUs * ShrinkCfg<2, 9>::BMS;
     if (cost9 < cost_default) {
       if (rt <= 1) launch_shrink_rt<1, 9>(a, (int)n9, s);
-      else launch_shrink_rt<2, 9>(a, (int)n9, s);
+      else if (rt == 2) launch_shrink_rt<2, 9>(a, (int)n9, s);
+      else launch_shrink_rt<4, 9>(a, (int)n9, s);
       return launch_status();
     }
     plan_tiles(a, rows, n);

@@ -146,23 +146,28 @@ def test_random_routings_vs_oracle(pkg, dev, segs, rank_idx, transposed):
 _CFG5_SEGS = (16997, 24338, 8047, 16138)  # config 5's segments: 259 tiles of 256 rows, 230 of 288
 
 
-@pytest.mark.parametrize("rank,lengths,ids,layout", [
-    (64, (20001, 333, 16000, 4097, 30000), (0, -1, 1, 2, 0), 0),   # 256-row tiles
-    (128, (9000, 77, 31000, 641), (1, 0, -1, 1), 0),                # 128-row tiles
+@pytest.mark.parametrize("rank,lengths,ids,layout,K", [
+    (64, (20001, 333, 16000, 4097, 30000), (0, -1, 1, 2, 0), 0, 96),   # 256-row tiles
+    (128, (9000, 77, 31000, 641), (1, 0, -1, 1), 0, 96),                # 128-row tiles
     # 288-row tiles of 9 waves in the four-segment call, the default tiles in each segment's own
-    (64, _CFG5_SEGS, (0, 1, 2, 0), 0), (64, _CFG5_SEGS, (0, 1, 2, 0), 1),
-    (32, _CFG5_SEGS, (2, 0, 1, 1), 0), (32, _CFG5_SEGS, (2, 0, 1, 1), 1),
-    # config 4's sixteen 4608-row samples at rank 128 (three rounds of 128-row tiles)
-    (128, (4608,) * 16, (0, 1, 2, 0) * 4, 0), (128, (4608,) * 16, (0, 1, 2, 0) * 4, 1),
+    (64, _CFG5_SEGS, (0, 1, 2, 0), 0, 96), (64, _CFG5_SEGS, (0, 1, 2, 0), 1, 96),
+    (32, _CFG5_SEGS, (2, 0, 1, 1), 0, 96), (32, _CFG5_SEGS, (2, 0, 1, 1), 1, 96),
+    # config 4's sixteen 4608-row samples at rank 128: one round of 288-row tiles of 9 waves (256
+    # tiles) instead of three of 128 rows; 4608 rows alone take the 128-row tiles. K = 1000 runs
+    # 16 k-tiles (the three-stage ring wraps five times and ends inside a period; the last
+    # k-tile is partly past K)
+    (128, (4608,) * 16, (0, 1, 2, 0) * 4, 0, 96), (128, (4608,) * 16, (0, 1, 2, 0) * 4, 1, 96),
+    (128, (4608,) * 16, (2, 1, 0, 1) * 4, 0, 1000), (128, (4608,) * 16, (2, 1, 0, 1) * 4, 1, 1000),
 ], ids=["rank64", "rank128", "rank64_9waves", "rank64_9waves_layout1", "rank32_9waves", "rank32_9waves_layout1",
-        "rank128_16segments", "rank128_16segments_layout1"])
-def test_shrink_segments_match_single_segment_calls(pkg, dev, rank, lengths, ids, layout):
+        "rank128_16segments", "rank128_16segments_layout1", "rank128_16segments_k1000",
+        "rank128_16segments_k1000_layout1"])
+def test_shrink_segments_match_single_segment_calls(pkg, dev, rank, lengths, ids, layout, K):
     """Ragged segments (tiles ending inside a segment's last 32 rows, a base-only segment between
     adapter segments, more tiles than the GPU runs at once): each segment's h rows and fragments
     equal those of a call on that segment alone, bit for bit, and h matches the fp64 product.
     Layout 1 takes the operand as [K, r] (lora_b of the backward shrink)."""
     from dmd_system_amd import kernels
-    K, M = 96, sum(lengths)
+    M = sum(lengths)
     g = torch.Generator().manual_seed(21)
     x = torch.randn(M, K, generator=g).to(torch.bfloat16)
     As = [((torch.rand(rank, K, generator=g) * 2 - 1) / math.sqrt(K)).to(torch.bfloat16) for _ in range(3)]
