@@ -43,6 +43,10 @@ struct GemmArgs {
   int32_t accumulate;
   int32_t tiles_m, tiles_n;
   int32_t group_m;  // row tiles per group of the tile order (set by launch_gemm)
+  // >= 0: this launch runs 128x128 quarters of the 256x256 tiles tail_base, tail_base + 1, ... of
+  // the tile order of a tiles_m x tiles_n grid of 256x256 tiles (four workgroups per tile);
+  // -1: one workgroup per tile of its own size (set by launch_gemm)
+  int32_t tail_base;
   AdapterTable ext;  // NT: B_a [Ncols, r]; NN: A_a [r, Ncols]
   SegTable seg;
   // Gated residual epilogue (gemm_kernel<C, true>): the stored value is
@@ -649,7 +653,7 @@ __device__ __forceinline__ void contract_tile(f32x16 (&acc)[C::TM][C::TN], const
 // are dealt round-robin over the 8 XCDs), then groups of group_m row-tiles
 // walked column by column so concurrently running tiles share P rows and Q
 // columns in L2.
-template <class C>
+template <int BM, int BN>
 __device__ __forceinline__ void tile_origin(const GemmArgs &args, int p, int &m0, int &n0) {
   const int nblocks = args.tiles_m * args.tiles_n;
   const int id = xcd_remap(p, nblocks);
@@ -659,8 +663,8 @@ __device__ __forceinline__ void tile_origin(const GemmArgs &args, int p, int &m0
   const int gsize = min(args.tiles_m - first_m, args.group_m);
   const int tm = first_m + (id % per_group) % gsize;
   const int tn = (id % per_group) / gsize;
-  m0 = tm * C::BM;
-  n0 = tn * C::BN;
+  m0 = tm * BM;
+  n0 = tn * BN;
 }
 
 // This lane's 4 entries of a per-column vector (bf16 when BF16, else f32) at columns c .. c + 3
@@ -905,7 +909,17 @@ __global__ __launch_bounds__(C::THREADS, C::WAVES_PER_SIMD) void gemm_kernel(con
   const int wm0 = (wave / C::WN) * (C::BM / C::WM);
   const int wn0 = (wave % C::WN) * (C::BN / C::WN);
   int m0, n0;
-  tile_origin<C>(args, blockIdx.x, m0, n0);
+  if (C::BM == 128 && C::BN == 128 && args.tail_base >= 0) {
+    // quarter q of the 256x256 tile tail_base + blockIdx.x / 4; a quarter wholly past the
+    // matrix (a narrow last row or column tile) has nothing to compute or store
+    const int q = blockIdx.x % 4;
+    tile_origin<256, 256>(args, args.tail_base + (int)blockIdx.x / 4, m0, n0);
+    m0 += 128 * (q / 2);
+    n0 += 128 * (q % 2);
+    if (m0 >= args.M || n0 >= args.Ncols) return;  // uniform over the workgroup, before any barrier
+  } else {
+    tile_origin<C::BM, C::BN>(args, blockIdx.x, m0, n0);
+  }
   f32x16 acc[C::TM][C::TN];
 #pragma unroll
   for (int i = 0; i < C::TM; ++i)
@@ -938,15 +952,30 @@ using CfgNN128 = GemmCfg<128, 128, 2, 2, true>;
 // shapes, bit-equal output.
 constexpr int kGroupM = 4;
 
+// One workgroup per tile of C's size, the first `nblocks` of the tile order (all when < 0).
 template <class C, bool RESID = false, int STK = 0>
-static int launch_gemm(GemmArgs &a, hipStream_t stream) {
+static int launch_gemm(GemmArgs &a, hipStream_t stream, int64_t nblocks = -1) {
   a.tiles_m = (a.M + C::BM - 1) / C::BM;
   a.tiles_n = (a.Ncols + C::BN - 1) / C::BN;
+  a.tail_base = -1;
   if (a.group_m <= 0) a.group_m = kGroupM;
-  const int64_t nblocks = (int64_t)a.tiles_m * a.tiles_n;
+  if (nblocks < 0) nblocks = (int64_t)a.tiles_m * a.tiles_n;
   if (nblocks == 0) return MLORA_OK;
   if (nblocks > INT32_MAX) return MLORA_ERR_LIMIT;
   hipLaunchKernelGGL((gemm_kernel<C, RESID, STK>), dim3((unsigned)nblocks), dim3(C::THREADS), 0, stream, a);
+  return launch_status();
+}
+
+// The 256x256 tiles from `first` on, as 128x128 quarters of the Small configuration.
+template <class Small, bool RESID = false, int STK = 0>
+static int launch_tail(GemmArgs &a, hipStream_t stream, int64_t first) {
+  static_assert(Small::BM == 128 && Small::BN == 128, "quarters of 256x256 tiles");
+  a.tiles_m = (a.M + 255) / 256;
+  a.tiles_n = (a.Ncols + 255) / 256;
+  const int64_t tail = (int64_t)a.tiles_m * a.tiles_n - first;
+  a.tail_base = (int32_t)first;
+  if (a.group_m <= 0) a.group_m = kGroupM;
+  hipLaunchKernelGGL((gemm_kernel<Small, RESID, STK>), dim3((unsigned)(4 * tail)), dim3(Small::THREADS), 0, stream, a);
   return launch_status();
 }
 
@@ -954,11 +983,21 @@ static int launch_gemm(GemmArgs &a, hipStream_t stream) {
 // whenever it still gives every CU a tile; the 4-wave 128x128 tile otherwise.
 // (A persistent form whose k-tile ring runs across output tiles, and
 // 256x128 tiles with a 3-stage ring, both measured slower.)
+// A grid of 256x256 tiles a little over whole rounds of the 256 CUs (1284 tiles at 27280 x 3072:
+// five rounds and four tiles) would spend a whole tile's time on its last few tiles. Those
+// tiles (at most 128, the last of the tile order) then run in a second launch as 128x128
+// quarters, two workgroups per CU, in a quarter to a half of that time. Every output keeps
+// the same k order and MFMA sequence in both tile sizes, so the result is the same bit for bit.
 template <class Big, class Small, bool RESID = false, int STK = 0>
 static int dispatch_gemm(GemmArgs &a, hipStream_t stream) {
+  constexpr int64_t kCUs = 256, kMaxTail = 128;
   const int64_t big_tiles = (int64_t)((a.M + 255) / 256) * ((a.Ncols + 255) / 256);
-  if (big_tiles >= 256) return launch_gemm<Big, RESID, STK>(a, stream);
-  return launch_gemm<Small, RESID, STK>(a, stream);
+  if (big_tiles < kCUs) return launch_gemm<Small, RESID, STK>(a, stream);
+  const int64_t tail = big_tiles % kCUs;
+  if (tail == 0 || tail > kMaxTail) return launch_gemm<Big, RESID, STK>(a, stream);
+  const int st = launch_gemm<Big, RESID, STK>(a, stream, big_tiles - tail);
+  if (st) return st;
+  return launch_tail<Small, RESID, STK>(a, stream, big_tiles - tail);
 }
 
 static int fill_common(GemmArgs &a, int64_t M, int64_t Kc, int64_t Ncols, const void *e, int64_t lde,
