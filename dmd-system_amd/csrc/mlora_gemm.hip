@@ -944,6 +944,10 @@ using CfgF8128 = GemmCfg<128, 128, 2, 2, false, true>;
 using CfgNN256 = GemmCfg<256, 256, 4, 2, true, false, 128, 2, true, true>;
 using CfgNT128 = GemmCfg<128, 128, 2, 2, false>;
 using CfgNN128 = GemmCfg<128, 128, 2, 2, true>;
+// Quarters of a partly filled last round of 256x256 tiles (dispatch_gemm): 8 waves and four
+// stages (three k-tiles in flight), one workgroup per CU
+using CfgNT128T = GemmCfg<128, 128, 4, 2, false, false, 128, 4>;
+using CfgNN128T = GemmCfg<128, 128, 4, 2, true, false, 128, 4>;
 
 // Row tiles per group of the tile order: an XCD's 32 concurrent 256x256 tiles
 // then cover 4 row tiles x up to 8 column tiles (P, streamed from HBM, shared
@@ -966,16 +970,16 @@ static int launch_gemm(GemmArgs &a, hipStream_t stream, int64_t nblocks = -1) {
   return launch_status();
 }
 
-// The 256x256 tiles from `first` on, as 128x128 quarters of the Small configuration.
-template <class Small, bool RESID = false, int STK = 0>
+// The 256x256 tiles from `first` on, as 128x128 quarters of configuration Q.
+template <class Q, bool RESID = false, int STK = 0>
 static int launch_tail(GemmArgs &a, hipStream_t stream, int64_t first) {
-  static_assert(Small::BM == 128 && Small::BN == 128, "quarters of 256x256 tiles");
+  static_assert(Q::BM == 128 && Q::BN == 128, "quarters of 256x256 tiles");
   a.tiles_m = (a.M + 255) / 256;
   a.tiles_n = (a.Ncols + 255) / 256;
   const int64_t tail = (int64_t)a.tiles_m * a.tiles_n - first;
   a.tail_base = (int32_t)first;
   if (a.group_m <= 0) a.group_m = kGroupM;
-  hipLaunchKernelGGL((gemm_kernel<Small, RESID, STK>), dim3((unsigned)(4 * tail)), dim3(Small::THREADS), 0, stream, a);
+  hipLaunchKernelGGL((gemm_kernel<Q, RESID, STK>), dim3((unsigned)(4 * tail)), dim3(Q::THREADS), 0, stream, a);
   return launch_status();
 }
 
@@ -985,19 +989,29 @@ static int launch_tail(GemmArgs &a, hipStream_t stream, int64_t first) {
 // 256x128 tiles with a 3-stage ring, both measured slower.)
 // A grid of 256x256 tiles a little over whole rounds of the 256 CUs (1284 tiles at 27280 x 3072:
 // five rounds and four tiles) would spend a whole tile's time on its last few tiles. Those
-// tiles (at most 128, the last of the tile order) then run in a second launch as 128x128
-// quarters, two workgroups per CU, in a quarter to a half of that time. Every output keeps
-// the same k order and MFMA sequence in both tile sizes, so the result is the same bit for bit.
+// tiles (at most 64, the last of the tile order) then run in a second launch as 128x128
+// quarters of 8 waves with four stages, one round of at most 256 workgroups: config 3's
+// 27280 x 3072 forward and NN dX took 10% and 7% less time per launch, its step 2.6% less.
+// (The 4-wave two-stage 128x128 tile was no faster than no split. Tails of 104 and 128 tiles,
+// two rounds of quarters, were 2-6% faster per launch in isolation but left config 4's step
+// 0.6% slower.) Every output keeps the same k order and MFMA sequence in both tile sizes, so
+// the result is the same bit for bit. The e4m3 GEMM keeps its tail (its quarters measured 1%
+// slower).
 template <class Big, class Small, bool RESID = false, int STK = 0>
 static int dispatch_gemm(GemmArgs &a, hipStream_t stream) {
-  constexpr int64_t kCUs = 256, kMaxTail = 128;
+  constexpr int64_t kCUs = 256, kMaxTail = 64;
   const int64_t big_tiles = (int64_t)((a.M + 255) / 256) * ((a.Ncols + 255) / 256);
   if (big_tiles < kCUs) return launch_gemm<Small, RESID, STK>(a, stream);
   const int64_t tail = big_tiles % kCUs;
   if (tail == 0 || tail > kMaxTail) return launch_gemm<Big, RESID, STK>(a, stream);
-  const int st = launch_gemm<Big, RESID, STK>(a, stream, big_tiles - tail);
-  if (st) return st;
-  return launch_tail<Small, RESID, STK>(a, stream, big_tiles - tail);
+  using Tail = std::conditional_t<Big::F8, void, std::conditional_t<Big::NN, CfgNN128T, CfgNT128T>>;
+  if constexpr (std::is_void_v<Tail>) {
+    return launch_gemm<Big, RESID, STK>(a, stream);
+  } else {
+    const int st = launch_gemm<Big, RESID, STK>(a, stream, big_tiles - tail);
+    if (st) return st;
+    return launch_tail<Tail, RESID, STK>(a, stream, big_tiles - tail);
+  }
 }
 
 static int fill_common(GemmArgs &a, int64_t M, int64_t Kc, int64_t Ncols, const void *e, int64_t lde,

@@ -1,13 +1,14 @@
 """Grids of 256x256 output tiles a little over whole rounds of the 256 CUs.
 
 Such a grid (1284 tiles at 27280 x 3072: five rounds and four tiles) runs its whole rounds as
-256x256 tiles and its last few tiles (at most 128) as 128x128 quarters in a second launch. Every
-output keeps its k order and MFMA sequence in both tile sizes, so the GEMMs must give the same
-bits as calls on row blocks of 1024 rows (fewer than 256 tiles: 128x128 tiles throughout), and
-the fp64 oracle's result within the bf16 tolerance. Covered: the forward GEMM with bias and
-three rank-128 segments (config 3's routing), the NN dX, the e4m3 forward, a tail of 104 tiles
-(27280 x 14336), and quarters wholly past the matrix (a last row tile of 100 rows and a last
-column tile of 128 columns).
+256x256 tiles and its last few tiles (at most 64) as 128x128 quarters (8 waves) in a second
+launch. Every output keeps its k order and MFMA sequence in all tile sizes, so the GEMMs must
+give the same bits as calls on row blocks of 1024 rows (fewer than 256 tiles: 4-wave 128x128
+tiles throughout), and the fp64 oracle's result within the bf16 tolerance. Covered: the forward
+GEMM with bias and three rank-128 segments (config 3's routing), the NN dX, a tail of 64 tiles
+(5000 x 4096: 256 quarters), one of 104 tiles (27280 x 14336, run as 256x256 tiles), quarters
+wholly past the matrix (a last row tile of 100 rows and a last column tile of 128 columns), and
+the e4m3 forward (which runs its tail as 256x256 tiles).
 """
 import math
 
@@ -54,9 +55,10 @@ def _row_blocks(M, rows=1024):
 
 @pytest.mark.parametrize("M,K,N,lengths,ids", [
     (27280, 320, 3072, CFG3_SEGS, (0, 1, 2)),            # 1284 tiles: a tail of 4
-    (27280, 192, 14336, CFG3_SEGS, (2, -1, 0)),          # 5992 tiles: a tail of 104
+    (5000, 256, 4096, (2100, 2900), (0, 2)),             # 20 x 16 tiles: a tail of 64
+    (27280, 192, 14336, CFG3_SEGS, (2, -1, 0)),          # 5992 tiles: a tail of 104 (not split)
     (4964, 200, 3200, (2000, 2964), (1, 0)),              # 20 x 13 tiles: quarters past M and N
-], ids=["tail4", "tail104", "narrow_edges"])
+], ids=["tail4", "tail64", "tail104", "narrow_edges"])
 def test_forward_tail_equals_row_blocks(pkg, dev, M, K, N, lengths, ids):
     from dmd_system_amd import kernels
     print(f"tail forward M={M} K={K} N={N}", flush=True)
