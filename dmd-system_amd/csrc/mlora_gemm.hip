@@ -944,10 +944,11 @@ using CfgF8128 = GemmCfg<128, 128, 2, 2, false, true>;
 using CfgNN256 = GemmCfg<256, 256, 4, 2, true, false, 128, 2, true, true>;
 using CfgNT128 = GemmCfg<128, 128, 2, 2, false>;
 using CfgNN128 = GemmCfg<128, 128, 2, 2, true>;
-// Quarters of a partly filled last round of 256x256 tiles (dispatch_gemm): 8 waves and four
-// stages (three k-tiles in flight), one workgroup per CU
-using CfgNT128T = GemmCfg<128, 128, 4, 2, false, false, 128, 4>;
-using CfgNN128T = GemmCfg<128, 128, 4, 2, true, false, 128, 4>;
+// 128x128 tiles of 8 waves (32x64 each) with three stages (two k-tiles in flight), one workgroup
+// per CU: grids of at most 256 such tiles, and the quarters of a partly filled last round of
+// 256x256 tiles (dispatch_gemm)
+using CfgNT128W = GemmCfg<128, 128, 4, 2, false, false, 128, 3>;
+using CfgNN128W = GemmCfg<128, 128, 4, 2, true, false, 128, 3>;
 
 // Row tiles per group of the tile order: an XCD's 32 concurrent 256x256 tiles
 // then cover 4 row tiles x up to 8 column tiles (P, streamed from HBM, shared
@@ -983,34 +984,44 @@ static int launch_tail(GemmArgs &a, hipStream_t stream, int64_t first) {
   return launch_status();
 }
 
-// Tile choice (measured on MI355X at the Wan shapes): the 8-wave 256x256 tile
-// whenever it still gives every CU a tile; the 4-wave 128x128 tile otherwise.
-// (A persistent form whose k-tile ring runs across output tiles, and
-// 256x128 tiles with a 3-stage ring, both measured slower.)
+// Tile choice (measured on MI355X):
+// * At least 256 tiles of 256x256: the 8-wave 256x256 tile (the persistent form whose k-tile ring
+//   runs across output tiles, and 256x128 tiles with a 3-stage ring, both measured slower).
+// * Fewer, and at most 256 tiles of 128x128: one 8-wave 128x128 workgroup per CU with three
+//   stages (CfgNT128W / CfgNN128W), 15-35% faster than the 4-wave two-stage tile, two per CU, at
+//   48-192 tiles (512-2048 rows, K 1536-8960); with more tiles (two rounds or more of one
+//   workgroup per CU) it measured 2-32% slower (7% faster only for a forward at K = 3072).
+// * Otherwise the 4-wave two-stage 128x128 tile, two workgroups per CU.
 // A grid of 256x256 tiles a little over whole rounds of the 256 CUs (1284 tiles at 27280 x 3072:
 // five rounds and four tiles) would spend a whole tile's time on its last few tiles. Those
 // tiles (at most 64, the last of the tile order) then run in a second launch as 128x128
-// quarters of 8 waves with four stages, one round of at most 256 workgroups: config 3's
-// 27280 x 3072 forward and NN dX took 10% and 7% less time per launch, its step 2.6% less.
+// quarters of the 8-wave configuration, one round of at most 256 workgroups: config 3's
+// 27280 x 3072 forward and NN dX took 10% and 7% less time per launch, its step 2.9% less.
 // (The 4-wave two-stage 128x128 tile was no faster than no split. Tails of 104 and 128 tiles,
 // two rounds of quarters, were 2-6% faster per launch in isolation but left config 4's step
-// 0.6% slower.) Every output keeps the same k order and MFMA sequence in both tile sizes, so
-// the result is the same bit for bit. The e4m3 GEMM keeps its tail (its quarters measured 1%
-// slower).
+// 0.6% slower.) Every output keeps the same k order and MFMA sequence in all tile sizes, so
+// the result is the same bit for bit. The e4m3 GEMM keeps the 4-wave 128x128 tile for small
+// grids and its tail as 256x256 tiles (its 8-wave quarters measured 1% slower).
 template <class Big, class Small, bool RESID = false, int STK = 0>
 static int dispatch_gemm(GemmArgs &a, hipStream_t stream) {
   constexpr int64_t kCUs = 256, kMaxTail = 64;
+  using Wide = std::conditional_t<Big::F8, void, std::conditional_t<Big::NN, CfgNN128W, CfgNT128W>>;
   const int64_t big_tiles = (int64_t)((a.M + 255) / 256) * ((a.Ncols + 255) / 256);
-  if (big_tiles < kCUs) return launch_gemm<Small, RESID, STK>(a, stream);
+  if (big_tiles < kCUs) {
+    if constexpr (!std::is_void_v<Wide>) {
+      const int64_t tiles = (int64_t)((a.M + 127) / 128) * ((a.Ncols + 127) / 128);
+      if (tiles <= kCUs) return launch_gemm<Wide, RESID, STK>(a, stream);
+    }
+    return launch_gemm<Small, RESID, STK>(a, stream);
+  }
   const int64_t tail = big_tiles % kCUs;
-  if (tail == 0 || tail > kMaxTail) return launch_gemm<Big, RESID, STK>(a, stream);
-  using Tail = std::conditional_t<Big::F8, void, std::conditional_t<Big::NN, CfgNN128T, CfgNT128T>>;
-  if constexpr (std::is_void_v<Tail>) {
+  if constexpr (std::is_void_v<Wide>) {
     return launch_gemm<Big, RESID, STK>(a, stream);
   } else {
+    if (tail == 0 || tail > kMaxTail) return launch_gemm<Big, RESID, STK>(a, stream);
     const int st = launch_gemm<Big, RESID, STK>(a, stream, big_tiles - tail);
     if (st) return st;
-    return launch_tail<Tail, RESID, STK>(a, stream, big_tiles - tail);
+    return launch_tail<Wide, RESID, STK>(a, stream, big_tiles - tail);
   }
 }
 

@@ -3,8 +3,8 @@
 Such a grid (1284 tiles at 27280 x 3072: five rounds and four tiles) runs its whole rounds as
 256x256 tiles and its last few tiles (at most 64) as 128x128 quarters (8 waves) in a second
 launch. Every output keeps its k order and MFMA sequence in all tile sizes, so the GEMMs must
-give the same bits as calls on row blocks of 1024 rows (fewer than 256 tiles: 4-wave 128x128
-tiles throughout), and the fp64 oracle's result within the bf16 tolerance. Covered: the forward
+give the same bits as calls on row blocks of 1024 rows (fewer than 256 tiles: 128x128 tiles
+throughout), and the fp64 oracle's result within the bf16 tolerance. Covered: the forward
 GEMM with bias and three rank-128 segments (config 3's routing), the NN dX, a tail of 64 tiles
 (5000 x 4096: 256 quarters), one of 104 tiles (27280 x 14336, run as 256x256 tiles), quarters
 wholly past the matrix (a last row tile of 100 rows and a last column tile of 128 columns), and
