@@ -7,8 +7,9 @@ give the same bits as calls on row blocks of 1024 rows (fewer than 256 tiles: 12
 throughout), and the fp64 oracle's result within the bf16 tolerance. Covered: the forward
 GEMM with bias and three rank-128 segments (config 3's routing), the NN dX, a tail of 64 tiles
 (5000 x 4096: 256 quarters), one of 104 tiles (27280 x 14336, run as 256x256 tiles), quarters
-wholly past the matrix (a last row tile of 100 rows and a last column tile of 128 columns), and
-the e4m3 forward (which runs its tail as 256x256 tiles).
+wholly past the matrix (a last row tile of 100 rows and a last column tile of 128 columns), the
+stacked forward and dX of three linears that read one input, the gated-residual epilogue on bf16
+and float32 streams, and the e4m3 forward (which runs its tail as 256x256 tiles).
 """
 import math
 
@@ -114,5 +115,68 @@ def test_fp8_forward_tail_equals_row_blocks(pkg, dev):
     torch.cuda.synchronize()
     for r0, r1 in _row_blocks(M):
         yb = kernels.gemm_fwd_fp8(xq[r0:r1], xs[r0:r1], wq, ws, b, h[r0:r1], bs, _sub_routing(pkg, routing, r0, r1))
+        torch.cuda.synchronize()
+        assert torch.equal(y[r0:r1], yb), (r0, r1)
+
+
+def test_stacked_forward_tail_equals_row_blocks(pkg, dev):
+    """Three linears that read one input as one GEMM (27280 x 3 x 3072: 3852 tiles, a tail of 12):
+    each quarter stores into its own linear's output."""
+    from dmd_system_amd import kernels
+    M, K, N, G, R = 27280, 256, 3072, 3, 128
+    print(f"tail stacked forward M={M} K={K} N={G}x{N}", flush=True)
+    routing = pkg.SegmentRouting.from_lengths(CFG3_SEGS, (0, 1, 2))
+    g = torch.Generator().manual_seed(11)
+    x = torch.randn(M, K, generator=g).to(torch.bfloat16).to(dev)
+    w = (torch.randn(G * N, K, generator=g) / math.sqrt(K)).to(torch.bfloat16).to(dev)
+    b = (torch.randn(G * N, generator=g) / math.sqrt(K)).to(torch.bfloat16).to(dev)
+    h = (torch.randn(M, G * R, generator=g) * 0.3).to(torch.bfloat16).to(dev)
+    bs = [(torch.randn(G * N, R, generator=g) * 0.05).to(torch.bfloat16).to(dev) for _ in range(3)]
+    ys = kernels.gemm_fwd_stacked(x, w, b, h, bs, routing, N, R)
+    torch.cuda.synchronize()
+    for r0, r1 in _row_blocks(M):
+        yb = kernels.gemm_fwd_stacked(x[r0:r1], w, b, h[r0:r1], bs, _sub_routing(pkg, routing, r0, r1), N, R)
+        torch.cuda.synchronize()
+        for y, y1 in zip(ys, yb):
+            assert torch.equal(y[r0:r1], y1), (r0, r1)
+
+
+def test_stacked_dx_tail_equals_row_blocks(pkg, dev):
+    """dX of three stacked linears (27280 x 3072 output: 1284 tiles, a tail of 4)."""
+    from dmd_system_amd import kernels
+    M, K, N, G, R = 27280, 3072, 256, 3, 64
+    print(f"tail stacked dX M={M} K={K} N={G}x{N}", flush=True)
+    routing = pkg.SegmentRouting.from_lengths(CFG3_SEGS, (2, 0, 1))
+    g = torch.Generator().manual_seed(12)
+    dys = [torch.randn(M, N, generator=g).to(torch.bfloat16).to(dev) for _ in range(G)]
+    w_t = (torch.randn(K, G * N, generator=g) / math.sqrt(G * N)).to(torch.bfloat16).to(dev)
+    gr = (torch.randn(M, G * R, generator=g) * 0.3).to(torch.bfloat16).to(dev)
+    a_t = [((torch.rand(K, G * R, generator=g) * 2 - 1) / math.sqrt(K)).to(torch.bfloat16).to(dev) for _ in range(3)]
+    dx = kernels.gemm_dx_stacked(dys, w_t, gr, a_t, routing)
+    torch.cuda.synchronize()
+    for r0, r1 in _row_blocks(M):
+        db = kernels.gemm_dx_stacked([d[r0:r1] for d in dys], w_t, gr[r0:r1], a_t, _sub_routing(pkg, routing, r0, r1))
+        torch.cuda.synchronize()
+        assert torch.equal(dx[r0:r1], db), (r0, r1)
+
+
+@pytest.mark.parametrize("stream_dtype", [torch.bfloat16, torch.float32], ids=["bf16_stream", "f32_stream"])
+def test_gated_forward_tail_equals_row_blocks(pkg, dev, stream_dtype):
+    """The gated-residual epilogue (16 gate rows of 1705 rows) on a grid with a tail of 4."""
+    from dmd_system_amd import kernels
+    M, K, N = 27280, 256, 3072
+    print(f"tail gated forward M={M} K={K} N={N} {stream_dtype}", flush=True)
+    routing = pkg.SegmentRouting.from_lengths(CFG3_SEGS, (1, 2, 0))
+    x, w, b, h, bs = _operands(dev, M, K, N, 128, seed=13)
+    g = torch.Generator().manual_seed(14)
+    res = torch.randn(M, N, generator=g).to(stream_dtype).to(dev)
+    gate = torch.randn(16, N, generator=g).to(dev)
+    per = M // 16
+    y = kernels.gemm_fwd_gated(x, w, b, h, bs, routing, res, gate)
+    torch.cuda.synchronize()
+    for r0 in range(0, M, 2 * per):  # row blocks on gate-row boundaries
+        r1 = min(r0 + 2 * per, M)
+        yb = kernels.gemm_fwd_gated(x[r0:r1], w, b, h[r0:r1], bs, _sub_routing(pkg, routing, r0, r1), res[r0:r1],
+                                    gate[r0 // per:r1 // per].contiguous())
         torch.cuda.synchronize()
         assert torch.equal(y[r0:r1], yb), (r0, r1)
