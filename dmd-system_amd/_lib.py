@@ -12,7 +12,7 @@ from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "libmlora.so"
 
-ABI_VERSION = 8
+ABI_VERSION = 9
 MAX_SEGMENTS = 128
 MAX_ADAPTERS = 32
 MAX_RANK = 256
@@ -68,6 +68,7 @@ SIGNATURES = {
     "mlora_quantize_rows_fp8": (_int, [_vp, _i64, _i64, _i64, _vp, _vp, _i64, _vp, _vp]),
     "mlora_dequant_rows_fp8": (_int, [_vp, _i64, _vp, _i64, _i64, _vp, _i64, _vp]),
     "mlora_div_rows_bf16": (_int, [_vp, _i64, _vp, _i64, _i64, _vp, _i64, _vp]),
+    "mlora_div_rows_bf16_batch": (_int, [_pvp, _pi64, _vp, _i64, _pi64, _pvp, _pi64, _i32, _vp]),
     "mlora_gemm_fwd_fp8": (_int, [_vp, _i64, _vp, _i64, _i64, _vp, _i64, _vp, _i64, _vp, _int, _vp, _i64,
                                   _pvp, _pi32, _i32, _pi64, _pi32, _i32, _vp, _i64, _int, _vp]),
     "mlora_f32_shrink": (_int, [_vp, _i64, _i64, _i64, _pvp, _int, _pi32, _pf32, _i32,

@@ -8,7 +8,9 @@
 //   mlora_dequant_rows_fp8  : e4m3 rows times a per-row fp32 scale back to bf16
 //                             (the frozen base W for the bf16 dX GEMM)
 //   mlora_div_rows_bf16     : bf16 rows divided by a per-row fp32 value
-//                             (lora_b / w_scale for the e4m3 forward)
+//                             (lora_b / w_scale for the e4m3 forward); the
+//                             _batch form divides several such matrices (every
+//                             adapter's lora_b) in one launch
 //
 // Quantisation of row m: v[k] = x[m,k] (times col_scale[k] when given, one
 // fp32 product); amax = max_k |v[k]|; scale[m] = amax / 448 and
@@ -199,20 +201,39 @@ struct DivArgs {
   int32_t M, K;
 };
 
-__global__ __launch_bounds__(256) void div_rows_kernel(const DivArgs a) {
-  const int lane = threadIdx.x & 63;
-  const int m = blockIdx.x * 4 + wave_id();
-  if (m >= a.M) return;
-  const float d = a.div[m];
-  const uint16_t *xrow = a.x + (int64_t)m * a.ldx;
-  uint16_t *yrow = a.y + (int64_t)m * a.ldy;
-  for (int k = 8 * lane; k < a.K; k += 512) {
+// One row divided by d, a wave per row (K a multiple of 8).
+__device__ __forceinline__ void div_row(const uint16_t *xrow, uint16_t *yrow, float d, int K, int lane) {
+  for (int k = 8 * lane; k < K; k += 512) {
     const u32x4 v = *(const MLORA_GLOBAL u32x4 *)(xrow + k);
     uint32_t o[4];
 #pragma unroll
     for (int w = 0; w < 4; ++w) o[w] = pack2_bf16(bf16_to_f32(v[w] & 0xffff) / d, bf16_to_f32(v[w] >> 16) / d);
     *(MLORA_GLOBAL u32x4 *)(yrow + k) = u32x4{o[0], o[1], o[2], o[3]};
   }
+}
+
+__global__ __launch_bounds__(256) void div_rows_kernel(const DivArgs a) {
+  const int m = blockIdx.x * 4 + wave_id();
+  if (m >= a.M) return;
+  div_row(a.x + (int64_t)m * a.ldx, a.y + (int64_t)m * a.ldy, a.div[m], a.K, threadIdx.x & 63);
+}
+
+// Several matrices of M rows divided by the same per-row values (the lora_b of every adapter by
+// w_scale): matrix blockIdx.y, four rows per workgroup.
+struct DivBatchArgs {
+  const uint16_t *x[kMaxAdapters];
+  uint16_t *y[kMaxAdapters];
+  int64_t ldx[kMaxAdapters], ldy[kMaxAdapters];
+  int32_t K[kMaxAdapters];
+  const float *div;
+  int32_t M;
+};
+
+__global__ __launch_bounds__(256) void div_rows_batch_kernel(const DivBatchArgs a) {
+  const int i = blockIdx.y;
+  const int m = blockIdx.x * 4 + wave_id();
+  if (m >= a.M) return;
+  div_row(a.x[i] + (int64_t)m * a.ldx[i], a.y[i] + (int64_t)m * a.ldy[i], a.div[m], a.K[i], threadIdx.x & 63);
 }
 
 }  // namespace mlora
@@ -275,5 +296,36 @@ extern "C" int mlora_div_rows_bf16(const void *x, int64_t ldx, const float *div,
   DivArgs a{static_cast<const uint16_t *>(x), div, static_cast<uint16_t *>(y), ldx, ldy, (int32_t)M, (int32_t)K};
   hipLaunchKernelGGL(div_rows_kernel, dim3((unsigned)((M + 3) / 4)), dim3(256), 0, static_cast<hipStream_t>(stream),
                      a);
+  return launch_status();
+}
+
+extern "C" int mlora_div_rows_bf16_batch(const void *const *x, const int64_t *ldx, const float *div, int64_t M,
+                                         const int64_t *K, void *const *y, const int64_t *ldy, int32_t n,
+                                         void *stream) {
+  if (n < 0 || M < 0) return MLORA_ERR_INVALID;
+  if (n > kMaxAdapters || M > INT32_MAX - 4) return MLORA_ERR_LIMIT;
+  if (n == 0 || M == 0) return MLORA_OK;
+  if (x == nullptr || ldx == nullptr || K == nullptr || y == nullptr || ldy == nullptr) return MLORA_ERR_INVALID;
+  DivBatchArgs a{};
+  bool work = false;
+  for (int i = 0; i < n; ++i) {
+    if (K[i] < 0) return MLORA_ERR_INVALID;
+    if (K[i] > INT32_MAX / 2) return MLORA_ERR_LIMIT;
+    int st = check_bf16_matrix(x[i], ldx[i], M, K[i]);
+    if (st) return st;
+    if ((st = check_bf16_matrix(y[i], ldy[i], M, K[i]))) return st;
+    a.x[i] = static_cast<const uint16_t *>(x[i]);
+    a.y[i] = static_cast<uint16_t *>(y[i]);
+    a.ldx[i] = ldx[i];
+    a.ldy[i] = ldy[i];
+    a.K[i] = (int32_t)K[i];
+    work = work || K[i] > 0;
+  }
+  if (!work) return MLORA_OK;
+  if (div == nullptr) return MLORA_ERR_INVALID;
+  a.div = div;
+  a.M = (int32_t)M;
+  hipLaunchKernelGGL(div_rows_batch_kernel, dim3((unsigned)((M + 3) / 4), (unsigned)n), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), a);
   return launch_status();
 }

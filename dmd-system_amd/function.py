@@ -300,7 +300,7 @@ class MultiLoRAFP8Function(torch.autograd.Function):
         # epilogue multiplies back: h / x_scale[m] (shrink) and lora_b / w_scale[n]
         A_ops, B_ops, _, _, h_rows, h_frag = _prepare(ctx, x, wq.shape[0], ab, scales, routing, grad0=8,
                                                       row_div=x_scale)
-        B_div = [kernels.div_rows_bf16(b, w_scale) for b in B_ops]
+        B_div = kernels.div_rows_bf16_many(B_ops, w_scale)
         y = kernels.gemm_fwd_fp8(xq, x_scale, wq, w_scale, bias, h_rows, B_div, routing)
         ctx.dx_bf16 = bool(dx_bf16)
         _save(ctx, x, wq if ctx.dx_bf16 else wq_t, w_scale, *A_ops, *B_ops, frag=h_frag)

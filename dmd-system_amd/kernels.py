@@ -526,6 +526,26 @@ def div_rows_bf16(x: torch.Tensor, div: torch.Tensor) -> torch.Tensor:
     return y
 
 
+def div_rows_bf16_many(xs: Sequence[torch.Tensor], div: torch.Tensor) -> list[torch.Tensor]:
+    """[bf16(x[m, k] / div[m]) for x in xs]: matrices of one row count, MAX_ADAPTERS per launch."""
+    if not xs:
+        return []
+    M = xs[0].shape[0]
+    for x in xs:
+        _check_rows("x", x)
+        _require(x.shape[0] == M, "the matrices share their row count")
+    _check_scale("div", div, M)
+    ys = [torch.empty(x.shape, dtype=torch.bfloat16, device=x.device) for x in xs]
+    lib = _lib.load()
+    for i0 in range(0, len(xs), _lib.MAX_ADAPTERS):
+        xb, yb = xs[i0:i0 + _lib.MAX_ADAPTERS], ys[i0:i0 + _lib.MAX_ADAPTERS]
+        _lib.check("mlora_div_rows_bf16_batch", lib.mlora_div_rows_bf16_batch(
+            _lib.ptr_array([x.data_ptr() for x in xb]), _lib.i64_array([x.stride(0) for x in xb]), div.data_ptr(),
+            M, _lib.i64_array([x.shape[1] for x in xb]), _lib.ptr_array([y.data_ptr() for y in yb]),
+            _lib.i64_array([y.stride(0) for y in yb]), len(xb), _stream(xs[0])))
+    return ys
+
+
 def gemm_fwd_fp8(xq: torch.Tensor, x_scale: torch.Tensor, wq: torch.Tensor, w_scale: torch.Tensor | None,
                  bias: torch.Tensor | None, h_rows: torch.Tensor | None, bs: Sequence[torch.Tensor],
                  routing: SegmentRouting) -> torch.Tensor:

@@ -45,7 +45,7 @@
 extern "C" {
 #endif
 
-#define MLORA_ABI_VERSION 8
+#define MLORA_ABI_VERSION 9
 
 /* Limits of one call (kernel-argument tables). Callers with more segments
  * split the rows into several calls; the Python host layer does this. */
@@ -366,6 +366,15 @@ int mlora_dequant_rows_fp8(const void *q, int64_t ldq, const float *scale, int64
 int mlora_div_rows_bf16(const void *x, int64_t ldx, const float *div, int64_t M, int64_t K,
                         void *y, int64_t ldy,
                         void *stream);
+
+/* mlora_div_rows_bf16 over n <= MLORA_MAX_ADAPTERS matrices of M rows in one launch:
+ * y[i][m, k] = bf16( x[i][m,k] / div[m] ), matrix i [M, K[i]] with pitches ldx[i] / ldy[i]
+ * (every adapter's lora_b / w_scale for one e4m3 forward, the same values bit for bit).
+ * x, ldx, K, y and ldy are host arrays of n entries; div [M] is a device array.
+ * No counterpart in the reference: it replaces n launches of mlora_div_rows_bf16. */
+int mlora_div_rows_bf16_batch(const void *const *x, const int64_t *ldx, const float *div, int64_t M,
+                              const int64_t *K, void *const *y, const int64_t *ldy, int32_t n,
+                              void *stream);
 
 /* mlora_gemm_fwd with an e4m3 base contraction (v_mfma_scale_f32_32x32x64_f8f6f4):
  *   Y[m, n] = bf16( x_scale[m]·w_scale[n]·( Σ_k xq[m,k]·wq[n,k] + Σ_j h_rows[m,j]·B_a[n,j] ) + bias[n] )

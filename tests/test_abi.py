@@ -35,7 +35,7 @@ def test_library_exports_every_declared_symbol(lib, pkg):
 
 
 def test_abi_version_and_status_strings(lib, pkg):
-    assert lib.mlora_abi_version() == pkg._lib.ABI_VERSION == 8
+    assert lib.mlora_abi_version() == pkg._lib.ABI_VERSION == 9
     for code in (0, -1, -2, -3, -4, -5):
         assert lib.mlora_status_string(code)
     assert b"unknown" in lib.mlora_status_string(-99)
@@ -186,6 +186,24 @@ def test_fp8_entry_points_validate_before_launch(lib, pkg):
     assert lib.mlora_dequant_rows_fp8(0x1000, 32, None, 4, 32, 0x2000, 32, None) == L.ERR_INVALID
     assert lib.mlora_div_rows_bf16(0x1000, 32, None, 4, 32, 0x2000, 32, None) == L.ERR_INVALID
     assert lib.mlora_div_rows_bf16(0x1000, 4, 0x3000, 4, 8, 0x2000, 8, None) == L.ERR_INVALID
+
+    def div_batch(xs=(0x1000, 0x4000), lds=(64, 32), div=0x3000, M=4, ks=(64, 32), ys=(0x2000, 0x5000),
+                  ldys=None, n=None):
+        n = len(xs) if n is None else n
+        return lib.mlora_div_rows_bf16_batch(L.ptr_array(list(xs)), L.i64_array(list(lds)), div, M,
+                                             L.i64_array(list(ks)), L.ptr_array(list(ys)),
+                                             L.i64_array(list(ldys or lds)), n, None)
+    assert div_batch(div=None) == L.ERR_INVALID                       # rows to divide, no divisors
+    assert div_batch(div=None, ks=(0, 0)) == L.OK                     # nothing to divide
+    assert div_batch(M=0, div=None) == L.OK
+    assert div_batch(lds=(64, 16)) == L.ERR_INVALID                   # pitch below the width
+    assert div_batch(xs=(0x1000, 0x4008)) == L.ERR_UNSUPPORTED        # 16-byte rows
+    assert div_batch(ks=(64, 36), lds=(64, 40)) == L.ERR_UNSUPPORTED  # widths in 8-element chunks
+    assert div_batch(ks=(64, -8)) == L.ERR_INVALID
+    assert div_batch(n=-1) == L.ERR_INVALID
+    assert div_batch(xs=[0x1000] * (L.MAX_ADAPTERS + 1), lds=[64] * (L.MAX_ADAPTERS + 1),
+                     ks=[64] * (L.MAX_ADAPTERS + 1), ys=[0x2000] * (L.MAX_ADAPTERS + 1)) == L.ERR_LIMIT
+    assert div_batch(n=0) == L.OK
 
     def fwd8(M=64, K=64, N=64, ldx=64, xs=0x6000, ws=0x7000, off=None, ids=None):
         off = off if off is not None else [0, M]

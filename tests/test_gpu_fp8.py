@@ -73,6 +73,27 @@ def test_dequant_rows_bit_exact(pkg, dev):
     assert np.array_equal(y.float().cpu().numpy(), want)
 
 
+def test_batched_row_division_equals_single_calls(pkg, dev):
+    """div_rows_bf16_many (one launch per 32 matrices) gives each matrix's div_rows_bf16 bits:
+    ranks 8-256 and widths past a 512-element pass, 35 matrices (two launches), divisors over
+    many binades; and the quotients are the RNE bf16 of the fp32 quotient."""
+    print("batched row division", flush=True)
+    g = torch.Generator().manual_seed(41)
+    M = 1536
+    widths = [64, 32, 128, 8, 256, 576] + [16 * (1 + i % 9) for i in range(29)]
+    xs = [(torch.randn(M, w, generator=g) * 0.05).to(torch.bfloat16).to(dev) for w in widths]
+    div = torch.exp(torch.randn(M, generator=g) * 4).to(dev)
+    got = pkg.kernels.div_rows_bf16_many(xs, div)
+    torch.cuda.synchronize()
+    assert len(got) == len(xs)
+    for x, y in zip(xs, got):
+        assert y.shape == x.shape and torch.equal(y, pkg.kernels.div_rows_bf16(x, div))
+    x0 = xs[0].float().cpu().numpy()
+    q = x0 / div.cpu().numpy()[:, None]  # float32 division, IEEE round to nearest
+    assert q.dtype == np.float32
+    assert np.array_equal(got[0].float().cpu().numpy(), O.bf16_round(q))
+
+
 def test_bf16_rounding_is_rne_with_ties_and_subnormals(pkg, dev):
     """The kernels' fp32 -> bf16 rounding (the gfx950 packed conversion) is
     round-to-nearest-even bit for bit: dequantisation products that land exactly
