@@ -111,7 +111,7 @@ struct GemmCfg {
   // SPREAD) and its Q into the slot its own barrier frees — 1.5 k-tiles in
   // flight instead of 1 in the same 160 KB.
   static constexpr bool RING5 = RING5_;
-  static_assert(!RING5 || (!F8 && A_BYTES == 32768 && B_BYTES == 32768), "slots hold one 256-row operand tile");
+  static_assert(!RING5 || (A_BYTES == 32768 && B_BYTES == 32768), "slots hold one 256-row operand tile");
   static constexpr int PERIOD = RING5 ? 5 : STAGES;  // steps until the LDS offsets repeat
   static constexpr int AHEAD = RING5 ? 2 : STAGES;   // a step loads the k-tile this far ahead
   static constexpr int B_BASE = RING5 ? 0 : STAGES * A_BYTES;
@@ -514,7 +514,6 @@ __device__ __forceinline__ void contract_tile(f32x16 (&acc)[C::TM][C::TN], const
   int ntile = (src.klim + bk - 1) / bk;
   // e4m3: the main contraction is padded to a multiple of S k-tiles (zero
   // chunks) so the bf16 LoRA k-tiles start at stage 0
-  if constexpr (C::F8) ntile = (ntile + S - 1) / S * S;
   const int n_main = ntile;  // e4m3 k-tiles (F8), before the first LoRA tile
   if (ntile == 0) {
     first_seg();
@@ -572,9 +571,21 @@ __device__ __forceinline__ void contract_tile(f32x16 (&acc)[C::TM][C::TN], const
   lds_pipeline_barrier();
   int t = 0;
   bool done = false;
-  // Runs steps from tile 0 until every tile is done or t reaches stop_at; the
-  // stage loop is unrolled so every LDS offset is a constant.
+  // Runs steps from tile t until every tile is done or t reaches stop_at; the
+  // stage loop is unrolled so every LDS offset is a constant. e4m3: the bf16
+  // LoRA k-tiles start where the e4m3 ones end, at phase t % S, so a partial
+  // period runs first.
   auto run = [&](int stop_at, auto &&step) {
+    if constexpr (C::F8) {
+      const int p0 = t % S;
+      if (p0 != 0 && !done && t < stop_at) static_for<S>([&](auto st) -> bool {
+          if (decltype(st)::value < p0) return true;
+          step(st);
+          ++t;
+          done = t >= n_real;
+          return !done && t < stop_at;
+        });
+    }
     while (!done && t < stop_at) static_for<S>([&](auto st) -> bool {
         step(st);
         ++t;
@@ -590,8 +601,8 @@ __device__ __forceinline__ void contract_tile(f32x16 (&acc)[C::TM][C::TN], const
   Half<C> h0, h1;  // fragments of the current and the next substep
   if constexpr (C::F8) {
     // e4m3 steps (NSUB / 2 substeps of TMN scaled MFMAs), the same barrier
-    // and load placement as the bf16 steps. n_main is a multiple of S, so the
-    // bf16 LoRA k-tiles start at stage 0.
+    // and load placement as the bf16 steps (RING5: the P half of tile t+2 in
+    // the substeps before the barrier, the Q half after it).
     constexpr int NS8 = NSUB / 2;
     Frag8<C> f;
 #pragma unroll
@@ -599,7 +610,7 @@ __device__ __forceinline__ void contract_tile(f32x16 (&acc)[C::TM][C::TN], const
 #pragma unroll
     for (int r = 0; r < C::TN; ++r) f.b[r] = read_frag8<C, 0>(C::TM + r, 0, lds, fa);
     run(n_main, [&](auto st) {
-      constexpr int ST = decltype(st)::value, NS = (ST + 1) % S;
+      constexpr int ST = decltype(st)::value, NS = (ST + 1) % S, LS = (ST + C::AHEAD) % S;
       const bool live = advance();
       const int k0 = t_in_src * bk;
       static_for<NS8>([&](auto u_c) {
@@ -607,9 +618,10 @@ __device__ __forceinline__ void contract_tile(f32x16 (&acc)[C::TM][C::TN], const
         if constexpr (U == NS8 - 1) {
           wait_vmcnt<WAIT>();  // this wave's loads of tile t + 1
           lds_pipeline_barrier();
-          mma_fp8<C, NS, 0, ST, 0, NDMA>(acc, f, lds, fa, pipe, k0, kmask, live, wave, lane);
+          mma_fp8<C, NS, 0, LS, PQ, NDMA>(acc, f, lds, fa, pipe, k0, kmask, live, wave, lane);
         } else {
-          mma_fp8<C, ST, U + 1, ST, 0, 0>(acc, f, lds, fa, pipe, k0, kmask, live, wave, lane);
+          constexpr int Q0 = U * PQ / (NS8 - 1), Q1 = (U + 1) * PQ / (NS8 - 1);
+          mma_fp8<C, ST, U + 1, LS, Q0, Q1>(acc, f, lds, fa, pipe, k0, kmask, live, wave, lane);
         }
         return true;
       });
@@ -939,7 +951,7 @@ __global__ __launch_bounds__(C::THREADS, C::WAVES_PER_SIMD) void gemm_kernel(con
 }
 
 using CfgNT256 = GemmCfg<256, 256, 4, 2, false, false, 128, 2, true, true>;
-using CfgF8256 = GemmCfg<256, 256, 4, 2, false, true>;
+using CfgF8256 = GemmCfg<256, 256, 4, 2, false, true, 128, 2, true, true>;
 using CfgF8128 = GemmCfg<128, 128, 2, 2, false, true>;
 using CfgNN256 = GemmCfg<256, 256, 4, 2, true, false, 128, 2, true, true>;
 using CfgNT128 = GemmCfg<128, 128, 2, 2, false>;
