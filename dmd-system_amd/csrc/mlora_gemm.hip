@@ -71,7 +71,7 @@ struct GemmArgs {
 };
 
 template <int BM_, int BN_, int WM_, int WN_, bool NN_, bool F8_ = false, int KB_ = 128, int STAGES_ = 2,
-          bool RING5_ = false, bool SPREAD_ = false>
+          bool RING5_ = false, bool SPREAD_ = false, bool PP_ = false>
 struct GemmCfg {
   static constexpr int BM = BM_, BN = BN_, WM = WM_, WN = WN_;
   static constexpr bool NN = NN_;
@@ -123,6 +123,9 @@ struct GemmCfg {
   // spread over all the substeps before the barrier instead of the first one
   // (fewer loads queued at the texture unit at once: 1-3% per launch).
   static constexpr bool SPREAD = SPREAD_;
+  // PP: the ping-pong schedule of contract_tile_pp (8-wave 256x256 bf16 tiles on the 5-slot ring)
+  static constexpr bool PP = PP_;
+  static_assert(!PP || (RING5 && !F8 && NW == 8), "the ping-pong schedule runs 8-wave bf16 tiles on the 5-slot ring");
   static constexpr int p_off(int ph) { return RING5 ? ((2 * ph) % 5) * A_BYTES : ph * A_BYTES; }
   static constexpr int q_off(int ph) { return RING5 ? ((2 * ph + 1) % 5) * A_BYTES : ph * B_BYTES; }
   static_assert(LDS_BYTES <= 163840, "the ring must fit the 160 KB of LDS");
@@ -661,6 +664,324 @@ __device__ __forceinline__ void contract_tile(f32x16 (&acc)[C::TM][C::TN], const
   wait_vmcnt<0>();
 }
 
+// Direct-to-LDS loads of one operand for the ping-pong schedule (contract_tile_pp): a k-tile of
+// 32 KB is 32 blocks of 1 KB, and each of a group's four waves issues 8 of them. Block blk holds
+// P (or NT Q) rows RPD·blk .. RPD·blk + RPD - 1, or NN Q contraction rows QRPD·blk ..; the lane
+// layout and swizzle are those of Pipe.
+template <class C>
+struct PPLoad {
+  __amdgpu_buffer_rsrc_t r;
+  int32_t off[2];  // this lane's offset in an even / odd block at k = 0 (kOOB: past the operand)
+  int32_t ld_b, klim, esz;
+  int32_t p_rows;  // P: tile rows below this index belong to an earlier segment (read as zero)
+
+  // P: rows [row_lo, row_hi) of the tile at m0; NT Q: the Ncols - n0 rows from n0
+  __device__ __forceinline__ void init_rows(const char *base, int64_t ldb, int64_t rows, int32_t masked, const KSource &s,
+                                            int lane) {
+    klim = s.klim;
+    esz = s.esz;
+    ld_b = (int32_t)ldb;
+    p_rows = masked;
+    r = make_rsrc(base, rows * ldb);
+#pragma unroll
+    for (int par = 0; par < 2; ++par) off[par] = (lane / C::CPR) * ld_b + 16 * chunk(par, lane);
+  }
+  // the logical chunk this lane fetches in an even / odd block (the swizzle of Pipe)
+  static __device__ __forceinline__ int chunk(int par, int lane) {
+    return (lane % C::CPR) ^ swzk<C::CPR>(C::RPD * par + lane / C::CPR);
+  }
+  __device__ __forceinline__ void init_p(const KSource &s, int m0, int lane) {
+    init_rows(s.P + (int64_t)m0 * s.ldp_b, s.ldp_b, s.row_hi - m0, max(s.row_lo, m0) - m0, s, lane);
+  }
+  __device__ __forceinline__ void init_q(const KSource &s, int n0, int Ncols, int lane) {
+    if constexpr (!C::NN) {
+      init_rows(s.Q + (int64_t)n0 * s.ldq_b, s.ldq_b, Ncols - n0, 0, s, lane);
+    } else {
+      // rows are contraction indices, chunk c of row k at slot c ^ (4 * (k & 3))
+      klim = s.klim;
+      esz = s.esz;
+      ld_b = (int32_t)s.ldq_b;
+      p_rows = 0;
+      r = make_rsrc(s.Q + 2 * n0, (int64_t)s.klim * s.ldq_b);
+      const int p = lane % C::QCPR, rl = lane / C::QCPR;
+#pragma unroll
+      for (int par = 0; par < 2; ++par) {
+        const int cc = p ^ (4 * ((C::QRPD * par + rl) & 3));
+        off[par] = (n0 + 8 * cc < Ncols) ? rl * ld_b + 16 * cc : kOOB;
+      }
+    }
+  }
+  // Whether a k-tile needs the masks of issue (wave-uniform): rows of an earlier segment, a
+  // partial last k-tile, or a tile past the last one. Every main-contraction tile of a whole
+  // number of k-tiles needs none.
+  __device__ __forceinline__ bool masked(bool kmask, bool live) const { return p_rows > 0 || kmask || !live; }
+  // Block blk of the k-tile at k0 into the LDS operand tile at `tile`. live == false turns
+  // every lane's offset out of range: no data moves. MASK: apply the masks (see masked).
+  template <bool NNQ, bool MASK>
+  __device__ __forceinline__ void issue(MLORA_LDS char *tile, int blk, int k0, bool kmask, bool live, int lane) const {
+    // lane-derived values other than the offsets are recomputed here (VALU is idle in the phase
+    // that issues loads) instead of being held in registers across the k-loop
+    int32_t o = off[blk & 1], soff;
+    if constexpr (!NNQ) {
+      const int row = C::RPD * blk;
+      if constexpr (MASK) {
+        if (p_rows > 0 && row + lane / C::CPR < p_rows) o = kOOB;  // rows of an earlier segment
+        if (kmask && k0 + (16 / esz) * chunk(blk & 1, lane) >= klim) o = kOOB;
+        if (!live) o = kOOB;
+      }
+      soff = row * ld_b + k0 * esz;
+    } else {
+      const int row = C::QRPD * blk;
+      if constexpr (MASK) {
+        if (kmask && k0 + row + lane / C::QCPR >= klim) o = kOOB;
+        if (!live) o = kOOB;
+      }
+      soff = (k0 + row) * ld_b;
+    }
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, tile + blk * 1024, 16, o, soff, 0, 0);
+  }
+};
+
+// A barrier between two phases of the ping-pong schedule; nothing is scheduled across it.
+__device__ __forceinline__ void phase_barrier() {
+  __builtin_amdgcn_sched_barrier(0);
+  lds_pipeline_barrier();
+  __builtin_amdgcn_sched_barrier(0);
+}
+
+// The contraction of one 256x256 bf16 tile (8 waves, 64x128 each) in a ping-pong schedule. Waves
+// 0-3 and 4-7 share the SIMDs pairwise (wave w with w + 4) and alternate phases: while one wave
+// of a SIMD multiplies a whole k-tile from registers (32 MFMAs, no other instruction), the other
+// reads all of its fragments of a k-tile from LDS and issues its loads; every phase ends at a
+// workgroup barrier. So the MFMA pipe of each SIMD is fed by one wave at a time, without the
+// fragment reads' waits or the loads' issue between its MFMAs.
+//
+// Waves 0-3 (Q side) load every Q tile and lead: step t = [issue Q(t+1), read k-tile t] then
+// [MFMAs of t, wait for Q(t+1)]. Waves 4-7 (P side) load every P tile, one phase behind:
+// [issue P(t+2), read t, wait for P(t+1)] then [MFMAs of t]. The LDS ring is RING5's (k-tile
+// t's P in slot 2t % 5, Q in 2t + 1): Q(t+1) goes to the slot of P(t-1) and P(t+2) to that of
+// Q(t-1), both last read in the phase before. k-tile t+1 has landed by the barrier before its
+// first reads, as each side waits for its own loads of it. The k-tiles are KWalk's sequence
+// (contract_tile): the main contraction, then the LoRA tiles; each accumulator takes its MFMAs
+// in the same k order as in contract_tile, so the results are the same bit for bit.
+template <class C, int STK = 0>
+__device__ __forceinline__ void contract_tile_pp(f32x16 (&acc)[C::TM][C::TN], const GemmArgs &args,
+                                                 MLORA_LDS char *lds, int wm0, int wn0, int m0, int n0, int tid) {
+  static_assert(C::RING5 && !C::F8 && C::NW == 8 && C::NSUB == 4, "8-wave 256x256 bf16 tiles on the 5-slot ring");
+  constexpr int LPW = 8;  // 1 KB loads per loading wave and k-tile
+  constexpr int S = C::PERIOD, NSUB = C::NSUB;
+  const int wave = wave_id(), lane = tid & 63;
+  const bool qside = wave < 4;
+  const int blk0 = (wave & 3) * LPW;
+  const int row_end = min(m0 + C::BM, args.M);
+  const int ecol = STK == 1 ? __builtin_amdgcn_readfirstlane((n0 / args.group_cols) * args.group_ecols) : 0;
+  int grp = 0;
+  int seg = -1;
+  auto first_seg = [&]() {
+    if (seg < 0) seg = args.E != nullptr ? seg_of_row(args.seg, m0) : args.seg.n;
+  };
+  KSource src{static_cast<const char *>(args.P), static_cast<const char *>(args.Q), 2 * args.ldp, 2 * args.ldq, 0,
+              args.M, args.Kc, 2};
+  int bk = C::KB / 2;
+  int ntile = (src.klim + bk - 1) / bk;
+  if (ntile == 0) {
+    first_seg();
+    if (!next_lora_source(args, C::NN, m0, row_end, seg, src, ecol)) return;
+    ntile = (src.klim + bk - 1) / bk;
+  }
+  bool kmask = ntile * bk != src.klim;
+  PPLoad<C> ld;
+  auto point = [&]() {
+    if (qside) ld.init_q(src, n0, args.Ncols, lane);
+    else ld.init_p(src, m0, lane);
+  };
+  point();
+  int t_in_src = 0, n_real = 1;
+  bool exhausted = false;
+  // the walk of contract_tile (every source is bf16 here)
+  auto advance = [&]() -> bool {
+    if (exhausted) return false;
+    if (t_in_src + 1 < ntile) {
+      ++t_in_src;
+      ++n_real;
+      return true;
+    }
+    if constexpr (STK == 2) {
+      if (grp + 1 < args.groups) {
+        ++grp;
+        src = KSource{reinterpret_cast<const char *>(args.Pg[grp]),
+                      reinterpret_cast<const char *>(args.Q) + 2 * (int64_t)grp * args.group_cols, 2 * args.ldp,
+                      2 * args.ldq, 0, args.M, args.group_cols, 2};
+        kmask = src.klim % bk != 0;
+        point();
+        t_in_src = 0;
+        ++n_real;
+        return true;
+      }
+    }
+    first_seg();
+    if (!next_lora_source(args, C::NN, m0, row_end, seg, src, ecol)) {
+      exhausted = true;
+      return false;
+    }
+    ntile = (src.klim + bk - 1) / bk;
+    kmask = src.klim % bk != 0;
+    point();
+    t_in_src = 0;
+    ++n_real;
+    return true;
+  };
+  // this wave's 8 loads of the current k-tile (NNQ: of an NN Q tile) into the LDS operand tile
+  auto issue_loads = [&](auto nnq, MLORA_LDS char *tile, bool live) {
+    constexpr bool NNQ = decltype(nnq)::value;
+    const int k0 = t_in_src * bk;
+    if (ld.masked(kmask, live)) {
+#pragma unroll
+      for (int q = 0; q < LPW; ++q) ld.template issue<NNQ, true>(tile, blk0 + q, k0, kmask, live, lane);
+    } else {
+#pragma unroll
+      for (int q = 0; q < LPW; ++q) ld.template issue<NNQ, false>(tile, blk0 + q, k0, kmask, live, lane);
+    }
+  };
+  auto issue_tile = [&](MLORA_LDS char *tile, bool live) { issue_loads(std::false_type{}, tile, live); };
+  auto issue_q_tile = [&](MLORA_LDS char *tile, bool live) { issue_loads(std::bool_constant<C::NN>{}, tile, live); };
+  // this lane's fragment offsets in substep h (phase-0 layout; see FragAddr)
+  int32_t fa[NSUB], fb[C::NN ? C::TN : NSUB];
+  {
+    const int z = swzk<C::CPR>(lane & 31);
+#pragma unroll
+    for (int h = 0; h < NSUB; ++h) {
+      const int slot = (2 * h + (lane >> 5)) ^ z;
+      fa[h] = (wm0 + (lane & 31)) * C::KB + 16 * slot;
+      if constexpr (!C::NN) fb[h] = (wn0 + (lane & 31)) * C::KB + 16 * slot;
+    }
+    if constexpr (C::NN) {
+      const int i = lane & 15, h = lane >> 5, g1 = (lane >> 4) & 1;
+      const int m = (i >> 2) & 3;
+#pragma unroll
+      for (int j = 0; j < C::TN; ++j) {
+        const int c = (wn0 + 32 * j + 16 * g1) / 8 + ((i & 3) >> 1);
+        fb[j] = (8 * h + (i >> 2)) * C::QROW + 16 * (c ^ (4 * m)) + 8 * (i & 1);
+      }
+    }
+  }
+  Half<C> f[NSUB];
+  // fragment offset o moved by a multiple of 64 KB (the part of an LDS offset past the 16-bit
+  // immediate of a ds_read): added in the phase that reads, not held across the loop, and kept
+  // apart from the immediates that follow
+  auto hi = [](int32_t o, int add) -> int32_t { return add == 0 ? o : opaque_vgpr(opaque_vgpr(o) + add); };
+  // all of this wave's fragments of the k-tile in phase PH
+  auto read_tile = [&](auto ph_c) {
+    constexpr int PH = decltype(ph_c)::value;
+    constexpr int PO = C::p_off(PH), QO = C::q_off(PH);
+    static_for<NSUB>([&](auto h_c) {
+      constexpr int H = decltype(h_c)::value;
+      const int32_t pa = hi(fa[H], PO & ~65535);
+#pragma unroll
+      for (int i = 0; i < C::TM; ++i) f[H].a[i] = *(const lds_u4 *)(lds + pa + (PO & 65535) + 32 * C::KB * i);
+      if constexpr (!C::NN) {
+        const int32_t qa = hi(fb[H], QO & ~65535);
+#pragma unroll
+        for (int j = 0; j < C::TN; ++j) f[H].b[j] = *(const lds_u4 *)(lds + qa + (QO & 65535) + 32 * C::KB * j);
+      }
+      return true;
+    });
+    if constexpr (C::NN) {
+      static_for<NSUB>([&](auto h_c) {
+        constexpr int H = decltype(h_c)::value;
+        lds_read_tr16<C::TN, 4 * C::QROW>(lds + (C::q_off(PH) + 16 * C::QROW * H), fb, f[H].b);
+        return true;
+      });
+    }
+  };
+  auto compute = [&]() {
+#pragma unroll
+    for (int h = 0; h < NSUB; ++h)
+#pragma unroll
+      for (int g = 0; g < C::TMN; ++g) {
+        const int j = g / C::TM, i = g % C::TM;
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(f[h].b[j]), as_bf16x8(f[h].a[i]), acc[i][j], 0, 0, 0);
+      }
+  };
+  // k-tiles of the main contraction that need no mask (all but a partial last one): the steps
+  // whose loads read only those run in whole periods of a loop of their own, without the walk
+  // and the mask decisions, so the phases that issue loads carry no more than the loads and
+  // reads themselves
+  const int n_full = STK == 2 ? 0 : args.Kc / bk;
+  int t = 0;
+  bool done = false;
+  if (qside) {
+    issue_q_tile(lds + C::B_BASE + C::q_off(0), true);
+    wait_vmcnt<0>();
+    phase_barrier();
+    while (t + S + 1 <= n_full) static_for<S>([&](auto st) -> bool {  // loads Q(t+1) .. Q(t+S)
+        constexpr int ST = decltype(st)::value;
+        ++t_in_src;
+        ++n_real;
+#pragma unroll
+        for (int q = 0; q < LPW; ++q)
+          ld.template issue<C::NN, false>(lds + C::B_BASE + C::q_off((ST + 1) % S), blk0 + q, t_in_src * bk, false, true,
+                                          lane);
+        read_tile(st);
+        phase_barrier();
+        compute();
+        wait_vmcnt<0>();
+        phase_barrier();
+        ++t;
+        return true;
+      });
+    while (!done) static_for<S>([&](auto st) -> bool {
+        constexpr int ST = decltype(st)::value;
+        const bool live = advance();  // Q(t + 1)
+        issue_q_tile(lds + C::B_BASE + C::q_off((ST + 1) % S), live);
+        read_tile(st);
+        phase_barrier();
+        compute();
+        wait_vmcnt<0>();
+        phase_barrier();
+        ++t;
+        done = t >= n_real;
+        return !done;
+      });
+    phase_barrier();  // the P side's last MFMA phase
+  } else {
+    issue_tile(lds + C::p_off(0), true);
+    issue_tile(lds + C::p_off(1), advance());
+    wait_vmcnt<LPW>();  // P(0)
+    phase_barrier();
+    phase_barrier();  // the Q side reads k-tile 0
+    while (t + S + 2 <= n_full) static_for<S>([&](auto st) -> bool {  // loads P(t+2) .. P(t+S+1)
+        constexpr int ST = decltype(st)::value;
+        ++t_in_src;
+        ++n_real;
+#pragma unroll
+        for (int q = 0; q < LPW; ++q)
+          ld.template issue<false, false>(lds + C::p_off((ST + 2) % S), blk0 + q, t_in_src * bk, false, true, lane);
+        read_tile(st);
+        wait_vmcnt<LPW>();  // P(t + 1)
+        phase_barrier();
+        compute();
+        phase_barrier();
+        ++t;
+        return true;
+      });
+    while (!done) static_for<S>([&](auto st) -> bool {
+        constexpr int ST = decltype(st)::value;
+        const bool live = advance();  // P(t + 2)
+        issue_tile(lds + C::p_off((ST + 2) % S), live);
+        read_tile(st);
+        wait_vmcnt<LPW>();  // P(t + 1)
+        phase_barrier();
+        compute();
+        phase_barrier();
+        ++t;
+        done = t >= n_real;
+        return !done;
+      });
+  }
+  wait_vmcnt<0>();
+}
+
 // Output tile of physical index p: XCD-contiguous logical ids (workgroups
 // are dealt round-robin over the 8 XCDs), then groups of group_m row-tiles
 // walked column by column so concurrently running tiles share P rows and Q
@@ -939,9 +1260,13 @@ __global__ __launch_bounds__(C::THREADS, C::WAVES_PER_SIMD) void gemm_kernel(con
     for (int j = 0; j < C::TN; ++j)
 #pragma unroll
       for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
-  FragAddr<C> fa;
-  fa.init(wm0, wn0, lane);
-  contract_tile<C, STK>(acc, args, lds, fa, m0, n0, tid);
+  if constexpr (C::PP) {
+    contract_tile_pp<C, STK>(acc, args, lds, wm0, wn0, m0, n0, tid);
+  } else {
+    FragAddr<C> fa;
+    fa.init(wm0, wn0, lane);
+    contract_tile<C, STK>(acc, args, lds, fa, m0, n0, tid);
+  }
   if constexpr (STK == 1) {
     const int g = __builtin_amdgcn_readfirstlane(n0 / args.group_cols);
     store_tile<C, RESID>(acc, args, lds, m0, n0, wm0, wn0, lane, args.Yg[g], g * args.group_cols);
@@ -950,7 +1275,7 @@ __global__ __launch_bounds__(C::THREADS, C::WAVES_PER_SIMD) void gemm_kernel(con
   }
 }
 
-using CfgNT256 = GemmCfg<256, 256, 4, 2, false, false, 128, 2, true, true>;
+using CfgNT256 = GemmCfg<256, 256, 4, 2, false, false, 128, 2, true, true, true>;
 using CfgF8256 = GemmCfg<256, 256, 4, 2, false, true, 128, 2, true, true>;
 using CfgF8128 = GemmCfg<128, 128, 2, 2, false, true>;
 using CfgNN256 = GemmCfg<256, 256, 4, 2, true, false, 128, 2, true, true>;
