@@ -274,6 +274,11 @@ __device__ __forceinline__ int32_t opaque_vgpr(int32_t x) {
   asm volatile("" : "+v"(x));
   return x;
 }
+// The same for a wave-uniform value: computed from where it is used (no hoisted copies).
+__device__ __forceinline__ int32_t opaque_sgpr(int32_t x) {
+  asm volatile("" : "+s"(x));
+  return x;
+}
 
 template <class C>
 struct FragAddr {
@@ -664,42 +669,41 @@ __device__ __forceinline__ void contract_tile(f32x16 (&acc)[C::TM][C::TN], const
   wait_vmcnt<0>();
 }
 
-// Direct-to-LDS loads of one operand for the ping-pong schedule (contract_tile_pp): a k-tile of
-// 32 KB is 32 blocks of 1 KB, and each of a group's four waves issues 8 of them. Block blk holds
-// P (or NT Q) rows RPD·blk .. RPD·blk + RPD - 1, or NN Q contraction rows QRPD·blk ..; the lane
-// layout and swizzle are those of Pipe.
+// Direct-to-LDS loads of one operand for the ping-pong schedule (contract_tile_pp). An operand
+// k-tile of 32 KB is 32 blocks of 1 KB: block blk holds P (or NT Q) rows RPD·blk .. RPD·blk +
+// RPD - 1, or NN Q contraction rows QRPD·blk ..; the lane layout and swizzle are those of Pipe.
+// Every source is bf16 here.
 template <class C>
 struct PPLoad {
   __amdgpu_buffer_rsrc_t r;
   int32_t off[2];  // this lane's offset in an even / odd block at k = 0 (kOOB: past the operand)
-  int32_t ld_b, klim, esz;
+  int32_t ld_b, klim;
   int32_t p_rows;  // P: tile rows below this index belong to an earlier segment (read as zero)
 
-  // P: rows [row_lo, row_hi) of the tile at m0; NT Q: the Ncols - n0 rows from n0
-  __device__ __forceinline__ void init_rows(const char *base, int64_t ldb, int64_t rows, int32_t masked, const KSource &s,
+  // the logical chunk this lane fetches in an even / odd block (the swizzle of Pipe)
+  static __device__ __forceinline__ int chunk(int par, int lane) {
+    return (lane % C::CPR) ^ swzk<C::CPR>(C::RPD * par + lane / C::CPR);
+  }
+  __device__ __forceinline__ void init_rows(const char *base, int64_t ldb, int64_t rows, int32_t masked, int32_t kl,
                                             int lane) {
-    klim = s.klim;
-    esz = s.esz;
+    klim = kl;
     ld_b = (int32_t)ldb;
     p_rows = masked;
     r = make_rsrc(base, rows * ldb);
 #pragma unroll
     for (int par = 0; par < 2; ++par) off[par] = (lane / C::CPR) * ld_b + 16 * chunk(par, lane);
   }
-  // the logical chunk this lane fetches in an even / odd block (the swizzle of Pipe)
-  static __device__ __forceinline__ int chunk(int par, int lane) {
-    return (lane % C::CPR) ^ swzk<C::CPR>(C::RPD * par + lane / C::CPR);
-  }
+  // P: rows [row_lo, row_hi) of the tile at m0
   __device__ __forceinline__ void init_p(const KSource &s, int m0, int lane) {
-    init_rows(s.P + (int64_t)m0 * s.ldp_b, s.ldp_b, s.row_hi - m0, max(s.row_lo, m0) - m0, s, lane);
+    init_rows(s.P + (int64_t)m0 * s.ldp_b, s.ldp_b, s.row_hi - m0, max(s.row_lo, m0) - m0, s.klim, lane);
   }
+  // Q: NT, the Ncols - n0 rows from n0; NN, rows are contraction indices, chunk c of row k at
+  // slot c ^ (4 * (k & 3))
   __device__ __forceinline__ void init_q(const KSource &s, int n0, int Ncols, int lane) {
     if constexpr (!C::NN) {
-      init_rows(s.Q + (int64_t)n0 * s.ldq_b, s.ldq_b, Ncols - n0, 0, s, lane);
+      init_rows(s.Q + (int64_t)n0 * s.ldq_b, s.ldq_b, Ncols - n0, 0, s.klim, lane);
     } else {
-      // rows are contraction indices, chunk c of row k at slot c ^ (4 * (k & 3))
       klim = s.klim;
-      esz = s.esz;
       ld_b = (int32_t)s.ldq_b;
       p_rows = 0;
       r = make_rsrc(s.Q + 2 * n0, (int64_t)s.klim * s.ldq_b);
@@ -715,21 +719,21 @@ struct PPLoad {
   // partial last k-tile, or a tile past the last one. Every main-contraction tile of a whole
   // number of k-tiles needs none.
   __device__ __forceinline__ bool masked(bool kmask, bool live) const { return p_rows > 0 || kmask || !live; }
-  // Block blk of the k-tile at k0 into the LDS operand tile at `tile`. live == false turns
-  // every lane's offset out of range: no data moves. MASK: apply the masks (see masked).
+  // Block blk of the k-tile at k0 to LDS address dst. live == false turns every lane's offset
+  // out of range: no data moves. MASK: apply the masks (see masked). Lane-derived values other
+  // than the offsets are recomputed here (VALU is idle in the phases that issue loads) instead of
+  // being held in registers across the k-loop.
   template <bool NNQ, bool MASK>
-  __device__ __forceinline__ void issue(MLORA_LDS char *tile, int blk, int k0, bool kmask, bool live, int lane) const {
-    // lane-derived values other than the offsets are recomputed here (VALU is idle in the phase
-    // that issues loads) instead of being held in registers across the k-loop
+  __device__ __forceinline__ void issue(MLORA_LDS char *dst, int blk, int k0, bool kmask, bool live, int lane) const {
     int32_t o = off[blk & 1], soff;
     if constexpr (!NNQ) {
       const int row = C::RPD * blk;
       if constexpr (MASK) {
         if (p_rows > 0 && row + lane / C::CPR < p_rows) o = kOOB;  // rows of an earlier segment
-        if (kmask && k0 + (16 / esz) * chunk(blk & 1, lane) >= klim) o = kOOB;
+        if (kmask && k0 + 8 * chunk(blk & 1, lane) >= klim) o = kOOB;
         if (!live) o = kOOB;
       }
-      soff = row * ld_b + k0 * esz;
+      soff = row * ld_b + 2 * k0;
     } else {
       const int row = C::QRPD * blk;
       if constexpr (MASK) {
@@ -738,7 +742,7 @@ struct PPLoad {
       }
       soff = (k0 + row) * ld_b;
     }
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, tile + blk * 1024, 16, o, soff, 0, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, dst, 16, o, soff, 0, 0);
   }
 };
 
@@ -750,29 +754,38 @@ __device__ __forceinline__ void phase_barrier() {
 }
 
 // The contraction of one 256x256 bf16 tile (8 waves, 64x128 each) in a ping-pong schedule. Waves
-// 0-3 and 4-7 share the SIMDs pairwise (wave w with w + 4) and alternate phases: while one wave
-// of a SIMD multiplies a whole k-tile from registers (32 MFMAs, no other instruction), the other
-// reads all of its fragments of a k-tile from LDS and issues its loads; every phase ends at a
-// workgroup barrier. So the MFMA pipe of each SIMD is fed by one wave at a time, without the
-// fragment reads' waits or the loads' issue between its MFMAs.
+// 0-3 (X) and 4-7 (Y) share the SIMDs pairwise (wave w with w + 4) and alternate phases: while
+// one wave of a SIMD multiplies a whole k-tile from registers (32 MFMAs, no other instruction),
+// the other issues its loads and reads all of its fragments of a k-tile from LDS; every phase
+// ends at a workgroup barrier. So the MFMA pipe of each SIMD is fed by one wave at a time,
+// without the fragment reads' waits or the loads' issue between its MFMAs.
 //
-// Waves 0-3 (Q side) load every Q tile and lead: step t = [issue Q(t+1), read k-tile t] then
-// [MFMAs of t, wait for Q(t+1)]. Waves 4-7 (P side) load every P tile, one phase behind:
-// [issue P(t+2), read t, wait for P(t+1)] then [MFMAs of t]. The LDS ring is RING5's (k-tile
-// t's P in slot 2t % 5, Q in 2t + 1): Q(t+1) goes to the slot of P(t-1) and P(t+2) to that of
-// Q(t-1), both last read in the phase before. k-tile t+1 has landed by the barrier before its
-// first reads, as each side waits for its own loads of it. The k-tiles are KWalk's sequence
-// (contract_tile): the main contraction, then the LoRA tiles; each accumulator takes its MFMAs
-// in the same k order as in contract_tile, so the results are the same bit for bit.
+// LDS: three Q slots of 32 KB (k-tile t's Q in slot t % 3), and P in 128-row halves, two slots
+// of 16 KB for the top halves and two for the bottom ones (t % 2): X computes rows 0-127 and
+// reads only the top halves, Y rows 128-255 and the bottom ones. Phase 2t: X reads k-tile t and
+// issues Q(t+2) blocks 0-15 and Pbot(t+1); phase 2t+1: Y reads k-tile t and issues Q(t+2)
+// blocks 16-31 and Ptop(t+2). Each load goes to the slot of k-tile t-1 (Q, Pbot) or t (Ptop),
+// whose last reads were in the phase before. Every wave waits for its previous phase's loads at
+// the end of each of its read phases (vmcnt(8)): a load has three phases to land.
+//
+// The k-tiles are contract_tile's sequence (the main contraction, then the LoRA tiles), walked
+// by both sides; X's P loads trail its walk by one k-tile. Each accumulator takes its MFMAs in
+// the same k order as in contract_tile, so the results are the same bit for bit.
 template <class C, int STK = 0>
 __device__ __forceinline__ void contract_tile_pp(f32x16 (&acc)[C::TM][C::TN], const GemmArgs &args,
                                                  MLORA_LDS char *lds, int wm0, int wn0, int m0, int n0, int tid) {
-  static_assert(C::RING5 && !C::F8 && C::NW == 8 && C::NSUB == 4, "8-wave 256x256 bf16 tiles on the 5-slot ring");
-  constexpr int LPW = 8;  // 1 KB loads per loading wave and k-tile
-  constexpr int S = C::PERIOD, NSUB = C::NSUB;
+  static_assert(C::RING5 && !C::F8 && C::NW == 8 && C::NSUB == 4 && C::KB == 128,
+                "8-wave 256x256 bf16 tiles of 128-byte k-tile rows");
+  constexpr int QB = 0, PT = 3 * 32768, PB = PT + 2 * 16384;  // Q slots, P-top and P-bottom half slots
+  constexpr int PER = 6;                                      // steps until the slots repeat
+  static_assert(PB + 2 * 16384 <= C::LDS_BYTES, "the ring fits the LDS");
+  constexpr int NSUB = C::NSUB;
   const int wave = wave_id(), lane = tid & 63;
-  const bool qside = wave < 4;
-  const int blk0 = (wave & 3) * LPW;
+  const bool xside = wave < 4;
+  const int lw = wave & 3;
+  const int qblk0 = (xside ? 0 : 16) + 4 * lw;  // this wave's 4 Q blocks
+  const int pblk0 = (xside ? 16 : 0) + 4 * lw;  // and 4 P blocks (X: bottom half, Y: top half)
+  // the walk of contract_tile
   const int row_end = min(m0 + C::BM, args.M);
   const int ecol = STK == 1 ? __builtin_amdgcn_readfirstlane((n0 / args.group_cols) * args.group_ecols) : 0;
   int grp = 0;
@@ -782,7 +795,7 @@ __device__ __forceinline__ void contract_tile_pp(f32x16 (&acc)[C::TM][C::TN], co
   };
   KSource src{static_cast<const char *>(args.P), static_cast<const char *>(args.Q), 2 * args.ldp, 2 * args.ldq, 0,
               args.M, args.Kc, 2};
-  int bk = C::KB / 2;
+  constexpr int bk = C::KB / 2;
   int ntile = (src.klim + bk - 1) / bk;
   if (ntile == 0) {
     first_seg();
@@ -790,15 +803,17 @@ __device__ __forceinline__ void contract_tile_pp(f32x16 (&acc)[C::TM][C::TN], co
     ntile = (src.klim + bk - 1) / bk;
   }
   bool kmask = ntile * bk != src.klim;
-  PPLoad<C> ld;
-  auto point = [&]() {
-    if (qside) ld.init_q(src, n0, args.Ncols, lane);
-    else ld.init_p(src, m0, lane);
-  };
-  point();
+  PPLoad<C> lq, lp;
+  lq.init_q(src, n0, args.Ncols, lane);
+  lp.init_p(src, m0, lane);
+  bool lp_stale = false;  // X: lp is to follow the walk's source at the next step
   int t_in_src = 0, n_real = 1;
   bool exhausted = false;
-  // the walk of contract_tile (every source is bf16 here)
+  auto repoint = [&]() {
+    lq.init_q(src, n0, args.Ncols, lane);
+    if (xside) lp_stale = true;
+    else lp.init_p(src, m0, lane);
+  };
   auto advance = [&]() -> bool {
     if (exhausted) return false;
     if (t_in_src + 1 < ntile) {
@@ -813,7 +828,7 @@ __device__ __forceinline__ void contract_tile_pp(f32x16 (&acc)[C::TM][C::TN], co
                       reinterpret_cast<const char *>(args.Q) + 2 * (int64_t)grp * args.group_cols, 2 * args.ldp,
                       2 * args.ldq, 0, args.M, args.group_cols, 2};
         kmask = src.klim % bk != 0;
-        point();
+        repoint();
         t_in_src = 0;
         ++n_real;
         return true;
@@ -826,33 +841,40 @@ __device__ __forceinline__ void contract_tile_pp(f32x16 (&acc)[C::TM][C::TN], co
     }
     ntile = (src.klim + bk - 1) / bk;
     kmask = src.klim % bk != 0;
-    point();
+    repoint();
     t_in_src = 0;
     ++n_real;
     return true;
   };
-  // this wave's 8 loads of the current k-tile (NNQ: of an NN Q tile) into the LDS operand tile
-  auto issue_loads = [&](auto nnq, MLORA_LDS char *tile, bool live) {
-    constexpr bool NNQ = decltype(nnq)::value;
-    const int k0 = t_in_src * bk;
-    if (ld.masked(kmask, live)) {
+  // this wave's 4 blocks (from blk0) of a k-tile of loader l into the LDS tile at `base` (P: a
+  // 128-row half slot, block blk at (blk & 15) KB)
+  auto issue4 = [&](auto nnq, auto is_p, const PPLoad<C> &l, MLORA_LDS char *base, int blk0, int k0, bool km,
+                    bool live) {
+    constexpr bool NNQ = decltype(nnq)::value, ISP = decltype(is_p)::value;
+    if (l.masked(km, live)) {
 #pragma unroll
-      for (int q = 0; q < LPW; ++q) ld.template issue<NNQ, true>(tile, blk0 + q, k0, kmask, live, lane);
+      for (int q = 0; q < 4; ++q)
+        l.template issue<NNQ, true>(base + 1024 * (ISP ? (blk0 + q) & 15 : blk0 + q), blk0 + q, k0, km, live, lane);
     } else {
 #pragma unroll
-      for (int q = 0; q < LPW; ++q) ld.template issue<NNQ, false>(tile, blk0 + q, k0, kmask, live, lane);
+      for (int q = 0; q < 4; ++q)
+        l.template issue<NNQ, false>(base + 1024 * (ISP ? (blk0 + q) & 15 : blk0 + q), blk0 + q, k0, km, live, lane);
     }
   };
-  auto issue_tile = [&](MLORA_LDS char *tile, bool live) { issue_loads(std::false_type{}, tile, live); };
-  auto issue_q_tile = [&](MLORA_LDS char *tile, bool live) { issue_loads(std::bool_constant<C::NN>{}, tile, live); };
-  // this lane's fragment offsets in substep h (phase-0 layout; see FragAddr)
+  auto issue_q = [&](MLORA_LDS char *base, int k0, bool km, bool live) {
+    issue4(std::bool_constant<C::NN>{}, std::false_type{}, lq, base, qblk0, k0, km, live);
+  };
+  auto issue_p = [&](MLORA_LDS char *base, int k0, bool km, bool live) {
+    issue4(std::false_type{}, std::true_type{}, lp, base, pblk0, k0, km, live);
+  };
+  // this lane's fragment offsets in substep h (P: within a half slot; see FragAddr)
   int32_t fa[NSUB], fb[C::NN ? C::TN : NSUB];
   {
     const int z = swzk<C::CPR>(lane & 31);
 #pragma unroll
     for (int h = 0; h < NSUB; ++h) {
       const int slot = (2 * h + (lane >> 5)) ^ z;
-      fa[h] = (wm0 + (lane & 31)) * C::KB + 16 * slot;
+      fa[h] = ((wm0 & 127) + (lane & 31)) * C::KB + 16 * slot;
       if constexpr (!C::NN) fb[h] = (wn0 + (lane & 31)) * C::KB + 16 * slot;
     }
     if constexpr (C::NN) {
@@ -870,10 +892,10 @@ __device__ __forceinline__ void contract_tile_pp(f32x16 (&acc)[C::TM][C::TN], co
   // immediate of a ds_read): added in the phase that reads, not held across the loop, and kept
   // apart from the immediates that follow
   auto hi = [](int32_t o, int add) -> int32_t { return add == 0 ? o : opaque_vgpr(opaque_vgpr(o) + add); };
-  // all of this wave's fragments of the k-tile in phase PH
-  auto read_tile = [&](auto ph_c) {
+  // all of this wave's fragments of the k-tile in phase PH (P from the half slots at PBASE)
+  auto read_tile = [&](auto ph_c, auto pbase_c) {
     constexpr int PH = decltype(ph_c)::value;
-    constexpr int PO = C::p_off(PH), QO = C::q_off(PH);
+    constexpr int PO = decltype(pbase_c)::value + (PH % 2) * 16384, QO = QB + (PH % 3) * 32768;
     static_for<NSUB>([&](auto h_c) {
       constexpr int H = decltype(h_c)::value;
       const int32_t pa = hi(fa[H], PO & ~65535);
@@ -889,7 +911,7 @@ __device__ __forceinline__ void contract_tile_pp(f32x16 (&acc)[C::TM][C::TN], co
     if constexpr (C::NN) {
       static_for<NSUB>([&](auto h_c) {
         constexpr int H = decltype(h_c)::value;
-        lds_read_tr16<C::TN, 4 * C::QROW>(lds + (C::q_off(PH) + 16 * C::QROW * H), fb, f[H].b);
+        lds_read_tr16<C::TN, 4 * C::QROW>(lds + (QO + 16 * C::QROW * H), fb, f[H].b);
         return true;
       });
     }
@@ -904,73 +926,97 @@ __device__ __forceinline__ void contract_tile_pp(f32x16 (&acc)[C::TM][C::TN], co
       }
   };
   // k-tiles of the main contraction that need no mask (all but a partial last one): the steps
-  // whose loads read only those run in whole periods of a loop of their own, without the walk
-  // and the mask decisions, so the phases that issue loads carry no more than the loads and
-  // reads themselves
+  // whose loads read only those run in a loop of their own, without the walk and the mask
+  // decisions, so the phases that issue loads carry no more than the loads and reads themselves;
+  // the walk takes over, at k-tile t + 1, in the phase where that loop stopped
   const int n_full = STK == 2 ? 0 : args.Kc / bk;
   int t = 0;
   bool done = false;
-  if (qside) {
-    issue_q_tile(lds + C::B_BASE + C::q_off(0), true);
-    wait_vmcnt<0>();
+  // prologue: k-tiles 0 and 1 of this side's loads; the walk ends at k-tile 1
+  issue_q(lds + QB, 0, kmask, true);
+  issue_p(lds + (xside ? PB : PT), 0, kmask, true);
+  const bool live1 = advance();
+  issue_q(lds + QB + 32768, t_in_src * bk, kmask, live1);
+  if (xside) {
+    wait_vmcnt<8>();  // Q(0) blocks 0-15
     phase_barrier();
-    while (t + S + 1 <= n_full) static_for<S>([&](auto st) -> bool {  // loads Q(t+1) .. Q(t+S)
+    bool live_prev = live1;  // whether k-tile t + 1 (the walk's) exists
+    while (t + 2 < n_full) static_for<PER>([&](auto st) -> bool {  // Q(t+2) and Pbot(t+1) main
         constexpr int ST = decltype(st)::value;
-        ++t_in_src;
-        ++n_real;
-#pragma unroll
-        for (int q = 0; q < LPW; ++q)
-          ld.template issue<C::NN, false>(lds + C::B_BASE + C::q_off((ST + 1) % S), blk0 + q, t_in_src * bk, false, true,
-                                          lane);
-        read_tile(st);
+        if (t + 2 >= n_full) return false;
+        issue_q(lds + QB + ((ST + 2) % 3) * 32768, (t + 2) * bk, false, true);
+        issue_p(lds + PB + ((ST + 1) % 2) * 16384, (t + 1) * bk, false, true);
+        read_tile(st, std::integral_constant<int, PT>{});
+        wait_vmcnt<8>();  // this wave's loads of the phase before
         phase_barrier();
         compute();
-        wait_vmcnt<0>();
         phase_barrier();
         ++t;
         return true;
       });
-    while (!done) static_for<S>([&](auto st) -> bool {
+    if (n_full >= 2) {  // the walk at k-tile t + 1 (the main contraction)
+      t_in_src = t + 1;
+      n_real = t + 2;
+    }
+    const int st0 = t % PER;
+    bool first = true;
+    while (!done) static_for<PER>([&](auto st) -> bool {
         constexpr int ST = decltype(st)::value;
-        const bool live = advance();  // Q(t + 1)
-        issue_q_tile(lds + C::B_BASE + C::q_off((ST + 1) % S), live);
-        read_tile(st);
+        if (first && ST < st0) return true;  // the walk starts where the main loop stopped
+        first = false;
+        if (lp_stale) {  // the P loads of this step read k-tile t + 1, the walk's
+          lp.init_p(src, m0, lane);
+          lp_stale = false;
+        }
+        const int k0_p = t_in_src * bk;
+        const bool km_p = kmask, live_p = live_prev;
+        const bool live = advance();  // k-tile t + 2
+        issue_q(lds + QB + ((ST + 2) % 3) * 32768, t_in_src * bk, kmask, live);
+        issue_p(lds + PB + ((ST + 1) % 2) * 16384, k0_p, km_p, live_p);
+        live_prev = live;
+        read_tile(st, std::integral_constant<int, PT>{});
+        wait_vmcnt<8>();
         phase_barrier();
         compute();
-        wait_vmcnt<0>();
         phase_barrier();
         ++t;
         done = t >= n_real;
         return !done;
       });
-    phase_barrier();  // the P side's last MFMA phase
+    phase_barrier();  // Y's last MFMA phase
   } else {
-    issue_tile(lds + C::p_off(0), true);
-    issue_tile(lds + C::p_off(1), advance());
-    wait_vmcnt<LPW>();  // P(0)
+    issue_p(lds + PT + 16384, t_in_src * bk, kmask, live1);
+    wait_vmcnt<8>();  // Q(0) blocks 16-31, Ptop(0)
     phase_barrier();
-    phase_barrier();  // the Q side reads k-tile 0
-    while (t + S + 2 <= n_full) static_for<S>([&](auto st) -> bool {  // loads P(t+2) .. P(t+S+1)
+    phase_barrier();  // X reads k-tile 0
+    while (t + 2 < n_full) static_for<PER>([&](auto st) -> bool {  // Q(t+2) and Ptop(t+2) main
         constexpr int ST = decltype(st)::value;
-        ++t_in_src;
-        ++n_real;
-#pragma unroll
-        for (int q = 0; q < LPW; ++q)
-          ld.template issue<false, false>(lds + C::p_off((ST + 2) % S), blk0 + q, t_in_src * bk, false, true, lane);
-        read_tile(st);
-        wait_vmcnt<LPW>();  // P(t + 1)
+        if (t + 2 >= n_full) return false;
+        issue_q(lds + QB + ((ST + 2) % 3) * 32768, (t + 2) * bk, false, true);
+        issue_p(lds + PT + (ST % 2) * 16384, (t + 2) * bk, false, true);
+        read_tile(st, std::integral_constant<int, PB>{});
+        wait_vmcnt<8>();
         phase_barrier();
         compute();
         phase_barrier();
         ++t;
         return true;
       });
-    while (!done) static_for<S>([&](auto st) -> bool {
+    if (n_full >= 2) {
+      t_in_src = t + 1;
+      n_real = t + 2;
+    }
+    const int st0 = t % PER;
+    bool first = true;
+    while (!done) static_for<PER>([&](auto st) -> bool {
         constexpr int ST = decltype(st)::value;
-        const bool live = advance();  // P(t + 2)
-        issue_tile(lds + C::p_off((ST + 2) % S), live);
-        read_tile(st);
-        wait_vmcnt<LPW>();  // P(t + 1)
+        if (first && ST < st0) return true;
+        first = false;
+        const bool live = advance();  // k-tile t + 2
+        issue_q(lds + QB + ((ST + 2) % 3) * 32768, t_in_src * bk, kmask, live);
+        issue_p(lds + PT + (ST % 2) * 16384, t_in_src * bk, kmask, live);
+        read_tile(st, std::integral_constant<int, PB>{});
+        wait_vmcnt<8>();
         phase_barrier();
         compute();
         phase_barrier();
