@@ -847,18 +847,19 @@ __device__ __forceinline__ void contract_tile_pp(f32x16 (&acc)[C::TM][C::TN], co
     return true;
   };
   // this wave's 4 blocks (from blk0) of a k-tile of loader l into the LDS tile at `base` (P: a
-  // 128-row half slot, block blk at (blk & 15) KB)
+  // 128-row half slot, block blk at (blk & 15) KB). The destinations are this wave's block
+  // offset, taken opaque where it is used, plus constants: one scalar add per load instead of
+  // dozens of precomputed addresses that do not fit the scalar registers.
   auto issue4 = [&](auto nnq, auto is_p, const PPLoad<C> &l, MLORA_LDS char *base, int blk0, int k0, bool km,
                     bool live) {
     constexpr bool NNQ = decltype(nnq)::value, ISP = decltype(is_p)::value;
+    MLORA_LDS char *wb = base + opaque_sgpr(1024 * (ISP ? blk0 & 15 : blk0));
     if (l.masked(km, live)) {
 #pragma unroll
-      for (int q = 0; q < 4; ++q)
-        l.template issue<NNQ, true>(base + 1024 * (ISP ? (blk0 + q) & 15 : blk0 + q), blk0 + q, k0, km, live, lane);
+      for (int q = 0; q < 4; ++q) l.template issue<NNQ, true>(wb + 1024 * q, blk0 + q, k0, km, live, lane);
     } else {
 #pragma unroll
-      for (int q = 0; q < 4; ++q)
-        l.template issue<NNQ, false>(base + 1024 * (ISP ? (blk0 + q) & 15 : blk0 + q), blk0 + q, k0, km, live, lane);
+      for (int q = 0; q < 4; ++q) l.template issue<NNQ, false>(wb + 1024 * q, blk0 + q, k0, km, live, lane);
     }
   };
   auto issue_q = [&](MLORA_LDS char *base, int k0, bool km, bool live) {
