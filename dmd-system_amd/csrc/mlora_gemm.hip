@@ -15,7 +15,8 @@
 // accumulators stay in registers. Operand k-tiles of 32 contraction elements
 // stream through a ring of LDS stages filled by direct-to-LDS loads issued
 // one by one between the MFMAs, STAGES-1 k-tiles ahead (one barrier per
-// k-tile). Global reads use raw buffer
+// k-tile); the 256x256 NT tile instead alternates MFMA-only and load/read
+// phases between the two waves of each SIMD (contract_tile_pp). Global reads use raw buffer
 // resources; out-of-range rows/columns are given an offset past the buffer and
 // read as zero, so tails need no branches. NN operands stay in their natural
 // layout in LDS and are read with the gfx950 transposing LDS read
