@@ -769,6 +769,9 @@ __device__ __forceinline__ void phase_barrier() {
 // whose last reads were in the phase before. Every wave waits for its previous phase's loads at
 // the end of each of its read phases (vmcnt(8)): a load has three phases to land.
 //
+// The last step drains every wave's loads before the last barrier; after it X stages its rows
+// while Y still multiplies, so the epilogue (store_staged) needs no workgroup barrier.
+//
 // The k-tiles are contract_tile's sequence (the main contraction, then the LoRA tiles), walked
 // by both sides; X's P loads trail its walk by one k-tile. Each accumulator takes its MFMAs in
 // the same k order as in contract_tile, so the results are the same bit for bit.
@@ -980,12 +983,14 @@ __device__ __forceinline__ void contract_tile_pp(f32x16 (&acc)[C::TM][C::TN], co
         wait_vmcnt<8>();
         phase_barrier();
         compute();
+        if (t + 1 >= n_real) wait_vmcnt<0>();  // last k-tile: every load drained before the last barrier
         phase_barrier();
         ++t;
         done = t >= n_real;
         return !done;
       });
-    phase_barrier();  // Y's last MFMA phase
+    // no barrier for Y's last MFMA phase: every wave's reads and loads are done, and the
+    // epilogue stages rows 0-127 (X) and 128-255 (Y) without a workgroup barrier
   } else {
     issue_p(lds + PT + 16384, t_in_src * bk, kmask, live1);
     wait_vmcnt<8>();  // Q(0) blocks 16-31, Ptop(0)
@@ -1018,10 +1023,12 @@ __device__ __forceinline__ void contract_tile_pp(f32x16 (&acc)[C::TM][C::TN], co
         issue_q(lds + QB + ((ST + 2) % 3) * 32768, t_in_src * bk, kmask, live);
         issue_p(lds + PT + (ST % 2) * 16384, t_in_src * bk, kmask, live);
         read_tile(st, std::integral_constant<int, PB>{});
-        wait_vmcnt<8>();
+        const bool last = t + 1 >= n_real;
+        if (last) wait_vmcnt<0>();  // every load drained before the last barrier
+        else wait_vmcnt<8>();
         phase_barrier();
         compute();
-        phase_barrier();
+        if (!last) phase_barrier();
         ++t;
         done = t >= n_real;
         return !done;
@@ -1135,7 +1142,10 @@ __device__ __forceinline__ void store_staged(const f32x16 (&acc)[C::TM][C::TN], 
 #pragma unroll
     for (int q = 0; q < C::TN * 4; ++q) b0[q] = cols4<true>(ev.rb, ncol + 8 * q);
   }
-  lds_pipeline_barrier();  // every wave's operand loads have landed and been read
+  // every wave's operand loads have landed and been read (the ping-pong schedule ensures that
+  // for the rows a wave stages by the time it leaves its k-loop)
+  if constexpr (!C::PP) lds_pipeline_barrier();
+  else asm volatile("" ::: "memory");
   const int rowb = (wm0 + l31) * ROWB + 8 * hh;
   const int w8 = wn0 >> 3;
   const int z = l31 % CH;
