@@ -124,9 +124,9 @@ struct GemmCfg {
   // spread over all the substeps before the barrier instead of the first one
   // (fewer loads queued at the texture unit at once: 1-3% per launch).
   static constexpr bool SPREAD = SPREAD_;
-  // PP: the ping-pong schedule of contract_tile_pp (8-wave 256x256 bf16 tiles on the 5-slot ring)
+  // PP: the ping-pong schedule of contract_tile_pp (8-wave 256x256 bf16 NT tiles; its own LDS ring)
   static constexpr bool PP = PP_;
-  static_assert(!PP || (RING5 && !F8 && NW == 8), "the ping-pong schedule runs 8-wave bf16 tiles on the 5-slot ring");
+  static_assert(!PP || (RING5 && !F8 && !NN && NW == 8), "the ping-pong schedule runs 8-wave bf16 NT tiles on the 5-slot ring");
   static constexpr int p_off(int ph) { return RING5 ? ((2 * ph) % 5) * A_BYTES : ph * A_BYTES; }
   static constexpr int q_off(int ph) { return RING5 ? ((2 * ph + 1) % 5) * A_BYTES : ph * B_BYTES; }
   static_assert(LDS_BYTES <= 163840, "the ring must fit the 160 KB of LDS");
@@ -670,10 +670,9 @@ __device__ __forceinline__ void contract_tile(f32x16 (&acc)[C::TM][C::TN], const
   wait_vmcnt<0>();
 }
 
-// Direct-to-LDS loads of one operand for the ping-pong schedule (contract_tile_pp). An operand
-// k-tile of 32 KB is 32 blocks of 1 KB: block blk holds P (or NT Q) rows RPD·blk .. RPD·blk +
-// RPD - 1, or NN Q contraction rows QRPD·blk ..; the lane layout and swizzle are those of Pipe.
-// Every source is bf16 here.
+// Direct-to-LDS loads of one operand for the ping-pong schedule (contract_tile_pp, NT tiles). An
+// operand k-tile of 32 KB is 32 blocks of 1 KB: block blk holds rows RPD·blk .. RPD·blk + RPD - 1
+// of P or Q; the lane layout and swizzle are those of Pipe. Every source is bf16 here.
 template <class C>
 struct PPLoad {
   __amdgpu_buffer_rsrc_t r;
@@ -698,23 +697,9 @@ struct PPLoad {
   __device__ __forceinline__ void init_p(const KSource &s, int m0, int lane) {
     init_rows(s.P + (int64_t)m0 * s.ldp_b, s.ldp_b, s.row_hi - m0, max(s.row_lo, m0) - m0, s.klim, lane);
   }
-  // Q: NT, the Ncols - n0 rows from n0; NN, rows are contraction indices, chunk c of row k at
-  // slot c ^ (4 * (k & 3))
+  // Q: the Ncols - n0 rows from n0
   __device__ __forceinline__ void init_q(const KSource &s, int n0, int Ncols, int lane) {
-    if constexpr (!C::NN) {
-      init_rows(s.Q + (int64_t)n0 * s.ldq_b, s.ldq_b, Ncols - n0, 0, s.klim, lane);
-    } else {
-      klim = s.klim;
-      ld_b = (int32_t)s.ldq_b;
-      p_rows = 0;
-      r = make_rsrc(s.Q + 2 * n0, (int64_t)s.klim * s.ldq_b);
-      const int p = lane % C::QCPR, rl = lane / C::QCPR;
-#pragma unroll
-      for (int par = 0; par < 2; ++par) {
-        const int cc = p ^ (4 * ((C::QRPD * par + rl) & 3));
-        off[par] = (n0 + 8 * cc < Ncols) ? rl * ld_b + 16 * cc : kOOB;
-      }
-    }
+    init_rows(s.Q + (int64_t)n0 * s.ldq_b, s.ldq_b, Ncols - n0, 0, s.klim, lane);
   }
   // Whether a k-tile needs the masks of issue (wave-uniform): rows of an earlier segment, a
   // partial last k-tile, or a tile past the last one. Every main-contraction tile of a whole
@@ -724,26 +709,16 @@ struct PPLoad {
   // out of range: no data moves. MASK: apply the masks (see masked). Lane-derived values other
   // than the offsets are recomputed here (VALU is idle in the phases that issue loads) instead of
   // being held in registers across the k-loop.
-  template <bool NNQ, bool MASK>
+  template <bool MASK>
   __device__ __forceinline__ void issue(MLORA_LDS char *dst, int blk, int k0, bool kmask, bool live, int lane) const {
-    int32_t o = off[blk & 1], soff;
-    if constexpr (!NNQ) {
-      const int row = C::RPD * blk;
-      if constexpr (MASK) {
-        if (p_rows > 0 && row + lane / C::CPR < p_rows) o = kOOB;  // rows of an earlier segment
-        if (kmask && k0 + 8 * chunk(blk & 1, lane) >= klim) o = kOOB;
-        if (!live) o = kOOB;
-      }
-      soff = row * ld_b + 2 * k0;
-    } else {
-      const int row = C::QRPD * blk;
-      if constexpr (MASK) {
-        if (kmask && k0 + row + lane / C::QCPR >= klim) o = kOOB;
-        if (!live) o = kOOB;
-      }
-      soff = (k0 + row) * ld_b;
+    int32_t o = off[blk & 1];
+    const int row = C::RPD * blk;
+    if constexpr (MASK) {
+      if (p_rows > 0 && row + lane / C::CPR < p_rows) o = kOOB;  // rows of an earlier segment
+      if (kmask && k0 + 8 * chunk(blk & 1, lane) >= klim) o = kOOB;
+      if (!live) o = kOOB;
     }
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, dst, 16, o, soff, 0, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, dst, 16, o, row * ld_b + 2 * k0, 0, 0);
   }
 };
 
@@ -778,8 +753,8 @@ __device__ __forceinline__ void phase_barrier() {
 template <class C, int STK = 0>
 __device__ __forceinline__ void contract_tile_pp(f32x16 (&acc)[C::TM][C::TN], const GemmArgs &args,
                                                  MLORA_LDS char *lds, int wm0, int wn0, int m0, int n0, int tid) {
-  static_assert(C::RING5 && !C::F8 && C::NW == 8 && C::NSUB == 4 && C::KB == 128,
-                "8-wave 256x256 bf16 tiles of 128-byte k-tile rows");
+  static_assert(C::RING5 && !C::F8 && !C::NN && C::NW == 8 && C::NSUB == 4 && C::KB == 128,
+                "8-wave 256x256 bf16 NT tiles of 128-byte k-tile rows");
   constexpr int QB = 0, PT = 3 * 32768, PB = PT + 2 * 16384;  // Q slots, P-top and P-bottom half slots
   constexpr int PER = 6;                                      // steps until the slots repeat
   static_assert(PB + 2 * 16384 <= C::LDS_BYTES, "the ring fits the LDS");
@@ -854,42 +829,32 @@ __device__ __forceinline__ void contract_tile_pp(f32x16 (&acc)[C::TM][C::TN], co
   // 128-row half slot, block blk at (blk & 15) KB). The destinations are this wave's block
   // offset, taken opaque where it is used, plus constants: one scalar add per load instead of
   // dozens of precomputed addresses that do not fit the scalar registers.
-  auto issue4 = [&](auto nnq, auto is_p, const PPLoad<C> &l, MLORA_LDS char *base, int blk0, int k0, bool km,
-                    bool live) {
-    constexpr bool NNQ = decltype(nnq)::value, ISP = decltype(is_p)::value;
+  auto issue4 = [&](auto is_p, const PPLoad<C> &l, MLORA_LDS char *base, int blk0, int k0, bool km, bool live) {
+    constexpr bool ISP = decltype(is_p)::value;
     MLORA_LDS char *wb = base + opaque_sgpr(1024 * (ISP ? blk0 & 15 : blk0));
     if (l.masked(km, live)) {
 #pragma unroll
-      for (int q = 0; q < 4; ++q) l.template issue<NNQ, true>(wb + 1024 * q, blk0 + q, k0, km, live, lane);
+      for (int q = 0; q < 4; ++q) l.template issue<true>(wb + 1024 * q, blk0 + q, k0, km, live, lane);
     } else {
 #pragma unroll
-      for (int q = 0; q < 4; ++q) l.template issue<NNQ, false>(wb + 1024 * q, blk0 + q, k0, km, live, lane);
+      for (int q = 0; q < 4; ++q) l.template issue<false>(wb + 1024 * q, blk0 + q, k0, km, live, lane);
     }
   };
   auto issue_q = [&](MLORA_LDS char *base, int k0, bool km, bool live) {
-    issue4(std::bool_constant<C::NN>{}, std::false_type{}, lq, base, qblk0, k0, km, live);
+    issue4(std::false_type{}, lq, base, qblk0, k0, km, live);
   };
   auto issue_p = [&](MLORA_LDS char *base, int k0, bool km, bool live) {
-    issue4(std::false_type{}, std::true_type{}, lp, base, pblk0, k0, km, live);
+    issue4(std::true_type{}, lp, base, pblk0, k0, km, live);
   };
   // this lane's fragment offsets in substep h (P: within a half slot; see FragAddr)
-  int32_t fa[NSUB], fb[C::NN ? C::TN : NSUB];
+  int32_t fa[NSUB], fb[NSUB];
   {
     const int z = swzk<C::CPR>(lane & 31);
 #pragma unroll
     for (int h = 0; h < NSUB; ++h) {
       const int slot = (2 * h + (lane >> 5)) ^ z;
       fa[h] = ((wm0 & 127) + (lane & 31)) * C::KB + 16 * slot;
-      if constexpr (!C::NN) fb[h] = (wn0 + (lane & 31)) * C::KB + 16 * slot;
-    }
-    if constexpr (C::NN) {
-      const int i = lane & 15, h = lane >> 5, g1 = (lane >> 4) & 1;
-      const int m = (i >> 2) & 3;
-#pragma unroll
-      for (int j = 0; j < C::TN; ++j) {
-        const int c = (wn0 + 32 * j + 16 * g1) / 8 + ((i & 3) >> 1);
-        fb[j] = (8 * h + (i >> 2)) * C::QROW + 16 * (c ^ (4 * m)) + 8 * (i & 1);
-      }
+      fb[h] = (wn0 + (lane & 31)) * C::KB + 16 * slot;
     }
   }
   Half<C> f[NSUB];
@@ -906,20 +871,11 @@ __device__ __forceinline__ void contract_tile_pp(f32x16 (&acc)[C::TM][C::TN], co
       const int32_t pa = hi(fa[H], PO & ~65535);
 #pragma unroll
       for (int i = 0; i < C::TM; ++i) f[H].a[i] = *(const lds_u4 *)(lds + pa + (PO & 65535) + 32 * C::KB * i);
-      if constexpr (!C::NN) {
-        const int32_t qa = hi(fb[H], QO & ~65535);
+      const int32_t qa = hi(fb[H], QO & ~65535);
 #pragma unroll
-        for (int j = 0; j < C::TN; ++j) f[H].b[j] = *(const lds_u4 *)(lds + qa + (QO & 65535) + 32 * C::KB * j);
-      }
+      for (int j = 0; j < C::TN; ++j) f[H].b[j] = *(const lds_u4 *)(lds + qa + (QO & 65535) + 32 * C::KB * j);
       return true;
     });
-    if constexpr (C::NN) {
-      static_for<NSUB>([&](auto h_c) {
-        constexpr int H = decltype(h_c)::value;
-        lds_read_tr16<C::TN, 4 * C::QROW>(lds + (QO + 16 * C::QROW * H), fb, f[H].b);
-        return true;
-      });
-    }
   };
   auto compute = [&]() {
 #pragma unroll
