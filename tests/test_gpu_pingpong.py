@@ -1,8 +1,9 @@
 """Edge cases of the 256x256 NT GEMM's ping-pong schedule, against the other tile shapes.
 
 A grid of 20480 x 4096 outputs is 1280 tiles of 256x256, whole rounds of the 256 CUs, so the
-whole launch runs the ping-pong tile; calls on row blocks of 1024 rows (256 tiles of 128x128)
-run the interleaved 128x128 tile. Every output keeps its k order and MFMA sequence in both, so
+whole launch runs the ping-pong tile (N = 4000 adds a last column of partial 256x256 tiles, 16 x 80
+tiles); calls on row blocks of 1024 rows (at most 256 tiles of 128x128) run the interleaved 128x128
+tile. Every output keeps its k order and MFMA sequence in both, so
 they must agree bit for bit. Covered: contractions shorter than two k-tiles (the walk runs from
 the first step), a partial last k-tile, the LoRA-only product (K = 0), LoRA ranks that are not a
 whole number of k-tiles, segment boundaries inside a tile (rows of another segment masked), a
@@ -19,7 +20,7 @@ from oracle import multilora_oracle as O
 pytestmark = pytest.mark.gpu
 
 TOL = 2e-3
-M, N = 20480, 4096
+M = 20480
 SEGS = (7001, 6479, 3000, 4000)   # boundaries inside 256-row tiles
 IDS = (0, 1, -1, 2)               # ranks 128, 64 and 96 (not a whole number of 64-wide k-tiles)
 RANKS = (128, 64, 96)
@@ -40,7 +41,7 @@ def _sub_routing(pkg, routing, r0, r1):
     return pkg.SegmentRouting.from_lengths(lengths, ids)
 
 
-def _operands(dev, K, seed):
+def _operands(dev, K, N, seed):
     g = torch.Generator().manual_seed(seed)
     x = torch.randn(M, K, generator=g).to(torch.bfloat16).to(dev)
     w = (torch.randn(N, K, generator=g) / math.sqrt(max(K, 1))).to(torch.bfloat16).to(dev)
@@ -50,13 +51,14 @@ def _operands(dev, K, seed):
     return x, w, b, h, bs
 
 
-@pytest.mark.parametrize("K", [0, 64, 104, 136, 1000, 1600])
+@pytest.mark.parametrize("K,N", [(0, 4096), (64, 4096), (104, 4096), (136, 4096), (1000, 4096), (1600, 4096),
+                                 (136, 4000), (1000, 4000)])
 @pytest.mark.parametrize("accumulate", [False, True], ids=["store", "accumulate"])
-def test_pingpong_equals_row_blocks(pkg, dev, K, accumulate):
+def test_pingpong_equals_row_blocks(pkg, dev, K, N, accumulate):
     from dmd_system_amd import kernels
     print(f"ping-pong forward M={M} K={K} N={N} accumulate={accumulate}", flush=True)
     routing = pkg.SegmentRouting.from_lengths(SEGS, IDS)
-    x, w, b, h, bs = _operands(dev, K, seed=K + 7 * accumulate)
+    x, w, b, h, bs = _operands(dev, K, N, seed=K + N + 7 * accumulate)
     bias = None if K == 0 else b
     y0 = (torch.randn(M, N, generator=torch.Generator().manual_seed(3)) * 0.5).to(torch.bfloat16).to(dev)
     y = y0.clone() if accumulate else None
